@@ -1,0 +1,270 @@
+"""MoE routing and the expert FFN on the GPU (same API as the reference's
+``python/ccut/blocks/moe.py``), plus the fused quantized expert forward.
+
+Data flow (reference ``blocks/moe.py:1-15``)::
+
+    logits = router(x)                         # [T, E]
+    w, ids = topk_softmax(logits, k)           # ccq_topk_softmax
+    schedule = align(ids)                      # ccq_moe_align: experts in
+                                               # first-appearance order
+    h_e = down_e(silu(gate_e(x)) * up_e(x))    # grouped dequant-GEMM kernels
+    y[t] = sum_s w[t, s] * h_{ids[t,s]}[t]     # ccq_moe_combine
+
+The reference-API functions take numpy (returning numpy, as the reference)
+or CUDA tensors (staying on the device).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ccut import _dev
+from ccut._lib import call, ccq_w4_experts, lib
+from ccut.quant import awq
+
+__all__ = [
+    "topk_softmax",
+    "topk",
+    "route_experts",
+    "expert_ffn",
+    "moe_combine",
+    "shared_expert_add",
+    "moe_align",
+    "W4Experts",
+    "moe_forward_w4",
+]
+
+_MODE_SOFTMAX_ALL, _MODE_TOPK_THEN_SOFTMAX, _MODE_RAW_EXP, _MODE_PLAIN = 0, 1, 2, 3
+
+
+def _route(logits, k: int, mode: int):
+    lg = _dev.to_device(logits, torch.float32)
+    if lg.dim() != 2:
+        raise ValueError(f"router logits must be [T, E], got {tuple(lg.shape)}")
+    T, E = lg.shape
+    w = torch.empty((T, k), dtype=torch.float32, device=lg.device)
+    ids = torch.empty((T, k), dtype=torch.int64, device=lg.device)
+    call("ccq_topk_softmax", lg.data_ptr(), w.data_ptr(), ids.data_ptr(), T, E, k, mode, _dev.stream_ptr())
+    if _dev.is_host(logits):
+        return _dev.to_host(w), _dev.to_host(ids)
+    return w, ids
+
+
+def topk(x, k: int):
+    """Per row top-k (values descending, ties to the lowest index), returns
+    ``(vals [rows, k], idx [rows, k] int64)`` (reference ``moe.py:46-68``)."""
+    vals, idx = _route(x, k, _MODE_PLAIN)
+    if isinstance(x, np.ndarray):
+        vals = vals.astype(x.dtype, copy=False)
+    return vals, idx
+
+
+def topk_softmax(logits, k: int, norm_topk_prob: bool = True):
+    """Routing weights (reference ``moe.py:71-89``): ``norm_topk_prob`` ->
+    softmax over the k largest logits; otherwise global softmax, then the k
+    largest probabilities (not renormalised)."""
+    return _route(logits, k, _MODE_TOPK_THEN_SOFTMAX if norm_topk_prob else _MODE_SOFTMAX_ALL)
+
+
+def route_experts(gate_logits, top_k: int, norm_topk: int):
+    """Fused top-k + softmax (reference ``moe.py:92-119``); ``norm_topk=0``
+    normalises exp of the raw selected logits (it disagrees with
+    ``topk_softmax(norm_topk_prob=False)`` as in the reference)."""
+    return _route(gate_logits, top_k, _MODE_TOPK_THEN_SOFTMAX if norm_topk else _MODE_RAW_EXP)
+
+
+def expert_ffn(x, w_gate, w_up, w_down):
+    """``down(silu(x @ Wg) * (x @ Wu))`` on already-dequantized float32
+    weights ``Wg, Wu [hidden, inter]``, ``Wd [inter, hidden]`` (reference
+    ``moe.py:122-141``).  Library GEMMs + the float64 SiLU kernel."""
+    xd = _dev.to_device(x, torch.float32)
+    g = xd @ _dev.to_device(w_gate, torch.float32)
+    u = xd @ _dev.to_device(w_up, torch.float32)
+    h = torch.empty_like(g)
+    call("ccq_silu_mul", g.data_ptr(), u.data_ptr(), h.data_ptr(), g.numel(), _dev.stream_ptr())
+    y = h @ _dev.to_device(w_down, torch.float32)
+    return _dev.to_host(y) if _dev.is_host(x) else y
+
+
+@dataclass
+class Schedule:
+    """Expert-sorted tile schedule produced by ``ccq_moe_align``."""
+
+    sorted_ids: torch.Tensor   # [max_tiles * tile_m] int32, -1 = padding
+    tile_expert: torch.Tensor  # [max_tiles] int32
+    meta: torch.Tensor         # [2] int32: tiles, distinct experts
+    counts: torch.Tensor       # [E] int32
+    tile_m: int
+
+    def host(self) -> dict:
+        nt = int(self.meta[0].item())
+        return {
+            "num_tiles": nt,
+            "num_experts_active": int(self.meta[1].item()),
+            "sorted_ids": self.sorted_ids[: nt * self.tile_m].cpu().numpy(),
+            "tile_expert": self.tile_expert[:nt].cpu().numpy(),
+            "counts": self.counts.cpu().numpy(),
+        }
+
+
+def moe_align(expert_ids, num_experts: int, tile_m: int = 16) -> Schedule:
+    """Group the T*k assignments by expert (first-appearance order, tokens
+    ascending), padded to ``tile_m`` -- the permutation of the reference's
+    ``moe_combine`` (``moe.py:163-167``)."""
+    ids = _dev.to_device(expert_ids, torch.int64).reshape(-1)
+    n = ids.numel()
+    mt = max(1, lib().ccq_moe_align_max_tiles(n, num_experts, tile_m))
+    dev = ids.device
+    sch = Schedule(torch.empty(mt * tile_m, dtype=torch.int32, device=dev),
+                   torch.empty(mt, dtype=torch.int32, device=dev),
+                   torch.zeros(2, dtype=torch.int32, device=dev),
+                   torch.empty(num_experts, dtype=torch.int32, device=dev), tile_m)
+    call("ccq_moe_align", ids.data_ptr(), n, num_experts, tile_m, sch.sorted_ids.data_ptr(),
+         sch.tile_expert.data_ptr(), sch.meta.data_ptr(), sch.counts.data_ptr(), _dev.stream_ptr())
+    return sch
+
+
+def moe_combine(x, expert_ids, weights, expert_outputs=None, expert_fn=expert_ffn, w_lookup=None):
+    """``y[t] = sum_e w[t,e] * expert_e(x[t])`` with the tokens of each expert
+    batched (reference ``moe.py:144-174``).  The grouping is computed on the
+    GPU; ``expert_fn`` is called once per expert, in first-appearance order,
+    with that expert's rows; the weighted sum is ``ccq_moe_combine``.
+    ``expert_outputs`` is accepted for signature compatibility (the reference
+    ignores it too).  Ids outside ``[0, E)`` contribute nothing."""
+    xd = _dev.to_device(x, torch.float32)
+    ids = _dev.to_device(expert_ids, torch.int64)
+    wts = _dev.to_device(weights, torch.float32)
+    T, H = xd.shape
+    k = ids.shape[1]
+    E = int(ids.max().item()) + 1 if ids.numel() else 1
+    sch = moe_align(ids, max(E, 1), tile_m=1).host()
+    rows = torch.zeros((T * k, H), dtype=torch.float32, device=xd.device)
+    flat = sch["sorted_ids"]
+    pos = 0
+    for eid in _experts_in_order(sch):
+        cnt = int(sch["counts"][eid])
+        a = torch.from_numpy(flat[pos: pos + cnt].astype(np.int64)).to(xd.device)
+        pos += cnt
+        wg, wu, wd = w_lookup(eid)
+        y = expert_fn(xd[a // k], wg, wu, wd)
+        rows[a] = _dev.to_device(y, torch.float32)
+    out = torch.empty((T, H), dtype=torch.float32, device=xd.device)
+    call("ccq_moe_combine", rows.data_ptr(), wts.data_ptr(), out.data_ptr(), 0, T, k, H, _dev.stream_ptr())
+    return _dev.to_host(out) if _dev.is_host(x) else out
+
+
+def _experts_in_order(sch: dict) -> list[int]:
+    """Distinct experts of a tile_m=1 schedule, in first-appearance order."""
+    te = sch["tile_expert"][: sch["num_tiles"]].tolist()
+    order, last = [], None
+    for e in te:
+        if e != last:
+            order.append(e)
+            last = e
+    return order
+
+
+def shared_expert_add(y, shared_out, gate_value: float) -> None:
+    """``y += gate_value * shared_out`` in place (reference ``moe.py:177-179``)."""
+    if isinstance(y, torch.Tensor):
+        y.add_(_dev.to_device(shared_out, y.dtype), alpha=float(gate_value))
+    else:
+        y += gate_value * shared_out
+
+
+# ---------------------------------------------------------------------------
+# fused quantized expert forward (AWQ int4 experts)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class W4Experts:
+    """All experts of one MoE layer, AWQ int4, resident in HBM in the tile
+    layout.  gate/up are ``[hidden -> inter]``, down ``[inter -> hidden]``."""
+
+    w_gate: torch.Tensor
+    z_gate: torch.Tensor
+    s_gate: torch.Tensor
+    w_up: torch.Tensor
+    z_up: torch.Tensor
+    s_up: torch.Tensor
+    w_down: torch.Tensor
+    z_down: torch.Tensor
+    s_down: torch.Tensor
+    num_experts: int
+    hidden: int
+    inter: int
+    group_size: int = 128
+
+    @staticmethod
+    def from_awq(gate: tuple, up: tuple, down: tuple, group_size: int = 128) -> "W4Experts":
+        """Each of ``gate``/``up``/``down`` is ``(qweight [E, K, N/8],
+        qzeros [E, K/G, N/8], scales [E, K/G, N])`` in AWQ layout."""
+        def stack(t, K, N):
+            qw, qz, sc = (_dev.to_device(a) for a in t)
+            E = qw.shape[0]
+            qw = qw.view(torch.int32).reshape(E, K, N // 8)
+            tiled = torch.empty_like(qw)
+            for e in range(E):
+                call("ccq_awq_repack", qw[e].data_ptr(), tiled[e].data_ptr(), K, N, _dev.stream_ptr())
+            if sc.dtype not in (torch.float16, torch.bfloat16):
+                sc = sc.to(torch.float16)
+            return tiled, qz.view(torch.int32).reshape(E, K // group_size, N // 8).contiguous(), sc.contiguous()
+
+        E = _dev.to_device(gate[0]).shape[0]
+        sg = _dev.to_device(gate[2])
+        hidden = sg.shape[1] * group_size
+        inter = sg.shape[2]
+        g = stack(gate, hidden, inter)
+        u = stack(up, hidden, inter)
+        d = stack(down, inter, hidden)
+        return W4Experts(*g, *u, *d, num_experts=E, hidden=hidden, inter=inter, group_size=group_size)
+
+    def descriptor(self) -> ccq_w4_experts:
+        code = 1 if self.s_gate.dtype == torch.float16 else 2
+        return ccq_w4_experts(self.w_gate.data_ptr(), self.z_gate.data_ptr(), self.s_gate.data_ptr(),
+                              self.w_up.data_ptr(), self.z_up.data_ptr(), self.s_up.data_ptr(),
+                              self.w_down.data_ptr(), self.z_down.data_ptr(), self.s_down.data_ptr(),
+                              code, self.num_experts, self.hidden, self.inter, self.group_size)
+
+    @property
+    def bytes_per_expert(self) -> int:
+        ts = (self.w_gate, self.z_gate, self.s_gate, self.w_up, self.z_up, self.s_up, self.w_down, self.z_down,
+              self.s_down)
+        return sum(t.numel() * t.element_size() for t in ts) // self.num_experts
+
+
+def moe_ffn_w4(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, experts: W4Experts,
+               out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Expert FFN + weighted combine for already-routed tokens (one call of
+    ``ccq_moe_w4_ffn``: align, gate/up + SiLU, down, combine)."""
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"activations must be float16 or bfloat16, got {x.dtype}")
+    x = x.contiguous()
+    T, H = x.shape
+    if H != experts.hidden:
+        raise ValueError(f"x has {H} features, experts expect {experts.hidden}")
+    k = ids.shape[1]
+    out_dtype = out_dtype or x.dtype
+    y = torch.empty((T, H), dtype=out_dtype, device=x.device)
+    desc = experts.descriptor()
+    nbytes = lib().ccq_moe_w4_workspace_size(T, k, desc)
+    ws = _dev.workspace("moe_w4", nbytes, x.device)
+    ids = ids.to(torch.int64).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    call("ccq_moe_w4_ffn", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], ids.data_ptr(), weights.data_ptr(),
+         y.data_ptr(), _dev.DTYPE_CODE[out_dtype], T, k, desc, ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
+    return y
+
+
+def moe_forward_w4(x: torch.Tensor, router_logits: torch.Tensor, experts: W4Experts, top_k: int,
+                   norm_topk_prob: bool = True, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Routed MoE layer on AWQ experts: ``topk_softmax`` then the fused FFN
+    (the compute of ``ExpertPipeline.step``, reference
+    ``experts/pipeline.py:145-179``, and ``moe_forward``,
+    ``models/generic.py:361-378``)."""
+    w, ids = topk_softmax(router_logits, top_k, norm_topk_prob)
+    return moe_ffn_w4(x, ids, w, experts, out_dtype)

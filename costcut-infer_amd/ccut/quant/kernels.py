@@ -1,0 +1,107 @@
+"""GPU versions of the reference's quant kernels (``python/ccut/quant/
+kernels.py``), same names and argument meaning.
+
+Each function accepts numpy arrays (then returns / fills numpy, like the
+reference) or CUDA tensors (then stays on the device).  The work runs in
+libccq_hip.so; results are bit-identical to the reference for the codecs and
+dequantizers.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from ccut import _dev
+from ccut._lib import call
+
+__all__ = [
+    "fp8_e4m3_to_float32",
+    "float32_to_fp8_e4m3",
+    "fp8_dequant_row",
+    "fp8_dequant_mat",
+    "int4_dequant_row",
+    "silu_mul_fused",
+    "group_broadcast_scale",
+]
+
+
+def _finish(out_dev: torch.Tensor, like, out=None):
+    """Return on the caller's side: numpy in -> numpy out (or fill ``out``)."""
+    if out is not None:
+        if isinstance(out, torch.Tensor):
+            if out.data_ptr() != out_dev.data_ptr():
+                out.copy_(out_dev.reshape(out.shape))
+            return out
+        np.copyto(out, _dev.to_host(out_dev).reshape(out.shape))
+        return out
+    return _dev.to_host(out_dev) if _dev.is_host(like) else out_dev
+
+
+def fp8_e4m3_to_float32(code):
+    """e4m3fn bytes -> float32 (reference ``kernels.py:52-74``)."""
+    c = _dev.to_device(code, torch.uint8).reshape(-1)
+    out = torch.empty(c.numel(), dtype=torch.float32, device=c.device)
+    call("ccq_fp8_to_f32", c.data_ptr(), out.data_ptr(), c.numel(), _dev.stream_ptr())
+    return _finish(out, code)
+
+
+def float32_to_fp8_e4m3(x):
+    """float32 -> e4m3fn, round-half-up, saturating (reference ``kernels.py:77-123``)."""
+    v = _dev.to_device(x, torch.float32).reshape(-1)
+    out = torch.empty(v.numel(), dtype=torch.uint8, device=v.device)
+    call("ccq_f32_to_fp8", v.data_ptr(), out.data_ptr(), v.numel(), _dev.stream_ptr())
+    return _finish(out, x)
+
+
+def fp8_dequant_mat(w, scale, out):
+    """``out[i,j] = fp8(w[i,j]) * scale[i]`` (reference ``kernels.py:150-171``)."""
+    wd = _dev.to_device(w, torch.uint8)
+    rows, cols = wd.shape
+    sd = _dev.to_device(scale, torch.float32).reshape(-1)
+    if sd.numel() != rows:
+        raise ValueError(f"fp8_dequant_mat: scale has {sd.numel()} entries for {rows} rows")
+    dst = out if (isinstance(out, torch.Tensor) and out.is_cuda and out.is_contiguous()
+                  and out.dtype == torch.float32) else torch.empty((rows, cols), dtype=torch.float32,
+                                                                  device=wd.device)
+    call("ccq_fp8_dequant", wd.data_ptr(), sd.data_ptr(), dst.data_ptr(), rows, cols, _dev.stream_ptr())
+    return _finish(dst, w, out)
+
+
+fp8_dequant_row = fp8_dequant_mat  # identical arithmetic (reference kernels.py:126-147)
+
+
+def int4_dequant_row(packed, scale, out):
+    """Signed-nibble int4 with per-input-column scale (reference ``kernels.py:276-295``)."""
+    pd = _dev.to_device(packed, torch.uint8)
+    sd = _dev.to_device(scale, torch.float32).reshape(-1)
+    rows, cols = pd.shape[0], sd.numel()
+    if cols % 2 or pd.shape[1] < cols // 2:
+        raise ValueError(f"int4_dequant_row: packed {tuple(pd.shape)} does not hold {cols} columns")
+    pd = pd[:, : cols // 2].contiguous()
+    dst = out if (isinstance(out, torch.Tensor) and out.is_cuda and out.is_contiguous()
+                  and out.dtype == torch.float32) else torch.empty((rows, cols), dtype=torch.float32,
+                                                                  device=pd.device)
+    call("ccq_int4_dequant", pd.data_ptr(), sd.data_ptr(), dst.data_ptr(), rows, cols, _dev.stream_ptr())
+    return _finish(dst, packed, out)
+
+
+def silu_mul_fused(gate, up, out):
+    """``out = silu(gate) * up`` computed in float64, stored float32
+    (reference ``kernels.py:219-231``)."""
+    g = _dev.to_device(gate, torch.float32)
+    u = _dev.to_device(up, torch.float32)
+    if g.shape != u.shape:
+        raise ValueError(f"silu_mul_fused: shapes {tuple(g.shape)} and {tuple(u.shape)} differ")
+    dst = out if (isinstance(out, torch.Tensor) and out.is_cuda and out.is_contiguous()
+                  and out.dtype == torch.float32) else torch.empty(g.shape, dtype=torch.float32, device=g.device)
+    call("ccq_silu_mul", g.data_ptr(), u.data_ptr(), dst.data_ptr(), g.numel(), _dev.stream_ptr())
+    return _finish(dst, gate, out)
+
+
+def group_broadcast_scale(scale_groups, group_size: int, out):
+    """``out[i*G + j] = s[i]`` (reference ``kernels.py:258-268``); a layout
+    expansion, done with a device copy."""
+    s = _dev.to_device(scale_groups, torch.float32).reshape(-1)
+    res = s.repeat_interleave(int(group_size))
+    return _finish(res, scale_groups, out)

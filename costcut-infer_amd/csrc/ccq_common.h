@@ -1,0 +1,112 @@
+// Shared device/host helpers for libccq_hip (gfx950 / CDNA4).
+//
+// Conventions of the C ABI (declared in include/ccq.h):
+//   * every entry point returns int: 0 ok, <0 argument error (message in
+//     ccq_last_error()), >0 a hipError_t from a launch;
+//   * all buffers are caller-owned device pointers; launches are ordered on
+//     the caller's stream (a hipStream_t passed as void*); nothing allocates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/ccq.h"
+
+namespace ccq {
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char* fmt, ...);
+int arg_error(const char* fmt, ...);           // sets message, returns CCQ_EINVAL
+int launch_status(const char* what);           // hipGetLastError -> code
+
+#define CCQ_REQUIRE(cond, ...)                                  \
+  do {                                                          \
+    if (!(cond)) return ::ccq::arg_error(__VA_ARGS__);          \
+  } while (0)
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
+
+// ----------------------------------------------------------- vector types --
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
+
+// --------------------------------------------------------- scalar codecs --
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  _Float16 h;
+  uint16_t v = (uint16_t)b;
+  __builtin_memcpy(&h, &v, 2);
+  return (float)h;
+}
+
+// float -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t v;
+  __builtin_memcpy(&v, &h, 2);
+  return v;
+}
+
+// e4m3fn byte -> float (exact).  exp==0: m*2^-9; exp==15,m==7: NaN.
+__device__ __forceinline__ float fp8_e4m3_to_f32(uint32_t b) {
+  uint32_t s = (b & 0x80u) << 24;
+  uint32_t e = (b >> 3) & 0xFu;
+  uint32_t m = b & 0x7u;
+  if (e == 0) {
+    float v = (float)m * 0.001953125f;  // m / 8 * 2^-6
+    return __uint_as_float(__float_as_uint(v) | s);
+  }
+  if (e == 15 && m == 7) return __uint_as_float(0x7fc00000u | s);
+  return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// float -> e4m3fn with round-to-nearest-even, saturating to +-448, NaN->0x7F.
+__device__ __forceinline__ uint32_t f32_to_fp8_rne(float v) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7Fu;
+  if (a >= 0x43e00000u) return sign | 0x7Eu;            // >= 448
+  if (a < 0x3c800000u) {                                 // < 2^-6: subnormal grid m*2^-9
+    float t = __uint_as_float(a) * 512.0f;               // exact scaling
+    float fl = floorf(t);
+    float fr = t - fl;
+    uint32_t m = (uint32_t)fl;
+    if (fr > 0.5f || (fr == 0.5f && (m & 1u))) m += 1;
+    return sign | m;                                     // m == 8 is 0x08 = 2^-6
+  }
+  // normal: keep 3 mantissa bits, RNE on the 20 dropped bits
+  uint32_t e = (a >> 23) - 120u;                         // e4m3 exponent code 1..15
+  uint32_t mant = (a >> 20) & 7u;
+  uint32_t rest = a & 0xFFFFFu;
+  uint32_t code = (e << 3) | mant;
+  if (rest > 0x80000u || (rest == 0x80000u && (mant & 1u))) code += 1;
+  if (code > 0x7Eu) code = 0x7Eu;
+  return sign | code;
+}
+
+// --------------------------------------------------------- wave helpers --
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+template <typename T>
+__device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+}  // namespace ccq

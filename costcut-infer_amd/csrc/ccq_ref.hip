@@ -1,0 +1,247 @@
+// Reference-format kernels: e4m3fn codecs, per-row FP8 dequant, signed-nibble
+// int4 dequant, and the float32 Linear forward on those formats.
+//
+// These reproduce python/ccut/quant/kernels.py bit for bit (dequant, codecs)
+// and quant/weight_only.py / quant/method.py within float32 summation order
+// (the matmuls).  All are HBM-bound streaming kernels.
+#include "ccq_common.h"
+
+#include <math.h>
+
+namespace ccq {
+
+// float -> e4m3fn with the reference's rounding: round-half-UP on the
+// magnitude, |v| >= 464 -> 0x7E, NaN -> 0x7F, sign only for v < 0
+// (kernels.py:77-123).  Works on the bit pattern so that it does not depend
+// on the denormal mode of the float pipeline.
+__device__ __forceinline__ uint32_t f32_to_fp8_halfup(float v) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7Fu;                       // NaN
+  if (a == 0) return 0u;                                   // +0 and -0 -> 0x00
+  uint32_t sign = (u >> 24) & 0x80u;
+  if (a >= 0x43e80000u) return sign | 0x7Eu;               // >= 464
+  if (a < 0x3c800000u) {                                   // < 2^-6
+    if ((a >> 23) == 0) return sign;                       // f32 denormal: rounds to 0
+    float t = __uint_as_float(a) * 512.0f;                 // exact
+    float fl = floorf(t);
+    uint32_t m = (uint32_t)fl + ((t - fl) >= 0.5f ? 1u : 0u);
+    return sign | (m >= 8u ? 0x08u : m);
+  }
+  int e = (int)(a >> 23) - 127;                            // floor(log2 v), exact
+  float m = __uint_as_float((a & 0x007fffffu) | (127u << 23)) - 1.0f;  // v*2^-e - 1, exact
+  float t = m * 8.0f;                                      // exact
+  float fl = floorf(t);
+  uint32_t mant = (uint32_t)fl + ((t - fl) >= 0.5f ? 1u : 0u);
+  int ec = e + 7;
+  if (mant >= 8u) {
+    mant = 0;
+    ec += 1;
+  }
+  if (ec >= 15 && mant > 6u) mant = 6;
+  return sign | (((uint32_t)ec & 0xFu) << 3) | mant;
+}
+
+__global__ void fp8_to_f32_kernel(const uint8_t* __restrict__ code, float* __restrict__ out, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) out[i] = fp8_e4m3_to_f32(code[i]);
+}
+
+__global__ void f32_to_fp8_kernel(const float* __restrict__ x, uint8_t* __restrict__ out, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) out[i] = (uint8_t)f32_to_fp8_halfup(x[i]);
+}
+
+// out[r, c] = fp8(w[r, c]) * scale[r]; one float32 multiply of two exact
+// operands = the reference's float64 product rounded once to float32.
+__global__ void fp8_dequant_kernel(const uint8_t* __restrict__ w, const float* __restrict__ scale,
+                                   float* __restrict__ out, int64_t rows, int64_t cols) {
+  int64_t n = rows * cols;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    int64_t r = i / cols;
+    out[i] = fp8_e4m3_to_f32(w[i]) * scale[r];
+  }
+}
+
+__device__ __forceinline__ float nib_signed(uint32_t v) {
+  int q = (int)(v & 0xFu);
+  return (float)(q >= 8 ? q - 16 : q);
+}
+
+// packed [rows, cols/2]: byte j -> columns 2j (low nibble), 2j+1 (high).
+__global__ void int4_dequant_kernel(const uint8_t* __restrict__ packed, const float* __restrict__ scale,
+                                    float* __restrict__ out, int64_t rows, int64_t cols) {
+  int64_t half = cols / 2;
+  int64_t n = rows * half;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    int64_t r = i / half, j = i - r * half;
+    uint32_t b = packed[i];
+    out[r * cols + 2 * j] = nib_signed(b) * scale[2 * j];
+    out[r * cols + 2 * j + 1] = nib_signed(b >> 4) * scale[2 * j + 1];
+  }
+}
+
+// ----------------------------------------------------------------------------
+// float32 Linear on the reference formats: y[b, r] = sum_c x[b, c] * W[r, c].
+// One wave per output row r (the row of W is contiguous), BB batch rows per
+// pass with the weight element dequantized once per pass.  W elements are
+// formed exactly as the dequant kernels above, then FMA-accumulated in fp32.
+// ----------------------------------------------------------------------------
+constexpr int kLinBB = 8;
+
+template <bool kFp8>
+__global__ __launch_bounds__(256) void ref_linear_f32_kernel(const float* __restrict__ x,
+                                                             const uint8_t* __restrict__ w,
+                                                             const float* __restrict__ scale,
+                                                             float* __restrict__ y, int64_t batch,
+                                                             int64_t in_f, int64_t out_f) {
+  const int lane = lane_id();
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= out_f) return;
+  const int64_t b0 = (int64_t)blockIdx.y * kLinBB;
+  const int nb = (int)min<int64_t>(kLinBB, batch - b0);
+  const int64_t row_bytes = kFp8 ? in_f : in_f / 2;
+  const uint8_t* wr = w + r * row_bytes;
+  float acc[kLinBB];
+#pragma unroll
+  for (int b = 0; b < kLinBB; ++b) acc[b] = 0.f;
+  for (int64_t byte = lane; byte < row_bytes; byte += 64) {
+    uint32_t v = wr[byte];
+    if (kFp8) {
+      const float wv = fp8_e4m3_to_f32(v) * scale[r];  // W[r,c] as fp8_dequant_mat forms it
+      const int64_t c = byte;
+#pragma unroll
+      for (int b = 0; b < kLinBB; ++b)
+        if (b < nb) acc[b] = fmaf(x[(b0 + b) * in_f + c], wv, acc[b]);
+    } else {
+      const int64_t c = 2 * byte;
+      float w0 = nib_signed(v) * scale[c];
+      float w1 = nib_signed(v >> 4) * scale[c + 1];
+#pragma unroll
+      for (int b = 0; b < kLinBB; ++b)
+        if (b < nb) {
+          const float* xr = x + (b0 + b) * in_f + c;
+          acc[b] = fmaf(xr[0], w0, acc[b]);
+          acc[b] = fmaf(xr[1], w1, acc[b]);
+        }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < kLinBB; ++b) {
+    float v = acc[b];
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    acc[b] = v;
+  }
+  if (lane == 0)
+    for (int b = 0; b < nb; ++b) y[(b0 + b) * out_f + r] = acc[b];
+}
+
+// out = g / (1 + exp(-g)) * u in float64, stored float32 (kernels.py:219-231)
+__global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ out,
+                                int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    const double t = (double)g[i];
+    out[i] = (float)((t / (1.0 + exp(-t))) * (double)u[i]);
+  }
+}
+
+__global__ void zero_f32_kernel(float* __restrict__ y, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) y[i] = 0.f;
+}
+
+static int grid_for(int64_t n, int block) {
+  int64_t g = cdiv(n, block);
+  return (int)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
+}
+
+}  // namespace ccq
+
+using namespace ccq;
+
+extern "C" int ccq_fp8_to_f32(const uint8_t* code, float* out, int64_t n, void* stream) {
+  CCQ_REQUIRE(n >= 0, "ccq_fp8_to_f32: n < 0");
+  if (n == 0) return 0;
+  CCQ_REQUIRE(code && out, "ccq_fp8_to_f32: null pointer");
+  hipLaunchKernelGGL(fp8_to_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), code, out, n);
+  return launch_status("ccq_fp8_to_f32");
+}
+
+extern "C" int ccq_f32_to_fp8(const float* x, uint8_t* out, int64_t n, void* stream) {
+  CCQ_REQUIRE(n >= 0, "ccq_f32_to_fp8: n < 0");
+  if (n == 0) return 0;
+  CCQ_REQUIRE(x && out, "ccq_f32_to_fp8: null pointer");
+  hipLaunchKernelGGL(f32_to_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), x, out, n);
+  return launch_status("ccq_f32_to_fp8");
+}
+
+extern "C" int ccq_silu_mul(const float* gate, const float* up, float* out, int64_t n, void* stream) {
+  CCQ_REQUIRE(n >= 0, "ccq_silu_mul: n < 0");
+  if (n == 0) return 0;
+  CCQ_REQUIRE(gate && up && out, "ccq_silu_mul: null pointer");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), gate, up, out, n);
+  return launch_status("ccq_silu_mul");
+}
+
+extern "C" int ccq_fp8_dequant(const uint8_t* w, const float* scale, float* out, int64_t rows, int64_t cols,
+                               void* stream) {
+  CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_fp8_dequant: negative shape");
+  if (rows == 0 || cols == 0) return 0;
+  CCQ_REQUIRE(w && scale && out, "ccq_fp8_dequant: null pointer");
+  hipLaunchKernelGGL(fp8_dequant_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream), w,
+                     scale, out, rows, cols);
+  return launch_status("ccq_fp8_dequant");
+}
+
+extern "C" int ccq_int4_dequant(const uint8_t* packed, const float* scale, float* out, int64_t rows,
+                                int64_t cols, void* stream) {
+  CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_int4_dequant: negative shape");
+  CCQ_REQUIRE(cols % 2 == 0, "ccq_int4_dequant: cols=%lld must be even (2 nibbles per byte)", (long long)cols);
+  if (rows == 0 || cols == 0) return 0;
+  CCQ_REQUIRE(packed && scale && out, "ccq_int4_dequant: null pointer");
+  hipLaunchKernelGGL(int4_dequant_kernel, dim3(grid_for(rows * cols / 2, 256)), dim3(256), 0, as_stream(stream),
+                     packed, scale, out, rows, cols);
+  return launch_status("ccq_int4_dequant");
+}
+
+static int ref_linear(bool fp8, const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
+                      int64_t in_f, int64_t out_f, void* stream, const char* name) {
+  CCQ_REQUIRE(batch >= 0 && in_f >= 0 && out_f >= 0, "%s: negative shape", name);
+  CCQ_REQUIRE(fp8 || in_f % 2 == 0, "%s: in_features=%lld must be even", name, (long long)in_f);
+  if (batch == 0 || out_f == 0) return 0;
+  CCQ_REQUIRE(x && w && scale && y, "%s: null pointer", name);
+  CCQ_REQUIRE(batch <= (int64_t)65535 * kLinBB, "%s: batch too large", name);
+  dim3 grid((unsigned)cdiv(out_f, 4), (unsigned)cdiv(batch, kLinBB));
+  CCQ_REQUIRE(grid.x <= 0x7fffffffu, "%s: out_features too large", name);
+  if (in_f == 0) {  // empty sum; a fill kernel rather than a memset node
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_for(batch * out_f, 256)), dim3(256), 0, as_stream(stream), y,
+                       batch * out_f);
+    return launch_status(name);
+  }
+  if (fp8)
+    hipLaunchKernelGGL(ref_linear_f32_kernel<true>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+                       in_f, out_f);
+  else
+    hipLaunchKernelGGL(ref_linear_f32_kernel<false>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+                       in_f, out_f);
+  return launch_status(name);
+}
+
+extern "C" int ccq_int4_linear_f32(const float* x, const uint8_t* packed, const float* scale, float* y,
+                                   int64_t batch, int64_t in_features, int64_t out_features, void* stream) {
+  return ref_linear(false, x, packed, scale, y, batch, in_features, out_features, stream, "ccq_int4_linear_f32");
+}
+
+extern "C" int ccq_fp8_linear_f32(const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
+                                  int64_t in_features, int64_t out_features, void* stream) {
+  return ref_linear(true, x, w, scale, y, batch, in_features, out_features, stream, "ccq_fp8_linear_f32");
+}

@@ -1,0 +1,397 @@
+// Routing: top-k selection + softmax, expert-sorted tile schedule, combine.
+//
+// topk        reference python/ccut/blocks/moe.py:46-68
+// topk_softmax reference python/ccut/blocks/moe.py:71-89
+// route_experts reference python/ccut/blocks/moe.py:92-119 (norm_topk=0)
+// token grouping reference python/ccut/blocks/moe.py:163-173,
+//               python/ccut/models/generic.py:366-378
+#include "ccq_common.h"
+
+#include <math.h>
+
+namespace ccq {
+
+constexpr int kMaxE = 1024;      // experts per row held in registers (16 per lane)
+constexpr int kMaxK = 16;
+
+// numpy's pairwise float32 summation for n <= 128 elements (the branch
+// numpy takes for the k <= 16 routing weights): 8 interleaved partial sums,
+// combined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then the tail in order.
+__device__ float np_pairwise_sum_small(const float* a, int n) {
+  if (n < 8) {
+    float res = 0.f;  // numpy starts from -0.0; identical for these inputs
+    for (int i = 0; i < n; ++i) res += a[i];
+    return res;
+  }
+  float r[8];
+  for (int j = 0; j < 8; ++j) r[j] = a[j];
+  int i = 8;
+  for (; i < n - (n % 8); i += 8)
+    for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; ++i) res += a[i];
+  return res;
+}
+
+// One wave per token row.  Lane l holds columns l, l+64, ... (<= 16 values).
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restrict__ logits,
+                                                           float* __restrict__ weights,
+                                                           int64_t* __restrict__ ids, int64_t T, int E,
+                                                           int k, int mode) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const float* lr = logits + row * E;
+  const int per = (E + 63) / 64;
+  float v[16];
+  bool used[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    int c = lane + 64 * i;
+    v[i] = (i < per && c < E) ? lr[c] : -INFINITY;
+    used[i] = !(i < per && c < E);  // out-of-range slots never selectable
+  }
+  if (mode == 0) {
+    // p = exp(x - max) / max(sum, 1e-30) in float32 (blocks/moe.py:80-81)
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (!used[i]) m = fmaxf(m, v[i]);
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (!used[i]) {
+        v[i] = expf(v[i] - m);
+        s += v[i];
+      }
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    const float d = fmaxf(s, 1e-30f);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (!used[i]) v[i] = v[i] / d;
+  }
+  // k passes of "first value strictly greater than the running best" with the
+  // best starting at -1e30 (ties -> lowest column; NaN never picked).
+  float sel_v[kMaxK];
+  int sel_i[kMaxK];
+  for (int j = 0; j < k; ++j) {
+    float bv = -1.0e30f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      int c = lane + 64 * i;
+      if (!used[i] && v[i] > bv) {  // per lane columns are increasing
+        bv = v[i];
+        bi = c;
+      }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      float ov = __shfl_xor(bv, off, 64);
+      int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (bi == 0x7fffffff) {  // nothing > -1e30: reference stores (-1e30, -1)
+      bi = -1;                // and its used[-1] = 1 marks the last column
+      bv = -1.0e30f;
+    }
+    const int mark = bi >= 0 ? bi : E - 1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (lane + 64 * i == mark) used[i] = true;
+    sel_v[j] = bv;
+    sel_i[j] = bi;
+  }
+  if (lane != 0) return;
+  float w[kMaxK];
+  if (mode == 0 || mode == 3) {
+    for (int j = 0; j < k; ++j) w[j] = sel_v[j];
+  } else if (mode == 1) {
+    // v = vals - vals.max(); exp; / max(exp.sum(), 1e-30)  (blocks/moe.py:86-88)
+    float m = sel_v[0];
+    for (int j = 1; j < k; ++j) m = fmaxf(m, sel_v[j]);
+    float ex[kMaxK];
+    for (int j = 0; j < k; ++j) ex[j] = expf(sel_v[j] - m);
+    const float d = fmaxf(np_pairwise_sum_small(ex, k), 1e-30f);
+    for (int j = 0; j < k; ++j) w[j] = ex[j] / d;
+  } else {
+    // route_experts norm_topk=0: exp(v)/sum(exp(v)) with a float64 running sum
+    // (blocks/moe.py:114-118)
+    float ex[kMaxK];
+    double s = 0.0;
+    for (int j = 0; j < k; ++j) {
+      ex[j] = expf(sel_v[j]);
+      s += (double)ex[j];
+    }
+    for (int j = 0; j < k; ++j) w[j] = s > 0.0 ? (float)((double)ex[j] / s) : 0.f;
+  }
+  for (int j = 0; j < k; ++j) {
+    weights[row * k + j] = w[j];
+    ids[row * k + j] = sel_i[j];
+  }
+}
+
+// ----------------------------------------------------------------------------
+// moe_align: one workgroup of 16 waves; wave w owns the contiguous segment
+// [w*seg, (w+1)*seg) of the flat assignments, so "segment order, then order
+// inside a segment" is the global order.  Stable ranks inside a 64-lane chunk
+// come from ballot key matching (no atomics decide any position).
+// ----------------------------------------------------------------------------
+constexpr int kAlignWaves = 16;
+
+struct AlignSmem {
+  int cnt[kMaxE];
+  int first[kMaxE];
+  int rank[kMaxE];
+  int base[kMaxE];
+  int inv[kMaxE];
+  int wave_off[kAlignWaves][kMaxE];
+  int wave_flags[kAlignWaves];
+  int nactive;
+};
+
+__device__ __forceinline__ uint64_t match_key(int key, bool valid, int nbits) {
+  uint64_t same = __ballot(valid);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t bal = __ballot(valid && bit);
+    same &= bit ? bal : ~bal;
+  }
+  return valid ? same : 0ull;
+}
+
+__global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restrict__ ids, int n, int E,
+                                                         int tile_m, int32_t* __restrict__ sorted_ids,
+                                                         int32_t* __restrict__ tile_expert,
+                                                         int32_t* __restrict__ meta,
+                                                         int32_t* __restrict__ counts_out) {
+  __shared__ AlignSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int e = tid; e < E; e += 1024) {
+    sm.cnt[e] = 0;
+    sm.first[e] = 0x7fffffff;
+  }
+  for (int e = tid; e < kAlignWaves * E; e += 1024) (&sm.wave_off[0][0])[(e / E) * kMaxE + e % E] = 0;
+  __syncthreads();
+  const int seg = (n + kAlignWaves - 1) / kAlignWaves;
+  const int s0 = min(n, w * seg), s1 = min(n, s0 + seg);
+  // pass A: per-expert counts (total and per wave) and first appearance
+  for (int c = s0; c < s1; c += 64) {
+    const int a = c + lane;
+    int e = -1;
+    if (a < s1) {
+      int64_t v = ids[a];
+      e = (v >= 0 && v < E) ? (int)v : -1;
+    }
+    const bool valid = e >= 0;
+    const uint64_t same = match_key(e, valid, nbits);
+    const uint64_t lower = same & ((1ull << lane) - 1ull);
+    if (valid && lower == 0) {  // leader of its key in this chunk
+      atomicAdd(&sm.cnt[e], __popcll(same));
+      sm.wave_off[w][e] += __popcll(same);  // only this wave writes row w
+      atomicMin(&sm.first[e], a);           // the leader is the lowest index
+    }
+  }
+  __syncthreads();
+  // pass B: expert ranks = order of first appearance
+  int nflags = 0;
+  for (int c = s0; c < s1; c += 64) {
+    const int a = c + lane;
+    bool flag = false;
+    if (a < s1) {
+      int64_t v = ids[a];
+      flag = (v >= 0 && v < E) && sm.first[(int)v] == a;
+    }
+    nflags += __popcll(__ballot(flag));
+  }
+  if (lane == 0) sm.wave_flags[w] = nflags;
+  __syncthreads();
+  {
+    int before = 0;
+    for (int i = 0; i < w; ++i) before += sm.wave_flags[i];
+    for (int c = s0; c < s1; c += 64) {
+      const int a = c + lane;
+      int e = -1;
+      bool flag = false;
+      if (a < s1) {
+        int64_t v = ids[a];
+        if (v >= 0 && v < E) {
+          e = (int)v;
+          flag = sm.first[e] == a;
+        }
+      }
+      const uint64_t fl = __ballot(flag);
+      if (flag) sm.rank[e] = before + __popcll(fl & ((1ull << lane) - 1ull));
+      before += __popcll(fl);
+    }
+  }
+  if (tid == 0) {
+    int tot = 0;
+    for (int i = 0; i < kAlignWaves; ++i) tot += sm.wave_flags[i];
+    sm.nactive = tot;
+  }
+  __syncthreads();
+  const int nactive = sm.nactive;
+  for (int e = tid; e < E; e += 1024) {
+    if (sm.cnt[e] > 0) sm.inv[sm.rank[e]] = e;
+    counts_out[e] = sm.cnt[e];
+  }
+  // per-wave exclusive offsets inside each expert (wave order = global order)
+  for (int e = tid; e < E; e += 1024) {
+    int run = 0;
+    for (int i = 0; i < kAlignWaves; ++i) {
+      const int c = sm.wave_off[i][e];
+      sm.wave_off[i][e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  // padded bases in rank order (serial scan by one wave, nactive <= 1024)
+  if (w == 0) {
+    int carry = 0;
+    for (int r0 = 0; r0 < nactive; r0 += 64) {
+      const int r = r0 + lane;
+      int p = 0;
+      if (r < nactive) p = (int)cdiv(sm.cnt[sm.inv[r]], tile_m) * tile_m;
+      int incl = p;
+      for (int off = 1; off < 64; off <<= 1) {
+        int o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      if (r < nactive) sm.base[sm.inv[r]] = carry + incl - p;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) {
+      meta[0] = carry / tile_m;
+      meta[1] = nactive;
+    }
+  }
+  __syncthreads();
+  // pass C: positions
+  {
+    for (int c = s0; c < s1; c += 64) {
+      const int a = c + lane;
+      int e = -1;
+      if (a < s1) {
+        int64_t v = ids[a];
+        e = (v >= 0 && v < E) ? (int)v : -1;
+      }
+      const bool valid = e >= 0;
+      const uint64_t same = match_key(e, valid, nbits);
+      const int r = __popcll(same & ((1ull << lane) - 1ull));
+      int off = 0;
+      if (valid) off = sm.wave_off[w][e];
+      __builtin_amdgcn_wave_barrier();
+      if (valid) {
+        sorted_ids[sm.base[e] + off + r] = a;
+        if (r == 0) sm.wave_off[w][e] = off + __popcll(same);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  // padding and tile -> expert map
+  for (int i = tid; i < nactive; i += 1024) {
+    const int e = sm.inv[i];
+    const int b = sm.base[e], c = sm.cnt[e];
+    const int p = (int)cdiv(c, tile_m) * tile_m;
+    for (int j = c; j < p; ++j) sorted_ids[b + j] = -1;
+    for (int t = b / tile_m; t < (b + p) / tile_m; ++t) tile_expert[t] = e;
+  }
+}
+
+// y[t, h] = sum_s w[t, s] * rows[t*k + s, h], slot order, float32.  Slots
+// whose id is outside [0, E) (dropped by the schedule) contribute nothing.
+template <int YT>
+__global__ void moe_combine_kernel(const float* __restrict__ rows, const float* __restrict__ wts,
+                                   const int64_t* __restrict__ ids, int64_t E, void* __restrict__ y,
+                                   int64_t T, int k, int64_t H) {
+  const int64_t t = blockIdx.y;
+  for (int64_t h = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; h < H; h += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (int s = 0; s < k; ++s) {
+      if (ids) {
+        int64_t e = ids[t * k + s];
+        if (e < 0 || e >= E) continue;
+      }
+      acc = fmaf(wts[t * k + s], rows[(t * k + s) * H + h], acc);
+    }
+    if (YT == CCQ_F32)
+      ((float*)y)[t * H + h] = acc;
+    else if (YT == CCQ_BF16)
+      ((uint16_t*)y)[t * H + h] = (uint16_t)f32_to_bf16_bits(acc);
+    else
+      ((uint16_t*)y)[t * H + h] = (uint16_t)f32_to_f16_bits(acc);
+  }
+}
+
+int launch_combine(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y, int y_dtype,
+                   int64_t T, int64_t k, int64_t H, hipStream_t st) {
+  dim3 grid((unsigned)imin64(cdiv(H, 256), 64), (unsigned)T);
+  if (y_dtype == CCQ_F32)
+    hipLaunchKernelGGL(moe_combine_kernel<CCQ_F32>, grid, dim3(256), 0, st, rows, wts, ids, E, y, T, (int)k, H);
+  else if (y_dtype == CCQ_BF16)
+    hipLaunchKernelGGL(moe_combine_kernel<CCQ_BF16>, grid, dim3(256), 0, st, rows, wts, ids, E, y, T, (int)k, H);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<CCQ_F16>, grid, dim3(256), 0, st, rows, wts, ids, E, y, T, (int)k, H);
+  return launch_status("moe_combine");
+}
+
+int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
+                     tile_expert, meta, counts);
+  return launch_status("moe_align");
+}
+
+}  // namespace ccq
+
+using namespace ccq;
+
+extern "C" int ccq_topk_softmax(const float* logits, float* weights, int64_t* ids, int64_t T, int64_t E, int64_t k,
+                                int mode, void* stream) {
+  CCQ_REQUIRE(T >= 0, "ccq_topk_softmax: T < 0");
+  CCQ_REQUIRE(E >= 1 && E <= kMaxE, "ccq_topk_softmax: E=%lld outside [1, %d]", (long long)E, kMaxE);
+  CCQ_REQUIRE(k >= 1 && k <= kMaxK && k <= E, "ccq_topk_softmax: k=%lld outside [1, min(%d, E)]", (long long)k,
+              kMaxK);
+  CCQ_REQUIRE(mode >= 0 && mode <= 3, "ccq_topk_softmax: mode=%d not in {0,1,2,3}", mode);
+  if (T == 0) return 0;
+  CCQ_REQUIRE(logits && weights && ids, "ccq_topk_softmax: null pointer");
+  CCQ_REQUIRE(T <= (int64_t)4 * 0x7fffffff, "ccq_topk_softmax: T too large");
+  hipLaunchKernelGGL(topk_softmax_kernel, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, as_stream(stream), logits,
+                     weights, ids, T, (int)E, (int)k, mode);
+  return launch_status("ccq_topk_softmax");
+}
+
+extern "C" int64_t ccq_moe_align_max_tiles(int64_t num_assignments, int64_t num_experts, int64_t tile_m) {
+  if (num_assignments <= 0 || num_experts <= 0 || tile_m <= 0) return 0;
+  return cdiv(num_assignments, tile_m) + (num_assignments < num_experts ? num_assignments : num_experts);
+}
+
+extern "C" int ccq_moe_align(const int64_t* ids, int64_t num_assignments, int64_t num_experts, int64_t tile_m,
+                             int32_t* sorted_ids, int32_t* tile_expert, int32_t* meta, int32_t* counts,
+                             void* stream) {
+  CCQ_REQUIRE(num_assignments >= 0 && num_assignments <= 65536,
+              "ccq_moe_align: num_assignments=%lld outside [0, 65536]", (long long)num_assignments);
+  CCQ_REQUIRE(num_experts >= 1 && num_experts <= kMaxE, "ccq_moe_align: num_experts=%lld outside [1, %d]",
+              (long long)num_experts, kMaxE);
+  CCQ_REQUIRE(tile_m >= 1 && tile_m <= 4096, "ccq_moe_align: tile_m=%lld outside [1, 4096]", (long long)tile_m);
+  CCQ_REQUIRE(meta && counts && (num_assignments == 0 || (ids && sorted_ids && tile_expert)),
+              "ccq_moe_align: null pointer");
+  return launch_align(ids, num_assignments, num_experts, tile_m, sorted_ids, tile_expert, meta, counts,
+                      as_stream(stream));
+}
+
+extern "C" int ccq_moe_combine(const float* rows, const float* weights, void* y, int y_dtype, int64_t T, int64_t k,
+                               int64_t H, void* stream) {
+  CCQ_REQUIRE(T >= 0 && k >= 1 && H >= 0, "ccq_moe_combine: bad shape");
+  CCQ_REQUIRE(y_dtype == CCQ_F32 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F16, "ccq_moe_combine: bad y_dtype");
+  CCQ_REQUIRE(T <= 65535, "ccq_moe_combine: T=%lld > 65535", (long long)T);
+  if (T == 0 || H == 0) return 0;
+  CCQ_REQUIRE(rows && weights && y, "ccq_moe_combine: null pointer");
+  return launch_combine(rows, weights, nullptr, 0, y, y_dtype, T, k, H, as_stream(stream));
+}

@@ -1,0 +1,740 @@
+// AWQ int4 on gfx950: dequant, re-pack into MFMA-ready tiles, the skinny
+// (decode) GEMM and the MoE expert FFN built on it.
+//
+// Tile layout ("T16x128"): the weight W[K, N] (in x out) is stored as tiles of
+// 128 K-rows x 16 N-columns, tile (kt, nt) at dword offset ((nt*KT + kt)*64 +
+// lane)*4, i.e. 1 KiB per tile, one 16-byte slice per lane.  Dword j of lane l
+// holds the 8 nibbles of column n = nt*16 + (l & 15) at
+// k = kt*128 + 32*j + 8*(l >> 4) + e, e = 0..7, element e in nibble
+// (e even ? e/2 : 4 + e/2).  With that order
+//     ((dword >> 4r) & 0x000F000F) | MAGIC        r = 0..3
+// yields the (e = 2r, 2r+1) pair of the B operand of
+// v_mfma_f32_16x16x32_{bf16,f16} as two 16-bit values MAGIC + q, where MAGIC
+// is 128 (bf16 0x4300) or 1024 (fp16 0x6400) -- one VALU op per two weights.
+// A wave-wide 16-byte load of one tile is a fully coalesced 1 KiB transfer
+// that feeds 4 MFMAs (K = 4 x 32).
+//
+// Per quantization group (G = 128 by default) the kernel accumulates
+//     tmp = sum_k x[m,k] * (MAGIC + q[k,n])
+//     acc += s[g,n] * (tmp - (MAGIC + z[g,n]) * Sx[m,g]),  Sx = sum_k x[m,k]
+// which equals sum_k x * (q - z) * s exactly up to float32 rounding; Sx comes
+// from one extra MFMA against a ones operand, already in the accumulator
+// layout.
+#include "ccq_common.h"
+
+#include <math.h>
+
+namespace ccq {
+
+int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st);
+int launch_combine(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y, int y_dtype,
+                   int64_t T, int64_t k, int64_t H, hipStream_t st);
+
+// shift of column 8c + j inside an AWQ word: 4 * AWQ_REVERSE_ORDER[j]
+__device__ __forceinline__ int awq_shift(int j) { return 4 * ((j >> 1) + 4 * (j & 1)); }
+// nibble slot of element e (k offset 0..7) inside a tile dword
+__device__ __forceinline__ int tile_nib(int e) { return (e & 1) ? 4 + (e >> 1) : (e >> 1); }
+
+__device__ __forceinline__ float scale_at(const uint16_t* s, int64_t i, int bf16) {
+  uint32_t b = s[i];
+  return bf16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// ------------------------------------------------------------------ dequant --
+__global__ void awq_dequant_kernel(const uint32_t* __restrict__ qw, const uint32_t* __restrict__ qz,
+                                   const uint16_t* __restrict__ sc, int sbf16, float* __restrict__ out,
+                                   int64_t K, int64_t N, int64_t G) {
+  const int64_t N8 = N / 8, words = K * N8;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = i / N8, c = i - k * N8, g = k / G;
+    const uint32_t w = qw[i], z = qz[g * N8 + c];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int sh = awq_shift(j);
+      const int q = (int)((w >> sh) & 15u) - (int)((z >> sh) & 15u);
+      // |q - z| <= 15 times an 11-bit significand: the float32 product is exact
+      out[k * N + 8 * c + j] = (float)q * scale_at(sc, g * N + 8 * c + j, sbf16);
+    }
+  }
+}
+
+__global__ void awq_repack_kernel(const uint32_t* __restrict__ qw, uint32_t* __restrict__ tiled, int64_t K,
+                                  int64_t N) {
+  const int64_t KT = K / 128, N8 = N / 8, total = (N / 16) * KT * 256;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int j = (int)(idx & 3), l = (int)((idx >> 2) & 63);
+    const int64_t tile = idx >> 8, kt = tile % KT, nt = tile / KT;
+    const int64_t n = nt * 16 + (l & 15);
+    const int sh = awq_shift((int)(n & 7));
+    const int64_t kb = kt * 128 + 32 * j + 8 * (l >> 4);
+    uint32_t o = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o |= ((qw[(kb + e) * N8 + (n >> 3)] >> sh) & 15u) << (4 * tile_nib(e));
+    tiled[idx] = o;
+  }
+}
+
+__global__ void awq_unpack_tiled_kernel(const uint32_t* __restrict__ tiled, uint32_t* __restrict__ qw, int64_t K,
+                                        int64_t N) {
+  const int64_t KT = K / 128, N8 = N / 8, words = K * N8;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = i / N8, c = i - k * N8, kt = k >> 7;
+    const int kk = (int)(k & 127), js = kk >> 5, lq = (kk >> 3) & 3, e = kk & 7;
+    uint32_t o = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t n = 8 * c + j, nt = n >> 4;
+      const int l = lq * 16 + (int)(n & 15);
+      const uint32_t d = tiled[((nt * KT + kt) * 64 + l) * 4 + js];
+      o |= ((d >> (4 * tile_nib(e))) & 15u) << awq_shift(j);
+    }
+    qw[i] = o;
+  }
+}
+
+// ------------------------------------------------------------- MFMA pieces --
+template <typename AT>
+struct Act;
+template <>
+struct Act<__bf16> {
+  using vec = bf16x8;
+  static constexpr uint32_t kMagic2 = 0x43004300u;  // bf16 128.0 twice
+  static constexpr float kMagic = 128.0f;
+  static constexpr uint32_t kOne2 = 0x3F803F80u;
+};
+template <>
+struct Act<_Float16> {
+  using vec = f16x8;
+  static constexpr uint32_t kMagic2 = 0x64006400u;  // fp16 1024.0 twice
+  static constexpr float kMagic = 1024.0f;
+  static constexpr uint32_t kOne2 = 0x3C003C00u;
+};
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <typename AT>
+__device__ __forceinline__ typename Act<AT>::vec dq_b(uint32_t w) {
+  u32x4 r;
+  r[0] = (w & 0x000F000Fu) | Act<AT>::kMagic2;
+  r[1] = ((w >> 4) & 0x000F000Fu) | Act<AT>::kMagic2;
+  r[2] = ((w >> 8) & 0x000F000Fu) | Act<AT>::kMagic2;
+  r[3] = ((w >> 12) & 0x000F000Fu) | Act<AT>::kMagic2;
+  return __builtin_bit_cast(typename Act<AT>::vec, r);
+}
+
+__device__ __forceinline__ void store_val(void* y, int64_t i, float v, int dt) {
+  if (dt == CCQ_F32)
+    reinterpret_cast<float*>(y)[i] = v;
+  else if (dt == CCQ_BF16)
+    reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else
+    reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_f16_bits(v);
+}
+
+// ---------------------------------------------------------- skinny kernel --
+enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ROWS = 2 };
+
+struct SkinnyP {
+  const void* x;
+  int64_t ldx;
+  const int32_t* rows;        // per tile 16 row ids (-1 = padding); null = dense rows
+  int row_div;                // activation row = row id / row_div
+  const int32_t* tile_expert; // expert of each tile; null = single weight
+  const int32_t* meta;        // meta[0] = number of valid tiles; null = gridDim.y
+  const uint32_t* w0;
+  const uint32_t* z0;
+  const uint16_t* s0;
+  const uint32_t* w1;         // second weight (up projection) for EPI_SILU
+  const uint32_t* z1;
+  const uint16_t* s1;
+  int64_t w_es, z_es, s_es;   // per-expert strides (elements)
+  int scale_bf16;
+  void* y;
+  int64_t ldy;
+  int y_dtype;
+  int M, K, N, KT, G;
+  int nblocks, splits, ktps;
+  float* partial;
+  int* counters;
+};
+
+// One wave = one job (nt-block of NB tiles, K-split sp) for one row tile of
+// 16 rows.  grid = (ceil(jobs / 4), row tiles); 4 independent waves per WG.
+template <typename AT, int NB, int GS, int EPI>
+__global__ __launch_bounds__(256) void w4_skinny_kernel(const SkinnyP p) {
+  using V = typename Act<AT>::vec;
+  constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
+  constexpr int NG = 4 / GS;  // quantization groups per 128-row tile
+  const int lane = threadIdx.x & 63;
+  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tile = blockIdx.y;
+  if (job >= p.nblocks * p.splits) return;
+  if (p.meta != nullptr && tile >= p.meta[0]) return;
+  const int nb = job / p.splits;
+  const int sp = job - nb * p.splits;
+  const int ex = p.tile_expert ? p.tile_expert[tile] : 0;
+
+  const int r = lane & 15, kq = lane >> 4;
+  int rid;
+  bool rvalid;
+  if (p.rows) {
+    rid = p.rows[tile * 16 + r];
+    rvalid = rid >= 0;
+  } else {
+    rid = tile * 16 + r;
+    rvalid = rid < p.M;
+  }
+  const AT* xr = reinterpret_cast<const AT*>(p.x) + (int64_t)(rvalid ? rid / p.row_div : 0) * p.ldx + 8 * kq;
+
+  const int kt0 = sp * p.ktps;
+  const int kt1 = min(p.KT, kt0 + p.ktps);
+  const int64_t N8 = p.N >> 3;
+  const uint32_t* wb[NACC];
+  const uint32_t* zb[NACC];
+  const uint16_t* sb[NACC];
+  wb[0] = p.w0 + (int64_t)ex * p.w_es;
+  zb[0] = p.z0 + (int64_t)ex * p.z_es;
+  sb[0] = p.s0 + (int64_t)ex * p.s_es;
+  if (NACC == 2) {
+    wb[NACC - 1] = p.w1 + (int64_t)ex * p.w_es;
+    zb[NACC - 1] = p.z1 + (int64_t)ex * p.z_es;
+    sb[NACC - 1] = p.s1 + (int64_t)ex * p.s_es;
+  }
+  int ncol[NB], zsh[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    ncol[t] = (nb * NB + t) * 16 + (lane & 15);
+    zsh[t] = awq_shift(ncol[t] & 7);
+  }
+
+  f32x4 acc[NACC][NB];
+#pragma unroll
+  for (int q = 0; q < NACC; ++q)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) acc[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 ones_u = {Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2};
+  const V ones = __builtin_bit_cast(V, ones_u);
+
+  for (int kt = kt0; kt < kt1; ++kt) {
+    V a[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (rvalid)
+        a[j] = *reinterpret_cast<const V*>(xr + (int64_t)kt * 128 + 32 * j);
+      else
+        a[j] = __builtin_bit_cast(V, u32x4{0u, 0u, 0u, 0u});
+    }
+    u32x4 wv[NACC][NB];
+#pragma unroll
+    for (int q = 0; q < NACC; ++q)
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+        wv[q][t] = *reinterpret_cast<const u32x4*>(wb[q] + (((int64_t)(nb * NB + t) * p.KT + kt) * 64 + lane) * 4);
+    f32x4 sx[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      sx[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jj = 0; jj < GS; ++jj) sx[g] = mfma16(a[g * GS + jj], ones, sx[g]);
+    }
+#pragma unroll
+    for (int q = 0; q < NACC; ++q)
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int64_t grp = (int64_t)kt * NG + g;
+          const float s = scale_at(sb[q], grp * p.N + ncol[t], p.scale_bf16);
+          const int z = (int)((zb[q][grp * N8 + (ncol[t] >> 3)] >> zsh[t]) & 15u);
+          f32x4 tmp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int jj = 0; jj < GS; ++jj) tmp = mfma16(a[g * GS + jj], dq_b<AT>(wv[q][t][g * GS + jj]), tmp);
+          const float c = Act<AT>::kMagic + (float)z;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[q][t][i] = fmaf(s, fmaf(-c, sx[g][i], tmp[i]), acc[q][t][i]);
+        }
+  }
+
+  // rows held by this lane in the accumulator layout: 4*kq + i
+  int orid[4];
+  bool ovalid[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    orid[i] = __shfl(rid, 4 * kq + i, 64);
+    ovalid[i] = p.rows ? orid[i] >= 0 : orid[i] < p.M;
+  }
+  if (p.splits > 1) {
+    constexpr int TE = 16 * 16 * NB * NACC;
+    const int64_t cidx = (int64_t)tile * p.nblocks + nb;
+    float* part = p.partial + cidx * p.splits * TE;
+#pragma unroll
+    for (int q = 0; q < NACC; ++q)
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (ovalid[i]) part[sp * TE + ((4 * kq + i) * NACC + q) * (16 * NB) + t * 16 + (lane & 15)] = acc[q][t][i];
+    __threadfence();
+    int old = 0;
+    if (lane == 0) old = atomicAdd(&p.counters[cidx], 1);
+    old = __shfl(old, 0, 64);
+    if (old != p.splits - 1) return;
+    __threadfence();
+#pragma unroll
+    for (int q = 0; q < NACC; ++q)
+#pragma unroll
+      for (int t = 0; t < NB; ++t) acc[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < p.splits; ++s)
+#pragma unroll
+      for (int q = 0; q < NACC; ++q)
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (ovalid[i])
+              acc[q][t][i] += __builtin_nontemporal_load(
+                  &part[s * TE + ((4 * kq + i) * NACC + q) * (16 * NB) + t * 16 + (lane & 15)]);
+    if (lane == 0) p.counters[cidx] = 0;  // ready for the next call
+  }
+#pragma unroll
+  for (int t = 0; t < NB; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!ovalid[i]) continue;
+      const int64_t o = (int64_t)orid[i] * p.ldy + ncol[t];
+      if (EPI == EPI_SILU) {
+        const float g = acc[0][t][i], u = acc[NACC - 1][t][i];
+        store_val(p.y, o, g / (1.0f + expf(-g)) * u, p.y_dtype);
+      } else {
+        store_val(p.y, o, acc[0][t][i], p.y_dtype);
+      }
+    }
+}
+
+// --------------------------------------------------------------- planning --
+struct SkinnyPlan {
+  int nb, nblocks, splits, ktps;
+  size_t partial_floats, counters;
+};
+
+// Split-K arrival counters live in a fixed header of kCounterSlots ints at the
+// start of every workspace: a plan only splits K when tiles * nblocks < 2048
+// (fewer jobs than the 2048-wave target), so 2048 slots always suffice, and
+// because the last arriving wave resets its slot, the header is all zero
+// between calls whatever shapes share the workspace.
+constexpr int kCounterSlots = 2048;
+constexpr size_t kCounterBytes = kCounterSlots * sizeof(int);
+
+static SkinnyPlan plan_skinny(int64_t tiles, int64_t K, int64_t N, int nacc, int NB) {
+  SkinnyPlan pl;
+  const int64_t KT = K / 128, NT = N / 16;
+  if (NT % NB) NB = 1;
+  pl.nb = NB;
+  pl.nblocks = (int)(NT / NB);
+  const int64_t per_split = (int64_t)pl.nblocks * (tiles > 0 ? tiles : 1);
+  int64_t splits = cdiv(2048, per_split);  // aim for >= 8 waves per CU
+  if (splits < 1) splits = 1;
+  if (splits > KT) splits = KT;
+  pl.ktps = (int)cdiv(KT, splits);
+  pl.splits = (int)cdiv(KT, pl.ktps);
+  pl.partial_floats = pl.splits > 1 ? (size_t)tiles * pl.nblocks * pl.splits * 256 * NB * nacc : 0;
+  pl.counters = pl.splits > 1 ? (size_t)tiles * pl.nblocks : 0;  // < kCounterSlots
+  return pl;
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// [counter header][partials]
+static size_t plan_bytes(const SkinnyPlan& pl) {
+  return pl.splits > 1 ? kCounterBytes + align256(pl.partial_floats * sizeof(float)) : 0;
+}
+
+template <typename AT, int NB, int EPI>
+static void launch_skinny_gs(const SkinnyP& p, dim3 grid, hipStream_t st) {
+  if (p.G == 128)
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 4, EPI>), grid, dim3(256), 0, st, p);
+  else if (p.G == 64)
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 2, EPI>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 1, EPI>), grid, dim3(256), 0, st, p);
+}
+
+template <int EPI>
+static void launch_skinny(const SkinnyP& p, int x_bf16, int NB, dim3 grid, hipStream_t st) {
+  if (x_bf16) {
+    if (NB == 2)
+      launch_skinny_gs<__bf16, 2, EPI>(p, grid, st);
+    else
+      launch_skinny_gs<__bf16, 1, EPI>(p, grid, st);
+  } else {
+    if (NB == 2)
+      launch_skinny_gs<_Float16, 2, EPI>(p, grid, st);
+    else
+      launch_skinny_gs<_Float16, 1, EPI>(p, grid, st);
+  }
+}
+
+static int gemm_nb(int64_t M) { return M <= 4 ? 1 : 2; }
+
+static bool valid_group(int64_t G) { return G == 32 || G == 64 || G == 128; }
+
+}  // namespace ccq
+
+using namespace ccq;
+
+static int grid1d(int64_t n) {
+  int64_t g = cdiv(n, 256);
+  return (int)(g < 1 ? 1 : (g > 65536 ? 65536 : g));
+}
+
+extern "C" int ccq_awq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, int scale_dtype,
+                               float* out, int64_t K, int64_t N, int64_t group_size, void* stream) {
+  CCQ_REQUIRE(K >= 0 && N >= 0, "ccq_awq_dequant: negative shape");
+  CCQ_REQUIRE(N % 8 == 0, "ccq_awq_dequant: N=%lld not a multiple of 8", (long long)N);
+  CCQ_REQUIRE(group_size > 0 && K % group_size == 0, "ccq_awq_dequant: K=%lld not a multiple of group %lld",
+              (long long)K, (long long)group_size);
+  CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_awq_dequant: scale_dtype must be f16|bf16");
+  if (K == 0 || N == 0) return 0;
+  CCQ_REQUIRE(qweight && qzeros && scales && out, "ccq_awq_dequant: null pointer");
+  hipLaunchKernelGGL(awq_dequant_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
+                     (const uint32_t*)qweight, (const uint32_t*)qzeros, (const uint16_t*)scales,
+                     scale_dtype == CCQ_BF16 ? 1 : 0, out, K, N, group_size);
+  return launch_status("ccq_awq_dequant");
+}
+
+extern "C" int ccq_awq_repack(const int32_t* qweight, int32_t* tiled, int64_t K, int64_t N, void* stream) {
+  CCQ_REQUIRE(K >= 0 && N >= 0, "ccq_awq_repack: negative shape");
+  CCQ_REQUIRE(K % 128 == 0 && N % 16 == 0, "ccq_awq_repack: need K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
+              (long long)K, (long long)N);
+  if (K == 0 || N == 0) return 0;
+  CCQ_REQUIRE(qweight && tiled, "ccq_awq_repack: null pointer");
+  CCQ_REQUIRE((const void*)qweight != (const void*)tiled, "ccq_awq_repack: in-place repack is not supported");
+  hipLaunchKernelGGL(awq_repack_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
+                     (const uint32_t*)qweight, (uint32_t*)tiled, K, N);
+  return launch_status("ccq_awq_repack");
+}
+
+extern "C" int ccq_awq_unpack_tiled(const int32_t* tiled, int32_t* qweight, int64_t K, int64_t N, void* stream) {
+  CCQ_REQUIRE(K >= 0 && N >= 0, "ccq_awq_unpack_tiled: negative shape");
+  CCQ_REQUIRE(K % 128 == 0 && N % 16 == 0, "ccq_awq_unpack_tiled: need K %% 128 == 0 and N %% 16 == 0");
+  if (K == 0 || N == 0) return 0;
+  CCQ_REQUIRE(qweight && tiled, "ccq_awq_unpack_tiled: null pointer");
+  CCQ_REQUIRE((const void*)qweight != (const void*)tiled, "ccq_awq_unpack_tiled: in-place is not supported");
+  hipLaunchKernelGGL(awq_unpack_tiled_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
+                     (const uint32_t*)tiled, (uint32_t*)qweight, K, N);
+  return launch_status("ccq_awq_unpack_tiled");
+}
+
+extern "C" size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || N <= 0 || K % 128 || N % 16) return 0;
+  SkinnyPlan pl = plan_skinny(cdiv(M, 16), K, N, 1, gemm_nb(M));
+  return plan_bytes(pl);
+}
+
+extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, const int32_t* qzeros,
+                           const void* scales, int scale_dtype, void* y, int y_dtype, int64_t M, int64_t K,
+                           int64_t N, int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  CCQ_REQUIRE(M >= 0 && K >= 0 && N >= 0, "ccq_w4_gemm: negative shape");
+  CCQ_REQUIRE(K % 128 == 0 && N % 16 == 0, "ccq_w4_gemm: need K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
+              (long long)K, (long long)N);
+  CCQ_REQUIRE(valid_group(group_size), "ccq_w4_gemm: group_size=%lld not in {32, 64, 128}", (long long)group_size);
+  CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_w4_gemm: x_dtype must be f16|bf16");
+  CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_w4_gemm: scale_dtype must be f16|bf16");
+  CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_w4_gemm: bad y_dtype");
+  CCQ_REQUIRE(cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large for the skinny kernel", (long long)M);
+  if (M == 0 || N == 0) return 0;
+  CCQ_REQUIRE(K > 0, "ccq_w4_gemm: K == 0");
+  CCQ_REQUIRE(x && w_tiled && qzeros && scales && y, "ccq_w4_gemm: null pointer");
+  CCQ_REQUIRE(aligned(x, 16) && aligned(w_tiled, 16), "ccq_w4_gemm: x and w_tiled must be 16-byte aligned");
+  const int64_t tiles = cdiv(M, 16);
+  SkinnyPlan pl = plan_skinny(tiles, K, N, 1, gemm_nb(M));
+  const size_t need = plan_bytes(pl);
+  CCQ_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
+              "ccq_w4_gemm: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  CCQ_REQUIRE(need == 0 || aligned(workspace, 256), "ccq_w4_gemm: workspace must be 256-byte aligned");
+  SkinnyP p = {};
+  p.x = x;
+  p.ldx = K;
+  p.row_div = 1;
+  p.w0 = (const uint32_t*)w_tiled;
+  p.z0 = (const uint32_t*)qzeros;
+  p.s0 = (const uint16_t*)scales;
+  p.scale_bf16 = scale_dtype == CCQ_BF16;
+  p.y = y;
+  p.ldy = N;
+  p.y_dtype = y_dtype;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.N = (int)N;
+  p.KT = (int)(K / 128);
+  p.G = (int)group_size;
+  p.nblocks = pl.nblocks;
+  p.splits = pl.splits;
+  p.ktps = pl.ktps;
+  if (pl.splits > 1) {
+    p.counters = (int*)workspace;
+    p.partial = (float*)((char*)workspace + kCounterBytes);
+  }
+  dim3 grid((unsigned)cdiv((int64_t)pl.nblocks * pl.splits, 4), (unsigned)tiles);
+  launch_skinny<EPI_STORE>(p, x_dtype == CCQ_BF16, pl.nb, grid, as_stream(stream));
+  return launch_status("ccq_w4_gemm");
+}
+
+// ------------------------------------------------------------ MoE W4 FFN --
+namespace {
+
+int check_experts(const ccq_w4_experts* ex, const char* name) {
+  CCQ_REQUIRE(ex != nullptr, "%s: null expert descriptor", name);
+  CCQ_REQUIRE(ex->num_experts >= 1 && ex->num_experts <= 1024, "%s: num_experts=%lld outside [1, 1024]", name,
+              (long long)ex->num_experts);
+  CCQ_REQUIRE(ex->hidden > 0 && ex->inter > 0 && ex->hidden % 128 == 0 && ex->inter % 128 == 0,
+              "%s: hidden=%lld and inter=%lld must be positive multiples of 128", name, (long long)ex->hidden,
+              (long long)ex->inter);
+  CCQ_REQUIRE(valid_group(ex->group_size), "%s: group_size=%lld not in {32, 64, 128}", name,
+              (long long)ex->group_size);
+  CCQ_REQUIRE(ex->scale_dtype == CCQ_F16 || ex->scale_dtype == CCQ_BF16, "%s: scale_dtype must be f16|bf16", name);
+  return 0;
+}
+
+int check_expert_ptrs(const ccq_w4_experts* ex, bool gate_up, const char* name) {
+  if (gate_up) {
+    CCQ_REQUIRE(ex->w_gate && ex->z_gate && ex->s_gate && ex->w_up && ex->z_up && ex->s_up,
+                "%s: null gate/up weight pointer", name);
+    CCQ_REQUIRE(aligned(ex->w_gate, 16) && aligned(ex->w_up, 16), "%s: tiled weights must be 16-byte aligned",
+                name);
+  } else {
+    CCQ_REQUIRE(ex->w_down && ex->z_down && ex->s_down, "%s: null down weight pointer", name);
+    CCQ_REQUIRE(aligned(ex->w_down, 16), "%s: tiled weights must be 16-byte aligned", name);
+  }
+  return 0;
+}
+
+// Scratch of the two grouped stages (split-K partials + arrival counters).
+struct StageLayout {
+  SkinnyPlan gu, dn;
+  size_t off_gu_part, off_gu_cnt, off_dn_part, off_dn_cnt, total;
+};
+
+// [gate/up counter header][down counter header][gate/up partials][down partials]
+// The headers sit at fixed offsets so any shapes may share a workspace.
+StageLayout stage_layout(int64_t max_tiles, const ccq_w4_experts* ex) {
+  StageLayout L;
+  L.gu = plan_skinny(max_tiles, ex->hidden, ex->inter, 2, 1);
+  L.dn = plan_skinny(max_tiles, ex->inter, ex->hidden, 1, 1);
+  size_t o = 0;
+  L.off_gu_cnt = o;
+  o += kCounterBytes;
+  L.off_dn_cnt = o;
+  o += kCounterBytes;
+  L.off_gu_part = o;
+  o += align256(L.gu.partial_floats * 4);
+  L.off_dn_part = o;
+  o += align256(L.dn.partial_floats * 4);
+  L.total = o;
+  return L;
+}
+
+struct MoeLayout {
+  int64_t n, max_tiles;
+  StageLayout st;
+  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, off_stage, total;
+};
+
+MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes) {
+  MoeLayout L;
+  L.n = T * k;
+  L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, 16);
+  L.st = stage_layout(L.max_tiles, ex);
+  size_t o = 0;
+  L.off_stage = o;  // first: its counter headers stay at fixed offsets
+  o += L.st.total;
+  L.off_sorted = o;
+  o += align256((size_t)L.max_tiles * 16 * 4);
+  L.off_tile_expert = o;
+  o += align256((size_t)L.max_tiles * 4);
+  L.off_meta = o;
+  o += 256;
+  L.off_counts = o;
+  o += align256((size_t)ex->num_experts * 4);
+  L.off_inter = o;
+  o += align256((size_t)L.n * ex->inter * x_bytes);
+  L.off_rows = o;
+  o += align256((size_t)L.n * ex->hidden * 4);
+  L.total = o;
+  return L;
+}
+
+SkinnyP grouped_params(const int32_t* sorted_ids, const int32_t* tile_expert, const int32_t* meta,
+                       const ccq_w4_experts* ex) {
+  SkinnyP p = {};
+  p.rows = sorted_ids;
+  p.tile_expert = tile_expert;
+  p.meta = meta;
+  p.scale_bf16 = ex->scale_dtype == CCQ_BF16;
+  p.G = (int)ex->group_size;
+  return p;
+}
+
+int run_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids, const int32_t* tile_expert,
+                const int32_t* meta, int64_t max_tiles, void* inter, const ccq_w4_experts* ex,
+                const StageLayout& L, char* ws, hipStream_t st) {
+  const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
+  SkinnyP p = grouped_params(sorted_ids, tile_expert, meta, ex);
+  p.x = x;
+  p.ldx = H;
+  p.row_div = (int)k;
+  p.w0 = (const uint32_t*)ex->w_gate;
+  p.z0 = (const uint32_t*)ex->z_gate;
+  p.s0 = (const uint16_t*)ex->s_gate;
+  p.w1 = (const uint32_t*)ex->w_up;
+  p.z1 = (const uint32_t*)ex->z_up;
+  p.s1 = (const uint16_t*)ex->s_up;
+  p.w_es = H * I / 8;
+  p.z_es = (H / G) * (I / 8);
+  p.s_es = (H / G) * I;
+  p.y = inter;
+  p.ldy = I;
+  p.y_dtype = x_dtype;
+  p.K = (int)H;
+  p.N = (int)I;
+  p.KT = (int)(H / 128);
+  p.nblocks = L.gu.nblocks;
+  p.splits = L.gu.splits;
+  p.ktps = L.gu.ktps;
+  p.partial = (float*)(ws + L.off_gu_part);
+  p.counters = (int*)(ws + L.off_gu_cnt);
+  dim3 grid((unsigned)cdiv((int64_t)L.gu.nblocks * L.gu.splits, 4), (unsigned)max_tiles);
+  launch_skinny<EPI_SILU>(p, x_dtype == CCQ_BF16, L.gu.nb, grid, st);
+  return launch_status("moe_w4 gate_up");
+}
+
+int run_down(const void* inter, int x_dtype, const int32_t* sorted_ids, const int32_t* tile_expert,
+             const int32_t* meta, int64_t max_tiles, float* rows, const ccq_w4_experts* ex, const StageLayout& L,
+             char* ws, hipStream_t st) {
+  const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
+  SkinnyP d = grouped_params(sorted_ids, tile_expert, meta, ex);
+  d.x = inter;
+  d.ldx = I;
+  d.row_div = 1;
+  d.w0 = (const uint32_t*)ex->w_down;
+  d.z0 = (const uint32_t*)ex->z_down;
+  d.s0 = (const uint16_t*)ex->s_down;
+  d.w_es = I * H / 8;
+  d.z_es = (I / G) * (H / 8);
+  d.s_es = (I / G) * H;
+  d.y = rows;
+  d.ldy = H;
+  d.y_dtype = CCQ_F32;
+  d.K = (int)I;
+  d.N = (int)H;
+  d.KT = (int)(I / 128);
+  d.nblocks = L.dn.nblocks;
+  d.splits = L.dn.splits;
+  d.ktps = L.dn.ktps;
+  d.partial = (float*)(ws + L.off_dn_part);
+  d.counters = (int*)(ws + L.off_dn_cnt);
+  dim3 grid((unsigned)cdiv((int64_t)L.dn.nblocks * L.dn.splits, 4), (unsigned)max_tiles);
+  launch_skinny<EPI_ROWS>(d, x_dtype == CCQ_BF16, L.dn.nb, grid, st);
+  return launch_status("moe_w4 down");
+}
+
+int check_stage_args(const void* a, int x_dtype, const int32_t* sorted_ids, const int32_t* tile_expert,
+                     const int32_t* meta, int64_t max_tiles, const void* out, const ccq_w4_experts* ex,
+                     void* ws, size_t ws_bytes, bool gate_up, const char* name) {
+  int rc = check_experts(ex, name);
+  if (rc) return rc;
+  rc = check_expert_ptrs(ex, gate_up, name);
+  if (rc) return rc;
+  CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "%s: activation dtype must be f16|bf16", name);
+  CCQ_REQUIRE(max_tiles >= 1 && max_tiles <= 65535, "%s: max_tiles=%lld outside [1, 65535]", name,
+              (long long)max_tiles);
+  CCQ_REQUIRE(a && sorted_ids && tile_expert && meta && out, "%s: null pointer", name);
+  CCQ_REQUIRE(aligned(a, 16), "%s: activations must be 16-byte aligned", name);
+  const size_t need = stage_layout(max_tiles, ex).total;
+  CCQ_REQUIRE(need == 0 || (ws && ws_bytes >= need && aligned(ws, 256)),
+              "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", name, need, ws_bytes);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" size_t ccq_moe_w4_stage_workspace_size(int64_t max_tiles, const ccq_w4_experts* ex) {
+  if (max_tiles <= 0 || check_experts(ex, "ccq_moe_w4_stage_workspace_size") != 0) return 0;
+  return stage_layout(max_tiles, ex).total;
+}
+
+extern "C" int ccq_moe_w4_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids,
+                                  const int32_t* tile_expert, const int32_t* meta, int64_t max_tiles, void* inter,
+                                  const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_stage_args(x, x_dtype, sorted_ids, tile_expert, meta, max_tiles, inter, ex, workspace,
+                            workspace_bytes, true, "ccq_moe_w4_gate_up");
+  if (rc) return rc;
+  CCQ_REQUIRE(k >= 1 && k <= ex->num_experts, "ccq_moe_w4_gate_up: k=%lld outside [1, E]", (long long)k);
+  return run_gate_up(x, x_dtype, k, sorted_ids, tile_expert, meta, max_tiles, inter, ex,
+                     stage_layout(max_tiles, ex), (char*)workspace, as_stream(stream));
+}
+
+extern "C" int ccq_moe_w4_down(const void* inter, int x_dtype, const int32_t* sorted_ids, const int32_t* tile_expert,
+                               const int32_t* meta, int64_t max_tiles, float* rows, const ccq_w4_experts* ex,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_stage_args(inter, x_dtype, sorted_ids, tile_expert, meta, max_tiles, rows, ex, workspace,
+                            workspace_bytes, false, "ccq_moe_w4_down");
+  if (rc) return rc;
+  return run_down(inter, x_dtype, sorted_ids, tile_expert, meta, max_tiles, rows, ex, stage_layout(max_tiles, ex),
+                  (char*)workspace, as_stream(stream));
+}
+
+extern "C" size_t ccq_moe_w4_workspace_size(int64_t T, int64_t k, const ccq_w4_experts* ex) {
+  if (T <= 0 || k <= 0 || check_experts(ex, "ccq_moe_w4_workspace_size") != 0) return 0;
+  return moe_layout(T, k, ex, 2).total;
+}
+
+extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights, void* y,
+                              int y_dtype, int64_t T, int64_t k, const ccq_w4_experts* ex, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  int rc = check_experts(ex, "ccq_moe_w4_ffn");
+  if (rc) return rc;
+  CCQ_REQUIRE(T >= 0 && k >= 1 && k <= ex->num_experts, "ccq_moe_w4_ffn: bad T=%lld / k=%lld", (long long)T,
+              (long long)k);
+  CCQ_REQUIRE(T * k <= 65536, "ccq_moe_w4_ffn: T*k=%lld > 65536", (long long)(T * k));
+  CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_moe_w4_ffn: x_dtype must be f16|bf16");
+  CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_moe_w4_ffn: bad y_dtype");
+  CCQ_REQUIRE(T <= 65535, "ccq_moe_w4_ffn: T=%lld > 65535", (long long)T);
+  if (T == 0) return 0;
+  CCQ_REQUIRE(x && ids && weights && y, "ccq_moe_w4_ffn: null pointer");
+  rc = check_expert_ptrs(ex, true, "ccq_moe_w4_ffn");
+  if (rc) return rc;
+  rc = check_expert_ptrs(ex, false, "ccq_moe_w4_ffn");
+  if (rc) return rc;
+  CCQ_REQUIRE(aligned(x, 16), "ccq_moe_w4_ffn: x must be 16-byte aligned");
+  const MoeLayout L = moe_layout(T, k, ex, 2);
+  CCQ_REQUIRE(workspace && workspace_bytes >= L.total && aligned(workspace, 256),
+              "ccq_moe_w4_ffn: workspace of %zu bytes (256-byte aligned) needed, %zu given", L.total,
+              workspace_bytes);
+  hipStream_t st = as_stream(stream);
+  char* ws = (char*)workspace;
+  int32_t* sorted = (int32_t*)(ws + L.off_sorted);
+  int32_t* tile_expert = (int32_t*)(ws + L.off_tile_expert);
+  int32_t* meta = (int32_t*)(ws + L.off_meta);
+  int32_t* counts = (int32_t*)(ws + L.off_counts);
+  void* inter = ws + L.off_inter;
+  float* rows = (float*)(ws + L.off_rows);
+  char* sws = ws + L.off_stage;
+
+  rc = launch_align(ids, L.n, ex->num_experts, 16, sorted, tile_expert, meta, counts, st);
+  if (rc) return rc;
+  rc = run_gate_up(x, x_dtype, k, sorted, tile_expert, meta, L.max_tiles, inter, ex, L.st, sws, st);
+  if (rc) return rc;
+  rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, L.st, sws, st);
+  if (rc) return rc;
+  return launch_combine(rows, weights, ids, ex->num_experts, y, y_dtype, T, k, ex->hidden, st);
+}

@@ -1,0 +1,214 @@
+/*
+ * libccq_hip -- C ABI of the MI355X (gfx950) quantized expert-matmul path.
+ *
+ * The reference (CostCut-Infer) has no FFI: its boundary is a set of Python
+ * callables.  Each entry point below names the reference callable it replaces
+ * (file:line under python/ccut/).  Python binds this header with ctypes
+ * (costcut-infer_amd/ccut/_lib.py).
+ *
+ * Rules common to every entry point:
+ *   - return 0 on success; CCQ_EINVAL / CCQ_EUNSUPPORTED / CCQ_EWORKSPACE
+ *     (< 0) for argument errors, detected on the host before any launch (the
+ *     message is in ccq_last_error(), thread-local); > 0 is a hipError_t
+ *     reported by the launch;
+ *   - every pointer is a caller-allocated DEVICE pointer unless stated;
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream); work is
+ *     stream-ordered and asynchronous; nothing here allocates memory;
+ *   - matrices are row-major and dense (leading dimension = row length).
+ */
+#ifndef CCQ_H_
+#define CCQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CCQ_EINVAL (-1)
+#define CCQ_EUNSUPPORTED (-2)
+#define CCQ_EWORKSPACE (-3)
+
+/* element types of activations / outputs / scales */
+#define CCQ_F32 0
+#define CCQ_F16 1
+#define CCQ_BF16 2
+
+/* library version (major*10000 + minor*100 + patch) */
+int ccq_version(void);
+/* message of the last failed call on this thread ("" if none) */
+const char* ccq_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Reference formats (exact reference semantics, float32 I/O)
+ * ---------------------------------------------------------------------- */
+
+/* e4m3fn bytes -> float32, n elements.
+ * Replaces fp8_e4m3_to_float32 (quant/kernels.py:52-74). */
+int ccq_fp8_to_f32(const uint8_t* code, float* out, int64_t n, void* stream);
+
+/* float32 -> e4m3fn with the reference's round-half-up, saturation to 448
+ * (>= 464), NaN -> 0x7F, -0.0 -> 0x00.
+ * Replaces float32_to_fp8_e4m3 (quant/kernels.py:77-123). */
+int ccq_f32_to_fp8(const float* x, uint8_t* out, int64_t n, void* stream);
+
+/* out[r,c] = fp8(w[r,c]) * scale[r]   (w [rows,cols] e4m3fn, scale [rows]).
+ * Replaces fp8_dequant_mat / fp8_dequant_row (quant/kernels.py:126-171). */
+int ccq_fp8_dequant(const uint8_t* w, const float* scale, float* out,
+                    int64_t rows, int64_t cols, void* stream);
+
+/* out = gate / (1 + exp(-gate)) * up, computed in float64, stored float32.
+ * Replaces silu_mul_fused (quant/kernels.py:219-231). */
+int ccq_silu_mul(const float* gate, const float* up, float* out, int64_t n, void* stream);
+
+/* Reference int4: signed nibbles, low nibble first, one scale per INPUT column.
+ * packed [rows, cols/2] u8, scale [cols] f32 -> out [rows, cols] f32.
+ * Replaces int4_dequant_row (quant/kernels.py:276-295). */
+int ccq_int4_dequant(const uint8_t* packed, const float* scale, float* out,
+                     int64_t rows, int64_t cols, void* stream);
+
+/* y[b, r] = sum_c x[b,c] * W[r,c] in float32, W dequantized on the fly exactly
+ * as ccq_int4_dequant.  x [batch, in] f32, packed [out, in/2], y [batch, out].
+ * Replaces WeightOnlyMethod.apply (quant/weight_only.py:37-54). */
+int ccq_int4_linear_f32(const float* x, const uint8_t* packed, const float* scale,
+                        float* y, int64_t batch, int64_t in_features,
+                        int64_t out_features, void* stream);
+
+/* y[b, r] = sum_c x[b,c] * fp8(w[r,c]) * scale[r] in float32.
+ * Replaces LinearMethod.apply w8a16 / w8a8 (quant/method.py:100-140) and
+ * Fp8LinearMethod.apply (quant/fp8.py:33). */
+int ccq_fp8_linear_f32(const float* x, const uint8_t* w, const float* scale,
+                       float* y, int64_t batch, int64_t in_features,
+                       int64_t out_features, void* stream);
+
+/* ------------------------------------------------------------------------
+ * AWQ int4 (qweight int32 [K, N/8] AWQ order, qzeros int32 [K/G, N/8],
+ * scales f16|bf16 [K/G, N]; W[k,n] = (q - z) * s; y = x @ W)
+ * The reference only names these tensors (quant/compressed_tensors.py:209-211)
+ * and has no arithmetic for them; these entry points sit behind the same
+ * QuantizeMethodBase.apply boundary (quant/method.py:45-58).
+ * ---------------------------------------------------------------------- */
+
+/* W [K, N] float32, bit-exact (q - z) * s.  scale_dtype CCQ_F16 | CCQ_BF16. */
+int ccq_awq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                    int scale_dtype, float* out, int64_t K, int64_t N,
+                    int64_t group_size, void* stream);
+
+/* Re-pack qweight [K, N/8] into the gfx950 tile layout used by every GEMM
+ * below (same byte count: K*N/2).  Requires K % 128 == 0, N % 16 == 0.
+ * Load-time step, the hook of QuantizeMethodBase.process_weights_after_loading
+ * (quant/method.py:60-62).  `tiled` must not alias `qweight`. */
+int ccq_awq_repack(const int32_t* qweight, int32_t* tiled, int64_t K, int64_t N,
+                   void* stream);
+
+/* Inverse of ccq_awq_repack (test/export helper). */
+int ccq_awq_unpack_tiled(const int32_t* tiled, int32_t* qweight, int64_t K, int64_t N,
+                         void* stream);
+
+/* Bytes of workspace ccq_w4_gemm needs for this shape (0 if none).  The
+ * workspace must be zero-filled once before first use; every call leaves it
+ * zero again. */
+size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N);
+
+/* y [M, N] = x [M, K] @ dequant(W) with fp32 accumulation.
+ * x_dtype CCQ_F16 | CCQ_BF16; scale_dtype CCQ_F16 | CCQ_BF16;
+ * y_dtype CCQ_F16 | CCQ_BF16 | CCQ_F32.  w_tiled from ccq_awq_repack.
+ * group_size in {32, 64, 128}.  x must be 16-byte aligned.
+ * Replaces WeightOnlyMethod.apply (quant/weight_only.py:37-54) for AWQ. */
+int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled,
+                const int32_t* qzeros, const void* scales, int scale_dtype,
+                void* y, int y_dtype, int64_t M, int64_t K, int64_t N,
+                int64_t group_size, void* workspace, size_t workspace_bytes,
+                void* stream);
+
+/* ------------------------------------------------------------------------
+ * Routing and token grouping
+ * ---------------------------------------------------------------------- */
+
+/* Top-k routing weights.  logits [T, E] f32 -> weights [T, k] f32,
+ * ids [T, k] int64.  mode 1: top-k of the logits then softmax over the k
+ * (topk_softmax norm_topk_prob=True, blocks/moe.py:84-89); mode 0: softmax
+ * over all E then top-k of the probabilities (norm_topk_prob=False,
+ * blocks/moe.py:79-83); mode 2: exp(v)/sum(exp(v)) over the k raw logits
+ * (route_experts norm_topk=0, blocks/moe.py:113-118); mode 3: plain top-k,
+ * weights = the selected logits (topk, blocks/moe.py:46-68).  Selection is
+ * topk (blocks/moe.py:46-68): strict '>', ties to the lowest index.
+ * E <= 1024, 1 <= k <= 16, k <= E. */
+int ccq_topk_softmax(const float* logits, float* weights, int64_t* ids,
+                     int64_t T, int64_t E, int64_t k, int mode, void* stream);
+
+/* Upper bound of the number of tiles ccq_moe_align can emit. */
+int64_t ccq_moe_align_max_tiles(int64_t num_assignments, int64_t num_experts, int64_t tile_m);
+
+/* Expert-sorted, tile-padded schedule of the T*k assignments (a = t*k+slot).
+ * Experts in first-appearance order (t ascending, then slot), assignments
+ * ascending within an expert: the permutation of moe_combine
+ * (blocks/moe.py:163-167) and moe_forward (models/generic.py:366-370).
+ * Outputs: sorted_ids [max_tiles*tile_m] int32 (-1 = padding),
+ * tile_expert [max_tiles] int32, meta[0] = number of tiles,
+ * meta[1] = number of distinct experts, counts [E] int32 per expert.
+ * ids outside [0, E) are dropped.  num_assignments <= 65536, E <= 1024. */
+int ccq_moe_align(const int64_t* ids, int64_t num_assignments, int64_t num_experts,
+                  int64_t tile_m, int32_t* sorted_ids, int32_t* tile_expert,
+                  int32_t* meta, int32_t* counts, void* stream);
+
+/* y[t, :] = sum_{s<k} weights[t,s] * rows[t*k+s, :]   (slot order, fp32 sum).
+ * rows [T*k, H] f32; y dtype CCQ_F32 | CCQ_BF16 | CCQ_F16.
+ * The weighted combine of moe_combine (blocks/moe.py:172-173). */
+int ccq_moe_combine(const float* rows, const float* weights, void* y, int y_dtype,
+                    int64_t T, int64_t k, int64_t H, void* stream);
+
+/* ------------------------------------------------------------------------
+ * MoE expert FFN, AWQ int4 experts (gate/up [H -> I], down [I -> H])
+ * Weights of all E experts are stacked: w_gate/w_up tiled [E][H*I/8] int32,
+ * z_gate/z_up [E][H/G][I/8], s_gate/s_up [E][H/G][I]; w_down [E][I*H/8],
+ * z_down [E][I/G][H/8], s_down [E][I/G][H].
+ * Replaces expert_ffn (blocks/moe.py:122-141) + moe_combine
+ * (blocks/moe.py:144-174) as called by ExpertPipeline.step
+ * (experts/pipeline.py:155-179) and moe_forward (models/generic.py:348-378).
+ * ---------------------------------------------------------------------- */
+
+typedef struct ccq_w4_experts {
+  const int32_t* w_gate; const int32_t* z_gate; const void* s_gate;
+  const int32_t* w_up;   const int32_t* z_up;   const void* s_up;
+  const int32_t* w_down; const int32_t* z_down; const void* s_down;
+  int scale_dtype;           /* CCQ_F16 | CCQ_BF16 */
+  int64_t num_experts, hidden, inter, group_size;
+} ccq_w4_experts;
+
+/* Stage entry points of ccq_moe_w4_ffn, for callers that build the schedule
+ * themselves with ccq_moe_align (tile_m = 16, max_tiles from
+ * ccq_moe_align_max_tiles).  Rows are assignments a = t*k + slot.
+ * gate_up: inter[a, :] = silu(x[a/k] @ Wg_e) * (x[a/k] @ Wu_e), x_dtype out.
+ * down:    rows[a, :]  = inter[a] @ Wd_e, float32.
+ * The stage workspace (size below) must be zero-filled once before first use;
+ * every call leaves it zero again.  Calls sharing one workspace must not
+ * overlap in time. */
+size_t ccq_moe_w4_stage_workspace_size(int64_t max_tiles, const ccq_w4_experts* ex);
+int ccq_moe_w4_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids,
+                       const int32_t* tile_expert, const int32_t* meta, int64_t max_tiles,
+                       void* inter, const ccq_w4_experts* ex, void* workspace,
+                       size_t workspace_bytes, void* stream);
+int ccq_moe_w4_down(const void* inter, int x_dtype, const int32_t* sorted_ids,
+                    const int32_t* tile_expert, const int32_t* meta, int64_t max_tiles,
+                    float* rows, const ccq_w4_experts* ex, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for ccq_moe_w4_ffn (zero-filled once before first use;
+ * every call leaves its counters zero again). */
+size_t ccq_moe_w4_workspace_size(int64_t T, int64_t k, const ccq_w4_experts* ex);
+
+/* Full MoE FFN from routing: x [T, H] (x_dtype CCQ_BF16 | CCQ_F16),
+ * ids [T, k] int64 and weights [T, k] f32 (from ccq_topk_softmax),
+ * y [T, H] (y_dtype CCQ_BF16 | CCQ_F16 | CCQ_F32). */
+int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights,
+                   void* y, int y_dtype, int64_t T, int64_t k,
+                   const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CCQ_H_ */

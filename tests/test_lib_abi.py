@@ -1,0 +1,119 @@
+"""The C ABI (include/ccq.h): the library loads, exports every declared
+symbol, binds every signature, and rejects bad arguments on the host before
+touching a GPU (no device is needed for any call in this file)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ccq.h"
+
+
+def declared() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(ccq_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declares_the_path():
+    names = declared()
+    for must in ("ccq_w4_gemm", "ccq_awq_repack", "ccq_awq_dequant", "ccq_topk_softmax", "ccq_moe_align",
+                 "ccq_moe_w4_ffn", "ccq_int4_linear_f32", "ccq_fp8_linear_f32", "ccq_f32_to_fp8"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(built_lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(built_lib)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (ccq_\w+)", out))
+    missing = declared() - exported
+    assert not missing, f"declared but not exported: {sorted(missing)}"
+
+
+def test_ctypes_binding_covers_header(built_lib):
+    from ccut import _lib
+
+    assert set(_lib.SIGNATURES) == declared()
+    lib = _lib.lib()
+    assert lib.ccq_version() >= 100
+    assert isinstance(_lib.last_error(), str)
+
+
+@pytest.fixture(scope="module")
+def lib(built_lib):
+    from ccut import _lib
+
+    return _lib.lib()
+
+
+def test_w4_gemm_rejects_bad_shapes(lib):
+    from ccut._lib import CCQ_BF16, CCQ_EINVAL, CCQ_F16, last_error
+
+    p = ctypes.c_void_p(16)  # never dereferenced: validation comes first
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 100, 64, 128, None, 0, None)
+    assert rc == CCQ_EINVAL and "K % 128" in last_error()
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 96, None, 0, None)
+    assert rc == CCQ_EINVAL and "group_size" in last_error()
+    rc = lib.ccq_w4_gemm(p, 7, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0, None)
+    assert rc == CCQ_EINVAL and "x_dtype" in last_error()
+    rc = lib.ccq_w4_gemm(None, CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0, None)
+    assert rc == CCQ_EINVAL and "null" in last_error()
+    rc = lib.ccq_w4_gemm(ctypes.c_void_p(18), CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0,
+                         None)
+    assert rc == CCQ_EINVAL and "aligned" in last_error()
+    # M == 0 is an empty product: success without a launch
+    assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None, 0, None) == 0
+
+
+def test_w4_gemm_workspace_contract(lib):
+    from ccut._lib import CCQ_F16, CCQ_EINVAL, last_error
+
+    need = lib.ccq_w4_gemm_workspace_size(1, 2048, 5632)
+    assert need > 0 and need % 256 == 0
+    assert lib.ccq_w4_gemm_workspace_size(1, 100, 64) == 0
+    p = ctypes.c_void_p(256)
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 2048, 5632, 128, p, need - 1, None)
+    assert rc == CCQ_EINVAL and "workspace" in last_error()
+
+
+def test_routing_rejects_bad_args(lib):
+    from ccut._lib import CCQ_EINVAL, last_error
+
+    p = ctypes.c_void_p(256)
+    assert lib.ccq_topk_softmax(p, p, p, 4, 2000, 4, 1, None) == CCQ_EINVAL and "E=" in last_error()
+    assert lib.ccq_topk_softmax(p, p, p, 4, 64, 17, 1, None) == CCQ_EINVAL
+    assert lib.ccq_topk_softmax(p, p, p, 4, 64, 8, 9, None) == CCQ_EINVAL and "mode" in last_error()
+    assert lib.ccq_topk_softmax(p, p, p, 0, 64, 8, 1, None) == 0
+    assert lib.ccq_moe_align(p, 10, 8, 0, p, p, p, p, None) == CCQ_EINVAL
+    assert lib.ccq_moe_align(p, 70000, 8, 16, p, p, p, p, None) == CCQ_EINVAL
+    assert lib.ccq_moe_align_max_tiles(96, 64, 16) == 6 + 64
+    assert lib.ccq_moe_align_max_tiles(6, 64, 16) == 1 + 6
+    assert lib.ccq_moe_combine(p, p, p, 9, 2, 2, 8, None) == CCQ_EINVAL
+
+
+def test_reference_format_rejects(lib):
+    from ccut._lib import CCQ_EINVAL, last_error
+
+    p = ctypes.c_void_p(256)
+    assert lib.ccq_int4_dequant(p, p, p, 3, 7, None) == CCQ_EINVAL and "even" in last_error()
+    assert lib.ccq_int4_linear_f32(p, p, p, p, 2, 7, 4, None) == CCQ_EINVAL
+    assert lib.ccq_fp8_dequant(p, p, p, -1, 4, None) == CCQ_EINVAL
+    assert lib.ccq_awq_repack(p, p, 128, 24, None) == CCQ_EINVAL
+    assert lib.ccq_awq_repack(p, p, 128, 32, None) == CCQ_EINVAL and "in-place" in last_error()
+    assert lib.ccq_awq_dequant(p, p, p, 1, p, 130, 64, 128, None) == CCQ_EINVAL
+
+
+def test_moe_w4_descriptor_validation(lib):
+    from ccut._lib import CCQ_EINVAL, ccq_w4_experts, last_error
+
+    ex = ccq_w4_experts(*([256] * 9), 1, 64, 2048, 1400, 128)  # inter not a multiple of 128
+    p = ctypes.c_void_p(256)
+    assert lib.ccq_moe_w4_ffn(p, 2, p, p, p, 2, 1, 6, ctypes.byref(ex), p, 1 << 30, None) == CCQ_EINVAL
+    assert "multiples of 128" in last_error()
+    ex.inter = 1408
+    assert lib.ccq_moe_w4_workspace_size(16, 6, ctypes.byref(ex)) > 0
