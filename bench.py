@@ -5,16 +5,23 @@ Headline workload: int4 (AWQ, group 128) MoE expert FFN decode -- 64 experts,
 top-6 routing from softmax of N(0,1) router logits over [T, 64], hidden 2048,
 expert intermediate 1408, bf16 activations, T = 16 tokens.  One step is one
 MoE layer: top-k softmax -> expert schedule -> gate/up (+SiLU*up) -> down ->
-weighted combine.  Steps rotate over 4 distinct layer weight sets (1.15 GB)
-so the 256 MiB Infinity Cache cannot serve repeated weights.  ``value`` is
-algorithmic bytes (weights of the experts actually routed + activations)
-per second of wall time for whole steps, inputs resident in HBM.
+weighted combine, replayed from a HIP graph.  Steps rotate over 4 distinct
+layer weight sets (1.15 GB) so the 256 MiB Infinity Cache cannot serve
+repeated weights.  ``value`` is algorithmic bytes (weights of the experts
+actually routed + activations) per second of wall time for whole steps, with
+inputs resident in HBM.
+
+``roofline`` is the dominant kernel of the step (the fused gate/up + SiLU
+dequant-GEMM): algorithmic bytes per launch / its average device time.
+Kernel device times come from :func:`device_time`: a spin kernel holds the
+stream while the host enqueues all launches, so they run back to back and
+the HIP events on that stream bracket device time only.
 
 Also reported (``extra``): the same layer at T=1, the AWQ skinny GEMM at
-K=4096 N=14336 M in {1,4,16} and the single AWQ GEMV K=2048 N=5632, each as
-kernel GB/s from HIP events.  ``cpu_baseline`` times the reference's
-algorithm (the CPU oracle: per-call dequant to float32, BLAS matmuls,
-per-expert grouping) on a bounded sample.
+K=4096 N=14336 M in {1,4,16} and the single AWQ GEMV K=2048 N=5632 (kernel
+GB/s).  ``cpu_baseline`` times the reference's algorithm (the CPU oracle:
+per-call dequant to float32, BLAS matmuls, per-expert grouping) on a
+bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -22,6 +29,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -39,6 +47,7 @@ PEAK_FP8 = 5.0332e15       # dense fp8 MFMA FLOP/s
 
 E, TOPK, HID, INTER, GROUP = 64, 6, 2048, 1408, 128
 LAYERS = 4
+METRIC = "int4 MoE decode GB/s (% HBM peak) + FP8/int4 prefill TFLOP/s (% MFMA peak)"
 
 
 def parse():
@@ -47,7 +56,6 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--tokens", type=int, default=16)
-    ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     return ap.parse_args()
@@ -57,6 +65,56 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# ---------------------------------------------------------------- timing --
+_SLEEP_CYCLES_PER_MS: float | None = None
+
+
+def _sleep_calibration() -> float:
+    """Cycles of ``torch.cuda._sleep`` per millisecond on this device."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        import torch
+
+        n = 1_000_000
+        torch.cuda._sleep(n)  # warm
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        torch.cuda._sleep(n)
+        b.record()
+        b.synchronize()
+        _SLEEP_CYCLES_PER_MS = n / max(a.elapsed_time(b), 1e-3)
+    return _SLEEP_CYCLES_PER_MS
+
+
+def device_time(launches, reps: int = 1) -> float:
+    """Average device seconds per launch of ``launches`` (callables that each
+    enqueue one kernel on the current stream), run back to back ``reps``
+    times.  The stream is held by a spin kernel while the host enqueues, and
+    the hold is lengthened until it outlasts the host's enqueue time."""
+    import torch
+
+    n = len(launches) * reps
+    hold_ms = 5.0
+    for _ in range(6):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        torch.cuda._sleep(int(_sleep_calibration() * hold_ms))
+        a.record()
+        for _r in range(reps):
+            for f in launches:
+                f()
+        b.record()
+        host_ms = (time.perf_counter() - t0) * 1e3
+        b.synchronize()
+        if host_ms < 0.8 * hold_ms:
+            return a.elapsed_time(b) * 1e-3 / n
+        hold_ms = 2.0 * host_ms + 5.0
+    raise RuntimeError("device_time: host enqueue never finished inside the stream hold")
+
+
+# -------------------------------------------------------------- workloads --
 class Layer:
     def __init__(self, idx: int, T: int, dev):
         import torch
@@ -74,7 +132,9 @@ class Layer:
 
 
 def moe_step_bytes(layer, x, T: int) -> tuple[int, int]:
-    """(algorithmic bytes of one layer step, distinct experts routed)."""
+    """(algorithmic bytes of one layer step, distinct experts routed):
+    weights of every routed expert once, activations in and out, router
+    logits, routing ids and weights."""
     import torch
 
     from ccut.blocks import moe
@@ -85,10 +145,11 @@ def moe_step_bytes(layer, x, T: int) -> tuple[int, int]:
     return uniq * layer.experts.bytes_per_expert + act, uniq
 
 
-def bench_moe(T: int, steps: int, warmup: int, use_graph: bool, dev, measure_stage: bool):
+def bench_moe(T: int, steps: int, warmup: int, dev):
+    """Whole MoE layer steps replayed from a HIP graph (wall time) plus the
+    device time of the gate/up kernel."""
     import torch
 
-    from ccut import _dev, _lib
     from ccut import workloads as wl
     from ccut.blocks import moe
 
@@ -104,120 +165,100 @@ def bench_moe(T: int, steps: int, warmup: int, use_graph: bool, dev, measure_sta
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    graph = None
-    if use_graph:
-        try:
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                for i in range(LAYERS):
-                    step(i)
-            torch.cuda.current_stream().wait_stream(s)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                for i in range(LAYERS):
-                    step(i)
-            graph.replay()
-            torch.cuda.synchronize()
-        except Exception as e:  # capture unsupported: fall back to eager timing
-            log(f"graph capture failed ({e!r}); timing eager launches")
-            graph = None
-    reps = max(1, steps // LAYERS) if graph is not None else steps
-    n_steps = reps * LAYERS if graph is not None else steps
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(LAYERS):
+            step(i)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(LAYERS):
+            step(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // LAYERS)
+    n_steps = reps * LAYERS
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    if graph is not None:
-        for _ in range(reps):
-            graph.replay()
-    else:
-        for i in range(steps):
-            step(i)
+    for _ in range(reps):
+        graph.replay()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     total_bytes = sum(per[i % LAYERS][0] for i in range(n_steps))
-    res = {
+    return {
         "T": T, "steps": n_steps, "ms_per_step": dt / n_steps * 1e3, "GBps": total_bytes / dt / 1e9,
-        "unique_experts": [p[1] for p in per], "bytes_per_step": [p[0] for p in per], "graph": graph is not None,
+        "unique_experts": [p[1] for p in per], "bytes_per_step": [p[0] for p in per],
+        "gate_up": time_gate_up(layers, x, T, dev),
     }
-    if measure_stage:
-        res["gate_up"] = time_gate_up(layers, x, T, steps=max(50, steps), dev=dev)
-    return res
 
 
-def time_gate_up(layers, x, T: int, steps: int, dev):
-    """Average duration of the gate/up kernel (the dominant one) from HIP
-    events on the stream it is launched on, rotating over the layers."""
-    import ctypes
-
+def time_gate_up(layers, x, T: int, dev):
+    """Device time of the gate/up + SiLU kernel (ccq_moe_w4_gate_up), the
+    dominant kernel of the step, rotating over the layers.  Algorithmic bytes
+    per launch: gate and up weights (int4 + fp16 scales + int4 zeros) of the
+    routed experts, the activations read and the intermediate written."""
     import torch
 
-    from ccut import _dev, _lib
+    from ccut import _lib
     from ccut.blocks import moe
 
     lib = _lib.lib()
     mt = lib.ccq_moe_align_max_tiles(T * TOPK, E, 16)
-    scheds, descs, inters, gu_bytes = [], [], [], []
+    stream = torch.cuda.current_stream().cuda_stream
+    launches, gu_bytes, keep = [], [], []
     for l in layers:
-        w, ids = moe.topk_softmax(l.logits, TOPK, True)
-        scheds.append(moe.moe_align(ids, E, 16))
-        descs.append(l.experts.descriptor())
-        inters.append(torch.empty((T * TOPK, INTER), dtype=torch.bfloat16, device=dev))
+        _, ids = moe.topk_softmax(l.logits, TOPK, True)
+        sch = moe.moe_align(ids, E, 16)
+        desc = l.experts.descriptor()
+        inter = torch.empty((T * TOPK, INTER), dtype=torch.bfloat16, device=dev)
+        keep.append((sch, desc, inter))
         uniq = int(torch.unique(ids).numel())
         ex = l.experts
         per_exp = sum(t.numel() * t.element_size() for t in (ex.w_gate, ex.z_gate, ex.s_gate, ex.w_up, ex.z_up,
                                                              ex.s_up)) // E
         gu_bytes.append(uniq * per_exp + x.numel() * 2 + T * TOPK * INTER * 2)
-    nbytes = lib.ccq_moe_w4_stage_workspace_size(mt, descs[0])
-    ws = _dev.workspace("bench_stage", nbytes, dev)
-    stream = torch.cuda.current_stream()
-
-    def launch(i):
-        j = i % len(layers)
-        s = scheds[j]
-        _lib.call("ccq_moe_w4_gate_up", x.data_ptr(), 2, TOPK, s.sorted_ids.data_ptr(), s.tile_expert.data_ptr(),
-                  s.meta.data_ptr(), mt, inters[j].data_ptr(), ctypes.byref(descs[j]), ws.data_ptr(), nbytes,
-                  stream.cuda_stream)
-
-    for i in range(10):
-        launch(i)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        args = (ctypes.c_void_p(x.data_ptr()), 2, TOPK, ctypes.c_void_p(sch.sorted_ids.data_ptr()),
+                ctypes.c_void_p(sch.tile_expert.data_ptr()), ctypes.c_void_p(sch.meta.data_ptr()), mt,
+                ctypes.c_void_p(inter.data_ptr()), ctypes.byref(desc), ctypes.c_void_p(stream))
+        launches.append(lambda a=args: lib.ccq_moe_w4_gate_up(*a))
+    for f in launches:
+        _lib.check(f(), "ccq_moe_w4_gate_up")
     torch.cuda.synchronize()
-    for i in range(steps):
-        starts[i].record(stream)
-        launch(i)
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    durs = [s.elapsed_time(e) * 1e-3 for s, e in zip(starts, ends)]
-    avg = sum(durs) / len(durs)
-    avg_bytes = sum(gu_bytes[i % len(layers)] for i in range(steps)) / steps
+    avg = device_time(launches, reps=25)
+    avg_bytes = sum(gu_bytes) / len(gu_bytes)
     return {"avg_us": avg * 1e6, "bytes": avg_bytes, "GBps": avg_bytes / avg / 1e9}
 
 
-def bench_gemm(M: int, K: int, N: int, steps: int, dev, copies: int):
-    """Kernel GB/s of ccq_w4_gemm from HIP events, rotating weight copies."""
+def bench_gemm(M: int, K: int, N: int, dev, copies: int):
+    """Device time of ccq_w4_gemm rotating over distinct weight copies
+    (> 512 MiB in total, so the Infinity Cache cannot serve repeats)."""
     import torch
 
+    from ccut import _lib
     from ccut import workloads as wl
     from ccut.quant import awq
 
+    lib = _lib.lib()
     ws = []
     for c in range(copies):
         qw, qz, s = wl.awq_linear(K, N, GROUP, seed=500 + c, device=dev)
         ws.append(awq.prepare(qw, qz, s, GROUP))
     x = wl.activations(M, K, seed=9, device=dev, dtype=torch.float16)
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
-    for i in range(10):
-        y.copy_(awq.gemm(x, ws[i % copies]))
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ref = awq.gemm(x, ws[0])  # through the Python API once
+    stream = torch.cuda.current_stream().cuda_stream
+    launches = []
+    for w in ws:
+        args = (ctypes.c_void_p(x.data_ptr()), 1, ctypes.c_void_p(w.w_tiled.data_ptr()),
+                ctypes.c_void_p(w.qzeros.data_ptr()), ctypes.c_void_p(w.scales.data_ptr()), 1,
+                ctypes.c_void_p(y.data_ptr()), 1, M, K, N, GROUP, ctypes.c_void_p(stream))
+        launches.append(lambda a=args: lib.ccq_w4_gemm(*a))
+    _lib.check(launches[0](), "ccq_w4_gemm")
     torch.cuda.synchronize()
-    for i in range(steps):
-        starts[i].record()
-        awq.gemm(x, ws[i % copies])
-        ends[i].record()
-    torch.cuda.synchronize()
-    avg = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps * 1e-3
+    if not torch.equal(y, ref):
+        raise RuntimeError("bench_gemm: raw launch and API disagree")
+    avg = device_time(launches, reps=4)
     nbytes = ws[0].nbytes + M * K * 2 + M * N * 2
     return {"M": M, "K": K, "N": N, "avg_us": avg * 1e6, "bytes": nbytes, "GBps": nbytes / avg / 1e9,
             "frac_hbm": nbytes / avg / PEAK_HBM, "TFLOPs": 2.0 * M * K * N / avg / 1e12}
@@ -280,24 +321,26 @@ def main():
     _lib.lib()
     dev = torch.device("cuda", 0)
     log(f"device {torch.cuda.get_device_name(0)}; MoE decode T={args.tokens}")
-    head = bench_moe(args.tokens, args.steps, args.warmup, not args.no_graph, dev, measure_stage=True)
-    log(f"moe decode T={args.tokens}: {head['GBps']:.1f} GB/s, {head['ms_per_step'] * 1e3:.1f} us/step")
+    head = bench_moe(args.tokens, args.steps, args.warmup, dev)
+    gu = head["gate_up"]
+    log(f"moe decode T={args.tokens}: {head['GBps']:.1f} GB/s, {head['ms_per_step'] * 1e3:.1f} us/step; "
+        f"gate/up kernel {gu['avg_us']:.2f} us = {gu['GBps']:.1f} GB/s")
     extra = {}
     if not args.no_extra:
-        t1 = bench_moe(1, args.steps, args.warmup, not args.no_graph, dev, measure_stage=True)
+        t1 = bench_moe(1, args.steps, args.warmup, dev)
         extra["moe_decode_T1"] = t1
-        log(f"moe decode T=1: {t1['GBps']:.1f} GB/s")
+        log(f"moe decode T=1: {t1['GBps']:.1f} GB/s, {t1['ms_per_step'] * 1e3:.1f} us/step; gate/up kernel "
+            f"{t1['gate_up']['avg_us']:.2f} us = {t1['gate_up']['GBps']:.1f} GB/s")
         for M in (1, 4, 16):
-            r = bench_gemm(M, 4096, 14336, steps=200, dev=dev, copies=24)
+            r = bench_gemm(M, 4096, 14336, dev=dev, copies=24)
             extra[f"awq_gemm_k4096_n14336_m{M}"] = r
-            log(f"awq gemm M={M}: {r['GBps']:.1f} GB/s ({r['avg_us']:.2f} us)")
-        r = bench_gemm(1, 2048, 5632, steps=200, dev=dev, copies=96)
+            log(f"awq gemm K=4096 N=14336 M={M}: {r['GBps']:.1f} GB/s ({r['avg_us']:.2f} us)")
+        r = bench_gemm(1, 2048, 5632, dev=dev, copies=96)
         extra["awq_gemv_k2048_n5632"] = r
-        log(f"awq gemv C1: {r['GBps']:.1f} GB/s ({r['avg_us']:.2f} us)")
-    gu = head["gate_up"]
+        log(f"awq gemv K=2048 N=5632: {r['GBps']:.1f} GB/s ({r['avg_us']:.2f} us)")
     cpu = None if args.no_cpu else cpu_baseline(args.tokens)
     out = {
-        "metric": "int4 MoE decode GB/s (% HBM peak) + FP8/int4 prefill TFLOP/s (% MFMA peak)",
+        "metric": METRIC,
         "value": round(head["GBps"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -312,7 +355,7 @@ def main():
         "config": {"workload": f"int4 MoE expert FFN decode: 64 experts top-6, hidden 2048, inter 1408, "
                                f"AWQ group 128, T={args.tokens}, 4 rotating layer weight sets",
                    "tokens": args.tokens, "experts": E, "top_k": TOPK, "hidden": HID, "inter": INTER,
-                   "group": GROUP, "hip_graph": head["graph"]},
+                   "group": GROUP, "hip_graph": True},
         "frac_hbm_peak": round(head["GBps"] * 1e9 / PEAK_HBM, 4),
         "roofline": {"bound": "hbm", "kernel": "w4_skinny_kernel<bf16,NB=1,G=128,SiLU> (MoE gate/up)",
                      "achieved": round(gu["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",

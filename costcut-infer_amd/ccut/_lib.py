@@ -56,17 +56,14 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_awq_dequant": (_int, [_vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
     "ccq_awq_repack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ccq_awq_unpack_tiled": (_int, [_vp, _vp, _i64, _i64, _vp]),
-    "ccq_w4_gemm_workspace_size": (_sz, [_i64, _i64, _i64]),
-    "ccq_w4_gemm": (_int, [_vp, _int, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "ccq_w4_gemm": (_int, [_vp, _int, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp]),
     "ccq_topk_softmax": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "ccq_moe_align_max_tiles": (_i64, [_i64, _i64, _i64]),
     "ccq_moe_align": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
     "ccq_moe_combine": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _vp]),
-    "ccq_moe_w4_stage_workspace_size": (_sz, [_i64, ctypes.POINTER(ccq_w4_experts)]),
     "ccq_moe_w4_gate_up": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _i64, _vp, ctypes.POINTER(ccq_w4_experts),
-                                  _vp, _sz, _vp]),
-    "ccq_moe_w4_down": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _vp, ctypes.POINTER(ccq_w4_experts), _vp, _sz,
-                               _vp]),
+                                  _vp]),
+    "ccq_moe_w4_down": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _vp, ctypes.POINTER(ccq_w4_experts), _vp]),
     "ccq_moe_w4_workspace_size": (_sz, [_i64, _i64, ctypes.POINTER(ccq_w4_experts)]),
     "ccq_moe_w4_ffn": (_int, [_vp, _int, _vp, _vp, _vp, _int, _i64, _i64,
                               ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),

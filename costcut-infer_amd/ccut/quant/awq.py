@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import torch
 
 from ccut import _dev
-from ccut._lib import call, lib
+from ccut._lib import call
 
 AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
 AWQ_REVERSE_ORDER = (0, 4, 1, 5, 2, 6, 3, 7)
@@ -128,9 +128,7 @@ def gemm(x: torch.Tensor, w: AwqWeights, out_dtype: torch.dtype | None = None) -
         raise ValueError(f"AWQ GEMM: x has {K} features, weight expects {w.K}")
     out_dtype = out_dtype or x.dtype
     y = torch.empty((M, w.N), dtype=out_dtype, device=x.device)
-    nbytes = lib().ccq_w4_gemm_workspace_size(M, K, w.N)
-    ws = _dev.workspace("w4_gemm", nbytes, x.device) if nbytes else None
     call("ccq_w4_gemm", x2.data_ptr(), _dev.DTYPE_CODE[x.dtype], w.w_tiled.data_ptr(), w.qzeros.data_ptr(),
          w.scales.data_ptr(), _scale_code(w.scales), y.data_ptr(), _dev.DTYPE_CODE[out_dtype], M, K, w.N,
-         w.group_size, ws.data_ptr() if ws is not None else None, nbytes, _dev.stream_ptr(x.device))
+         w.group_size, _dev.stream_ptr(x.device))
     return y.reshape(*x.shape[:-1], w.N)

@@ -14,26 +14,35 @@ namespace ccq {
 constexpr int kMaxE = 1024;      // experts per row held in registers (16 per lane)
 constexpr int kMaxK = 16;
 
-// numpy's pairwise float32 summation for n <= 128 elements (the branch
-// numpy takes for the k <= 16 routing weights): 8 interleaved partial sums,
-// combined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then the tail in order.
-__device__ float np_pairwise_sum_small(const float* a, int n) {
+// numpy's pairwise float32 summation of n <= 16 values, value j held by lane
+// j (other lanes hold 0): below 8 a plain running sum in index order;
+// otherwise 8 partial sums r[j] = a[j] (+ a[8+j] when n == 16) combined as
+// ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) -- float addition is commutative, so
+// the xor-shuffle tree forms exactly those sums -- then the tail in order.
+// The result is returned in every lane.
+__device__ float np_pairwise_sum16(float a, int n, int lane) {
   if (n < 8) {
-    float res = 0.f;  // numpy starts from -0.0; identical for these inputs
-    for (int i = 0; i < n; ++i) res += a[i];
+    float res = 0.f;  // numpy starts from -0.0; identical for these (positive) inputs
+    for (int i = 0; i < n; ++i) res += __shfl(a, i, 64);
     return res;
   }
-  float r[8];
-  for (int j = 0; j < 8; ++j) r[j] = a[j];
-  int i = 8;
-  for (; i < n - (n % 8); i += 8)
-    for (int j = 0; j < 8; ++j) r[j] += a[i + j];
-  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-  for (; i < n; ++i) res += a[i];
+  const int whole = n - (n % 8);  // 8 or 16
+  const float hi = __shfl(a, (lane + 8) & 63, 64);
+  float r = a + ((lane < 8 && 8 + lane < whole) ? hi : 0.f);
+  r += __shfl_xor(r, 1, 64);
+  r += __shfl_xor(r, 2, 64);
+  r += __shfl_xor(r, 4, 64);
+  float res = __shfl(r, 0, 64);
+  for (int i = whole; i < n; ++i) res += __shfl(a, i, 64);
   return res;
 }
 
-// One wave per token row.  Lane l holds columns l, l+64, ... (<= 16 values).
+// One wave per token row.  Lane l holds columns l, l+64, ... (PER values,
+// PER = ceil(E / 64) rounded up to 1, 2, 4 or 16); after selection pass j,
+// lane j holds slot j.  The code stays compact (a run-time loop over the k
+// passes, no per-slot arrays): the kernel runs on a handful of CUs, where a
+// large body costs more in cold instruction fetches than it saves.
+template <int PER>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restrict__ logits,
                                                            float* __restrict__ weights,
                                                            int64_t* __restrict__ ids, int64_t T, int E,
@@ -42,25 +51,24 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;
   const float* lr = logits + row * E;
-  const int per = (E + 63) / 64;
-  float v[16];
-  bool used[16];
+  float v[PER];
+  bool used[PER];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < PER; ++i) {
     int c = lane + 64 * i;
-    v[i] = (i < per && c < E) ? lr[c] : -INFINITY;
-    used[i] = !(i < per && c < E);  // out-of-range slots never selectable
+    v[i] = c < E ? lr[c] : -INFINITY;
+    used[i] = c >= E;  // out-of-range slots never selectable
   }
   if (mode == 0) {
     // p = exp(x - max) / max(sum, 1e-30) in float32 (blocks/moe.py:80-81)
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < PER; ++i)
       if (!used[i]) m = fmaxf(m, v[i]);
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < PER; ++i)
       if (!used[i]) {
         v[i] = expf(v[i] - m);
         s += v[i];
@@ -68,18 +76,18 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
     const float d = fmaxf(s, 1e-30f);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < PER; ++i)
       if (!used[i]) v[i] = v[i] / d;
   }
   // k passes of "first value strictly greater than the running best" with the
   // best starting at -1e30 (ties -> lowest column; NaN never picked).
-  float sel_v[kMaxK];
-  int sel_i[kMaxK];
+  float my_v = 0.f;
+  int my_i = 0;
   for (int j = 0; j < k; ++j) {
     float bv = -1.0e30f;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < PER; ++i) {
       int c = lane + 64 * i;
       if (!used[i] && v[i] > bv) {  // per lane columns are increasing
         bv = v[i];
@@ -100,37 +108,33 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
     }
     const int mark = bi >= 0 ? bi : E - 1;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < PER; ++i)
       if (lane + 64 * i == mark) used[i] = true;
-    sel_v[j] = bv;
-    sel_i[j] = bi;
+    if (lane == j) {
+      my_v = bv;
+      my_i = bi;
+    }
   }
-  if (lane != 0) return;
-  float w[kMaxK];
-  if (mode == 0 || mode == 3) {
-    for (int j = 0; j < k; ++j) w[j] = sel_v[j];
-  } else if (mode == 1) {
+  const bool mine = lane < k;
+  float w = my_v;  // modes 0 and 3: the selected values themselves
+  if (mode == 1) {
     // v = vals - vals.max(); exp; / max(exp.sum(), 1e-30)  (blocks/moe.py:86-88)
-    float m = sel_v[0];
-    for (int j = 1; j < k; ++j) m = fmaxf(m, sel_v[j]);
-    float ex[kMaxK];
-    for (int j = 0; j < k; ++j) ex[j] = expf(sel_v[j] - m);
-    const float d = fmaxf(np_pairwise_sum_small(ex, k), 1e-30f);
-    for (int j = 0; j < k; ++j) w[j] = ex[j] / d;
-  } else {
+    float m = mine ? my_v : -INFINITY;
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    const float e = mine ? expf(my_v - m) : 0.f;
+    const float d = fmaxf(np_pairwise_sum16(e, k, lane), 1e-30f);
+    w = e / d;
+  } else if (mode == 2) {
     // route_experts norm_topk=0: exp(v)/sum(exp(v)) with a float64 running sum
     // (blocks/moe.py:114-118)
-    float ex[kMaxK];
+    const float e = mine ? expf(my_v) : 0.f;
     double s = 0.0;
-    for (int j = 0; j < k; ++j) {
-      ex[j] = expf(sel_v[j]);
-      s += (double)ex[j];
-    }
-    for (int j = 0; j < k; ++j) w[j] = s > 0.0 ? (float)((double)ex[j] / s) : 0.f;
+    for (int j = 0; j < k; ++j) s += (double)__shfl(e, j, 64);
+    w = s > 0.0 ? (float)((double)e / s) : 0.f;
   }
-  for (int j = 0; j < k; ++j) {
-    weights[row * k + j] = w[j];
-    ids[row * k + j] = sel_i[j];
+  if (mine) {
+    weights[row * k + lane] = w;
+    ids[row * k + lane] = my_i;
   }
 }
 
@@ -306,38 +310,68 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
 
 // y[t, h] = sum_s w[t, s] * rows[t*k + s, h], slot order, float32.  Slots
 // whose id is outside [0, E) (dropped by the schedule) contribute nothing.
-template <int YT>
-__global__ void moe_combine_kernel(const float* __restrict__ rows, const float* __restrict__ wts,
-                                   const int64_t* __restrict__ ids, int64_t E, void* __restrict__ y,
-                                   int64_t T, int k, int64_t H) {
+// Four columns per thread (16-byte loads) when H % 4 == 0.
+template <int YT, bool VEC>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ rows,
+                                                          const float* __restrict__ wts,
+                                                          const int64_t* __restrict__ ids, int64_t E,
+                                                          void* __restrict__ y, int64_t T, int k, int64_t H) {
+  constexpr int CW = VEC ? 4 : 1;
   const int64_t t = blockIdx.y;
-  for (int64_t h = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; h < H; h += (int64_t)gridDim.x * blockDim.x) {
-    float acc = 0.f;
-    for (int s = 0; s < k; ++s) {
-      if (ids) {
-        int64_t e = ids[t * k + s];
-        if (e < 0 || e >= E) continue;
-      }
-      acc = fmaf(wts[t * k + s], rows[(t * k + s) * H + h], acc);
+  const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * CW;
+  if (h >= H) return;
+  float acc[CW];
+#pragma unroll
+  for (int c = 0; c < CW; ++c) acc[c] = 0.f;
+  for (int s = 0; s < k; ++s) {
+    const int64_t a = t * k + s;
+    if (ids) {
+      const int64_t e = ids[a];
+      if (e < 0 || e >= E) continue;
     }
-    if (YT == CCQ_F32)
-      ((float*)y)[t * H + h] = acc;
-    else if (YT == CCQ_BF16)
-      ((uint16_t*)y)[t * H + h] = (uint16_t)f32_to_bf16_bits(acc);
-    else
-      ((uint16_t*)y)[t * H + h] = (uint16_t)f32_to_f16_bits(acc);
+    const float wv = wts[a];
+    if (VEC) {
+      const f32x4 r = *reinterpret_cast<const f32x4*>(rows + a * H + h);
+#pragma unroll
+      for (int c = 0; c < CW; ++c) acc[c] = fmaf(wv, r[c], acc[c]);
+    } else {
+      acc[0] = fmaf(wv, rows[a * H + h], acc[0]);
+    }
   }
+#pragma unroll
+  for (int c = 0; c < CW; ++c) {
+    const int64_t o = t * H + h + c;
+    if (YT == CCQ_F32)
+      ((float*)y)[o] = acc[c];
+    else if (YT == CCQ_BF16)
+      ((uint16_t*)y)[o] = (uint16_t)f32_to_bf16_bits(acc[c]);
+    else
+      ((uint16_t*)y)[o] = (uint16_t)f32_to_f16_bits(acc[c]);
+  }
+}
+
+template <bool VEC>
+static void launch_combine_v(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y,
+                             int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st) {
+  const int64_t cols = VEC ? H / 4 : H;
+  dim3 grid((unsigned)cdiv(cols, 256), (unsigned)T);
+  if (y_dtype == CCQ_F32)
+    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F32, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+                       (int)k, H);
+  else if (y_dtype == CCQ_BF16)
+    hipLaunchKernelGGL((moe_combine_kernel<CCQ_BF16, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+                       (int)k, H);
+  else
+    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F16, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+                       (int)k, H);
 }
 
 int launch_combine(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y, int y_dtype,
                    int64_t T, int64_t k, int64_t H, hipStream_t st) {
-  dim3 grid((unsigned)imin64(cdiv(H, 256), 64), (unsigned)T);
-  if (y_dtype == CCQ_F32)
-    hipLaunchKernelGGL(moe_combine_kernel<CCQ_F32>, grid, dim3(256), 0, st, rows, wts, ids, E, y, T, (int)k, H);
-  else if (y_dtype == CCQ_BF16)
-    hipLaunchKernelGGL(moe_combine_kernel<CCQ_BF16>, grid, dim3(256), 0, st, rows, wts, ids, E, y, T, (int)k, H);
+  if (H % 4 == 0 && aligned(rows, 16))
+    launch_combine_v<true>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
   else
-    hipLaunchKernelGGL(moe_combine_kernel<CCQ_F16>, grid, dim3(256), 0, st, rows, wts, ids, E, y, T, (int)k, H);
+    launch_combine_v<false>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
   return launch_status("moe_combine");
 }
 
@@ -362,8 +396,17 @@ extern "C" int ccq_topk_softmax(const float* logits, float* weights, int64_t* id
   if (T == 0) return 0;
   CCQ_REQUIRE(logits && weights && ids, "ccq_topk_softmax: null pointer");
   CCQ_REQUIRE(T <= (int64_t)4 * 0x7fffffff, "ccq_topk_softmax: T too large");
-  hipLaunchKernelGGL(topk_softmax_kernel, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, as_stream(stream), logits,
-                     weights, ids, T, (int)E, (int)k, mode);
+  const dim3 grid((unsigned)cdiv(T, 4));
+  hipStream_t st = as_stream(stream);
+  if (E <= 64)
+    hipLaunchKernelGGL(topk_softmax_kernel<1>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
+  else if (E <= 128)
+    hipLaunchKernelGGL(topk_softmax_kernel<2>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
+  else if (E <= 256)
+    hipLaunchKernelGGL(topk_softmax_kernel<4>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
+  else
+    hipLaunchKernelGGL(topk_softmax_kernel<16>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k,
+                       mode);
   return launch_status("ccq_topk_softmax");
 }
 

@@ -131,6 +131,8 @@ __device__ __forceinline__ typename Act<AT>::vec dq_b(uint32_t w) {
   return __builtin_bit_cast(typename Act<AT>::vec, r);
 }
 
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
 __device__ __forceinline__ void store_val(void* y, int64_t i, float v, int dt) {
   if (dt == CCQ_F32)
     reinterpret_cast<float*>(y)[i] = v;
@@ -161,26 +163,33 @@ struct SkinnyP {
   void* y;
   int64_t ldy;
   int y_dtype;
-  int M, K, N, KT, G;
-  int nblocks, splits, ktps;
-  float* partial;
-  int* counters;
+  int M, N, KT;
+  int ktpw;                   // 128-row k-tiles per wave
 };
 
-// One wave = one job (nt-block of NB tiles, K-split sp) for one row tile of
-// 16 rows.  grid = (ceil(jobs / 4), row tiles); 4 independent waves per WG.
+// k-tiles whose packed weights, scales and zero words one wave holds in
+// registers at once: all of them are requested before the first multiply, so
+// each wave keeps KTW KiB (x2 for gate+up) of HBM reads in flight.
+constexpr int KTW = 4;
+
+// Workgroup = W waves (W = blockDim.x / 64) sharing one job: the 16-row tile
+// blockIdx.y times the 16*NB output columns of block blockIdx.x.  Wave w owns
+// the k-tiles [w*ktpw, (w+1)*ktpw) (ktpw <= KTW per chunk, more chunks if
+// larger); the W partial sums are added in wave order through LDS
+// (deterministic, no global atomics or fences), and wave 0 runs the epilogue.
 template <typename AT, int NB, int GS, int EPI>
-__global__ __launch_bounds__(256) void w4_skinny_kernel(const SkinnyP p) {
+__global__ __launch_bounds__(512) void w4_skinny_kernel(const SkinnyP p) {
   using V = typename Act<AT>::vec;
   constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
   constexpr int NG = 4 / GS;  // quantization groups per 128-row tile
+  constexpr int NV = NACC * NB * 4;
+  extern __shared__ float red[];  // [(W-1) * NV][64]
   const int lane = threadIdx.x & 63;
-  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int nb = blockIdx.x;
   const int tile = blockIdx.y;
-  if (job >= p.nblocks * p.splits) return;
-  if (p.meta != nullptr && tile >= p.meta[0]) return;
-  const int nb = job / p.splits;
-  const int sp = job - nb * p.splits;
+  if (p.meta != nullptr && tile >= p.meta[0]) return;  // whole workgroup
   const int ex = p.tile_expert ? p.tile_expert[tile] : 0;
 
   const int r = lane & 15, kq = lane >> 4;
@@ -193,10 +202,11 @@ __global__ __launch_bounds__(256) void w4_skinny_kernel(const SkinnyP p) {
     rid = tile * 16 + r;
     rvalid = rid < p.M;
   }
+  // padding rows read row 0 (always present) and multiply zeros instead
   const AT* xr = reinterpret_cast<const AT*>(p.x) + (int64_t)(rvalid ? rid / p.row_div : 0) * p.ldx + 8 * kq;
 
-  const int kt0 = sp * p.ktps;
-  const int kt1 = min(p.KT, kt0 + p.ktps);
+  const int kt0 = wave * p.ktpw;
+  const int kt1 = min(p.KT, kt0 + p.ktpw);
   const int64_t N8 = p.N >> 3;
   const uint32_t* wb[NACC];
   const uint32_t* zb[NACC];
@@ -215,102 +225,113 @@ __global__ __launch_bounds__(256) void w4_skinny_kernel(const SkinnyP p) {
     ncol[t] = (nb * NB + t) * 16 + (lane & 15);
     zsh[t] = awq_shift(ncol[t] & 7);
   }
+  const int sbf = p.scale_bf16;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+
+  auto load_x = [&](V (&a)[4], int kt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(xr + (int64_t)kt * 128 + 32 * j);
+      a[j] = __builtin_bit_cast(V, rvalid ? v : zero4);
+    }
+  };
 
   f32x4 acc[NACC][NB];
 #pragma unroll
   for (int q = 0; q < NACC; ++q)
 #pragma unroll
     for (int t = 0; t < NB; ++t) acc[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 ones_u = {Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2};
+  const u32x4 ones_u = {Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2};
   const V ones = __builtin_bit_cast(V, ones_u);
 
-  for (int kt = kt0; kt < kt1; ++kt) {
-    V a[4];
+  for (int c0 = kt0; c0 < kt1; c0 += KTW) {
+    const int nk = min(KTW, kt1 - c0);
+    u32x4 wv[KTW][NACC][NB];
+    float sv[KTW][NACC][NB][NG];
+    uint32_t zv[KTW][NACC][NB][NG];
+    // every weight / scale / zero load of the chunk first (tiles past the
+    // end re-read the last one: same addresses, no extra HBM traffic)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (rvalid)
-        a[j] = *reinterpret_cast<const V*>(xr + (int64_t)kt * 128 + 32 * j);
-      else
-        a[j] = __builtin_bit_cast(V, u32x4{0u, 0u, 0u, 0u});
-    }
-    u32x4 wv[NACC][NB];
+    for (int i = 0; i < KTW; ++i) {
+      const int kt = min(c0 + i, kt1 - 1);
 #pragma unroll
-    for (int q = 0; q < NACC; ++q)
+      for (int q = 0; q < NACC; ++q)
 #pragma unroll
-      for (int t = 0; t < NB; ++t)
-        wv[q][t] = *reinterpret_cast<const u32x4*>(wb[q] + (((int64_t)(nb * NB + t) * p.KT + kt) * 64 + lane) * 4);
-    f32x4 sx[NG];
+        for (int t = 0; t < NB; ++t) {
+          wv[i][q][t] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(wb[q] + (((int64_t)(nb * NB + t) * p.KT + kt) * 64 + lane) * 4));
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      sx[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int jj = 0; jj < GS; ++jj) sx[g] = mfma16(a[g * GS + jj], ones, sx[g]);
-    }
-#pragma unroll
-    for (int q = 0; q < NACC; ++q)
-#pragma unroll
-      for (int t = 0; t < NB; ++t)
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const int64_t grp = (int64_t)kt * NG + g;
-          const float s = scale_at(sb[q], grp * p.N + ncol[t], p.scale_bf16);
-          const int z = (int)((zb[q][grp * N8 + (ncol[t] >> 3)] >> zsh[t]) & 15u);
-          f32x4 tmp = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int jj = 0; jj < GS; ++jj) tmp = mfma16(a[g * GS + jj], dq_b<AT>(wv[q][t][g * GS + jj]), tmp);
-          const float c = Act<AT>::kMagic + (float)z;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[q][t][i] = fmaf(s, fmaf(-c, sx[g][i], tmp[i]), acc[q][t][i]);
+          for (int g = 0; g < NG; ++g) {
+            const int64_t grp = (int64_t)kt * NG + g;
+            sv[i][q][t][g] = scale_at(sb[q], grp * p.N + ncol[t], sbf);
+            zv[i][q][t][g] = zb[q][grp * N8 + (ncol[t] >> 3)];
+          }
         }
-  }
-
-  // rows held by this lane in the accumulator layout: 4*kq + i
-  int orid[4];
-  bool ovalid[4];
+    }
+    V a0[4], a1[4];
+    load_x(a0, c0);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    orid[i] = __shfl(rid, 4 * kq + i, 64);
-    ovalid[i] = p.rows ? orid[i] >= 0 : orid[i] < p.M;
-  }
-  if (p.splits > 1) {
-    constexpr int TE = 16 * 16 * NB * NACC;
-    const int64_t cidx = (int64_t)tile * p.nblocks + nb;
-    float* part = p.partial + cidx * p.splits * TE;
+    for (int i = 0; i < KTW; ++i) {
+      if (i >= nk) break;
+      V(&a)[4] = (i & 1) ? a1 : a0;
+      V(&an)[4] = (i & 1) ? a0 : a1;
+      if (i + 1 < nk) load_x(an, c0 + i + 1);
+      f32x4 sx[NG];
 #pragma unroll
-    for (int q = 0; q < NACC; ++q)
+      for (int g = 0; g < NG; ++g) {
+        sx[g] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < NB; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (ovalid[i]) part[sp * TE + ((4 * kq + i) * NACC + q) * (16 * NB) + t * 16 + (lane & 15)] = acc[q][t][i];
-    __threadfence();
-    int old = 0;
-    if (lane == 0) old = atomicAdd(&p.counters[cidx], 1);
-    old = __shfl(old, 0, 64);
-    if (old != p.splits - 1) return;
-    __threadfence();
-#pragma unroll
-    for (int q = 0; q < NACC; ++q)
-#pragma unroll
-      for (int t = 0; t < NB; ++t) acc[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < p.splits; ++s)
+        for (int jj = 0; jj < GS; ++jj) sx[g] = mfma16(a[g * GS + jj], ones, sx[g]);
+      }
 #pragma unroll
       for (int q = 0; q < NACC; ++q)
 #pragma unroll
         for (int t = 0; t < NB; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (ovalid[i])
-              acc[q][t][i] += __builtin_nontemporal_load(
-                  &part[s * TE + ((4 * kq + i) * NACC + q) * (16 * NB) + t * 16 + (lane & 15)]);
-    if (lane == 0) p.counters[cidx] = 0;  // ready for the next call
+          for (int g = 0; g < NG; ++g) {
+            f32x4 tmp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int jj = 0; jj < GS; ++jj) tmp = mfma16(a[g * GS + jj], dq_b<AT>(wv[i][q][t][g * GS + jj]), tmp);
+            const float c = Act<AT>::kMagic + (float)((zv[i][q][t][g] >> zsh[t]) & 15u);
+            const float s = sv[i][q][t][g];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[q][t][e] = fmaf(s, fmaf(-c, sx[g][e], tmp[e]), acc[q][t][e]);
+          }
+    }
   }
+
+  if (W > 1) {
+    if (wave > 0) {
+      float* dst = red + (size_t)(wave - 1) * NV * 64 + lane;
 #pragma unroll
-  for (int t = 0; t < NB; ++t)
+      for (int q = 0; q < NACC; ++q)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (!ovalid[i]) continue;
-      const int64_t o = (int64_t)orid[i] * p.ldy + ncol[t];
+        for (int t = 0; t < NB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[((q * NB + t) * 4 + i) * 64] = acc[q][t][i];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 1; w < W; ++w) {
+      const float* src = red + (size_t)(w - 1) * NV * 64 + lane;
+#pragma unroll
+      for (int q = 0; q < NACC; ++q)
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[q][t][i] += src[((q * NB + t) * 4 + i) * 64];
+    }
+  }
+
+  // rows held by this lane in the accumulator layout: 4*kq + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int orid = __shfl(rid, 4 * kq + i, 64);
+    const bool ovalid = p.rows ? orid >= 0 : orid < p.M;
+    if (!ovalid) continue;
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const int64_t o = (int64_t)orid * p.ldy + ncol[t];
       if (EPI == EPI_SILU) {
         const float g = acc[0][t][i], u = acc[NACC - 1][t][i];
         store_val(p.y, o, g / (1.0f + expf(-g)) * u, p.y_dtype);
@@ -318,72 +339,75 @@ __global__ __launch_bounds__(256) void w4_skinny_kernel(const SkinnyP p) {
         store_val(p.y, o, acc[0][t][i], p.y_dtype);
       }
     }
+  }
 }
 
 // --------------------------------------------------------------- planning --
 struct SkinnyPlan {
-  int nb, nblocks, splits, ktps;
-  size_t partial_floats, counters;
+  int nb;        // 16-column tiles per job
+  int nblocks;   // jobs per row tile
+  int waves;     // waves per workgroup (K split)
+  int ktpw;      // k-tiles per wave
+  size_t lds;    // dynamic LDS bytes
 };
 
-// Split-K arrival counters live in a fixed header of kCounterSlots ints at the
-// start of every workspace: a plan only splits K when tiles * nblocks < 2048
-// (fewer jobs than the 2048-wave target), so 2048 slots always suffice, and
-// because the last arriving wave resets its slot, the header is all zero
-// between calls whatever shapes share the workspace.
-constexpr int kCounterSlots = 2048;
-constexpr size_t kCounterBytes = kCounterSlots * sizeof(int);
-
-static SkinnyPlan plan_skinny(int64_t tiles, int64_t K, int64_t N, int nacc, int NB) {
+// K is split over the waves of a workgroup so that each wave holds at most
+// KTW k-tiles (all its weight loads in flight at once); at most 8 waves, so
+// K > 8*KTW*128 gives each wave several chunks.
+static SkinnyPlan plan_skinny(int64_t K, int64_t N, int64_t G, int nacc, int NB) {
   SkinnyPlan pl;
   const int64_t KT = K / 128, NT = N / 16;
-  if (NT % NB) NB = 1;
+  if (G < 64 && NB > 2) NB = 2;  // 4 column tiles x 4 groups would spill
+  if (NT % NB) NB = (NT % 2 == 0 && NB > 2) ? 2 : 1;
   pl.nb = NB;
   pl.nblocks = (int)(NT / NB);
-  const int64_t per_split = (int64_t)pl.nblocks * (tiles > 0 ? tiles : 1);
-  int64_t splits = cdiv(2048, per_split);  // aim for >= 8 waves per CU
-  if (splits < 1) splits = 1;
-  if (splits > KT) splits = KT;
-  pl.ktps = (int)cdiv(KT, splits);
-  pl.splits = (int)cdiv(KT, pl.ktps);
-  pl.partial_floats = pl.splits > 1 ? (size_t)tiles * pl.nblocks * pl.splits * 256 * NB * nacc : 0;
-  pl.counters = pl.splits > 1 ? (size_t)tiles * pl.nblocks : 0;  // < kCounterSlots
+  int64_t W = cdiv(KT, KTW);
+  if (W > 8) W = 8;
+  if (W < 1) W = 1;
+  pl.ktpw = (int)cdiv(KT, W);
+  pl.waves = (int)cdiv(KT, pl.ktpw);
+  pl.lds = (size_t)(pl.waves - 1) * nacc * NB * 4 * 64 * sizeof(float);
   return pl;
 }
 
-static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
-
-// [counter header][partials]
-static size_t plan_bytes(const SkinnyPlan& pl) {
-  return pl.splits > 1 ? kCounterBytes + align256(pl.partial_floats * sizeof(float)) : 0;
-}
-
 template <typename AT, int NB, int EPI>
-static void launch_skinny_gs(const SkinnyP& p, dim3 grid, hipStream_t st) {
-  if (p.G == 128)
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 4, EPI>), grid, dim3(256), 0, st, p);
-  else if (p.G == 64)
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 2, EPI>), grid, dim3(256), 0, st, p);
+static void launch_skinny_gs(const SkinnyP& p, dim3 grid, int waves, size_t lds, hipStream_t st, int G) {
+  const dim3 block(64 * waves);
+  if (G == 128)
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 4, EPI>), grid, block, lds, st, p);
+  else if (G == 64)
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 2, EPI>), grid, block, lds, st, p);
   else
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 1, EPI>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 1, EPI>), grid, block, lds, st, p);
 }
 
-template <int EPI>
-static void launch_skinny(const SkinnyP& p, int x_bf16, int NB, dim3 grid, hipStream_t st) {
-  if (x_bf16) {
-    if (NB == 2)
-      launch_skinny_gs<__bf16, 2, EPI>(p, grid, st);
-    else
-      launch_skinny_gs<__bf16, 1, EPI>(p, grid, st);
+template <typename AT, int EPI>
+static void launch_skinny_nb(const SkinnyP& p, const SkinnyPlan& pl, dim3 grid, hipStream_t st, int G) {
+  if constexpr (EPI != EPI_STORE) {
+    launch_skinny_gs<AT, 1, EPI>(p, grid, pl.waves, pl.lds, st, G);
   } else {
-    if (NB == 2)
-      launch_skinny_gs<_Float16, 2, EPI>(p, grid, st);
+    if (pl.nb == 1)
+      launch_skinny_gs<AT, 1, EPI>(p, grid, pl.waves, pl.lds, st, G);
+    else if (pl.nb == 2)
+      launch_skinny_gs<AT, 2, EPI>(p, grid, pl.waves, pl.lds, st, G);
     else
-      launch_skinny_gs<_Float16, 1, EPI>(p, grid, st);
+      launch_skinny_gs<AT, 4, EPI>(p, grid, pl.waves, pl.lds, st, G);
   }
 }
 
-static int gemm_nb(int64_t M) { return M <= 4 ? 1 : 2; }
+template <int EPI>
+static void launch_skinny(SkinnyP p, int x_bf16, const SkinnyPlan& pl, int64_t tiles, hipStream_t st, int G) {
+  p.ktpw = pl.ktpw;
+  const dim3 grid((unsigned)pl.nblocks, (unsigned)tiles);
+  if (x_bf16)
+    launch_skinny_nb<__bf16, EPI>(p, pl, grid, st, G);
+  else
+    launch_skinny_nb<_Float16, EPI>(p, pl, grid, st, G);
+}
+
+// 16-column tiles per job of the dense GEMM: more columns per wave re-use
+// each activation fragment over more weights once several rows are valid.
+static int gemm_nb(int64_t M) { return M <= 4 ? 1 : (M <= 8 ? 2 : 4); }
 
 static bool valid_group(int64_t G) { return G == 32 || G == 64 || G == 128; }
 
@@ -434,15 +458,9 @@ extern "C" int ccq_awq_unpack_tiled(const int32_t* tiled, int32_t* qweight, int6
   return launch_status("ccq_awq_unpack_tiled");
 }
 
-extern "C" size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N) {
-  if (M <= 0 || K <= 0 || N <= 0 || K % 128 || N % 16) return 0;
-  SkinnyPlan pl = plan_skinny(cdiv(M, 16), K, N, 1, gemm_nb(M));
-  return plan_bytes(pl);
-}
-
 extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, const int32_t* qzeros,
                            const void* scales, int scale_dtype, void* y, int y_dtype, int64_t M, int64_t K,
-                           int64_t N, int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+                           int64_t N, int64_t group_size, void* stream) {
   CCQ_REQUIRE(M >= 0 && K >= 0 && N >= 0, "ccq_w4_gemm: negative shape");
   CCQ_REQUIRE(K % 128 == 0 && N % 16 == 0, "ccq_w4_gemm: need K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
               (long long)K, (long long)N);
@@ -451,16 +469,13 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_w4_gemm: scale_dtype must be f16|bf16");
   CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_w4_gemm: bad y_dtype");
   CCQ_REQUIRE(cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large for the skinny kernel", (long long)M);
+  CCQ_REQUIRE(N / 16 <= 0x7fffffff, "ccq_w4_gemm: N=%lld too large", (long long)N);
   if (M == 0 || N == 0) return 0;
   CCQ_REQUIRE(K > 0, "ccq_w4_gemm: K == 0");
   CCQ_REQUIRE(x && w_tiled && qzeros && scales && y, "ccq_w4_gemm: null pointer");
   CCQ_REQUIRE(aligned(x, 16) && aligned(w_tiled, 16), "ccq_w4_gemm: x and w_tiled must be 16-byte aligned");
   const int64_t tiles = cdiv(M, 16);
-  SkinnyPlan pl = plan_skinny(tiles, K, N, 1, gemm_nb(M));
-  const size_t need = plan_bytes(pl);
-  CCQ_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
-              "ccq_w4_gemm: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-  CCQ_REQUIRE(need == 0 || aligned(workspace, 256), "ccq_w4_gemm: workspace must be 256-byte aligned");
+  const SkinnyPlan pl = plan_skinny(K, N, group_size, 1, gemm_nb(M));
   SkinnyP p = {};
   p.x = x;
   p.ldx = K;
@@ -473,19 +488,9 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   p.ldy = N;
   p.y_dtype = y_dtype;
   p.M = (int)M;
-  p.K = (int)K;
   p.N = (int)N;
   p.KT = (int)(K / 128);
-  p.G = (int)group_size;
-  p.nblocks = pl.nblocks;
-  p.splits = pl.splits;
-  p.ktps = pl.ktps;
-  if (pl.splits > 1) {
-    p.counters = (int*)workspace;
-    p.partial = (float*)((char*)workspace + kCounterBytes);
-  }
-  dim3 grid((unsigned)cdiv((int64_t)pl.nblocks * pl.splits, 4), (unsigned)tiles);
-  launch_skinny<EPI_STORE>(p, x_dtype == CCQ_BF16, pl.nb, grid, as_stream(stream));
+  launch_skinny<EPI_STORE>(p, x_dtype == CCQ_BF16, pl, tiles, as_stream(stream), (int)group_size);
   return launch_status("ccq_w4_gemm");
 }
 
@@ -518,45 +523,18 @@ int check_expert_ptrs(const ccq_w4_experts* ex, bool gate_up, const char* name) 
   return 0;
 }
 
-// Scratch of the two grouped stages (split-K partials + arrival counters).
-struct StageLayout {
-  SkinnyPlan gu, dn;
-  size_t off_gu_part, off_gu_cnt, off_dn_part, off_dn_cnt, total;
-};
-
-// [gate/up counter header][down counter header][gate/up partials][down partials]
-// The headers sit at fixed offsets so any shapes may share a workspace.
-StageLayout stage_layout(int64_t max_tiles, const ccq_w4_experts* ex) {
-  StageLayout L;
-  L.gu = plan_skinny(max_tiles, ex->hidden, ex->inter, 2, 1);
-  L.dn = plan_skinny(max_tiles, ex->inter, ex->hidden, 1, 1);
-  size_t o = 0;
-  L.off_gu_cnt = o;
-  o += kCounterBytes;
-  L.off_dn_cnt = o;
-  o += kCounterBytes;
-  L.off_gu_part = o;
-  o += align256(L.gu.partial_floats * 4);
-  L.off_dn_part = o;
-  o += align256(L.dn.partial_floats * 4);
-  L.total = o;
-  return L;
-}
-
+// Workspace of ccq_moe_w4_ffn: the schedule, the SiLU(gate)*up intermediate
+// and the per-assignment down rows.
 struct MoeLayout {
   int64_t n, max_tiles;
-  StageLayout st;
-  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, off_stage, total;
+  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, total;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes) {
   MoeLayout L;
   L.n = T * k;
   L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, 16);
-  L.st = stage_layout(L.max_tiles, ex);
   size_t o = 0;
-  L.off_stage = o;  // first: its counter headers stay at fixed offsets
-  o += L.st.total;
   L.off_sorted = o;
   o += align256((size_t)L.max_tiles * 16 * 4);
   L.off_tile_expert = o;
@@ -580,13 +558,11 @@ SkinnyP grouped_params(const int32_t* sorted_ids, const int32_t* tile_expert, co
   p.tile_expert = tile_expert;
   p.meta = meta;
   p.scale_bf16 = ex->scale_dtype == CCQ_BF16;
-  p.G = (int)ex->group_size;
   return p;
 }
 
 int run_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids, const int32_t* tile_expert,
-                const int32_t* meta, int64_t max_tiles, void* inter, const ccq_w4_experts* ex,
-                const StageLayout& L, char* ws, hipStream_t st) {
+                const int32_t* meta, int64_t max_tiles, void* inter, const ccq_w4_experts* ex, hipStream_t st) {
   const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
   SkinnyP p = grouped_params(sorted_ids, tile_expert, meta, ex);
   p.x = x;
@@ -604,22 +580,15 @@ int run_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids
   p.y = inter;
   p.ldy = I;
   p.y_dtype = x_dtype;
-  p.K = (int)H;
   p.N = (int)I;
   p.KT = (int)(H / 128);
-  p.nblocks = L.gu.nblocks;
-  p.splits = L.gu.splits;
-  p.ktps = L.gu.ktps;
-  p.partial = (float*)(ws + L.off_gu_part);
-  p.counters = (int*)(ws + L.off_gu_cnt);
-  dim3 grid((unsigned)cdiv((int64_t)L.gu.nblocks * L.gu.splits, 4), (unsigned)max_tiles);
-  launch_skinny<EPI_SILU>(p, x_dtype == CCQ_BF16, L.gu.nb, grid, st);
+  const SkinnyPlan pl = plan_skinny(H, I, G, 2, 1);
+  launch_skinny<EPI_SILU>(p, x_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
   return launch_status("moe_w4 gate_up");
 }
 
 int run_down(const void* inter, int x_dtype, const int32_t* sorted_ids, const int32_t* tile_expert,
-             const int32_t* meta, int64_t max_tiles, float* rows, const ccq_w4_experts* ex, const StageLayout& L,
-             char* ws, hipStream_t st) {
+             const int32_t* meta, int64_t max_tiles, float* rows, const ccq_w4_experts* ex, hipStream_t st) {
   const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
   SkinnyP d = grouped_params(sorted_ids, tile_expert, meta, ex);
   d.x = inter;
@@ -634,22 +603,16 @@ int run_down(const void* inter, int x_dtype, const int32_t* sorted_ids, const in
   d.y = rows;
   d.ldy = H;
   d.y_dtype = CCQ_F32;
-  d.K = (int)I;
   d.N = (int)H;
   d.KT = (int)(I / 128);
-  d.nblocks = L.dn.nblocks;
-  d.splits = L.dn.splits;
-  d.ktps = L.dn.ktps;
-  d.partial = (float*)(ws + L.off_dn_part);
-  d.counters = (int*)(ws + L.off_dn_cnt);
-  dim3 grid((unsigned)cdiv((int64_t)L.dn.nblocks * L.dn.splits, 4), (unsigned)max_tiles);
-  launch_skinny<EPI_ROWS>(d, x_dtype == CCQ_BF16, L.dn.nb, grid, st);
+  const SkinnyPlan pl = plan_skinny(I, H, G, 1, 1);
+  launch_skinny<EPI_ROWS>(d, x_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
   return launch_status("moe_w4 down");
 }
 
 int check_stage_args(const void* a, int x_dtype, const int32_t* sorted_ids, const int32_t* tile_expert,
                      const int32_t* meta, int64_t max_tiles, const void* out, const ccq_w4_experts* ex,
-                     void* ws, size_t ws_bytes, bool gate_up, const char* name) {
+                     bool gate_up, const char* name) {
   int rc = check_experts(ex, name);
   if (rc) return rc;
   rc = check_expert_ptrs(ex, gate_up, name);
@@ -659,38 +622,28 @@ int check_stage_args(const void* a, int x_dtype, const int32_t* sorted_ids, cons
               (long long)max_tiles);
   CCQ_REQUIRE(a && sorted_ids && tile_expert && meta && out, "%s: null pointer", name);
   CCQ_REQUIRE(aligned(a, 16), "%s: activations must be 16-byte aligned", name);
-  const size_t need = stage_layout(max_tiles, ex).total;
-  CCQ_REQUIRE(need == 0 || (ws && ws_bytes >= need && aligned(ws, 256)),
-              "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", name, need, ws_bytes);
   return 0;
 }
 
 }  // namespace
 
-extern "C" size_t ccq_moe_w4_stage_workspace_size(int64_t max_tiles, const ccq_w4_experts* ex) {
-  if (max_tiles <= 0 || check_experts(ex, "ccq_moe_w4_stage_workspace_size") != 0) return 0;
-  return stage_layout(max_tiles, ex).total;
-}
-
 extern "C" int ccq_moe_w4_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids,
                                   const int32_t* tile_expert, const int32_t* meta, int64_t max_tiles, void* inter,
-                                  const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_stage_args(x, x_dtype, sorted_ids, tile_expert, meta, max_tiles, inter, ex, workspace,
-                            workspace_bytes, true, "ccq_moe_w4_gate_up");
+                                  const ccq_w4_experts* ex, void* stream) {
+  int rc = check_stage_args(x, x_dtype, sorted_ids, tile_expert, meta, max_tiles, inter, ex, true,
+                            "ccq_moe_w4_gate_up");
   if (rc) return rc;
   CCQ_REQUIRE(k >= 1 && k <= ex->num_experts, "ccq_moe_w4_gate_up: k=%lld outside [1, E]", (long long)k);
-  return run_gate_up(x, x_dtype, k, sorted_ids, tile_expert, meta, max_tiles, inter, ex,
-                     stage_layout(max_tiles, ex), (char*)workspace, as_stream(stream));
+  return run_gate_up(x, x_dtype, k, sorted_ids, tile_expert, meta, max_tiles, inter, ex, as_stream(stream));
 }
 
 extern "C" int ccq_moe_w4_down(const void* inter, int x_dtype, const int32_t* sorted_ids, const int32_t* tile_expert,
                                const int32_t* meta, int64_t max_tiles, float* rows, const ccq_w4_experts* ex,
-                               void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_stage_args(inter, x_dtype, sorted_ids, tile_expert, meta, max_tiles, rows, ex, workspace,
-                            workspace_bytes, false, "ccq_moe_w4_down");
+                               void* stream) {
+  int rc = check_stage_args(inter, x_dtype, sorted_ids, tile_expert, meta, max_tiles, rows, ex, false,
+                            "ccq_moe_w4_down");
   if (rc) return rc;
-  return run_down(inter, x_dtype, sorted_ids, tile_expert, meta, max_tiles, rows, ex, stage_layout(max_tiles, ex),
-                  (char*)workspace, as_stream(stream));
+  return run_down(inter, x_dtype, sorted_ids, tile_expert, meta, max_tiles, rows, ex, as_stream(stream));
 }
 
 extern "C" size_t ccq_moe_w4_workspace_size(int64_t T, int64_t k, const ccq_w4_experts* ex) {
@@ -728,13 +681,12 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
   int32_t* counts = (int32_t*)(ws + L.off_counts);
   void* inter = ws + L.off_inter;
   float* rows = (float*)(ws + L.off_rows);
-  char* sws = ws + L.off_stage;
 
   rc = launch_align(ids, L.n, ex->num_experts, 16, sorted, tile_expert, meta, counts, st);
   if (rc) return rc;
-  rc = run_gate_up(x, x_dtype, k, sorted, tile_expert, meta, L.max_tiles, inter, ex, L.st, sws, st);
+  rc = run_gate_up(x, x_dtype, k, sorted, tile_expert, meta, L.max_tiles, inter, ex, st);
   if (rc) return rc;
-  rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, L.st, sws, st);
+  rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
   if (rc) return rc;
   return launch_combine(rows, weights, ids, ex->num_experts, y, y_dtype, T, k, ex->hidden, st);
 }

@@ -106,21 +106,17 @@ int ccq_awq_repack(const int32_t* qweight, int32_t* tiled, int64_t K, int64_t N,
 int ccq_awq_unpack_tiled(const int32_t* tiled, int32_t* qweight, int64_t K, int64_t N,
                          void* stream);
 
-/* Bytes of workspace ccq_w4_gemm needs for this shape (0 if none).  The
- * workspace must be zero-filled once before first use; every call leaves it
- * zero again. */
-size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N);
-
 /* y [M, N] = x [M, K] @ dequant(W) with fp32 accumulation.
  * x_dtype CCQ_F16 | CCQ_BF16; scale_dtype CCQ_F16 | CCQ_BF16;
  * y_dtype CCQ_F16 | CCQ_BF16 | CCQ_F32.  w_tiled from ccq_awq_repack.
- * group_size in {32, 64, 128}.  x must be 16-byte aligned.
+ * group_size in {32, 64, 128}.  x must be 16-byte aligned.  M <= 16 rows per
+ * weight pass (decode); larger M re-reads the weight once per 16 rows.
+ * Needs no workspace.
  * Replaces WeightOnlyMethod.apply (quant/weight_only.py:37-54) for AWQ. */
 int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled,
                 const int32_t* qzeros, const void* scales, int scale_dtype,
                 void* y, int y_dtype, int64_t M, int64_t K, int64_t N,
-                int64_t group_size, void* workspace, size_t workspace_bytes,
-                void* stream);
+                int64_t group_size, void* stream);
 
 /* ------------------------------------------------------------------------
  * Routing and token grouping
@@ -182,21 +178,17 @@ typedef struct ccq_w4_experts {
  * ccq_moe_align_max_tiles).  Rows are assignments a = t*k + slot.
  * gate_up: inter[a, :] = silu(x[a/k] @ Wg_e) * (x[a/k] @ Wu_e), x_dtype out.
  * down:    rows[a, :]  = inter[a] @ Wd_e, float32.
- * The stage workspace (size below) must be zero-filled once before first use;
- * every call leaves it zero again.  Calls sharing one workspace must not
- * overlap in time. */
-size_t ccq_moe_w4_stage_workspace_size(int64_t max_tiles, const ccq_w4_experts* ex);
+ * Stage calls need no workspace. */
 int ccq_moe_w4_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids,
                        const int32_t* tile_expert, const int32_t* meta, int64_t max_tiles,
-                       void* inter, const ccq_w4_experts* ex, void* workspace,
-                       size_t workspace_bytes, void* stream);
+                       void* inter, const ccq_w4_experts* ex, void* stream);
 int ccq_moe_w4_down(const void* inter, int x_dtype, const int32_t* sorted_ids,
                     const int32_t* tile_expert, const int32_t* meta, int64_t max_tiles,
-                    float* rows, const ccq_w4_experts* ex, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    float* rows, const ccq_w4_experts* ex, void* stream);
 
-/* Workspace bytes for ccq_moe_w4_ffn (zero-filled once before first use;
- * every call leaves its counters zero again). */
+/* Workspace bytes for ccq_moe_w4_ffn (schedule, intermediate and down rows;
+ * no initial contents required).  Calls sharing one workspace must not
+ * overlap in time. */
 size_t ccq_moe_w4_workspace_size(int64_t T, int64_t k, const ccq_w4_experts* ex);
 
 /* Full MoE FFN from routing: x [T, H] (x_dtype CCQ_BF16 | CCQ_F16),

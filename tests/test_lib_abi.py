@@ -55,30 +55,18 @@ def test_w4_gemm_rejects_bad_shapes(lib):
     from ccut._lib import CCQ_BF16, CCQ_EINVAL, CCQ_F16, last_error
 
     p = ctypes.c_void_p(16)  # never dereferenced: validation comes first
-    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 100, 64, 128, None, 0, None)
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 100, 64, 128, None)
     assert rc == CCQ_EINVAL and "K % 128" in last_error()
-    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 96, None, 0, None)
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 96, None)
     assert rc == CCQ_EINVAL and "group_size" in last_error()
-    rc = lib.ccq_w4_gemm(p, 7, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0, None)
+    rc = lib.ccq_w4_gemm(p, 7, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
     assert rc == CCQ_EINVAL and "x_dtype" in last_error()
-    rc = lib.ccq_w4_gemm(None, CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0, None)
+    rc = lib.ccq_w4_gemm(None, CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
     assert rc == CCQ_EINVAL and "null" in last_error()
-    rc = lib.ccq_w4_gemm(ctypes.c_void_p(18), CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0,
-                         None)
+    rc = lib.ccq_w4_gemm(ctypes.c_void_p(18), CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
     assert rc == CCQ_EINVAL and "aligned" in last_error()
     # M == 0 is an empty product: success without a launch
-    assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None, 0, None) == 0
-
-
-def test_w4_gemm_workspace_contract(lib):
-    from ccut._lib import CCQ_F16, CCQ_EINVAL, last_error
-
-    need = lib.ccq_w4_gemm_workspace_size(1, 2048, 5632)
-    assert need > 0 and need % 256 == 0
-    assert lib.ccq_w4_gemm_workspace_size(1, 100, 64) == 0
-    p = ctypes.c_void_p(256)
-    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 2048, 5632, 128, p, need - 1, None)
-    assert rc == CCQ_EINVAL and "workspace" in last_error()
+    assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None) == 0
 
 
 def test_routing_rejects_bad_args(lib):
