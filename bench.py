@@ -214,10 +214,7 @@ def time_gate_up(layers, x, T: int, dev):
         inter = torch.empty((T * TOPK, INTER), dtype=torch.bfloat16, device=dev)
         keep.append((sch, desc, inter))
         uniq = int(torch.unique(ids).numel())
-        ex = l.experts
-        per_exp = sum(t.numel() * t.element_size() for t in (ex.w_gate, ex.z_gate, ex.s_gate, ex.w_up, ex.z_up,
-                                                             ex.s_up)) // E
-        gu_bytes.append(uniq * per_exp + x.numel() * 2 + T * TOPK * INTER * 2)
+        gu_bytes.append(uniq * l.experts.gate_up_bytes_per_expert + x.numel() * 2 + T * TOPK * INTER * 2)
         args = (ctypes.c_void_p(x.data_ptr()), 2, TOPK, ctypes.c_void_p(sch.sorted_ids.data_ptr()),
                 ctypes.c_void_p(sch.tile_expert.data_ptr()), ctypes.c_void_p(sch.meta.data_ptr()), mt,
                 ctypes.c_void_p(inter.data_ptr()), ctypes.byref(desc), ctypes.c_void_p(stream))
@@ -251,15 +248,15 @@ def bench_gemm(M: int, K: int, N: int, dev, copies: int):
     launches = []
     for w in ws:
         args = (ctypes.c_void_p(x.data_ptr()), 1, ctypes.c_void_p(w.w_tiled.data_ptr()),
-                ctypes.c_void_p(w.qzeros.data_ptr()), ctypes.c_void_p(w.scales.data_ptr()), 1,
-                ctypes.c_void_p(y.data_ptr()), 1, M, K, N, GROUP, ctypes.c_void_p(stream))
+                ctypes.c_void_p(w.sz.data_ptr()), 1, ctypes.c_void_p(y.data_ptr()), 1, M, K, N, GROUP,
+                ctypes.c_void_p(stream))
         launches.append(lambda a=args: lib.ccq_w4_gemm(*a))
     _lib.check(launches[0](), "ccq_w4_gemm")
     torch.cuda.synchronize()
     if not torch.equal(y, ref):
         raise RuntimeError("bench_gemm: raw launch and API disagree")
     avg = device_time(launches, reps=4)
-    nbytes = ws[0].nbytes + M * K * 2 + M * N * 2
+    nbytes = ws[0].format_bytes + M * K * 2 + M * N * 2
     return {"M": M, "K": K, "N": N, "avg_us": avg * 1e6, "bytes": nbytes, "GBps": nbytes / avg / 1e9,
             "frac_hbm": nbytes / avg / PEAK_HBM, "TFLOPs": 2.0 * M * K * N / avg / 1e12}
 

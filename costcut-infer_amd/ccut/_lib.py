@@ -34,9 +34,9 @@ class CcqLibraryError(RuntimeError):
 
 class ccq_w4_experts(ctypes.Structure):
     _fields_ = [
-        ("w_gate", _vp), ("z_gate", _vp), ("s_gate", _vp),
-        ("w_up", _vp), ("z_up", _vp), ("s_up", _vp),
-        ("w_down", _vp), ("z_down", _vp), ("s_down", _vp),
+        ("w_gate", _vp), ("sz_gate", _vp),
+        ("w_up", _vp), ("sz_up", _vp),
+        ("w_down", _vp), ("sz_down", _vp),
         ("scale_dtype", _int),
         ("num_experts", _i64), ("hidden", _i64), ("inter", _i64), ("group_size", _i64),
     ]
@@ -56,7 +56,9 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_awq_dequant": (_int, [_vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
     "ccq_awq_repack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ccq_awq_unpack_tiled": (_int, [_vp, _vp, _i64, _i64, _vp]),
-    "ccq_w4_gemm": (_int, [_vp, _int, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp]),
+    "ccq_awq_sz_words": (_i64, [_i64, _i64]),
+    "ccq_awq_pack_sz": (_int, [_vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
+    "ccq_w4_gemm": (_int, [_vp, _int, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp]),
     "ccq_topk_softmax": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "ccq_moe_align_max_tiles": (_i64, [_i64, _i64, _i64]),
     "ccq_moe_align": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),

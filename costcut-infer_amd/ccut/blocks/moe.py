@@ -182,18 +182,17 @@ def shared_expert_add(y, shared_out, gate_value: float) -> None:
 
 @dataclass
 class W4Experts:
-    """All experts of one MoE layer, AWQ int4, resident in HBM in the tile
-    layout.  gate/up are ``[hidden -> inter]``, down ``[inter -> hidden]``."""
+    """All experts of one MoE layer, AWQ int4, resident in HBM in the GPU
+    layout (tiled weights + packed scale/zero words, see ``quant.awq``).
+    gate/up are ``[hidden -> inter]``, down ``[inter -> hidden]``."""
 
     w_gate: torch.Tensor
-    z_gate: torch.Tensor
-    s_gate: torch.Tensor
+    sz_gate: torch.Tensor
     w_up: torch.Tensor
-    z_up: torch.Tensor
-    s_up: torch.Tensor
+    sz_up: torch.Tensor
     w_down: torch.Tensor
-    z_down: torch.Tensor
-    s_down: torch.Tensor
+    sz_down: torch.Tensor
+    scale_dtype: torch.dtype
     num_experts: int
     hidden: int
     inter: int
@@ -207,13 +206,22 @@ class W4Experts:
             qw, qz, sc = (_dev.to_device(a) for a in t)
             E = qw.shape[0]
             qw = qw.view(torch.int32).reshape(E, K, N // 8)
-            tiled = torch.empty_like(qw)
-            for e in range(E):
-                call("ccq_awq_repack", qw[e].data_ptr(), tiled[e].data_ptr(), K, N, _dev.stream_ptr())
+            qz = qz.view(torch.int32).reshape(E, K // group_size, N // 8)
             if sc.dtype not in (torch.float16, torch.bfloat16):
                 sc = sc.to(torch.float16)
-            return tiled, qz.view(torch.int32).reshape(E, K // group_size, N // 8).contiguous(), sc.contiguous()
+            sc = sc.reshape(E, K // group_size, N).contiguous()
+            tiled = torch.empty_like(qw)
+            words = lib().ccq_awq_sz_words(K, group_size)
+            sz = torch.empty((E, N, words), dtype=torch.int32, device=qw.device)
+            code = 1 if sc.dtype == torch.float16 else 2
+            for e in range(E):
+                call("ccq_awq_repack", qw[e].data_ptr(), tiled[e].data_ptr(), K, N, _dev.stream_ptr())
+                call("ccq_awq_pack_sz", qz[e].contiguous().data_ptr(), sc[e].data_ptr(), code, sz[e].data_ptr(),
+                     K, N, group_size, _dev.stream_ptr())
+            return tiled, sz, sc.dtype
 
+        if group_size not in (32, 64, 128):
+            raise ValueError(f"AWQ group size {group_size} not in (32, 64, 128)")
         E = _dev.to_device(gate[0]).shape[0]
         sg = _dev.to_device(gate[2])
         hidden = sg.shape[1] * group_size
@@ -221,20 +229,31 @@ class W4Experts:
         g = stack(gate, hidden, inter)
         u = stack(up, hidden, inter)
         d = stack(down, inter, hidden)
-        return W4Experts(*g, *u, *d, num_experts=E, hidden=hidden, inter=inter, group_size=group_size)
+        if not (g[2] == u[2] == d[2]):
+            raise ValueError("gate, up and down scales must share one dtype")
+        return W4Experts(g[0], g[1], u[0], u[1], d[0], d[1], g[2], num_experts=E, hidden=hidden, inter=inter,
+                         group_size=group_size)
 
     def descriptor(self) -> ccq_w4_experts:
-        code = 1 if self.s_gate.dtype == torch.float16 else 2
-        return ccq_w4_experts(self.w_gate.data_ptr(), self.z_gate.data_ptr(), self.s_gate.data_ptr(),
-                              self.w_up.data_ptr(), self.z_up.data_ptr(), self.s_up.data_ptr(),
-                              self.w_down.data_ptr(), self.z_down.data_ptr(), self.s_down.data_ptr(),
+        code = 1 if self.scale_dtype == torch.float16 else 2
+        return ccq_w4_experts(self.w_gate.data_ptr(), self.sz_gate.data_ptr(), self.w_up.data_ptr(),
+                              self.sz_up.data_ptr(), self.w_down.data_ptr(), self.sz_down.data_ptr(),
                               code, self.num_experts, self.hidden, self.inter, self.group_size)
 
     @property
     def bytes_per_expert(self) -> int:
-        ts = (self.w_gate, self.z_gate, self.s_gate, self.w_up, self.z_up, self.s_up, self.w_down, self.z_down,
-              self.s_down)
-        return sum(t.numel() * t.element_size() for t in ts) // self.num_experts
+        """Bytes of one expert in the AWQ format (int4 weights, 16-bit scales,
+        int4 zeros of gate, up and down): the algorithmic traffic of reading
+        it once."""
+        H, I, G = self.hidden, self.inter, self.group_size
+        one = H * I // 2 + (H // G) * I * 2 + (H // G) * I // 2
+        down = I * H // 2 + (I // G) * H * 2 + (I // G) * H // 2
+        return 2 * one + down
+
+    @property
+    def gate_up_bytes_per_expert(self) -> int:
+        H, I, G = self.hidden, self.inter, self.group_size
+        return 2 * (H * I // 2 + (H // G) * I * 2 + (H // G) * I // 2)
 
 
 def moe_ffn_w4(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, experts: W4Experts,

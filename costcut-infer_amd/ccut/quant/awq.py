@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import torch
 
 from ccut import _dev
-from ccut._lib import call
+from ccut._lib import call, lib
 
 AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
 AWQ_REVERSE_ORDER = (0, 4, 1, 5, 2, 6, 3, 7)
@@ -44,29 +44,39 @@ def unpack_awq(packed: torch.Tensor) -> torch.Tensor:
 
 @dataclass
 class AwqWeights:
-    """One AWQ linear resident in HBM, re-packed for the GPU kernels.
+    """One AWQ linear resident in HBM, re-packed once for the GPU kernels.
 
     ``w_tiled`` has the bytes of ``qweight`` in the tile layout of
-    ``ccq_awq_repack``; ``qzeros`` and ``scales`` keep the AWQ layout."""
+    ``ccq_awq_repack``; ``sz`` holds one 32-bit word per (column, group) with
+    the scale bits and the zero point (``ccq_awq_pack_sz``)."""
 
     w_tiled: torch.Tensor
-    qzeros: torch.Tensor
-    scales: torch.Tensor
+    sz: torch.Tensor
+    scale_dtype: torch.dtype
     K: int
     N: int
     group_size: int
 
     @property
     def nbytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in (self.w_tiled, self.qzeros, self.scales))
+        """Bytes resident in HBM."""
+        return self.w_tiled.numel() * self.w_tiled.element_size() + self.sz.numel() * self.sz.element_size()
+
+    @property
+    def format_bytes(self) -> int:
+        """Bytes of the AWQ format itself (int4 weights, 16-bit scales, int4
+        zeros): the algorithmic traffic of one pass over the weight."""
+        groups = self.K // self.group_size
+        return self.K * self.N // 2 + groups * self.N * 2 + groups * self.N // 2
 
 
-def _scale_code(scales: torch.Tensor) -> int:
-    if scales.dtype == torch.float16:
+def _scale_code(scales) -> int:
+    dt = scales if isinstance(scales, torch.dtype) else scales.dtype
+    if dt == torch.float16:
         return 1
-    if scales.dtype == torch.bfloat16:
+    if dt == torch.bfloat16:
         return 2
-    raise ValueError(f"AWQ scales must be float16 or bfloat16, got {scales.dtype}")
+    raise ValueError(f"AWQ scales must be float16 or bfloat16, got {dt}")
 
 
 def repack(qweight, K: int, N: int) -> torch.Tensor:
@@ -83,6 +93,18 @@ def unpack_tiled(w_tiled: torch.Tensor, K: int, N: int) -> torch.Tensor:
     return out
 
 
+def pack_sz(qzeros, scales, K: int, N: int, group_size: int) -> torch.Tensor:
+    """``qzeros [K/G, N/8]`` + ``scales [K/G, N]`` -> ``sz [N, words]`` uint32
+    (stored as int32) with ``words = ccq_awq_sz_words(K, G)``."""
+    qz = _dev.to_device(qzeros).view(torch.int32).contiguous()
+    sc = _dev.to_device(scales).contiguous()
+    words = lib().ccq_awq_sz_words(K, group_size)
+    out = torch.empty((N, words), dtype=torch.int32, device=qz.device)
+    call("ccq_awq_pack_sz", qz.data_ptr(), sc.data_ptr(), _scale_code(sc), out.data_ptr(), K, N, group_size,
+         _dev.stream_ptr())
+    return out
+
+
 def prepare(qweight, qzeros, scales, group_size: int = 128) -> AwqWeights:
     """Upload (if needed) and re-pack one AWQ linear.  Validates shapes with
     the reference's error type (``ValueError``, ``quant/method.py:42``)."""
@@ -92,6 +114,8 @@ def prepare(qweight, qzeros, scales, group_size: int = 128) -> AwqWeights:
         sc = sc.to(torch.float16)
     if sc.dim() != 2:
         raise ValueError(f"AWQ scales must be 2-D [K/G, N], got {tuple(sc.shape)}")
+    if group_size not in (32, 64, 128):
+        raise ValueError(f"AWQ group size {group_size} not in (32, 64, 128)")
     groups, N = sc.shape
     K = groups * group_size
     qw = _dev.to_device(qweight).view(torch.int32)
@@ -101,7 +125,7 @@ def prepare(qweight, qzeros, scales, group_size: int = 128) -> AwqWeights:
         raise ValueError(f"AWQ qzeros has {qz.numel()} words, expected {groups * N // 8}")
     if K % 128 or N % 16:
         raise ValueError(f"AWQ GPU path needs K % 128 == 0 and N % 16 == 0 (K={K}, N={N})")
-    return AwqWeights(repack(qw, K, N), qz.reshape(groups, N // 8).contiguous(), sc.contiguous(), K, N,
+    return AwqWeights(repack(qw, K, N), pack_sz(qz.reshape(groups, N // 8), sc, K, N, group_size), sc.dtype, K, N,
                       group_size)
 
 
@@ -128,7 +152,7 @@ def gemm(x: torch.Tensor, w: AwqWeights, out_dtype: torch.dtype | None = None) -
         raise ValueError(f"AWQ GEMM: x has {K} features, weight expects {w.K}")
     out_dtype = out_dtype or x.dtype
     y = torch.empty((M, w.N), dtype=out_dtype, device=x.device)
-    call("ccq_w4_gemm", x2.data_ptr(), _dev.DTYPE_CODE[x.dtype], w.w_tiled.data_ptr(), w.qzeros.data_ptr(),
-         w.scales.data_ptr(), _scale_code(w.scales), y.data_ptr(), _dev.DTYPE_CODE[out_dtype], M, K, w.N,
-         w.group_size, _dev.stream_ptr(x.device))
+    call("ccq_w4_gemm", x2.data_ptr(), _dev.DTYPE_CODE[x.dtype], w.w_tiled.data_ptr(), w.sz.data_ptr(),
+         _scale_code(w.scale_dtype), y.data_ptr(), _dev.DTYPE_CODE[out_dtype], M, K, w.N, w.group_size,
+         _dev.stream_ptr(x.device))
     return y.reshape(*x.shape[:-1], w.N)

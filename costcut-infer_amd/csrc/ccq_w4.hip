@@ -1,7 +1,7 @@
 // AWQ int4 on gfx950: dequant, re-pack into MFMA-ready tiles, the skinny
 // (decode) GEMM and the MoE expert FFN built on it.
 //
-// Tile layout ("T16x128"): the weight W[K, N] (in x out) is stored as tiles of
+// Weight tile layout ("T16x128"): W[K, N] (in x out) is stored as tiles of
 // 128 K-rows x 16 N-columns, tile (kt, nt) at dword offset ((nt*KT + kt)*64 +
 // lane)*4, i.e. 1 KiB per tile, one 16-byte slice per lane.  Dword j of lane l
 // holds the 8 nibbles of column n = nt*16 + (l & 15) at
@@ -14,7 +14,14 @@
 // A wave-wide 16-byte load of one tile is a fully coalesced 1 KiB transfer
 // that feeds 4 MFMAs (K = 4 x 32).
 //
-// Per quantization group (G = 128 by default) the kernel accumulates
+// Scale/zero layout ("SZ"): one 32-bit word per (column, group), scale bits
+// (fp16 or bf16) in the low half and the 4-bit zero point in the high half,
+// stored column-major: sz[n][g], each column padded to a whole number of
+// 4-k-tile chunks (ccq_awq_sz_words).  A lane fetches the scales and zeros of
+// its column for 4 k-tiles with one 16-byte load, and no cache line is shared
+// between column tiles (so none is fetched twice by different XCDs).
+//
+// Per quantization group the kernel accumulates
 //     tmp = sum_k x[m,k] * (MAGIC + q[k,n])
 //     acc += s[g,n] * (tmp - (MAGIC + z[g,n]) * Sx[m,g]),  Sx = sum_k x[m,k]
 // which equals sum_k x * (q - z) * s exactly up to float32 rounding; Sx comes
@@ -39,6 +46,10 @@ __device__ __forceinline__ int tile_nib(int e) { return (e & 1) ? 4 + (e >> 1) :
 __device__ __forceinline__ float scale_at(const uint16_t* s, int64_t i, int bf16) {
   uint32_t b = s[i];
   return bf16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+__host__ __device__ inline int64_t sz_words_per_column(int64_t K, int64_t G) {
+  return ((K / 128 + 3) / 4) * 4 * (128 / G);
 }
 
 // ------------------------------------------------------------------ dequant --
@@ -93,6 +104,22 @@ __global__ void awq_unpack_tiled_kernel(const uint32_t* __restrict__ tiled, uint
       o |= ((d >> (4 * tile_nib(e))) & 15u) << awq_shift(j);
     }
     qw[i] = o;
+  }
+}
+
+// sz[n][g] = scale bits | zero << 16; padding words (g >= K/G) are 0.
+__global__ void awq_pack_sz_kernel(const uint32_t* __restrict__ qz, const uint16_t* __restrict__ sc,
+                                   uint32_t* __restrict__ sz, int64_t K, int64_t N, int64_t G) {
+  const int64_t groups = K / G, W = sz_words_per_column(K, G), total = N * W, N8 = N / 8;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / W, g = i - n * W;
+    uint32_t o = 0;
+    if (g < groups) {
+      const uint32_t z = (qz[g * N8 + (n >> 3)] >> awq_shift((int)(n & 7))) & 15u;
+      o = (uint32_t)sc[g * N + n] | (z << 16);
+    }
+    sz[i] = o;
   }
 }
 
@@ -153,88 +180,123 @@ struct SkinnyP {
   const int32_t* tile_expert; // expert of each tile; null = single weight
   const int32_t* meta;        // meta[0] = number of valid tiles; null = gridDim.y
   const uint32_t* w0;
-  const uint32_t* z0;
-  const uint16_t* s0;
+  const uint32_t* sz0;
   const uint32_t* w1;         // second weight (up projection) for EPI_SILU
-  const uint32_t* z1;
-  const uint16_t* s1;
-  int64_t w_es, z_es, s_es;   // per-expert strides (elements)
-  int scale_bf16;
+  const uint32_t* sz1;
+  int64_t w_es, sz_es;        // per-expert strides (words)
   void* y;
   int64_t ldy;
   int y_dtype;
-  int M, N, KT;
-  int ktpw;                   // 128-row k-tiles per wave
+  int M, N, K, KT;
+  int szw;                    // SZ words per column
+  int ktpw;                   // k-tiles per wave (a multiple of KTW)
+  int xs_rows;                // activation rows a workgroup may stage in LDS
+  int xs_ld;                  // LDS row stride of staged activations (elements)
 };
 
-// k-tiles whose packed weights, scales and zero words one wave holds in
-// registers at once: all of them are requested before the first multiply, so
-// each wave keeps KTW KiB (x2 for gate+up) of HBM reads in flight.
+// k-tiles whose packed weights, scales and zeros one wave holds in registers
+// at once: all of them are requested before the first multiply.
 constexpr int KTW = 4;
 
-// Workgroup = W waves (W = blockDim.x / 64) sharing one job: the 16-row tile
-// blockIdx.y times the 16*NB output columns of block blockIdx.x.  Wave w owns
-// the k-tiles [w*ktpw, (w+1)*ktpw) (ktpw <= KTW per chunk, more chunks if
-// larger); the W partial sums are added in wave order through LDS
-// (deterministic, no global atomics or fences), and wave 0 runs the epilogue.
-template <typename AT, int NB, int GS, int EPI>
-__global__ __launch_bounds__(512) void w4_skinny_kernel(const SkinnyP p) {
+template <typename ST>
+__device__ __forceinline__ float sz_scale(uint32_t word);
+template <>
+__device__ __forceinline__ float sz_scale<__bf16>(uint32_t word) {
+  return __uint_as_float(word << 16);
+}
+template <>
+__device__ __forceinline__ float sz_scale<_Float16>(uint32_t word) {
+  return f16_bits_to_f32(word & 0xFFFFu);
+}
+
+// One workgroup job: the 16-row tile `tile` times the 16*NB output columns of
+// block `nb`, K split over the W waves (wave w owns k-tiles
+// [w*ktpw, (w+1)*ktpw), processed in chunks of KTW).  STAGED: the valid rows
+// sit in LDS (rows [0, nrows)) next to an all-zero row at index xs_rows that
+// padding lanes read, so the loop has no per-lane branches or selects.
+// Otherwise every wave loads its A fragments from global memory.
+template <typename AT, typename ST, int NB, int GS, int EPI, bool STAGED>
+__device__ __forceinline__ void skinny_job(const SkinnyP& p, char* smem, int tile, int nb, int ex, int rid,
+                                           bool rvalid, int nrows) {
   using V = typename Act<AT>::vec;
   constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
-  constexpr int NG = 4 / GS;  // quantization groups per 128-row tile
-  constexpr int NV = NACC * NB * 4;
-  extern __shared__ float red[];  // [(W-1) * NV][64]
+  constexpr int NG = 4 / GS;               // quantization groups per 128-row tile
+  constexpr int NV = NACC * NB * 4;        // accumulator floats per lane
+  // k-tiles held per chunk: KTW, or KTW/2 when several groups per k-tile
+  // and accumulators would exceed the register budget (the halved chunk is
+  // still a whole number of 16-byte SZ records since NG >= 2 there)
+  constexpr int KC = (NG >= 2 && NACC * NB * NG >= 4) ? KTW / 2 : KTW;
+  constexpr int SZV = (KC * NG + 3) / 4;   // 16-byte SZ loads per chunk
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
-  const int nb = blockIdx.x;
-  const int tile = blockIdx.y;
-  if (p.meta != nullptr && tile >= p.meta[0]) return;  // whole workgroup
-  const int ex = p.tile_expert ? p.tile_expert[tile] : 0;
-
   const int r = lane & 15, kq = lane >> 4;
-  int rid;
-  bool rvalid;
-  if (p.rows) {
-    rid = p.rows[tile * 16 + r];
-    rvalid = rid >= 0;
-  } else {
-    rid = tile * 16 + r;
-    rvalid = rid < p.M;
-  }
-  // padding rows read row 0 (always present) and multiply zeros instead
-  const AT* xr = reinterpret_cast<const AT*>(p.x) + (int64_t)(rvalid ? rid / p.row_div : 0) * p.ldx + 8 * kq;
-
   const int kt0 = wave * p.ktpw;
   const int kt1 = min(p.KT, kt0 + p.ktpw);
-  const int64_t N8 = p.N >> 3;
-  const uint32_t* wb[NACC];
-  const uint32_t* zb[NACC];
-  const uint16_t* sb[NACC];
-  wb[0] = p.w0 + (int64_t)ex * p.w_es;
-  zb[0] = p.z0 + (int64_t)ex * p.z_es;
-  sb[0] = p.s0 + (int64_t)ex * p.s_es;
-  if (NACC == 2) {
-    wb[NACC - 1] = p.w1 + (int64_t)ex * p.w_es;
-    zb[NACC - 1] = p.z1 + (int64_t)ex * p.z_es;
-    sb[NACC - 1] = p.s1 + (int64_t)ex * p.s_es;
-  }
-  int ncol[NB], zsh[NB];
-#pragma unroll
-  for (int t = 0; t < NB; ++t) {
-    ncol[t] = (nb * NB + t) * 16 + (lane & 15);
-    zsh[t] = awq_shift(ncol[t] & 7);
-  }
-  const int sbf = p.scale_bf16;
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  auto load_x = [&](V (&a)[4], int kt) {
+  // weight tiles of column block t: uniform base + 16 bytes per lane
+  const uint32_t* wcol[NACC][NB];
+  const uint32_t* szl[NACC][NB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(xr + (int64_t)kt * 128 + 32 * j);
-      a[j] = __builtin_bit_cast(V, rvalid ? v : zero4);
+  for (int q = 0; q < NACC; ++q) {
+    const uint32_t* wbase = (q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es;
+    const uint32_t* zbase = (q == 0 ? p.sz0 : p.sz1) + (int64_t)ex * p.sz_es;
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      wcol[q][t] = wbase + (int64_t)(nb * NB + t) * p.KT * 256 + lane * 4;
+      szl[q][t] = zbase + (int64_t)((nb * NB + t) * 16 + r) * p.szw;
     }
+  }
+
+  u32x4 wv[KC][NACC][NB];
+  u32x4 szv[NACC][NB][SZV];
+  // every weight and scale/zero load of a chunk at once; tiles past the end
+  // of the wave's range re-read its last tile (same addresses, no extra HBM
+  // traffic) and contribute with a zero scale; SZ columns are padded to
+  // whole chunks
+  auto load_w = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      const int kt = min(c0 + i, kt1 - 1);
+#pragma unroll
+      for (int q = 0; q < NACC; ++q)
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+          wv[i][q][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wcol[q][t] + kt * 256));
+    }
+#pragma unroll
+    for (int q = 0; q < NACC; ++q)
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int v = 0; v < SZV; ++v) szv[q][t][v] = *reinterpret_cast<const u32x4*>(szl[q][t] + c0 * NG + 4 * v);
   };
+  // the first chunk's HBM reads are in flight while the activations are staged
+  if (kt0 < kt1) load_w(kt0);
+
+  AT* xs = reinterpret_cast<AT*>(smem);
+  float* red = reinterpret_cast<float*>(smem + (size_t)(p.xs_rows + 1) * p.xs_ld * sizeof(AT));
+  const AT* xl = nullptr;
+  const AT* xg = nullptr;
+  if constexpr (STAGED) {
+    const int chunks = p.K / 8;  // 16-byte pieces per row
+    for (int c = threadIdx.x; c < nrows * chunks; c += blockDim.x) {
+      const int s = c / chunks, off = c - s * chunks;
+      const int srid = __shfl(rid, s, 64);  // lanes 0..15 hold rows 0..15
+      const bool sval = p.rows ? srid >= 0 : srid < p.M;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (sval)
+        v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const AT*>(p.x) + (int64_t)(srid / p.row_div) * p.ldx +
+                                            8 * off);
+      *reinterpret_cast<u32x4*>(xs + s * p.xs_ld + 8 * off) = v;
+    }
+    for (int c = threadIdx.x; c < chunks; c += blockDim.x)
+      *reinterpret_cast<u32x4*>(xs + p.xs_rows * p.xs_ld + 8 * c) = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+    xl = xs + (r < nrows ? r : p.xs_rows) * p.xs_ld + 8 * kq;
+  } else {
+    xg = reinterpret_cast<const AT*>(p.x) + (int64_t)(rvalid ? rid / p.row_div : 0) * p.ldx + 8 * kq;
+  }
 
   f32x4 acc[NACC][NB];
 #pragma unroll
@@ -243,39 +305,23 @@ __global__ __launch_bounds__(512) void w4_skinny_kernel(const SkinnyP p) {
     for (int t = 0; t < NB; ++t) acc[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const u32x4 ones_u = {Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2};
   const V ones = __builtin_bit_cast(V, ones_u);
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  for (int c0 = kt0; c0 < kt1; c0 += KTW) {
-    const int nk = min(KTW, kt1 - c0);
-    u32x4 wv[KTW][NACC][NB];
-    float sv[KTW][NACC][NB][NG];
-    uint32_t zv[KTW][NACC][NB][NG];
-    // every weight / scale / zero load of the chunk first (tiles past the
-    // end re-read the last one: same addresses, no extra HBM traffic)
+  for (int c0 = kt0; c0 < kt1; c0 += KC) {
 #pragma unroll
-    for (int i = 0; i < KTW; ++i) {
+    for (int i = 0; i < KC; ++i) {
       const int kt = min(c0 + i, kt1 - 1);
+      const bool live = c0 + i < kt1;
+      V a[4];
 #pragma unroll
-      for (int q = 0; q < NACC; ++q)
-#pragma unroll
-        for (int t = 0; t < NB; ++t) {
-          wv[i][q][t] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(wb[q] + (((int64_t)(nb * NB + t) * p.KT + kt) * 64 + lane) * 4));
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            const int64_t grp = (int64_t)kt * NG + g;
-            sv[i][q][t][g] = scale_at(sb[q], grp * p.N + ncol[t], sbf);
-            zv[i][q][t][g] = zb[q][grp * N8 + (ncol[t] >> 3)];
-          }
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (STAGED) {
+          a[j] = *reinterpret_cast<const V*>(xl + kt * 128 + 32 * j);
+        } else {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(xg + (int64_t)kt * 128 + 32 * j);
+          a[j] = __builtin_bit_cast(V, rvalid ? v : zero4);
         }
-    }
-    V a0[4], a1[4];
-    load_x(a0, c0);
-#pragma unroll
-    for (int i = 0; i < KTW; ++i) {
-      if (i >= nk) break;
-      V(&a)[4] = (i & 1) ? a1 : a0;
-      V(&an)[4] = (i & 1) ? a0 : a1;
-      if (i + 1 < nk) load_x(an, c0 + i + 1);
+      }
       f32x4 sx[NG];
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
@@ -292,12 +338,14 @@ __global__ __launch_bounds__(512) void w4_skinny_kernel(const SkinnyP p) {
             f32x4 tmp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int jj = 0; jj < GS; ++jj) tmp = mfma16(a[g * GS + jj], dq_b<AT>(wv[i][q][t][g * GS + jj]), tmp);
-            const float c = Act<AT>::kMagic + (float)((zv[i][q][t][g] >> zsh[t]) & 15u);
-            const float s = sv[i][q][t][g];
+            const uint32_t word = szv[q][t][(i * NG + g) >> 2][(i * NG + g) & 3];
+            const float s = live ? sz_scale<ST>(word) : 0.f;
+            const float c = Act<AT>::kMagic + (float)(word >> 16);
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[q][t][e] = fmaf(s, fmaf(-c, sx[g][e], tmp[e]), acc[q][t][e]);
           }
     }
+    if (c0 + KC < kt1) load_w(c0 + KC);
   }
 
   if (W > 1) {
@@ -331,7 +379,7 @@ __global__ __launch_bounds__(512) void w4_skinny_kernel(const SkinnyP p) {
     if (!ovalid) continue;
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
-      const int64_t o = (int64_t)orid * p.ldy + ncol[t];
+      const int64_t o = (int64_t)orid * p.ldy + (nb * NB + t) * 16 + r;
       if (EPI == EPI_SILU) {
         const float g = acc[0][t][i], u = acc[NACC - 1][t][i];
         store_val(p.y, o, g / (1.0f + expf(-g)) * u, p.y_dtype);
@@ -342,18 +390,56 @@ __global__ __launch_bounds__(512) void w4_skinny_kernel(const SkinnyP p) {
   }
 }
 
+// Workgroup = W waves (W = blockDim.x / 64) sharing one job (row tile
+// blockIdx.y, column block blockIdx.x); the W partial sums are added in wave
+// order through LDS (deterministic, no global atomics or fences), and wave 0
+// runs the epilogue.  The valid rows of a tile are a prefix (dense rows < M;
+// the expert schedule pads at the end); when the rows up to the last valid one
+// fit the LDS budget (xs_rows) the workgroup stages them in LDS.
+template <typename AT, typename ST, int NB, int GS, int EPI>
+__global__ __launch_bounds__(512) void w4_skinny_kernel(const SkinnyP p) {
+  extern __shared__ __align__(16) char smem[];
+  const int lane = threadIdx.x & 63;
+  const int nb = blockIdx.x;
+  const int tile = blockIdx.y;
+  if (p.meta != nullptr && tile >= p.meta[0]) return;  // whole workgroup
+  const int ex = p.tile_expert ? p.tile_expert[tile] : 0;
+  const int r = lane & 15;
+  int rid;
+  bool rvalid;
+  if (p.rows) {
+    rid = p.rows[tile * 16 + r];
+    rvalid = rid >= 0;
+  } else {
+    rid = tile * 16 + r;
+    rvalid = rid < p.M;
+  }
+  const uint64_t vmask = __ballot(rvalid) & 0xFFFFull;
+  const int nrows = vmask ? 64 - __clzll(vmask) : 0;
+  if (nrows <= p.xs_rows)
+    skinny_job<AT, ST, NB, GS, EPI, true>(p, smem, tile, nb, ex, rid, rvalid, nrows);
+  else
+    skinny_job<AT, ST, NB, GS, EPI, false>(p, smem, tile, nb, ex, rid, rvalid, nrows);
+}
+
 // --------------------------------------------------------------- planning --
 struct SkinnyPlan {
   int nb;        // 16-column tiles per job
   int nblocks;   // jobs per row tile
   int waves;     // waves per workgroup (K split)
   int ktpw;      // k-tiles per wave
+  int xs_rows;   // activation rows staged in LDS
+  int xs_ld;     // their LDS row stride (elements)
   size_t lds;    // dynamic LDS bytes
 };
 
-// K is split over the waves of a workgroup so that each wave holds at most
-// KTW k-tiles (all its weight loads in flight at once); at most 8 waves, so
-// K > 8*KTW*128 gives each wave several chunks.
+// LDS a workgroup may spend on staged activation rows.
+constexpr size_t kStageBytes = 24 * 1024;
+
+// K is split over the waves of a workgroup so that each wave holds one chunk
+// of KTW k-tiles (all its weight loads in flight at once); at most 8 waves,
+// so K > 8*KTW*128 gives each wave several chunks.  Chunk starts are
+// multiples of KTW, the granularity of the padded SZ columns.
 static SkinnyPlan plan_skinny(int64_t K, int64_t N, int64_t G, int nacc, int NB) {
   SkinnyPlan pl;
   const int64_t KT = K / 128, NT = N / 16;
@@ -364,45 +450,58 @@ static SkinnyPlan plan_skinny(int64_t K, int64_t N, int64_t G, int nacc, int NB)
   int64_t W = cdiv(KT, KTW);
   if (W > 8) W = 8;
   if (W < 1) W = 1;
-  pl.ktpw = (int)cdiv(KT, W);
+  pl.ktpw = (int)(cdiv(cdiv(KT, W), KTW) * KTW);
   pl.waves = (int)cdiv(KT, pl.ktpw);
-  pl.lds = (size_t)(pl.waves - 1) * nacc * NB * 4 * 64 * sizeof(float);
+  pl.xs_ld = (int)(K + 8);  // 16 bytes of padding per row staggers LDS banks
+  const size_t row_bytes = (size_t)pl.xs_ld * 2;
+  pl.xs_rows = (int)imin64(16, (int64_t)(kStageBytes / row_bytes) - 1);  // + the zero row
+  pl.lds = (size_t)(pl.xs_rows + 1) * row_bytes + (size_t)(pl.waves - 1) * nacc * NB * 4 * 64 * sizeof(float);
   return pl;
 }
 
-template <typename AT, int NB, int EPI>
+template <typename AT, typename ST, int NB, int EPI>
 static void launch_skinny_gs(const SkinnyP& p, dim3 grid, int waves, size_t lds, hipStream_t st, int G) {
   const dim3 block(64 * waves);
   if (G == 128)
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 4, EPI>), grid, block, lds, st, p);
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, ST, NB, 4, EPI>), grid, block, lds, st, p);
   else if (G == 64)
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 2, EPI>), grid, block, lds, st, p);
-  else
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, NB, 1, EPI>), grid, block, lds, st, p);
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, ST, NB, 2, EPI>), grid, block, lds, st, p);
+  else if constexpr (NB <= 2)  // plan_skinny never pairs 4 column tiles with G = 32
+    hipLaunchKernelGGL((w4_skinny_kernel<AT, ST, NB, 1, EPI>), grid, block, lds, st, p);
 }
 
-template <typename AT, int EPI>
+template <typename AT, typename ST, int EPI>
 static void launch_skinny_nb(const SkinnyP& p, const SkinnyPlan& pl, dim3 grid, hipStream_t st, int G) {
   if constexpr (EPI != EPI_STORE) {
-    launch_skinny_gs<AT, 1, EPI>(p, grid, pl.waves, pl.lds, st, G);
+    launch_skinny_gs<AT, ST, 1, EPI>(p, grid, pl.waves, pl.lds, st, G);
   } else {
     if (pl.nb == 1)
-      launch_skinny_gs<AT, 1, EPI>(p, grid, pl.waves, pl.lds, st, G);
+      launch_skinny_gs<AT, ST, 1, EPI>(p, grid, pl.waves, pl.lds, st, G);
     else if (pl.nb == 2)
-      launch_skinny_gs<AT, 2, EPI>(p, grid, pl.waves, pl.lds, st, G);
+      launch_skinny_gs<AT, ST, 2, EPI>(p, grid, pl.waves, pl.lds, st, G);
     else
-      launch_skinny_gs<AT, 4, EPI>(p, grid, pl.waves, pl.lds, st, G);
+      launch_skinny_gs<AT, ST, 4, EPI>(p, grid, pl.waves, pl.lds, st, G);
   }
 }
 
 template <int EPI>
-static void launch_skinny(SkinnyP p, int x_bf16, const SkinnyPlan& pl, int64_t tiles, hipStream_t st, int G) {
+static void launch_skinny(SkinnyP p, int x_bf16, int s_bf16, const SkinnyPlan& pl, int64_t tiles, hipStream_t st,
+                          int G) {
   p.ktpw = pl.ktpw;
+  p.xs_rows = pl.xs_rows;
+  p.xs_ld = pl.xs_ld;
   const dim3 grid((unsigned)pl.nblocks, (unsigned)tiles);
-  if (x_bf16)
-    launch_skinny_nb<__bf16, EPI>(p, pl, grid, st, G);
-  else
-    launch_skinny_nb<_Float16, EPI>(p, pl, grid, st, G);
+  if (x_bf16) {
+    if (s_bf16)
+      launch_skinny_nb<__bf16, __bf16, EPI>(p, pl, grid, st, G);
+    else
+      launch_skinny_nb<__bf16, _Float16, EPI>(p, pl, grid, st, G);
+  } else {
+    if (s_bf16)
+      launch_skinny_nb<_Float16, __bf16, EPI>(p, pl, grid, st, G);
+    else
+      launch_skinny_nb<_Float16, _Float16, EPI>(p, pl, grid, st, G);
+  }
 }
 
 // 16-column tiles per job of the dense GEMM: more columns per wave re-use
@@ -458,9 +557,28 @@ extern "C" int ccq_awq_unpack_tiled(const int32_t* tiled, int32_t* qweight, int6
   return launch_status("ccq_awq_unpack_tiled");
 }
 
-extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, const int32_t* qzeros,
-                           const void* scales, int scale_dtype, void* y, int y_dtype, int64_t M, int64_t K,
-                           int64_t N, int64_t group_size, void* stream) {
+extern "C" int64_t ccq_awq_sz_words(int64_t K, int64_t group_size) {
+  if (K <= 0 || K % 128 || !valid_group(group_size)) return 0;
+  return sz_words_per_column(K, group_size);
+}
+
+extern "C" int ccq_awq_pack_sz(const int32_t* qzeros, const void* scales, int scale_dtype, uint32_t* sz, int64_t K,
+                               int64_t N, int64_t group_size, void* stream) {
+  CCQ_REQUIRE(K >= 0 && N >= 0, "ccq_awq_pack_sz: negative shape");
+  CCQ_REQUIRE(K % 128 == 0 && N % 16 == 0, "ccq_awq_pack_sz: need K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
+              (long long)K, (long long)N);
+  CCQ_REQUIRE(valid_group(group_size), "ccq_awq_pack_sz: group_size=%lld not in {32, 64, 128}", (long long)group_size);
+  CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_awq_pack_sz: scale_dtype must be f16|bf16");
+  if (K == 0 || N == 0) return 0;
+  CCQ_REQUIRE(qzeros && scales && sz, "ccq_awq_pack_sz: null pointer");
+  hipLaunchKernelGGL(awq_pack_sz_kernel, dim3(grid1d(N * sz_words_per_column(K, group_size))), dim3(256), 0,
+                     as_stream(stream), (const uint32_t*)qzeros, (const uint16_t*)scales, sz, K, N, group_size);
+  return launch_status("ccq_awq_pack_sz");
+}
+
+extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, const uint32_t* sz, int scale_dtype,
+                           void* y, int y_dtype, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                           void* stream) {
   CCQ_REQUIRE(M >= 0 && K >= 0 && N >= 0, "ccq_w4_gemm: negative shape");
   CCQ_REQUIRE(K % 128 == 0 && N % 16 == 0, "ccq_w4_gemm: need K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
               (long long)K, (long long)N);
@@ -469,11 +587,13 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_w4_gemm: scale_dtype must be f16|bf16");
   CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_w4_gemm: bad y_dtype");
   CCQ_REQUIRE(cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large for the skinny kernel", (long long)M);
-  CCQ_REQUIRE(N / 16 <= 0x7fffffff, "ccq_w4_gemm: N=%lld too large", (long long)N);
+  CCQ_REQUIRE(K <= (1 << 20) && N / 16 <= 0x7fffffff, "ccq_w4_gemm: K=%lld or N=%lld too large", (long long)K,
+              (long long)N);
   if (M == 0 || N == 0) return 0;
   CCQ_REQUIRE(K > 0, "ccq_w4_gemm: K == 0");
-  CCQ_REQUIRE(x && w_tiled && qzeros && scales && y, "ccq_w4_gemm: null pointer");
-  CCQ_REQUIRE(aligned(x, 16) && aligned(w_tiled, 16), "ccq_w4_gemm: x and w_tiled must be 16-byte aligned");
+  CCQ_REQUIRE(x && w_tiled && sz && y, "ccq_w4_gemm: null pointer");
+  CCQ_REQUIRE(aligned(x, 16) && aligned(w_tiled, 16) && aligned(sz, 16),
+              "ccq_w4_gemm: x, w_tiled and sz must be 16-byte aligned");
   const int64_t tiles = cdiv(M, 16);
   const SkinnyPlan pl = plan_skinny(K, N, group_size, 1, gemm_nb(M));
   SkinnyP p = {};
@@ -481,16 +601,17 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   p.ldx = K;
   p.row_div = 1;
   p.w0 = (const uint32_t*)w_tiled;
-  p.z0 = (const uint32_t*)qzeros;
-  p.s0 = (const uint16_t*)scales;
-  p.scale_bf16 = scale_dtype == CCQ_BF16;
+  p.sz0 = sz;
   p.y = y;
   p.ldy = N;
   p.y_dtype = y_dtype;
   p.M = (int)M;
   p.N = (int)N;
+  p.K = (int)K;
   p.KT = (int)(K / 128);
-  launch_skinny<EPI_STORE>(p, x_dtype == CCQ_BF16, pl, tiles, as_stream(stream), (int)group_size);
+  p.szw = (int)sz_words_per_column(K, group_size);
+  launch_skinny<EPI_STORE>(p, x_dtype == CCQ_BF16, scale_dtype == CCQ_BF16, pl, tiles, as_stream(stream),
+                           (int)group_size);
   return launch_status("ccq_w4_gemm");
 }
 
@@ -504,6 +625,7 @@ int check_experts(const ccq_w4_experts* ex, const char* name) {
   CCQ_REQUIRE(ex->hidden > 0 && ex->inter > 0 && ex->hidden % 128 == 0 && ex->inter % 128 == 0,
               "%s: hidden=%lld and inter=%lld must be positive multiples of 128", name, (long long)ex->hidden,
               (long long)ex->inter);
+  CCQ_REQUIRE(ex->hidden <= (1 << 20) && ex->inter <= (1 << 20), "%s: hidden/inter too large", name);
   CCQ_REQUIRE(valid_group(ex->group_size), "%s: group_size=%lld not in {32, 64, 128}", name,
               (long long)ex->group_size);
   CCQ_REQUIRE(ex->scale_dtype == CCQ_F16 || ex->scale_dtype == CCQ_BF16, "%s: scale_dtype must be f16|bf16", name);
@@ -512,13 +634,14 @@ int check_experts(const ccq_w4_experts* ex, const char* name) {
 
 int check_expert_ptrs(const ccq_w4_experts* ex, bool gate_up, const char* name) {
   if (gate_up) {
-    CCQ_REQUIRE(ex->w_gate && ex->z_gate && ex->s_gate && ex->w_up && ex->z_up && ex->s_up,
-                "%s: null gate/up weight pointer", name);
-    CCQ_REQUIRE(aligned(ex->w_gate, 16) && aligned(ex->w_up, 16), "%s: tiled weights must be 16-byte aligned",
-                name);
+    CCQ_REQUIRE(ex->w_gate && ex->sz_gate && ex->w_up && ex->sz_up, "%s: null gate/up weight pointer", name);
+    CCQ_REQUIRE(aligned(ex->w_gate, 16) && aligned(ex->w_up, 16) && aligned(ex->sz_gate, 16) &&
+                    aligned(ex->sz_up, 16),
+                "%s: tiled weights and sz must be 16-byte aligned", name);
   } else {
-    CCQ_REQUIRE(ex->w_down && ex->z_down && ex->s_down, "%s: null down weight pointer", name);
-    CCQ_REQUIRE(aligned(ex->w_down, 16), "%s: tiled weights must be 16-byte aligned", name);
+    CCQ_REQUIRE(ex->w_down && ex->sz_down, "%s: null down weight pointer", name);
+    CCQ_REQUIRE(aligned(ex->w_down, 16) && aligned(ex->sz_down, 16),
+                "%s: tiled weights and sz must be 16-byte aligned", name);
   }
   return 0;
 }
@@ -557,7 +680,6 @@ SkinnyP grouped_params(const int32_t* sorted_ids, const int32_t* tile_expert, co
   p.rows = sorted_ids;
   p.tile_expert = tile_expert;
   p.meta = meta;
-  p.scale_bf16 = ex->scale_dtype == CCQ_BF16;
   return p;
 }
 
@@ -569,21 +691,20 @@ int run_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids
   p.ldx = H;
   p.row_div = (int)k;
   p.w0 = (const uint32_t*)ex->w_gate;
-  p.z0 = (const uint32_t*)ex->z_gate;
-  p.s0 = (const uint16_t*)ex->s_gate;
+  p.sz0 = ex->sz_gate;
   p.w1 = (const uint32_t*)ex->w_up;
-  p.z1 = (const uint32_t*)ex->z_up;
-  p.s1 = (const uint16_t*)ex->s_up;
+  p.sz1 = ex->sz_up;
+  p.szw = (int)sz_words_per_column(H, G);
   p.w_es = H * I / 8;
-  p.z_es = (H / G) * (I / 8);
-  p.s_es = (H / G) * I;
+  p.sz_es = I * p.szw;
   p.y = inter;
   p.ldy = I;
   p.y_dtype = x_dtype;
   p.N = (int)I;
+  p.K = (int)H;
   p.KT = (int)(H / 128);
   const SkinnyPlan pl = plan_skinny(H, I, G, 2, 1);
-  launch_skinny<EPI_SILU>(p, x_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
+  launch_skinny<EPI_SILU>(p, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
   return launch_status("moe_w4 gate_up");
 }
 
@@ -595,18 +716,18 @@ int run_down(const void* inter, int x_dtype, const int32_t* sorted_ids, const in
   d.ldx = I;
   d.row_div = 1;
   d.w0 = (const uint32_t*)ex->w_down;
-  d.z0 = (const uint32_t*)ex->z_down;
-  d.s0 = (const uint16_t*)ex->s_down;
+  d.sz0 = ex->sz_down;
+  d.szw = (int)sz_words_per_column(I, G);
   d.w_es = I * H / 8;
-  d.z_es = (I / G) * (H / 8);
-  d.s_es = (I / G) * H;
+  d.sz_es = H * d.szw;
   d.y = rows;
   d.ldy = H;
   d.y_dtype = CCQ_F32;
   d.N = (int)H;
+  d.K = (int)I;
   d.KT = (int)(I / 128);
   const SkinnyPlan pl = plan_skinny(I, H, G, 1, 1);
-  launch_skinny<EPI_ROWS>(d, x_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
+  launch_skinny<EPI_ROWS>(d, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
   return launch_status("moe_w4 down");
 }
 

@@ -106,15 +106,25 @@ int ccq_awq_repack(const int32_t* qweight, int32_t* tiled, int64_t K, int64_t N,
 int ccq_awq_unpack_tiled(const int32_t* tiled, int32_t* qweight, int64_t K, int64_t N,
                          void* stream);
 
+/* 32-bit words per output column of the packed scale/zero array ("SZ"):
+ * K/G groups, padded to whole chunks of 4 k-tiles (0 for invalid shapes). */
+int64_t ccq_awq_sz_words(int64_t K, int64_t group_size);
+
+/* Pack qzeros [K/G, N/8] and scales [K/G, N] (scale_dtype CCQ_F16|CCQ_BF16)
+ * into sz [N, ccq_awq_sz_words(K, G)] uint32: word [n][g] = scale bits |
+ * zero << 16, padding words 0.  Load-time step next to ccq_awq_repack. */
+int ccq_awq_pack_sz(const int32_t* qzeros, const void* scales, int scale_dtype,
+                    uint32_t* sz, int64_t K, int64_t N, int64_t group_size, void* stream);
+
 /* y [M, N] = x [M, K] @ dequant(W) with fp32 accumulation.
- * x_dtype CCQ_F16 | CCQ_BF16; scale_dtype CCQ_F16 | CCQ_BF16;
- * y_dtype CCQ_F16 | CCQ_BF16 | CCQ_F32.  w_tiled from ccq_awq_repack.
- * group_size in {32, 64, 128}.  x must be 16-byte aligned.  M <= 16 rows per
- * weight pass (decode); larger M re-reads the weight once per 16 rows.
- * Needs no workspace.
+ * x_dtype CCQ_F16 | CCQ_BF16; scale_dtype (of the scales packed in sz)
+ * CCQ_F16 | CCQ_BF16; y_dtype CCQ_F16 | CCQ_BF16 | CCQ_F32.  w_tiled from
+ * ccq_awq_repack, sz from ccq_awq_pack_sz.  group_size in {32, 64, 128}.
+ * x, w_tiled and sz must be 16-byte aligned.  M <= 16 rows per weight pass
+ * (decode); larger M re-reads the weight once per 16 rows.  No workspace.
  * Replaces WeightOnlyMethod.apply (quant/weight_only.py:37-54) for AWQ. */
 int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled,
-                const int32_t* qzeros, const void* scales, int scale_dtype,
+                const uint32_t* sz, int scale_dtype,
                 void* y, int y_dtype, int64_t M, int64_t K, int64_t N,
                 int64_t group_size, void* stream);
 
@@ -157,19 +167,20 @@ int ccq_moe_combine(const float* rows, const float* weights, void* y, int y_dtyp
 
 /* ------------------------------------------------------------------------
  * MoE expert FFN, AWQ int4 experts (gate/up [H -> I], down [I -> H])
- * Weights of all E experts are stacked: w_gate/w_up tiled [E][H*I/8] int32,
- * z_gate/z_up [E][H/G][I/8], s_gate/s_up [E][H/G][I]; w_down [E][I*H/8],
- * z_down [E][I/G][H/8], s_down [E][I/G][H].
+ * Weights of all E experts are stacked: w_gate/w_up tiled [E][H*I/8] int32
+ * (ccq_awq_repack), sz_gate/sz_up [E][I][ccq_awq_sz_words(H, G)];
+ * w_down [E][I*H/8], sz_down [E][H][ccq_awq_sz_words(I, G)]
+ * (ccq_awq_pack_sz).
  * Replaces expert_ffn (blocks/moe.py:122-141) + moe_combine
  * (blocks/moe.py:144-174) as called by ExpertPipeline.step
  * (experts/pipeline.py:155-179) and moe_forward (models/generic.py:348-378).
  * ---------------------------------------------------------------------- */
 
 typedef struct ccq_w4_experts {
-  const int32_t* w_gate; const int32_t* z_gate; const void* s_gate;
-  const int32_t* w_up;   const int32_t* z_up;   const void* s_up;
-  const int32_t* w_down; const int32_t* z_down; const void* s_down;
-  int scale_dtype;           /* CCQ_F16 | CCQ_BF16 */
+  const int32_t* w_gate; const uint32_t* sz_gate;
+  const int32_t* w_up;   const uint32_t* sz_up;
+  const int32_t* w_down; const uint32_t* sz_down;
+  int scale_dtype;           /* CCQ_F16 | CCQ_BF16 (scales inside sz) */
   int64_t num_experts, hidden, inter, group_size;
 } ccq_w4_experts;
 

@@ -22,7 +22,7 @@ def declared() -> set[str]:
 
 def test_header_declares_the_path():
     names = declared()
-    for must in ("ccq_w4_gemm", "ccq_awq_repack", "ccq_awq_dequant", "ccq_topk_softmax", "ccq_moe_align",
+    for must in ("ccq_w4_gemm", "ccq_awq_repack", "ccq_awq_pack_sz", "ccq_awq_dequant", "ccq_topk_softmax", "ccq_moe_align",
                  "ccq_moe_w4_ffn", "ccq_int4_linear_f32", "ccq_fp8_linear_f32", "ccq_f32_to_fp8"):
         assert must in names
 
@@ -55,18 +55,18 @@ def test_w4_gemm_rejects_bad_shapes(lib):
     from ccut._lib import CCQ_BF16, CCQ_EINVAL, CCQ_F16, last_error
 
     p = ctypes.c_void_p(16)  # never dereferenced: validation comes first
-    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 100, 64, 128, None)
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 1, 100, 64, 128, None)
     assert rc == CCQ_EINVAL and "K % 128" in last_error()
-    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 96, None)
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 96, None)
     assert rc == CCQ_EINVAL and "group_size" in last_error()
-    rc = lib.ccq_w4_gemm(p, 7, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
+    rc = lib.ccq_w4_gemm(p, 7, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
     assert rc == CCQ_EINVAL and "x_dtype" in last_error()
-    rc = lib.ccq_w4_gemm(None, CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
+    rc = lib.ccq_w4_gemm(None, CCQ_BF16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
     assert rc == CCQ_EINVAL and "null" in last_error()
-    rc = lib.ccq_w4_gemm(ctypes.c_void_p(18), CCQ_BF16, p, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
+    rc = lib.ccq_w4_gemm(ctypes.c_void_p(18), CCQ_BF16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
     assert rc == CCQ_EINVAL and "aligned" in last_error()
     # M == 0 is an empty product: success without a launch
-    assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None) == 0
+    assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None) == 0
 
 
 def test_routing_rejects_bad_args(lib):
@@ -94,12 +94,27 @@ def test_reference_format_rejects(lib):
     assert lib.ccq_awq_repack(p, p, 128, 24, None) == CCQ_EINVAL
     assert lib.ccq_awq_repack(p, p, 128, 32, None) == CCQ_EINVAL and "in-place" in last_error()
     assert lib.ccq_awq_dequant(p, p, p, 1, p, 130, 64, 128, None) == CCQ_EINVAL
+    assert lib.ccq_awq_pack_sz(p, p, 1, p, 256, 24, 128, None) == CCQ_EINVAL
+    assert lib.ccq_awq_pack_sz(p, p, 1, p, 256, 32, 96, None) == CCQ_EINVAL and "group_size" in last_error()
+    assert lib.ccq_awq_pack_sz(p, p, 3, p, 256, 32, 128, None) == CCQ_EINVAL and "scale_dtype" in last_error()
+
+
+def test_sz_words_padding(lib):
+    """Scale/zero words per column: K/G groups rounded up to whole chunks of
+    4 k-tiles (512 rows)."""
+    assert lib.ccq_awq_sz_words(2048, 128) == 16
+    assert lib.ccq_awq_sz_words(1408, 128) == 12   # 11 k-tiles -> 12
+    assert lib.ccq_awq_sz_words(1408, 64) == 24
+    assert lib.ccq_awq_sz_words(128, 32) == 16     # 1 k-tile -> 4, 4 groups each
+    assert lib.ccq_awq_sz_words(4096, 128) == 32
+    assert lib.ccq_awq_sz_words(100, 128) == 0
+    assert lib.ccq_awq_sz_words(256, 96) == 0
 
 
 def test_moe_w4_descriptor_validation(lib):
     from ccut._lib import CCQ_EINVAL, ccq_w4_experts, last_error
 
-    ex = ccq_w4_experts(*([256] * 9), 1, 64, 2048, 1400, 128)  # inter not a multiple of 128
+    ex = ccq_w4_experts(*([256] * 6), 1, 64, 2048, 1400, 128)  # inter not a multiple of 128
     p = ctypes.c_void_p(256)
     assert lib.ccq_moe_w4_ffn(p, 2, p, p, p, 2, 1, 6, ctypes.byref(ex), p, 1 << 30, None) == CCQ_EINVAL
     assert "multiples of 128" in last_error()
