@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from ccut import _dev
-from ccut._lib import call, ccq_w4_experts, lib
+from ccut._lib import call, ccq_fp8_experts, ccq_w4_experts, lib
 from ccut.quant import awq
 
 __all__ = [
@@ -35,6 +35,8 @@ __all__ = [
     "moe_align",
     "W4Experts",
     "moe_forward_w4",
+    "Fp8Experts",
+    "moe_forward_fp8",
 ]
 
 _MODE_SOFTMAX_ALL, _MODE_TOPK_THEN_SOFTMAX, _MODE_RAW_EXP, _MODE_PLAIN = 0, 1, 2, 3
@@ -287,3 +289,95 @@ def moe_forward_w4(x: torch.Tensor, router_logits: torch.Tensor, experts: W4Expe
     ``models/generic.py:361-378``)."""
     w, ids = topk_softmax(router_logits, top_k, norm_topk_prob)
     return moe_ffn_w4(x, ids, w, experts, out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# fused quantized expert forward (FP8 e4m3fn experts, 128x128 block scales)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Fp8Experts:
+    """All experts of one MoE layer in block FP8, resident in HBM in the
+    MFMA tile layout (``ccq_fp8_block_repack``).  gate/up ``w [E, I, H]``
+    with scales ``[E, I/128, H/128]``; down ``w [E, H, I]`` with scales
+    ``[E, H/128, I/128]`` (row = output channel, as checkpoints store them)."""
+
+    w_gate: torch.Tensor
+    s_gate: torch.Tensor
+    w_up: torch.Tensor
+    s_up: torch.Tensor
+    w_down: torch.Tensor
+    s_down: torch.Tensor
+    num_experts: int
+    hidden: int
+    inter: int
+
+    @staticmethod
+    def from_block(gate: tuple, up: tuple, down: tuple) -> "Fp8Experts":
+        """Each of ``gate``/``up``/``down`` is ``(w [E, N, K] e4m3fn bytes,
+        s [E, N/128, K/128] float32)``."""
+        def one(t):
+            w = _dev.raw_u8(t[0]).reshape(t[0].shape) if isinstance(t[0], torch.Tensor) else \
+                _dev.to_device(np.ascontiguousarray(t[0]).view(np.uint8))
+            w = w.view(torch.uint8).contiguous()
+            sc = _dev.to_device(t[1], torch.float32).contiguous()
+            E, N, K = w.shape
+            if N % 128 or K % 128 or tuple(sc.shape) != (E, N // 128, K // 128):
+                raise ValueError(f"block FP8 expert weights [E, N, K] = {tuple(w.shape)} with scales "
+                                 f"{tuple(sc.shape)}: need N, K multiples of 128 and scales [E, N/128, K/128]")
+            tiled = torch.empty_like(w)
+            for e in range(E):
+                call("ccq_fp8_block_repack", w[e].data_ptr(), tiled[e].data_ptr(), N, K, _dev.stream_ptr())
+            return tiled, sc, E, N, K
+
+        wg, sg, E, I, H = one(gate)
+        wu, su, E2, I2, H2 = one(up)
+        wd, sd, E3, H3, I3 = one(down)
+        if not (E == E2 == E3 and I == I2 == I3 and H == H2 == H3):
+            raise ValueError("gate/up [E, I, H] and down [E, H, I] shapes disagree")
+        return Fp8Experts(wg, sg, wu, su, wd, sd, num_experts=E, hidden=H, inter=I)
+
+    def descriptor(self) -> ccq_fp8_experts:
+        return ccq_fp8_experts(self.w_gate.data_ptr(), self.s_gate.data_ptr(), self.w_up.data_ptr(),
+                               self.s_up.data_ptr(), self.w_down.data_ptr(), self.s_down.data_ptr(),
+                               self.num_experts, self.hidden, self.inter)
+
+    @property
+    def bytes_per_expert(self) -> int:
+        """Bytes of one expert (fp8 weights + float32 block scales of gate,
+        up and down): the algorithmic traffic of reading it once."""
+        H, I = self.hidden, self.inter
+        return 3 * H * I + 3 * (H // 128) * (I // 128) * 4
+
+
+def moe_ffn_fp8(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, experts: Fp8Experts,
+                out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Expert FFN + weighted combine for already-routed tokens on FP8 block
+    experts (one call of ``ccq_moe_fp8_ffn``)."""
+    if x.dtype not in _dev.DTYPE_CODE:
+        raise ValueError(f"activations must be float32, float16 or bfloat16, got {x.dtype}")
+    x = x.contiguous()
+    T, H = x.shape
+    if H != experts.hidden:
+        raise ValueError(f"x has {H} features, experts expect {experts.hidden}")
+    k = ids.shape[1]
+    out_dtype = out_dtype or x.dtype
+    y = torch.empty((T, H), dtype=out_dtype, device=x.device)
+    desc = experts.descriptor()
+    nbytes = lib().ccq_moe_fp8_workspace_size(T, k, desc)
+    ws = _dev.workspace("moe_fp8", nbytes, x.device)
+    ids = ids.to(torch.int64).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    call("ccq_moe_fp8_ffn", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], ids.data_ptr(), weights.data_ptr(),
+         y.data_ptr(), _dev.DTYPE_CODE[out_dtype], T, k, desc, ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
+    return y
+
+
+def moe_forward_fp8(x: torch.Tensor, router_logits: torch.Tensor, experts: Fp8Experts, top_k: int,
+                    norm_topk_prob: bool = True, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Routed MoE layer on block-FP8 experts: ``topk_softmax`` then the fused
+    FFN (the compute of ``moe_forward``, reference
+    ``models/generic.py:361-378``, with the block-scaled FP8 format)."""
+    w, ids = topk_softmax(router_logits, top_k, norm_topk_prob)
+    return moe_ffn_fp8(x, ids, w, experts, out_dtype)

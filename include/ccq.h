@@ -210,6 +210,66 @@ int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* 
                    const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+
+/* ------------------------------------------------------------------------
+ * FP8 e4m3fn with 128x128 block weight scales (w [N, K] bytes, row = output
+ * channel, s_w [N/128, K/128] f32: W[n,k] = fp8(w[n,k]) * s_w[n/128, k/128])
+ * and per-token-per-128 dynamic activation scales.  The reference has FP8
+ * with one scale per output row only (quant/kernels.py:150-171) and its
+ * "w8a8" does not quantize activations (quant/method.py:133-140); these
+ * entry points serve the block-scaled layout behind the same
+ * Fp8LinearMethod.apply boundary (quant/fp8.py:33, quant/method.py:45-58).
+ * ---------------------------------------------------------------------- */
+
+/* q [rows, K] e4m3fn, s [rows, K/128] f32: s = max(amax, 1e-12) / 448 over
+ * each 128-column block of a row, q = RNE(x / s) saturated to +-448.
+ * x_dtype CCQ_F32 | CCQ_F16 | CCQ_BF16, K % 128 == 0, q 8-byte aligned. */
+int ccq_fp8_act_quant(const void* x, int x_dtype, int64_t rows, int64_t K,
+                      uint8_t* q, float* s, void* stream);
+
+/* Re-pack w [N, K] e4m3fn into the gfx950 MFMA tile layout (same bytes);
+ * N % 16 == 0, K % 128 == 0, 16-byte aligned, not in place.  Load-time step
+ * (QuantizeMethodBase.process_weights_after_loading, quant/method.py:60-62). */
+int ccq_fp8_block_repack(const uint8_t* w, uint8_t* tiled, int64_t N, int64_t K,
+                         void* stream);
+/* Inverse of ccq_fp8_block_repack. */
+int ccq_fp8_block_unpack(const uint8_t* tiled, uint8_t* w, int64_t N, int64_t K,
+                         void* stream);
+
+/* Workspace of ccq_fp8_block_linear (the quantized activations). */
+size_t ccq_fp8_block_linear_workspace_size(int64_t M, int64_t K);
+
+/* y [M, N] = dequant(act_quant(x)) @ W^T with fp32 accumulation;
+ * K % 128 == 0, N % 128 == 0, w_tiled from ccq_fp8_block_repack. */
+int ccq_fp8_block_linear(const void* x, int x_dtype, const uint8_t* w_tiled,
+                         const float* s_w, void* y, int y_dtype, int64_t M, int64_t K,
+                         int64_t N, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* MoE experts, FP8 block: gate/up w [E][I, H] (tiled), s [E][I/128][H/128];
+ * down w [E][H, I] (tiled), s [E][H/128][I/128]. */
+typedef struct ccq_fp8_experts {
+  const uint8_t* w_gate; const float* s_gate;
+  const uint8_t* w_up;   const float* s_up;
+  const uint8_t* w_down; const float* s_down;
+  int64_t num_experts, hidden, inter;
+} ccq_fp8_experts;
+
+/* Workspace bytes of ccq_moe_fp8_ffn (schedule, quantized activations and
+ * intermediate, down rows; no initial contents required). */
+size_t ccq_moe_fp8_workspace_size(int64_t T, int64_t k, const ccq_fp8_experts* ex);
+
+/* Full MoE FFN on FP8 block experts: x [T, H] is quantized per token per
+ * 128; gate/up + SiLU*up with the intermediate rounded to bf16 and
+ * re-quantized per row per 128; down; weighted combine in slot order.
+ * Tokens are grouped by expert into 64-row tiles (ccq_moe_align).
+ * Replaces expert_ffn + moe_combine (blocks/moe.py:122-174) for FP8
+ * experts, as called by moe_forward (models/generic.py:348-378). */
+int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights,
+                    void* y, int y_dtype, int64_t T, int64_t k,
+                    const ccq_fp8_experts* ex, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

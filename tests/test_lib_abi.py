@@ -120,3 +120,28 @@ def test_moe_w4_descriptor_validation(lib):
     assert "multiples of 128" in last_error()
     ex.inter = 1408
     assert lib.ccq_moe_w4_workspace_size(16, 6, ctypes.byref(ex)) > 0
+
+
+def test_fp8_block_rejects_bad_args(lib):
+    from ccut._lib import CCQ_BF16, CCQ_EINVAL, ccq_fp8_experts, last_error
+
+    p = ctypes.c_void_p(256)
+    assert lib.ccq_fp8_act_quant(p, CCQ_BF16, 4, 100, p, p, None) == CCQ_EINVAL and "128" in last_error()
+    assert lib.ccq_fp8_act_quant(p, 9, 4, 128, p, p, None) == CCQ_EINVAL and "x_dtype" in last_error()
+    assert lib.ccq_fp8_act_quant(p, CCQ_BF16, 0, 128, p, p, None) == 0
+    assert lib.ccq_fp8_block_repack(p, p, 24, 128, None) == CCQ_EINVAL
+    assert lib.ccq_fp8_block_repack(p, p, 32, 128, None) == CCQ_EINVAL and "in-place" in last_error()
+    assert lib.ccq_fp8_block_linear_workspace_size(4, 100) == 0
+    need = lib.ccq_fp8_block_linear_workspace_size(4, 256)
+    assert need > 0 and need % 256 == 0
+    rc = lib.ccq_fp8_block_linear(p, CCQ_BF16, p, p, p, CCQ_BF16, 4, 256, 200, p, need, None)
+    assert rc == CCQ_EINVAL and "N %" in last_error()
+    rc = lib.ccq_fp8_block_linear(p, CCQ_BF16, p, p, p, CCQ_BF16, 4, 256, 256, p, need - 1, None)
+    assert rc == CCQ_EINVAL and "workspace" in last_error()
+    ex = ccq_fp8_experts(*([256] * 6), 8, 7168, 2000)
+    assert lib.ccq_moe_fp8_workspace_size(16, 8, ctypes.byref(ex)) == 0
+    assert lib.ccq_moe_fp8_ffn(p, CCQ_BF16, p, p, p, CCQ_BF16, 16, 8, ctypes.byref(ex), p, 1 << 40, None) == CCQ_EINVAL
+    assert "multiples of 128" in last_error()
+    ex.inter = 2048
+    assert lib.ccq_moe_fp8_workspace_size(16, 8, ctypes.byref(ex)) > 16 * 7168
+    assert lib.ccq_moe_fp8_ffn(p, CCQ_BF16, p, p, p, CCQ_BF16, 16, 9, ctypes.byref(ex), p, 1 << 40, None) == CCQ_EINVAL
