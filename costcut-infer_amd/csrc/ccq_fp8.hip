@@ -12,7 +12,8 @@
 // accumulator: acc += (s_a[row, kb] * s_w[nb, kb]) * mfma(q_a, q_w).
 //
 // Weight tile layout: tile (nt, kb) = 16 output channels x 128 K bytes =
-// 2 KiB at byte (nt*KB + kb)*2048; inside, [half h][lane l][16 bytes] with
+// 2 KiB at byte (nt*KB + kb)*2048 (each wave streams one contiguous run of
+// its 16 channels); inside, [half h][lane l][16 bytes] with
 // bytes k = kb*128 + 32*(l >> 4) + 16*h + e of channel nt*16 + (l & 15).  A
 // lane's 32 operand bytes (channel l & 15, K bytes 32*(l >> 4) .. +32) come
 // from two wave-wide 16-byte loads, each a contiguous 1 KiB transfer.  The
@@ -110,6 +111,7 @@ struct Fp8GP {
   int row_div;                 // activation row = row id / row_div
   const int32_t* tile_expert;  // null = one weight
   const int32_t* meta;         // meta[0] = valid tiles; null = all
+  int tile_div;                // kernel tiles per schedule tile (schedule rows / BM)
   const uint8_t* w0;           // tiled weights (gate for F8_SILU_Q)
   const float* sw0;            // block scales [N/128, K/128]
   const uint8_t* w1;           // up weights for F8_SILU_Q
@@ -124,7 +126,8 @@ struct Fp8GP {
   int M, N, K, KB;
 };
 
-constexpr int F8_BM = 64;         // rows per tile
+constexpr int F8_BM_SMALL = 64;   // rows per tile (decode-sized groups)
+constexpr int F8_BM_LARGE = 128;  // rows per tile when experts receive many tokens
 constexpr int F8_BN = 128;        // output channels per workgroup (one scale block)
 constexpr int F8_ALD = 128 + 16;  // LDS row stride of the A tile (bytes)
 
@@ -132,63 +135,83 @@ __device__ __forceinline__ f32x4 mfma_f8(const i32x8& a, const i32x8& b, f32x4 c
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-// Workgroup = 8 waves on one 64-row tile x 128 output channels (blockIdx.x =
+// Workgroup = 8 waves on one BM-row tile x 128 output channels (blockIdx.x =
 // channel block, blockIdx.y = tile).  Wave w owns channels [16w, 16w+16)
 // (one 16-channel MFMA column; F8_SILU_Q: the same channels of gate and
-// up).  Per 128-wide K block: the A tile (64 x 128 bytes) and its row scales
-// go through LDS (double-buffered, loaded one block ahead), the wave's weight
-// tiles go straight to registers one block ahead; 4 (or 8) MFMAs per wave.
+// up).  Per 128-wide K block: the A tile (BM x 128 bytes) and its row scales
+// go through LDS (double-buffered), the wave's weight tiles go straight to
+// registers; BM/16 (or 2*BM/16) MFMAs per wave.  Each tile streams its
+// expert's whole weight, so the tile height is chosen to hold all of an
+// expert's tokens whenever that is affordable (128 for prefill).
 constexpr int F8_WAVES = 8;
 
-template <int EPI>
+template <int EPI, int BM>
 __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   constexpr int NQ = EPI == F8_SILU_Q ? 2 : 1;  // weight matrices
   constexpr int NC = NQ;                        // 16-channel B tiles per wave
-  __shared__ __align__(16) uint8_t As[2][F8_BM * F8_ALD];
-  __shared__ __align__(16) float Ss[2][F8_BM];
-  __shared__ int Rid[F8_BM];
-  __shared__ float Red[F8_WAVES][F8_BM];
+  constexpr int RT = BM / 16;                   // 16-row MFMA tiles
+  constexpr int AP = BM * 8 / (64 * F8_WAVES);  // 16-byte A pieces per thread
+  __shared__ __align__(16) uint8_t As[2][BM * F8_ALD];
+  __shared__ __align__(16) float Ss[2][BM];
+  __shared__ int Rid[BM];
+  __shared__ float Red[F8_WAVES][BM];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nb = blockIdx.x, tile = blockIdx.y;
-  if (p.meta != nullptr && tile >= p.meta[0]) return;
-  const int ex = p.tile_expert ? p.tile_expert[tile] : 0;
-  if (tid < F8_BM) {
+  if (p.meta != nullptr && tile >= p.meta[0] * p.tile_div) return;
+  const int ex = p.tile_expert ? p.tile_expert[tile / p.tile_div] : 0;
+  if (tid < BM) {
     int rid;
     if (p.rows) {
-      rid = p.rows[tile * F8_BM + tid];
+      rid = p.rows[tile * BM + tid];
     } else {
-      rid = tile * F8_BM + tid;
+      rid = tile * BM + tid;
       if (rid >= p.M) rid = -1;
     }
     Rid[tid] = rid;
   }
-  __syncthreads();
+  // a tile of padding only (the tail of an expert's last schedule tile)
+  if (!__syncthreads_or(tid < BM && Rid[tid] >= 0)) return;
 
-  // A staging: 64 rows x 8 pieces of 16 bytes, one piece per thread
-  // (row = tid / 8, piece = tid % 8)
-  const int arow = tid >> 3, apart = tid & 7;
-  const bool aval = Rid[arow] >= 0;
-  const uint8_t* asrc = p.a + (int64_t)(aval ? Rid[arow] / p.row_div : 0) * p.lda + 16 * apart;
+  // A staging: BM rows x 8 pieces of 16 bytes, AP pieces per thread
+  // (piece i = tid + 512*j: row = i / 8, part = i % 8)
+  const uint8_t* asrc[AP];
+  bool aval[AP];
+#pragma unroll
+  for (int j = 0; j < AP; ++j) {
+    const int i = tid + 64 * F8_WAVES * j, row = i >> 3, part = i & 7;
+    aval[j] = Rid[row] >= 0;
+    asrc[j] = p.a + (int64_t)(aval[j] ? Rid[row] / p.row_div : 0) * p.lda + 16 * part;
+  }
   const float* ssrc = nullptr;
   bool sval = false;
-  if (tid < F8_BM) {
+  if (tid < BM) {
     const int rid = Rid[tid];
     sval = rid >= 0;
     ssrc = p.sa + (int64_t)(sval ? rid / p.row_div : 0) * p.ldsa;
   }
-  u32x4 ast;
-  float sst = 0.f;
-  auto load_a = [&](int kb) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(asrc + (int64_t)kb * 128);
-    ast = aval ? v : u32x4{0u, 0u, 0u, 0u};
-    if (tid < F8_BM) sst = sval ? ssrc[kb] : 0.f;
+  // A for a K block: AP 16-byte pieces per thread (+ one row scale for
+  // threads < BM), held in registers until written to LDS
+  struct AStage {
+    u32x4 v[AP];
+    float s;
   };
-  auto store_a = [&](int buf) {
-    *reinterpret_cast<u32x4*>(&As[buf][arow * F8_ALD + 16 * apart]) = ast;
-    if (tid < F8_BM) Ss[buf][tid] = sst;
+  auto load_a = [&](AStage& st, int kb) {
+#pragma unroll
+    for (int j = 0; j < AP; ++j) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(asrc[j] + (int64_t)kb * 128);
+      st.v[j] = aval[j] ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (tid < BM) st.s = sval ? ssrc[kb] : 0.f;
   };
-
+  auto store_a = [&](const AStage& st, int buf) {
+#pragma unroll
+    for (int j = 0; j < AP; ++j) {
+      const int i = tid + 64 * F8_WAVES * j, row = i >> 3, part = i & 7;
+      *reinterpret_cast<u32x4*>(&As[buf][row * F8_ALD + 16 * part]) = st.v[j];
+    }
+    if (tid < BM) Ss[buf][tid] = st.s;
+  };
   // weight tile of this wave: channel tile nt = nb*8 + wave, per matrix
   const uint8_t* wsrc[NC];
 #pragma unroll
@@ -198,7 +221,6 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
 #pragma unroll
   for (int q = 0; q < NQ; ++q) swb[q] = (q == 0 ? p.sw0 : p.sw1) + (int64_t)ex * p.sw_es + (int64_t)nb * p.KB;
 
-  i32x8 bcur[NC], bnxt[NC];
   auto load_b = [&](i32x8 (&b)[NC], int kb) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -209,9 +231,9 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
     }
   };
 
-  f32x4 acc[4][NC];
+  f32x4 acc[RT][NC];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -221,7 +243,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) sw[q] = swb[q][kb];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const uint8_t* ap = &As[buf][(rt * 16 + r) * F8_ALD + 32 * kq];
       const u32x4 lo = *reinterpret_cast<const u32x4*>(ap);
       const u32x4 hi = *reinterpret_cast<const u32x4*>(ap + 16);
@@ -236,41 +258,79 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[rt][c][i] = fmaf(sr[i] * s, t[c][i], acc[rt][c][i]);
       }
+      // keep one row tile's products live at a time (the scheduler would
+      // otherwise hoist every MFMA of the block and run out of registers)
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // software pipeline: block kb computes from buffer kb & 1 while block kb+1
-  // is fetched (A to registers then LDS, B to registers)
-  load_b(bcur, 0);
-  load_a(0);
-  store_a(0);
-  __syncthreads();
-  for (int kb = 0; kb < p.KB; kb += 2) {
-    const bool more1 = kb + 1 < p.KB;
-    if (more1) {
-      load_b(bnxt, kb + 1);
-      load_a(kb + 1);
+  // software pipeline: step kb computes block kb from LDS buffer kb & 1 and
+  // a weight register slot, then writes A(kb+1) to LDS; the loads of block
+  // kb+DEPTH (A first, then weights) are issued at its start.  Waits retire
+  // loads in issue order, so writing A(kb+1) only waits for loads issued up
+  // to A(kb+1) itself and the later weights stay in flight.  DEPTH is 2, or
+  // 1 where the registers of a third stage would cost a workgroup per CU
+  // (measured: two resident workgroups hide each other's barrier stalls
+  // better than a deeper single-workgroup pipeline).
+  constexpr int DEPTH = (EPI == F8_SILU_Q && BM == F8_BM_LARGE) || EPI == F8_ROWS ? 1 : 2;
+  if constexpr (DEPTH == 2) {
+    AStage as0, as1, as2;
+    i32x8 b0[NC], b1[NC], b2[NC];
+    auto step = [&](int kb, AStage& a_next, AStage& a_far, const i32x8 (&bc)[NC], i32x8 (&bfar)[NC]) {
+      if (kb + 2 < p.KB) {
+        load_a(a_far, kb + 2);
+        load_b(bfar, kb + 2);
+      }
+      compute(kb & 1, bc, kb);
+      if (kb + 1 < p.KB) store_a(a_next, (kb + 1) & 1);
+      __syncthreads();
+    };
+    load_a(as0, 0);
+    load_b(b0, 0);
+    if (p.KB > 1) {
+      load_a(as1, 1);
+      load_b(b1, 1);
     }
-    compute(0, bcur, kb);
-    if (more1) store_a(1);
+    store_a(as0, 0);
     __syncthreads();
-    if (!more1) break;
-    const bool more2 = kb + 2 < p.KB;
-    if (more2) {
-      load_b(bcur, kb + 2);
-      load_a(kb + 2);
+    for (int kb = 0; kb < p.KB; kb += 3) {
+      step(kb, as1, as2, b0, b2);
+      if (kb + 1 >= p.KB) break;
+      step(kb + 1, as2, as0, b1, b0);
+      if (kb + 2 >= p.KB) break;
+      step(kb + 2, as0, as1, b2, b1);
     }
-    compute(1, bnxt, kb + 1);
-    if (more2) store_a(0);
+  } else {
+    AStage as0, as1;
+    i32x8 b0[NC], b1[NC];
+    load_a(as0, 0);
+    load_b(b0, 0);
+    store_a(as0, 0);
     __syncthreads();
+    for (int kb = 0; kb < p.KB; kb += 2) {
+      if (kb + 1 < p.KB) {
+        load_a(as1, kb + 1);
+        load_b(b1, kb + 1);
+      }
+      compute(0, b0, kb);
+      if (kb + 1 < p.KB) store_a(as1, 1);
+      __syncthreads();
+      if (kb + 1 >= p.KB) break;
+      if (kb + 2 < p.KB) {
+        load_a(as0, kb + 2);
+        load_b(b0, kb + 2);
+      }
+      compute(1, b1, kb + 1);
+      if (kb + 2 < p.KB) store_a(as0, 0);
+      __syncthreads();
+    }
   }
 
   // epilogue: lane holds rows rt*16 + 4*kq + i, channel c*16 + r of its wave
   if constexpr (EPI == F8_SILU_Q) {
-    float h[4][4];
-    float am[4][4];
+    float h[RT][4];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float g = acc[rt][0][i], u = acc[rt][1][i];
@@ -283,17 +343,11 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
         float m = fabsf(hb);
 #pragma unroll
         for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        am[rt][i] = m;
+        if (r == 0) Red[wave][rt * 16 + 4 * kq + i] = m;
       }
-    if (r == 0) {
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Red[wave][rt * 16 + 4 * kq + i] = am[rt][i];
-    }
     __syncthreads();
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = rt * 16 + 4 * kq + i;
@@ -309,7 +363,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
       }
   } else {
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int rid = Rid[rt * 16 + 4 * kq + i];
@@ -345,11 +399,23 @@ int launch_act_quant(const void* x, int x_dtype, int64_t ldx, int64_t rows, int6
   return launch_status("fp8 act quant");
 }
 
+// bm: rows per schedule tile; kernel_bm: rows per kernel tile (a divisor)
 template <int EPI>
-static int launch_fp8_gemm(const Fp8GP& p, int64_t tiles, hipStream_t st) {
-  hipLaunchKernelGGL(fp8_gemm_kernel<EPI>, dim3((unsigned)(p.N / F8_BN), (unsigned)tiles), dim3(64 * F8_WAVES), 0,
-                     st, p);
+static int launch_fp8_gemm(Fp8GP p, int bm, int kernel_bm, int64_t tiles, hipStream_t st) {
+  p.tile_div = bm / kernel_bm;
+  const dim3 grid((unsigned)(p.N / F8_BN), (unsigned)(tiles * p.tile_div)), block(64 * F8_WAVES);
+  if (kernel_bm == F8_BM_LARGE)
+    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, F8_BM_LARGE>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, F8_BM_SMALL>), grid, block, 0, st, p);
   return launch_status("fp8 gemm");
+}
+
+// Tile height of a grouped call: 128 rows once the average expert receives
+// at least 32 tokens (each tile re-streams its expert's weights, so a tile
+// should hold all of them), 64 below that.
+static int fp8_tile_rows(int64_t assignments, int64_t experts) {
+  return assignments >= 32 * experts ? F8_BM_LARGE : F8_BM_SMALL;
 }
 
 }  // namespace ccq
@@ -422,7 +488,7 @@ extern "C" int ccq_fp8_block_linear(const void* x, int x_dtype, const uint8_t* w
               (long long)K, (long long)N);
   CCQ_REQUIRE(x_dtype == CCQ_F32 || x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_fp8_block_linear: bad x_dtype");
   CCQ_REQUIRE(y_dtype == CCQ_F32 || y_dtype == CCQ_F16 || y_dtype == CCQ_BF16, "ccq_fp8_block_linear: bad y_dtype");
-  CCQ_REQUIRE(cdiv(M, F8_BM) <= 65535 && N / F8_BN <= 65535, "ccq_fp8_block_linear: M or N too large");
+  CCQ_REQUIRE(cdiv(M, F8_BM_SMALL) <= 65535 && N / F8_BN <= 65535, "ccq_fp8_block_linear: M or N too large");
   if (M == 0 || N == 0) return 0;
   CCQ_REQUIRE(K > 0, "ccq_fp8_block_linear: K == 0");
   CCQ_REQUIRE(x && w_tiled && s_w && y, "ccq_fp8_block_linear: null pointer");
@@ -451,7 +517,8 @@ extern "C" int ccq_fp8_block_linear(const void* x, int x_dtype, const uint8_t* w
   p.N = (int)N;
   p.K = (int)K;
   p.KB = (int)(K / 128);
-  return launch_fp8_gemm<F8_STORE>(p, cdiv(M, F8_BM), st);
+  const int bm = M >= F8_BM_LARGE ? F8_BM_LARGE : F8_BM_SMALL;
+  return launch_fp8_gemm<F8_STORE>(p, bm, bm, cdiv(M, bm), st);
 }
 
 // ------------------------------------------------------------ MoE FP8 --
@@ -474,6 +541,7 @@ int check_fp8_experts(const ccq_fp8_experts* ex, const char* name) {
 
 struct F8MoeLayout {
   int64_t n, max_tiles;
+  int bm;
   size_t off_sorted, off_te, off_meta, off_counts, off_qx, off_sx, off_qh, off_sh, off_rows, total;
 };
 
@@ -481,10 +549,11 @@ F8MoeLayout f8_moe_layout(int64_t T, int64_t k, const ccq_fp8_experts* ex) {
   F8MoeLayout L;
   const int64_t H = ex->hidden, I = ex->inter;
   L.n = T * k;
-  L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, F8_BM);
+  L.bm = fp8_tile_rows(L.n, ex->num_experts);
+  L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, L.bm);
   size_t o = 0;
   L.off_sorted = o;
-  o += a256((size_t)L.max_tiles * F8_BM * 4);
+  o += a256((size_t)L.max_tiles * L.bm * 4);
   L.off_te = o;
   o += a256((size_t)L.max_tiles * 4);
   L.off_meta = o;
@@ -526,7 +595,7 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   if (T == 0) return 0;
   CCQ_REQUIRE(x && ids && weights && y, "ccq_moe_fp8_ffn: null pointer");
   const F8MoeLayout L = f8_moe_layout(T, k, ex);
-  CCQ_REQUIRE(L.max_tiles <= 65535, "ccq_moe_fp8_ffn: too many tiles");
+  CCQ_REQUIRE(L.max_tiles * 2 <= 65535, "ccq_moe_fp8_ffn: too many tiles");
   CCQ_REQUIRE(workspace && workspace_bytes >= L.total && aligned(workspace, 256),
               "ccq_moe_fp8_ffn: workspace of %zu bytes (256-byte aligned) needed, %zu given", L.total,
               workspace_bytes);
@@ -543,7 +612,7 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   float* sh = (float*)(ws + L.off_sh);
   float* rows = (float*)(ws + L.off_rows);
 
-  rc = launch_align(ids, L.n, ex->num_experts, F8_BM, sorted, te, meta, counts, st);
+  rc = launch_align(ids, L.n, ex->num_experts, L.bm, sorted, te, meta, counts, st);
   if (rc) return rc;
   rc = launch_act_quant(x, x_dtype, H, T, H, qx, H, sx, H / 128, st);
   if (rc) return rc;
@@ -570,7 +639,7 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   g.N = (int)I;
   g.K = (int)H;
   g.KB = (int)(H / 128);
-  rc = launch_fp8_gemm<F8_SILU_Q>(g, L.max_tiles, st);
+  rc = launch_fp8_gemm<F8_SILU_Q>(g, L.bm, L.bm, L.max_tiles, st);
   if (rc) return rc;
 
   Fp8GP d = {};
@@ -592,7 +661,8 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   d.N = (int)H;
   d.K = (int)I;
   d.KB = (int)(I / 128);
-  rc = launch_fp8_gemm<F8_ROWS>(d, L.max_tiles, st);
+  // down runs 64-row tiles (two resident workgroups per CU; see DEPTH)
+  rc = launch_fp8_gemm<F8_ROWS>(d, L.bm, F8_BM_SMALL, L.max_tiles, st);
   if (rc) return rc;
   return launch_combine(rows, weights, ids, ex->num_experts, y, y_dtype, T, k, H, st);
 }

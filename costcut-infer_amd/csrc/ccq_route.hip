@@ -145,8 +145,10 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
 // come from ballot key matching (no atomics decide any position).
 // ----------------------------------------------------------------------------
 constexpr int kAlignWaves = 16;
+constexpr int kIdCache = 32768;  // assignments whose expert ids are cached in LDS (int16)
 
 struct AlignSmem {
+  int16_t idc[kIdCache];
   int cnt[kMaxE];
   int first[kMaxE];
   int rank[kMaxE];
@@ -181,17 +183,36 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
     sm.first[e] = 0x7fffffff;
   }
   for (int e = tid; e < kAlignWaves * E; e += 1024) (&sm.wave_off[0][0])[(e / E) * kMaxE + e % E] = 0;
+  // the expert id of every assignment, read once (8 loads in flight per
+  // thread) into LDS; -1 for ids outside [0, E)
+  const bool cached = n <= kIdCache;
+  if (cached) {
+    for (int a0 = tid; a0 < n; a0 += 8 * 1024) {
+      int64_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int a = a0 + u * 1024;
+        v[u] = a < n ? ids[a] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int a = a0 + u * 1024;
+        if (a < n) sm.idc[a] = (int16_t)((v[u] >= 0 && v[u] < E) ? v[u] : -1);
+      }
+    }
+  }
+  auto expert_of = [&](int a) -> int {
+    if (cached) return sm.idc[a];
+    const int64_t v = ids[a];
+    return (v >= 0 && v < E) ? (int)v : -1;
+  };
   __syncthreads();
   const int seg = (n + kAlignWaves - 1) / kAlignWaves;
   const int s0 = min(n, w * seg), s1 = min(n, s0 + seg);
   // pass A: per-expert counts (total and per wave) and first appearance
   for (int c = s0; c < s1; c += 64) {
     const int a = c + lane;
-    int e = -1;
-    if (a < s1) {
-      int64_t v = ids[a];
-      e = (v >= 0 && v < E) ? (int)v : -1;
-    }
+    const int e = a < s1 ? expert_of(a) : -1;
     const bool valid = e >= 0;
     const uint64_t same = match_key(e, valid, nbits);
     const uint64_t lower = same & ((1ull << lane) - 1ull);
@@ -208,8 +229,8 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
     const int a = c + lane;
     bool flag = false;
     if (a < s1) {
-      int64_t v = ids[a];
-      flag = (v >= 0 && v < E) && sm.first[(int)v] == a;
+      const int e = expert_of(a);
+      flag = e >= 0 && sm.first[e] == a;
     }
     nflags += __popcll(__ballot(flag));
   }
@@ -220,15 +241,8 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
     for (int i = 0; i < w; ++i) before += sm.wave_flags[i];
     for (int c = s0; c < s1; c += 64) {
       const int a = c + lane;
-      int e = -1;
-      bool flag = false;
-      if (a < s1) {
-        int64_t v = ids[a];
-        if (v >= 0 && v < E) {
-          e = (int)v;
-          flag = sm.first[e] == a;
-        }
-      }
+      const int e = a < s1 ? expert_of(a) : -1;
+      const bool flag = e >= 0 && sm.first[e] == a;
       const uint64_t fl = __ballot(flag);
       if (flag) sm.rank[e] = before + __popcll(fl & ((1ull << lane) - 1ull));
       before += __popcll(fl);
@@ -280,11 +294,7 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
   {
     for (int c = s0; c < s1; c += 64) {
       const int a = c + lane;
-      int e = -1;
-      if (a < s1) {
-        int64_t v = ids[a];
-        e = (v >= 0 && v < E) ? (int)v : -1;
-      }
+      const int e = a < s1 ? expert_of(a) : -1;
       const bool valid = e >= 0;
       const uint64_t same = match_key(e, valid, nbits);
       const int r = __popcll(same & ((1ull << lane) - 1ull));
