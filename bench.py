@@ -19,7 +19,10 @@ the HIP events on that stream bracket device time only.
 
 Also reported (``extra``): the same layer at T=1, the AWQ skinny GEMM at
 K=4096 N=14336 M in {1,4,16} and the single AWQ GEMV K=2048 N=5632 (kernel
-GB/s).  ``cpu_baseline`` times the reference's algorithm (the CPU oracle:
+GB/s); the prefill workloads as TFLOP/s against the matching dense MFMA
+peak: int4 MoE prefill (128 experts, skewed top-8, hidden 2048, inter 768,
+T = 512 and 4096, bf16 MFMA) and FP8 block MoE prefill (256 experts, top-8,
+T = 2048, hidden 7168, inter 2048, FP8 MFMA).  ``cpu_baseline`` times the reference's algorithm (the CPU oracle:
 per-call dequant to float32, BLAS matmuls, per-expert grouping) on a
 bounded sample.
 
@@ -261,6 +264,69 @@ def bench_gemm(M: int, K: int, N: int, dev, copies: int):
             "frac_hbm": nbytes / avg / PEAK_HBM, "TFLOPs": 2.0 * M * K * N / avg / 1e12}
 
 
+def bench_int4_prefill(T: int, dev):
+    """int4 (AWQ g128) MoE prefill layer: 128 experts, top-8 of a skewed
+    router (logits N(0,1) + per-expert bias N(0,2)), hidden 2048, inter 768,
+    bf16 activations; device time of whole ccq_moe_w4_ffn calls (align,
+    grouped gate/up + SiLU, grouped down, combine) after routing."""
+    import torch
+
+    from ccut import workloads as wl
+    from ccut.blocks import moe
+
+    Ep, Hp, Ip, k = 128, 2048, 768, 8
+    ex = moe.W4Experts.from_awq(wl.awq_experts(Ep, Hp, Ip, GROUP, seed=71, device=dev),
+                                wl.awq_experts(Ep, Hp, Ip, GROUP, seed=72, device=dev),
+                                wl.awq_experts(Ep, Ip, Hp, GROUP, seed=73, device=dev), GROUP)
+    x = wl.activations(T, Hp, seed=74, device=dev)
+    lg = wl.router_logits(T, Ep, seed=75, device=dev, skew_std=2.0)
+    w, ids = moe.topk_softmax(lg, k, True)
+    moe.moe_ffn_w4(x, ids, w, ex)
+    torch.cuda.synchronize()
+    t = device_time([lambda: moe.moe_ffn_w4(x, ids, w, ex)], reps=10)
+    uniq = int(torch.unique(ids).numel())
+    flops = 2.0 * T * k * 3 * Hp * Ip
+    nbytes = uniq * ex.bytes_per_expert + T * Hp * 2 * 2
+    counts = torch.bincount(ids.reshape(-1), minlength=Ep)
+    return {"T": T, "us": t * 1e6, "TFLOPs": flops / t / 1e12, "frac_bf16_peak": flops / t / PEAK_BF16,
+            "GBps": nbytes / t / 1e9, "frac_hbm": nbytes / t / PEAK_HBM, "experts_routed": uniq,
+            "max_expert_rows": int(counts.max()), "min_expert_rows": int(counts.min())}
+
+
+def bench_fp8_prefill(dev, T: int = 2048):
+    """FP8 e4m3 block-scaled (128x128 weight blocks, per-token-per-128
+    activations) MoE prefill layer: 256 experts, top-8 (logits N(0,1)),
+    hidden 7168, inter 2048, bf16 activations; device time of whole
+    ccq_moe_fp8_ffn calls after routing.  HBM-bound: 11.3 GB of weights for
+    1.44 TFLOP (arithmetic intensity ~128 FLOP/B < the FP8 ridge ~629)."""
+    import torch
+
+    from ccut import workloads as wl
+    from ccut.blocks import moe
+
+    Ep, Hp, Ip, k = 256, 7168, 2048, 8
+    ex = moe.Fp8Experts.from_block(wl.fp8_block_weights(Ep, Ip, Hp, seed=81, device=dev),
+                                   wl.fp8_block_weights(Ep, Ip, Hp, seed=82, device=dev),
+                                   wl.fp8_block_weights(Ep, Hp, Ip, seed=83, device=dev))
+    torch.cuda.empty_cache()
+    x = wl.activations(T, Hp, seed=84, device=dev)
+    lg = wl.router_logits(T, Ep, seed=85, device=dev)
+    w, ids = moe.topk_softmax(lg, k, True)
+    moe.moe_ffn_fp8(x, ids, w, ex)
+    torch.cuda.synchronize()
+    t = device_time([lambda: moe.moe_ffn_fp8(x, ids, w, ex)], reps=5)
+    uniq = int(torch.unique(ids).numel())
+    flops = 2.0 * T * k * 3 * Hp * Ip
+    nbytes = uniq * ex.bytes_per_expert + T * Hp * 2 * 2
+    roof = min(PEAK_FP8, flops / nbytes * PEAK_HBM)
+    res = {"T": T, "us": t * 1e6, "TFLOPs": flops / t / 1e12, "frac_fp8_peak": flops / t / PEAK_FP8,
+           "frac_roofline": flops / t / roof, "roofline_TFLOPs": roof / 1e12, "GBps": nbytes / t / 1e9,
+           "frac_hbm": nbytes / t / PEAK_HBM, "experts_routed": uniq}
+    del ex
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(T: int, budget_s: float = 20.0):
     """The reference algorithm on the host: per-call dequant of each routed
     expert to float32 + BLAS matmuls + per-expert grouping (oracle)."""
@@ -335,6 +401,15 @@ def main():
         r = bench_gemm(1, 2048, 5632, dev=dev, copies=96)
         extra["awq_gemv_k2048_n5632"] = r
         log(f"awq gemv K=2048 N=5632: {r['GBps']:.1f} GB/s ({r['avg_us']:.2f} us)")
+        for Tp in (512, 4096):
+            r = bench_int4_prefill(Tp, dev)
+            extra[f"int4_moe_prefill_T{Tp}"] = r
+            log(f"int4 MoE prefill T={Tp}: {r['us']:.1f} us, {r['TFLOPs']:.1f} TFLOP/s "
+                f"({r['frac_bf16_peak']:.3f} of bf16 peak), {r['GBps']:.0f} GB/s")
+        r = bench_fp8_prefill(dev)
+        extra["fp8_moe_prefill_T2048"] = r
+        log(f"fp8 block MoE prefill T=2048: {r['us']:.1f} us, {r['TFLOPs']:.1f} TFLOP/s ({r['frac_fp8_peak']:.3f} "
+            f"of fp8 peak, {r['frac_roofline']:.3f} of its HBM roofline), {r['GBps']:.0f} GB/s")
     cpu = None if args.no_cpu else cpu_baseline(args.tokens)
     out = {
         "metric": METRIC,

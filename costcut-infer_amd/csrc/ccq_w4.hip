@@ -510,6 +510,246 @@ static int gemm_nb(int64_t M) { return M <= 4 ? 1 : (M <= 8 ? 2 : 4); }
 
 static bool valid_group(int64_t G) { return G == 32 || G == 64 || G == 128; }
 
+// ------------------------------------------------ prefill grouped GEMM --
+// For tiles with many rows (prefill, experts receiving tens to thousands of
+// tokens): a workgroup of 8 waves computes a BM-row tile x 128 output
+// columns, wave w owning the 16 columns of weight tile nb*8 + w (gate and up
+// for EPI_SILU).  Group size 128 = one k-tile, so per k-tile
+//     acc += s * (sum_k x * (MAGIC + q) - (MAGIC + z) * sum_k x)
+// with sum_k x of each row formed while the activation tile is staged.
+// The activation tile (BM x 128, bf16/fp16) goes through LDS, double-buffered
+// one k-tile ahead; the wave's packed weights go straight to registers one
+// k-tile ahead and are dequantized there (one AND/OR per weight pair).
+struct W4GP {
+  const void* x;
+  int64_t ldx;
+  const int32_t* rows;         // per tile BM row ids (-1 = padding); null = dense rows
+  int row_div;                 // activation row = row id / row_div
+  const int32_t* tile_expert;  // null = one weight
+  const int32_t* meta;         // meta[0] = valid schedule tiles; null = all
+  int tile_div;                // kernel tiles per schedule tile (schedule rows / BM)
+  const uint32_t* w0;
+  const uint32_t* sz0;
+  const uint32_t* w1;          // up projection (EPI_SILU)
+  const uint32_t* sz1;
+  int64_t w_es, sz_es;         // per-expert strides (words)
+  void* y;
+  int64_t ldy;
+  int y_dtype;
+  int M, N, K, KT, szw;
+};
+
+constexpr int WG_BM_SMALL = 64;
+constexpr int WG_BM_LARGE = 128;
+constexpr int WG_WAVES = 8;
+constexpr int WG_ALD = 128 + 8;  // LDS row stride of the activation tile (elements)
+
+template <typename AT, typename ST, int EPI, int BM>
+__global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
+  using V = typename Act<AT>::vec;
+  constexpr int NQ = EPI == EPI_SILU ? 2 : 1;
+  constexpr int RT = BM / 16;
+  constexpr int AP = BM * 16 / (64 * WG_WAVES);  // 16-byte activation pieces per thread
+  __shared__ __align__(16) AT As[2][BM * WG_ALD];
+  __shared__ __align__(16) float Sx[2][BM];
+  __shared__ int Rid[BM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = blockIdx.x, tile = blockIdx.y;
+  if (p.meta != nullptr && tile >= p.meta[0] * p.tile_div) return;
+  const int ex = p.tile_expert ? p.tile_expert[tile / p.tile_div] : 0;
+  if (tid < BM) {
+    int rid;
+    if (p.rows) {
+      rid = p.rows[tile * BM + tid];
+    } else {
+      rid = tile * BM + tid;
+      if (rid >= p.M) rid = -1;
+    }
+    Rid[tid] = rid;
+  }
+  if (!__syncthreads_or(tid < BM && Rid[tid] >= 0)) return;
+
+  // activation staging: piece i = tid + 512*j covers row i / 16, elements
+  // 8*(i % 16) .. +8 of the k-tile; the 16 pieces of a row sit in 16
+  // consecutive lanes, which also reduce the row sum
+  const AT* asrc[AP];
+  bool aval[AP];
+#pragma unroll
+  for (int j = 0; j < AP; ++j) {
+    const int i = tid + 64 * WG_WAVES * j, row = i >> 4, part = i & 15;
+    aval[j] = Rid[row] >= 0;
+    asrc[j] = reinterpret_cast<const AT*>(p.x) + (int64_t)(aval[j] ? Rid[row] / p.row_div : 0) * p.ldx + 8 * part;
+  }
+  struct AStage {
+    u32x4 v[AP];
+  };
+  auto load_a = [&](AStage& st, int kt) {
+#pragma unroll
+    for (int j = 0; j < AP; ++j) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(asrc[j] + (int64_t)kt * 128);
+      st.v[j] = aval[j] ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_a = [&](const AStage& st, int buf) {
+#pragma unroll
+    for (int j = 0; j < AP; ++j) {
+      const int i = tid + 64 * WG_WAVES * j, row = i >> 4, part = i & 15;
+      *reinterpret_cast<u32x4*>(&As[buf][row * WG_ALD + 8 * part]) = st.v[j];
+      const V a = __builtin_bit_cast(V, st.v[j]);
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += (float)a[e];
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+      if (part == 0) Sx[buf][row] = sum;
+    }
+  };
+
+  // the wave's weight column tile (16 columns) of each matrix
+  const int nt = nb * WG_WAVES + wave;
+  const int r = lane & 15, kq = lane >> 4;
+  const uint32_t* wsrc[NQ];
+  const uint32_t* zsrc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    wsrc[q] = (q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + (int64_t)nt * p.KT * 256 + lane * 4;
+    zsrc[q] = (q == 0 ? p.sz0 : p.sz1) + (int64_t)ex * p.sz_es + (int64_t)(nt * 16 + r) * p.szw;
+  }
+  struct BStage {
+    u32x4 w[NQ];
+    uint32_t z[NQ];
+  };
+  auto load_b = [&](BStage& st, int kt) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      st.w[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wsrc[q] + (int64_t)kt * 256));
+      st.z[q] = zsrc[q][kt];
+    }
+  };
+
+  f32x4 acc[RT][NQ];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) acc[rt][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf, const BStage& b) {
+    V bw[NQ][4];
+    float s[NQ], c[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bw[q][j] = dq_b<AT>(b.w[q][j]);
+      s[q] = sz_scale<ST>(b.z[q]);
+      c[q] = Act<AT>::kMagic + (float)(b.z[q] >> 16);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      V a[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const V*>(&As[buf][(rt * 16 + r) * WG_ALD + 32 * j + 8 * kq]);
+      const f32x4 sx = *reinterpret_cast<const f32x4*>(&Sx[buf][rt * 16 + 4 * kq]);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t = mfma16(a[j], bw[q][j], t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rt][q][i] = fmaf(s[q], fmaf(-c[q], sx[i], t[i]), acc[rt][q][i]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // pipeline: k-tile kt computes from LDS buffer kt & 1 and weight stage
+  // kt & 1 while the activations of kt+1 (issued first) and the weights of
+  // kt+1 are in flight
+  AStage as0, as1;
+  BStage bs0, bs1;
+  load_a(as0, 0);
+  load_b(bs0, 0);
+  store_a(as0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < p.KT; kt += 2) {
+    if (kt + 1 < p.KT) {
+      load_a(as1, kt + 1);
+      load_b(bs1, kt + 1);
+    }
+    compute(0, bs0);
+    if (kt + 1 < p.KT) store_a(as1, 1);
+    __syncthreads();
+    if (kt + 1 >= p.KT) break;
+    if (kt + 2 < p.KT) {
+      load_a(as0, kt + 2);
+      load_b(bs0, kt + 2);
+    }
+    compute(1, bs1);
+    if (kt + 2 < p.KT) store_a(as0, 0);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows rt*16 + 4*kq + i of column nt*16 + r
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rid = Rid[rt * 16 + 4 * kq + i];
+      if (rid < 0) continue;
+      const int64_t o = (int64_t)rid * p.ldy + nt * 16 + r;
+      if (EPI == EPI_SILU) {
+        const float g = acc[rt][0][i], u = acc[rt][NQ - 1][i];
+        store_val(p.y, o, g / (1.0f + expf(-g)) * u, p.y_dtype);
+      } else {
+        store_val(p.y, o, acc[rt][0][i], p.y_dtype);
+      }
+    }
+}
+
+// bm: rows per schedule tile.  Gate/up (two matrices) runs 64-row kernel
+// tiles (128 would spill registers), splitting 128-row schedule tiles.
+template <int EPI>
+static int launch_group_gemm(W4GP p, int x_bf16, int s_bf16, int bm, int64_t tiles, hipStream_t st) {
+  const int kbm = EPI == EPI_SILU ? WG_BM_SMALL : bm;
+  p.tile_div = bm / kbm;
+  bm = kbm;
+  const dim3 grid((unsigned)(p.N / 128), (unsigned)(tiles * p.tile_div)), block(64 * WG_WAVES);
+#define CCQ_LAUNCH_GG(AT, ST)                                                                     \
+  do {                                                                                            \
+    if constexpr (EPI != EPI_SILU) {                                                              \
+      if (bm == WG_BM_LARGE) {                                                                    \
+        hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, WG_BM_LARGE>), grid, block, 0, st, p); \
+        break;                                                                                    \
+      }                                                                                           \
+    }                                                                                             \
+    hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, WG_BM_SMALL>), grid, block, 0, st, p);  \
+  } while (0)
+  if (x_bf16) {
+    if (s_bf16)
+      CCQ_LAUNCH_GG(__bf16, __bf16);
+    else
+      CCQ_LAUNCH_GG(__bf16, _Float16);
+  } else {
+    if (s_bf16)
+      CCQ_LAUNCH_GG(_Float16, __bf16);
+    else
+      CCQ_LAUNCH_GG(_Float16, _Float16);
+  }
+#undef CCQ_LAUNCH_GG
+  return launch_status("w4 grouped gemm");
+}
+
+// Tile rows of the grouped kernel for n assignments over E experts (each
+// tile streams its expert's weights, so a tile should hold all of them).
+static int group_tile_rows(int64_t n, int64_t E) { return n >= 32 * E ? WG_BM_LARGE : WG_BM_SMALL; }
+// The grouped kernel replaces the 16-row decode kernel once the average
+// expert receives at least 16 rows (and the shape suits it: group 128,
+// N a multiple of 128).
+static bool use_group_gemm(int64_t n, int64_t E, int64_t G, int64_t N1, int64_t N2) {
+  return n >= 16 * E && G == 128 && N1 % 128 == 0 && N2 % 128 == 0;
+}
+
+
 }  // namespace ccq
 
 using namespace ccq;
@@ -586,7 +826,7 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_w4_gemm: x_dtype must be f16|bf16");
   CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_w4_gemm: scale_dtype must be f16|bf16");
   CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_w4_gemm: bad y_dtype");
-  CCQ_REQUIRE(cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large for the skinny kernel", (long long)M);
+  CCQ_REQUIRE(M > 64 || cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
   CCQ_REQUIRE(K <= (1 << 20) && N / 16 <= 0x7fffffff, "ccq_w4_gemm: K=%lld or N=%lld too large", (long long)K,
               (long long)N);
   if (M == 0 || N == 0) return 0;
@@ -594,6 +834,28 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   CCQ_REQUIRE(x && w_tiled && sz && y, "ccq_w4_gemm: null pointer");
   CCQ_REQUIRE(aligned(x, 16) && aligned(w_tiled, 16) && aligned(sz, 16),
               "ccq_w4_gemm: x, w_tiled and sz must be 16-byte aligned");
+  if (M > 64 && group_size == 128 && N % 128 == 0) {
+    // prefill-sized: tiles of 64/128 rows stream the weight once per tile
+    const int bm = M >= WG_BM_LARGE ? WG_BM_LARGE : WG_BM_SMALL;
+    CCQ_REQUIRE(cdiv(M, bm) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
+    W4GP g = {};
+    g.x = x;
+    g.ldx = K;
+    g.row_div = 1;
+    g.w0 = (const uint32_t*)w_tiled;
+    g.sz0 = sz;
+    g.y = y;
+    g.ldy = N;
+    g.y_dtype = y_dtype;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.KT = (int)(K / 128);
+    g.szw = (int)sz_words_per_column(K, group_size);
+    CCQ_REQUIRE(cdiv(M, bm) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
+    return launch_group_gemm<EPI_STORE>(g, x_dtype == CCQ_BF16, scale_dtype == CCQ_BF16, bm, cdiv(M, bm),
+                                        as_stream(stream));
+  }
   const int64_t tiles = cdiv(M, 16);
   const SkinnyPlan pl = plan_skinny(K, N, group_size, 1, gemm_nb(M));
   SkinnyP p = {};
@@ -650,16 +912,20 @@ int check_expert_ptrs(const ccq_w4_experts* ex, bool gate_up, const char* name) 
 // and the per-assignment down rows.
 struct MoeLayout {
   int64_t n, max_tiles;
+  int tile_m;       // rows per schedule tile: 16 (decode kernel) or 64/128 (grouped kernel)
+  bool grouped;
   size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, total;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes) {
   MoeLayout L;
   L.n = T * k;
-  L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, 16);
+  L.grouped = use_group_gemm(L.n, ex->num_experts, ex->group_size, ex->inter, ex->hidden);
+  L.tile_m = L.grouped ? group_tile_rows(L.n, ex->num_experts) : 16;
+  L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, L.tile_m);
   size_t o = 0;
   L.off_sorted = o;
-  o += align256((size_t)L.max_tiles * 16 * 4);
+  o += align256((size_t)L.max_tiles * L.tile_m * 4);
   L.off_tile_expert = o;
   o += align256((size_t)L.max_tiles * 4);
   L.off_meta = o;
@@ -803,11 +1069,58 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
   void* inter = ws + L.off_inter;
   float* rows = (float*)(ws + L.off_rows);
 
-  rc = launch_align(ids, L.n, ex->num_experts, 16, sorted, tile_expert, meta, counts, st);
+  CCQ_REQUIRE(L.max_tiles * 2 <= 65535, "ccq_moe_w4_ffn: too many tiles");
+  rc = launch_align(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st);
   if (rc) return rc;
-  rc = run_gate_up(x, x_dtype, k, sorted, tile_expert, meta, L.max_tiles, inter, ex, st);
-  if (rc) return rc;
-  rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
-  if (rc) return rc;
+  if (L.grouped) {
+    const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
+    W4GP g = {};
+    g.x = x;
+    g.ldx = H;
+    g.rows = sorted;
+    g.row_div = (int)k;
+    g.tile_expert = tile_expert;
+    g.meta = meta;
+    g.w0 = (const uint32_t*)ex->w_gate;
+    g.sz0 = ex->sz_gate;
+    g.w1 = (const uint32_t*)ex->w_up;
+    g.sz1 = ex->sz_up;
+    g.szw = (int)sz_words_per_column(H, G);
+    g.w_es = H * I / 8;
+    g.sz_es = I * g.szw;
+    g.y = inter;
+    g.ldy = I;
+    g.y_dtype = x_dtype;
+    g.N = (int)I;
+    g.K = (int)H;
+    g.KT = (int)(H / 128);
+    rc = launch_group_gemm<EPI_SILU>(g, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.tile_m, L.max_tiles, st);
+    if (rc) return rc;
+    W4GP d = {};
+    d.x = inter;
+    d.ldx = I;
+    d.rows = sorted;
+    d.row_div = 1;
+    d.tile_expert = tile_expert;
+    d.meta = meta;
+    d.w0 = (const uint32_t*)ex->w_down;
+    d.sz0 = ex->sz_down;
+    d.szw = (int)sz_words_per_column(I, G);
+    d.w_es = I * H / 8;
+    d.sz_es = H * d.szw;
+    d.y = rows;
+    d.ldy = H;
+    d.y_dtype = CCQ_F32;
+    d.N = (int)H;
+    d.K = (int)I;
+    d.KT = (int)(I / 128);
+    rc = launch_group_gemm<EPI_ROWS>(d, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.tile_m, L.max_tiles, st);
+    if (rc) return rc;
+  } else {
+    rc = run_gate_up(x, x_dtype, k, sorted, tile_expert, meta, L.max_tiles, inter, ex, st);
+    if (rc) return rc;
+    rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
+    if (rc) return rc;
+  }
   return launch_combine(rows, weights, ids, ex->num_experts, y, y_dtype, T, k, ex->hidden, st);
 }

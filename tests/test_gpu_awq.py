@@ -81,6 +81,15 @@ def test_gemm_parity_m_sweep(gpu, M, xdt):
     assert _gemm_case(gpu, M, 512, 256, 128, xdt, xdt, seed=M) <= TOL
 
 
+@pytest.mark.parametrize("M", [65, 128, 200, 513])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_gemm_prefill_grouped_kernel(gpu, M, xdt):
+    """M > 64 with group 128 and N % 128 == 0 runs the tiled prefill kernel
+    (64/128-row tiles, activations staged in LDS)."""
+    assert _gemm_case(gpu, M, 768, 384, 128, xdt, torch.float32, seed=M) <= TIGHT
+    assert _gemm_case(gpu, M, 768, 384, 128, xdt, xdt, seed=M + 1) <= TOL
+
+
 @pytest.mark.parametrize("G", [32, 64])
 def test_gemm_parity_groups(gpu, G):
     assert _gemm_case(gpu, 3, 384, 160, G, torch.float16, torch.float32, seed=G) <= TIGHT

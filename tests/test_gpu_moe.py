@@ -30,7 +30,7 @@ def _experts(E, H, I, G, seed):
     return one(H, I), one(H, I), one(I, H)
 
 
-def _run(gpu, E, H, I, G, T, k, seed, xdt=torch.bfloat16, ydt=torch.float32):
+def _run(gpu, E, H, I, G, T, k, seed, xdt=torch.bfloat16, ydt=torch.float32, skew=0.0):
     from ccut.blocks import moe
 
     gate, up, down = _experts(E, H, I, G, seed)
@@ -39,6 +39,8 @@ def _run(gpu, E, H, I, G, T, k, seed, xdt=torch.bfloat16, ydt=torch.float32):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn((T, H), generator=g).to(xdt)
     lg = torch.randn((T, E), generator=g)
+    if skew:
+        lg = lg + torch.randn((1, E), generator=g) * skew
     y = moe.moe_forward_w4(x.to(gpu), lg.to(gpu), ex, top_k=k, out_dtype=ydt).float().cpu().numpy()
     w0, ids0 = omoe.topk_softmax(lg.numpy(), k)
 
@@ -67,6 +69,19 @@ def test_moe_w4_decode_config(gpu, T):
     """64 experts, top-6, hidden 2048, expert intermediate 1408, group 128,
     bf16 activations and output."""
     assert _run(gpu, E=64, H=2048, I=1408, G=128, T=T, k=6, seed=100 + T, ydt=torch.bfloat16) <= TOL
+
+
+@pytest.mark.parametrize("T,k,E", [(64, 2, 8), (200, 2, 8), (96, 4, 6)])
+def test_moe_w4_grouped_prefill(gpu, T, k, E):
+    """Experts averaging >= 16 rows take the grouped prefill kernel (64-row
+    tiles below 32 rows per expert, 128-row above)."""
+    assert _run(gpu, E=E, H=256, I=384, G=128, T=T, k=k, seed=T + E) <= TOL
+
+
+def test_moe_w4_prefill_skewed_router(gpu):
+    """Skewed router (per-expert bias N(0, 2)): hot experts span many tiles,
+    cold ones get a few rows; hidden 2048, inter 768, 32 experts, top-8."""
+    assert _run(gpu, E=32, H=2048, I=768, G=128, T=160, k=8, seed=5, skew=2.0, ydt=torch.bfloat16) <= TOL
 
 
 def test_moe_combine_api_with_expert_fn(gpu):
