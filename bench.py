@@ -248,11 +248,13 @@ def bench_gemm(M: int, K: int, N: int, dev, copies: int):
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
     ref = awq.gemm(x, ws[0])  # through the Python API once
     stream = torch.cuda.current_stream().cuda_stream
+    nws = lib.ccq_w4_gemm_workspace_size(M, K, N, GROUP)
+    wsb = torch.empty(max(nws, 256), dtype=torch.uint8, device=dev)
     launches = []
     for w in ws:
         args = (ctypes.c_void_p(x.data_ptr()), 1, ctypes.c_void_p(w.w_tiled.data_ptr()),
                 ctypes.c_void_p(w.sz.data_ptr()), 1, ctypes.c_void_p(y.data_ptr()), 1, M, K, N, GROUP,
-                ctypes.c_void_p(stream))
+                ctypes.c_void_p(wsb.data_ptr()), nws, ctypes.c_void_p(stream))
         launches.append(lambda a=args: lib.ccq_w4_gemm(*a))
     _lib.check(launches[0](), "ccq_w4_gemm")
     torch.cuda.synchronize()

@@ -67,7 +67,8 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_awq_unpack_tiled": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ccq_awq_sz_words": (_i64, [_i64, _i64]),
     "ccq_awq_pack_sz": (_int, [_vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
-    "ccq_w4_gemm": (_int, [_vp, _int, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp]),
+    "ccq_w4_gemm_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "ccq_w4_gemm": (_int, [_vp, _int, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
     "ccq_topk_softmax": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "ccq_moe_align_max_tiles": (_i64, [_i64, _i64, _i64]),
     "ccq_moe_align": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),

@@ -152,7 +152,9 @@ def gemm(x: torch.Tensor, w: AwqWeights, out_dtype: torch.dtype | None = None) -
         raise ValueError(f"AWQ GEMM: x has {K} features, weight expects {w.K}")
     out_dtype = out_dtype or x.dtype
     y = torch.empty((M, w.N), dtype=out_dtype, device=x.device)
+    nbytes = lib().ccq_w4_gemm_workspace_size(M, K, w.N, w.group_size)
+    ws = _dev.workspace("w4_gemm", nbytes, x.device) if nbytes else None
     call("ccq_w4_gemm", x2.data_ptr(), _dev.DTYPE_CODE[x.dtype], w.w_tiled.data_ptr(), w.sz.data_ptr(),
          _scale_code(w.scale_dtype), y.data_ptr(), _dev.DTYPE_CODE[out_dtype], M, K, w.N, w.group_size,
-         _dev.stream_ptr(x.device))
+         ws.data_ptr() if ws is not None else None, nbytes, _dev.stream_ptr(x.device))
     return y.reshape(*x.shape[:-1], w.N)

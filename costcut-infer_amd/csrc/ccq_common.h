@@ -35,6 +35,7 @@ __host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ?
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
 
@@ -107,6 +108,47 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 template <typename T>
 __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, 64);
+}
+
+// ------------------------------------------------ LDS DMA pipeline pieces --
+// Byte offset of a __shared__ object inside the workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Global -> LDS without registers: lane l copies 16 (4) bytes from
+// base + voff into LDS at lds + 16*l (4*l).  base and lds are wave-uniform;
+// completion is counted by vmcnt.  Issued as inline assembly so that the
+// compiler adds no waits of its own for the LDS it writes: the pipelines
+// below order these copies with explicit wait_vmcnt + barrier.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that does not wait for outstanding global loads (the
+// __syncthreads fence would drain the whole pipeline); LDS reads of this
+// wave are completed first, so a slot may be refilled after the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (linear id b runs on
+// XCD b % 8).  Renumber ids 0..n-1 so that each XCD works through one
+// contiguous range: neighbouring logical ids (for instance the column blocks
+// of one row tile) then share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  const int q = n >> 3, r = n & 7, x = b & 7;
+  return x * q + (x < r ? x : r) + (b >> 3);
 }
 
 }  // namespace ccq

@@ -147,6 +147,15 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
+// 32x32x16: A lane l = row l & 31, B lane l = column l & 31, both with
+// k = 8*(l >> 5) + e; D register i of lane l = (row 8*(i/4) + 4*(l >> 5) + i%4,
+// column l & 31).
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
 
 template <typename AT>
 __device__ __forceinline__ typename Act<AT>::vec dq_b(uint32_t w) {
@@ -155,6 +164,19 @@ __device__ __forceinline__ typename Act<AT>::vec dq_b(uint32_t w) {
   r[1] = ((w >> 4) & 0x000F000Fu) | Act<AT>::kMagic2;
   r[2] = ((w >> 8) & 0x000F000Fu) | Act<AT>::kMagic2;
   r[3] = ((w >> 12) & 0x000F000Fu) | Act<AT>::kMagic2;
+  return __builtin_bit_cast(typename Act<AT>::vec, r);
+}
+
+// dq_b with one v_and_or_b32 per weight pair: the mask and the magic come in
+// as run-time values (an SGPR and a VGPR), since a VOP3 op on gfx9 takes no
+// literal and (w & literal) | literal would cost two ops.
+template <typename AT>
+__device__ __forceinline__ typename Act<AT>::vec dq_b3(uint32_t w, uint32_t mask_s, uint32_t magic_v) {
+  u32x4 r;
+  r[0] = (w & mask_s) | magic_v;
+  r[1] = ((w >> 4) & mask_s) | magic_v;
+  r[2] = ((w >> 8) & mask_s) | magic_v;
+  r[3] = ((w >> 12) & mask_s) | magic_v;
   return __builtin_bit_cast(typename Act<AT>::vec, r);
 }
 
@@ -511,23 +533,37 @@ static int gemm_nb(int64_t M) { return M <= 4 ? 1 : (M <= 8 ? 2 : 4); }
 static bool valid_group(int64_t G) { return G == 32 || G == 64 || G == 128; }
 
 // ------------------------------------------------ prefill grouped GEMM --
-// For tiles with many rows (prefill, experts receiving tens to thousands of
-// tokens): a workgroup of 8 waves computes a BM-row tile x 128 output
-// columns, wave w owning the 16 columns of weight tile nb*8 + w (gate and up
-// for EPI_SILU).  Group size 128 = one k-tile, so per k-tile
-//     acc += s * (sum_k x * (MAGIC + q) - (MAGIC + z) * sum_k x)
-// with sum_k x of each row formed while the activation tile is staged.
-// The activation tile (BM x 128, bf16/fp16) goes through LDS, double-buffered
-// one k-tile ahead; the wave's packed weights go straight to registers one
-// k-tile ahead and are dequantized there (one AND/OR per weight pair).
+// For tiles with many rows (prefill; experts receiving tens to thousands of
+// tokens).  A workgroup of 8 waves computes a 128-row tile against 128
+// columns of gate and of up (EPI_SILU) or 128 / 256 columns of one matrix.
+// The waves form a 2 (rows) x 4 (columns) grid, each owning 64 rows x 4
+// MFMA column tiles of 16, so every activation fragment read from LDS feeds
+// 4 MFMAs and every dequantized weight fragment 4 more.  Group size 128 is
+// one k-tile; per k-tile
+//     acc += s * (sum_k x * (MAGIC + q) - (MAGIC + z) * Sx)
+// where Sx is the sum of the row's 128 activations of that group, computed
+// beforehand (row_group_sums_kernel for a layer input, the gate/up epilogue
+// for the intermediate rows).
+//
+// Per k-tile the workgroup copies from HBM straight into LDS
+// (global_load_lds, no registers): the activation tile (128 rows x 256 B,
+// gathered through the tile's row ids), the packed weight tiles (1 KiB per
+// 16 columns), their scale/zero words and the rows' Sx.  Three k-tiles form
+// a ring, so two k-tiles of loads are in flight while one is multiplied,
+// with a single barrier per k-tile.  Activation rows keep their 16-byte
+// pieces XOR-swizzled by row (piece p of row r at position p ^ (r & 15)):
+// the MFMA operand reads of 16 consecutive rows then hit 16 different bank
+// groups.  Weights are dequantized in registers after the LDS read.
 struct W4GP {
   const void* x;
-  int64_t ldx;
-  const int32_t* rows;         // per tile BM row ids (-1 = padding); null = dense rows
+  int64_t ldx;                 // activation row stride (elements)
+  const float* sx;             // per-row group sums of x: sx[row * ldsx + kt]
+  int64_t ldsx;
+  const int32_t* rows;         // per tile 128 row ids (-1 = padding, at the end); null = dense rows
   int row_div;                 // activation row = row id / row_div
   const int32_t* tile_expert;  // null = one weight
-  const int32_t* meta;         // meta[0] = valid schedule tiles; null = all
-  int tile_div;                // kernel tiles per schedule tile (schedule rows / BM)
+  const int32_t* meta;         // meta[0] = valid schedule tiles; null = tiles
+  int tiles;
   const uint32_t* w0;
   const uint32_t* sz0;
   const uint32_t* w1;          // up projection (EPI_SILU)
@@ -536,193 +572,359 @@ struct W4GP {
   void* y;
   int64_t ldy;
   int y_dtype;
+  float* sxo;                  // EPI_SILU: group sums of the stored rows, sxo[row id * ldsxo + block]
+  int64_t ldsxo;
   int M, N, K, KT, szw;
+  uint32_t nib_mask;           // 0x000F000F (a run-time value, see dq_b3)
 };
 
-constexpr int WG_BM_SMALL = 64;
-constexpr int WG_BM_LARGE = 128;
-constexpr int WG_WAVES = 8;
-constexpr int WG_ALD = 128 + 8;  // LDS row stride of the activation tile (elements)
+constexpr int GG_BM = 128;
+constexpr int GG_A_BYTES = GG_BM * 256;  // 128 rows x 128 16-bit activations
+constexpr int GG_B_BYTES = 16 * 1024;    // up to 16 packed weight tiles
+constexpr int GG_SZ_BYTES = 256 * 4;     // up to 256 scale/zero words
+constexpr int GG_SX_BYTES = GG_BM * 4;
+constexpr int GG_B_OFF = GG_A_BYTES;
+constexpr int GG_SZ_OFF = GG_B_OFF + GG_B_BYTES;
+constexpr int GG_SX_OFF = GG_SZ_OFF + GG_SZ_BYTES;
+constexpr int GG_STAGE = GG_SX_OFF + GG_SX_BYTES;
+constexpr int GG_STAGES = 3;
+static_assert(GG_STAGES * GG_STAGE + GG_BM * 4 <= 160 * 1024, "LDS budget of one workgroup");
 
-template <typename AT, typename ST, int EPI, int BM>
+template <int N>
+__device__ __forceinline__ void wait_stage(int n) {
+  // n (wave-uniform) = copies this wave issues per k-tile, N = the largest
+  if constexpr (N > 0) {
+    if (n == N) {
+      wait_vmcnt<N>();
+      return;
+    }
+    wait_stage<N - 1>(n);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+// Row sums over the 32 lanes of each half-wave for 32 values per lane
+// (value r of a lane belongs to row r): a butterfly that halves the list at
+// every step, so lane l ends with the sum for row l & 31.
+__device__ __forceinline__ float half_wave_row_sums(float (&v)[32], int c32) {
+#pragma unroll
+  for (int m = 1, n = 32; m < 32; m <<= 1, n >>= 1) {
+    const bool up = (c32 & m) != 0;
+#pragma unroll
+    for (int j = 0; j < n / 2; ++j) {
+      const float keep = up ? v[2 * j + 1] : v[2 * j];
+      const float send = up ? v[2 * j] : v[2 * j + 1];
+      v[j] = keep + __shfl_xor(send, m, 64);
+    }
+  }
+  return v[0];
+}
+
+template <typename AT, typename ST, int EPI, int CTW>
 __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
   using V = typename Act<AT>::vec;
   constexpr int NQ = EPI == EPI_SILU ? 2 : 1;
-  constexpr int RT = BM / 16;
-  constexpr int AP = BM * 16 / (64 * WG_WAVES);  // 16-byte activation pieces per thread
-  __shared__ __align__(16) AT As[2][BM * WG_ALD];
-  __shared__ __align__(16) float Sx[2][BM];
-  __shared__ int Rid[BM];
+  constexpr int WGN = 64 * CTW;      // columns per matrix per workgroup
+  constexpr int TPM = WGN / 16;      // 16-column weight tiles per matrix per k-tile
+  constexpr int NBT = NQ * TPM;      // weight tiles per k-tile
+  constexpr int BPW = NBT / 8;       // weight tiles each wave copies
+  constexpr int NSZ = NQ * WGN;      // scale/zero words per k-tile
+  constexpr int C32 = CTW * NQ / 2;  // 32-column MFMA tiles per wave
+  constexpr int CQ = C32 / NQ;       // ... per matrix
+  static_assert(NBT % 8 == 0 && NBT <= 16 && NSZ <= 256 && NSZ % 64 == 0 && C32 >= 1, "tile shape");
+  __shared__ __align__(16) char smem[GG_STAGES * GG_STAGE];
+  __shared__ int Rid[GG_BM];
+
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nb = blockIdx.x, tile = blockIdx.y;
-  if (p.meta != nullptr && tile >= p.meta[0] * p.tile_div) return;
-  const int ex = p.tile_expert ? p.tile_expert[tile / p.tile_div] : 0;
-  if (tid < BM) {
+  const int mw = wave >> 2, nw = wave & 3;
+  const int nblk = p.N / WGN;
+  const int items = (p.meta != nullptr ? p.meta[0] : p.tiles) * nblk;
+  if ((int)blockIdx.x >= items) return;
+  const int item = xcd_remap(blockIdx.x, items);
+  const int tile = item / nblk, nb = item - tile * nblk;
+  const int ex = p.tile_expert != nullptr ? p.tile_expert[tile] : 0;
+  if (tid < GG_BM) {
     int rid;
-    if (p.rows) {
-      rid = p.rows[tile * BM + tid];
+    if (p.rows != nullptr) {
+      rid = p.rows[tile * GG_BM + tid];
     } else {
-      rid = tile * BM + tid;
+      rid = tile * GG_BM + tid;
       if (rid >= p.M) rid = -1;
     }
     Rid[tid] = rid;
   }
-  if (!__syncthreads_or(tid < BM && Rid[tid] >= 0)) return;
+  const int nvalid = __syncthreads_count(tid < GG_BM && Rid[tid] >= 0);
+  if (nvalid == 0) return;
+  const int rid0 = Rid[0];
 
-  // activation staging: piece i = tid + 512*j covers row i / 16, elements
-  // 8*(i % 16) .. +8 of the k-tile; the 16 pieces of a row sit in 16
-  // consecutive lanes, which also reduce the row sum
-  const AT* asrc[AP];
-  bool aval[AP];
+  // ---- copy plan of this wave (per k-tile) ----
+  // activations: rows 16*wave + 4*i + (lane >> 4), i = 0..3; the lane takes
+  // piece (lane & 15) ^ (row & 15), which lands at position lane & 15
+  uint32_t aoff[4];
 #pragma unroll
-  for (int j = 0; j < AP; ++j) {
-    const int i = tid + 64 * WG_WAVES * j, row = i >> 4, part = i & 15;
-    aval[j] = Rid[row] >= 0;
-    asrc[j] = reinterpret_cast<const AT*>(p.x) + (int64_t)(aval[j] ? Rid[row] / p.row_div : 0) * p.ldx + 8 * part;
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 4 * i + (lane >> 4);
+    const int rid = Rid[row] >= 0 ? Rid[row] : rid0;
+    const int piece = (lane & 15) ^ (4 * i + (lane >> 4));
+    aoff[i] = (uint32_t)((int64_t)(rid / p.row_div) * p.ldx * 2 + piece * 16);
   }
-  struct AStage {
-    u32x4 v[AP];
-  };
-  auto load_a = [&](AStage& st, int kt) {
+  const char* bsrc[BPW];
 #pragma unroll
-    for (int j = 0; j < AP; ++j) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(asrc[j] + (int64_t)kt * 128);
-      st.v[j] = aval[j] ? v : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store_a = [&](const AStage& st, int buf) {
-#pragma unroll
-    for (int j = 0; j < AP; ++j) {
-      const int i = tid + 64 * WG_WAVES * j, row = i >> 4, part = i & 15;
-      *reinterpret_cast<u32x4*>(&As[buf][row * WG_ALD + 8 * part]) = st.v[j];
-      const V a = __builtin_bit_cast(V, st.v[j]);
-      float sum = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sum += (float)a[e];
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
-      if (part == 0) Sx[buf][row] = sum;
-    }
-  };
-
-  // the wave's weight column tile (16 columns) of each matrix
-  const int nt = nb * WG_WAVES + wave;
-  const int r = lane & 15, kq = lane >> 4;
-  const uint32_t* wsrc[NQ];
-  const uint32_t* zsrc[NQ];
-#pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    wsrc[q] = (q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + (int64_t)nt * p.KT * 256 + lane * 4;
-    zsrc[q] = (q == 0 ? p.sz0 : p.sz1) + (int64_t)ex * p.sz_es + (int64_t)(nt * 16 + r) * p.szw;
+  for (int j = 0; j < BPW; ++j) {
+    const int b = wave * BPW + j, q = b / TPM, nt = nb * TPM + (b - q * TPM);
+    bsrc[j] = reinterpret_cast<const char*>((q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + (int64_t)nt * p.KT * 256);
   }
-  struct BStage {
-    u32x4 w[NQ];
-    uint32_t z[NQ];
-  };
-  auto load_b = [&](BStage& st, int kt) {
+  const bool has_sz = wave < NSZ / 64;
+  uint32_t zoff = 0;
+  const char* zsrc = nullptr;
+  if (has_sz) {
+    const int q = (64 * wave) / WGN, col = nb * WGN + (64 * wave - q * WGN) + lane;
+    zoff = (uint32_t)((int64_t)col * p.szw * 4);
+    zsrc = reinterpret_cast<const char*>((q == 0 ? p.sz0 : p.sz1) + (int64_t)ex * p.sz_es);
+  }
+  const bool has_sx = wave == 4 || wave == 5;
+  uint32_t soff = 0;
+  if (has_sx) {
+    const int row = 64 * (wave - 4) + lane;
+    const int rid = Rid[row] >= 0 ? Rid[row] : rid0;
+    soff = (uint32_t)((int64_t)(rid / p.row_div) * p.ldsx * 4);
+  }
+  const int ncopy = 4 + BPW + (has_sz ? 1 : 0) + (has_sx ? 1 : 0);
+  const uint32_t lds0 = lds_addr(smem);
+
+  auto issue = [&](int kt, int slot) {
+    const uint32_t st = lds0 + slot * GG_STAGE;
+    const char* xb = reinterpret_cast<const char*>(p.x) + (int64_t)kt * 256;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      st.w[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wsrc[q] + (int64_t)kt * 256));
-      st.z[q] = zsrc[q][kt];
-    }
+    for (int i = 0; i < 4; ++i) dma16(xb, aoff[i], st + (16 * wave + 4 * i) * 256);
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+      dma16(bsrc[j] + (int64_t)kt * 1024, lane * 16, st + GG_B_OFF + (wave * BPW + j) * 1024);
+    if (has_sz) dma4(zsrc + kt * 4, zoff, st + GG_SZ_OFF + wave * 256);
+    if (has_sx) dma4(p.sx + kt, soff, st + GG_SX_OFF + (wave - 4) * 256);
   };
 
-  f32x4 acc[RT][NQ];
+  // ---- MFMA side: v_mfma_f32_32x32x16; the wave owns rows mw*64 + 32*rt
+  // (rt = 0, 1) and C32 32-column tiles; lane (h, c32) = (lane >> 5, lane & 31) ----
+  const int c32 = lane & 31, h = lane >> 5;
+  // A operand of k-step s: row c32 of the 32-row tile, piece 2s + h (swizzled)
+  uint32_t adoff[8];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+  for (int s = 0; s < 8; ++s) adoff[s] = (mw * 64 + c32) * 256 + (((2 * s + h) ^ (c32 & 15)) * 16);
+  // B operand: column c32 of the tile = column c32 & 15 of 16-column weight
+  // tile (c32 >> 4); its k-step s sits in dword s >> 1 of the 16-byte slot
+  // of lane 16 * (2 * (s & 1) + h) + (c32 & 15)
+  uint32_t bdoff[C32][2];
+  uint32_t zdoff[C32];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) acc[rt][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < C32; ++c) {
+    const int q = c / CQ, cc = c - q * CQ;
+    const int t16 = q * TPM + nw * CTW + 2 * cc + (c32 >> 4);
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) bdoff[c][pp] = GG_B_OFF + t16 * 1024 + (16 * (2 * pp + h) + (c32 & 15)) * 16;
+    zdoff[c] = GG_SZ_OFF + (q * WGN + nw * CTW * 16 + cc * 32 + c32) * 4;
+  }
+  const bool active = mw * 64 < nvalid;
+  // Waves of the second row half (sharing SIMDs with the first) fold a
+  // k-tile's products at the start of the next one, so the two waves of a
+  // SIMD are not in their VALU-only phase at the same time.
+  const bool late = mw == 1;
 
-  auto compute = [&](int buf, const BStage& b) {
-    V bw[NQ][4];
-    float s[NQ], c[NQ];
+  f32x16 acc[2][C32], t[2][C32];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
+  for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bw[q][j] = dq_b<AT>(b.w[q][j]);
-      s[q] = sz_scale<ST>(b.z[q]);
-      c[q] = Act<AT>::kMagic + (float)(b.z[q] >> 16);
+    for (int c = 0; c < C32; ++c) {
+      acc[rt][c] = f32x16{};
+      t[rt][c] = f32x16{};
+    }
+  // zero-point term over windows of 2 groups on the fp32 MFMA (32x32x2):
+  // acc -= Sx[row][g] * s[g][col] * (MAGIC + z[g][col]); lane half h holds group 2m + h
+  float za[2], zb[C32], sc[C32], scp[C32];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) za[rt] = 0.f;
+#pragma unroll
+  for (int c = 0; c < C32; ++c) {
+    zb[c] = 0.f;
+    sc[c] = 0.f;
+    scp[c] = 0.f;
+  }
+  const uint32_t mask_s = p.nib_mask;
+  uint32_t magic_v = Act<AT>::kMagic2;
+  asm volatile("v_mov_b32 %0, %0" : "+v"(magic_v));  // keep the magic in a VGPR
+
+  auto fold = [&](const float (&s)[C32]) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int c = 0; c < C32; ++c)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[rt][c][i] = fmaf(s[c], t[rt][c][i], acc[rt][c][i]);
+  };
+
+  auto compute = [&](int slot, int kt) {
+    const char* S = smem + slot * GG_STAGE;
+    const bool mine = h == (kt & 1);
+    if (late && (kt & 1)) fold(scp);  // products of the even k-tile before
+    u32x4 bq[C32][2];
+#pragma unroll
+    for (int c = 0; c < C32; ++c) {
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) bq[c][pp] = *reinterpret_cast<const u32x4*>(S + bdoff[c][pp]);
+      const uint32_t z = *reinterpret_cast<const uint32_t*>(S + zdoff[c]);
+      sc[c] = sz_scale<ST>(z);
+      const float zc = sc[c] * (Act<AT>::kMagic + (float)(z >> 16));
+      zb[c] = mine ? zc : zb[c];
     }
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      V a[4];
+    for (int rt = 0; rt < 2; ++rt) {
+      const float sxr = *reinterpret_cast<const float*>(S + GG_SX_OFF + (mw * 64 + rt * 32 + c32) * 4);
+      za[rt] = mine ? -sxr : za[rt];
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const V*>(&As[buf][(rt * 16 + r) * WG_ALD + 32 * j + 8 * kq]);
-      const f32x4 sx = *reinterpret_cast<const f32x4*>(&Sx[buf][rt * 16 + 4 * kq]);
+    for (int s = 0; s < 8; ++s) {
+      V a[2];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      for (int rt = 0; rt < 2; ++rt) a[rt] = *reinterpret_cast<const V*>(S + rt * 32 * 256 + adoff[s]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) t = mfma16(a[j], bw[q][j], t);
+      for (int c = 0; c < C32; ++c) {
+        const V b = dq_b3<AT>(bq[c][s & 1][s >> 1], mask_s, magic_v);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[rt][q][i] = fmaf(s[q], fmaf(-c[q], sx[i], t[i]), acc[rt][q][i]);
+        for (int rt = 0; rt < 2; ++rt) t[rt][c] = mfma32(a[rt], b, s == 0 ? f32x16{} : t[rt][c]);
       }
-      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!late) fold(sc);
+#pragma unroll
+    for (int c = 0; c < C32; ++c) scp[c] = sc[c];
+    if ((kt & 1) == 1 || kt + 1 == p.KT) {
+      if (late) fold(scp);  // the window's products go in before its correction
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int c = 0; c < C32; ++c)
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(za[rt], zb[c], acc[rt][c], 0, 0, 0);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) za[rt] = 0.f;
+#pragma unroll
+      for (int c = 0; c < C32; ++c) zb[c] = 0.f;
     }
   };
 
-  // pipeline: k-tile kt computes from LDS buffer kt & 1 and weight stage
-  // kt & 1 while the activations of kt+1 (issued first) and the weights of
-  // kt+1 are in flight
-  AStage as0, as1;
-  BStage bs0, bs1;
-  load_a(as0, 0);
-  load_b(bs0, 0);
-  store_a(as0, 0);
-  __syncthreads();
-  for (int kt = 0; kt < p.KT; kt += 2) {
-    if (kt + 1 < p.KT) {
-      load_a(as1, kt + 1);
-      load_b(bs1, kt + 1);
+  // ---- pipeline: ring of 3 k-tiles, loads two k-tiles ahead ----
+  const int KT = p.KT;
+  issue(0, 0);
+  if (KT > 1) issue(1, 1);
+  for (int kt0 = 0; kt0 < KT; kt0 += GG_STAGES) {
+#pragma unroll
+    for (int s = 0; s < GG_STAGES; ++s) {
+      const int kt = kt0 + s;
+      if (kt >= KT) break;
+      if (kt + 1 < KT)
+        wait_stage<7>(ncopy);
+      else
+        wait_vmcnt<0>();
+      lds_barrier();
+      if (kt + 2 < KT) issue(kt + 2, (s + 2) % GG_STAGES);
+      if (active) compute(s, kt);
     }
-    compute(0, bs0);
-    if (kt + 1 < p.KT) store_a(as1, 1);
-    __syncthreads();
-    if (kt + 1 >= p.KT) break;
-    if (kt + 2 < p.KT) {
-      load_a(as0, kt + 2);
-      load_b(bs0, kt + 2);
-    }
-    compute(1, bs1);
-    if (kt + 2 < p.KT) store_a(as0, 0);
-    __syncthreads();
   }
 
-  // epilogue: lane holds rows rt*16 + 4*kq + i of column nt*16 + r
+  // ---- epilogue: register i of tile (rt, c) = row mw*64 + 32*rt + 8*(i/4) +
+  // 4*h + i%4 of column c32 of the tile ----
+  auto row_of = [&](int rt, int i) { return mw * 64 + 32 * rt + 8 * (i >> 2) + 4 * h + (i & 3); };
+  if constexpr (EPI == EPI_SILU) {
+    float rs[32];
+    const int64_t col = nb * WGN + nw * CTW * 16 + c32;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+    for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rid = Rid[rt * 16 + 4 * kq + i];
-      if (rid < 0) continue;
-      const int64_t o = (int64_t)rid * p.ldy + nt * 16 + r;
-      if (EPI == EPI_SILU) {
-        const float g = acc[rt][0][i], u = acc[rt][NQ - 1][i];
-        store_val(p.y, o, g / (1.0f + expf(-g)) * u, p.y_dtype);
-      } else {
-        store_val(p.y, o, acc[rt][0][i], p.y_dtype);
+      for (int i = 0; i < 16; ++i) {
+        const int row = row_of(rt, i);
+        float sum = 0.f;
+        if (row < nvalid) {
+          const float g = acc[rt][0][i], u = acc[rt][1][i];
+          const float hv = g * __frcp_rn(1.0f + __expf(-g)) * u;
+          const uint32_t hb = p.y_dtype == CCQ_BF16 ? f32_to_bf16_bits(hv) : f32_to_f16_bits(hv);
+          reinterpret_cast<uint16_t*>(p.y)[(int64_t)Rid[row] * p.ldy + col] = (uint16_t)hb;
+          sum = p.y_dtype == CCQ_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+        }
+        rs[rt * 16 + i] = sum;
       }
+    if (p.sxo != nullptr) {
+      // group sums of the stored rows over this block's 128 columns: 32 per
+      // wave by butterfly, then the 4 column waves through LDS
+      const float part_sum = half_wave_row_sums(rs, c32);
+      float* part = reinterpret_cast<float*>(smem);  // [4 column waves][128 rows]
+      lds_barrier();
+      part[nw * GG_BM + row_of(c32 >> 4, c32 & 15)] = part_sum;
+      lds_barrier();
+      if (tid < nvalid)
+        p.sxo[(int64_t)Rid[tid] * p.ldsxo + nb] =
+            ((part[tid] + part[GG_BM + tid]) + part[2 * GG_BM + tid]) + part[3 * GG_BM + tid];
     }
+  } else {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = row_of(rt, i);
+        if (row >= nvalid) continue;
+        const int64_t o = (int64_t)Rid[row] * p.ldy + nb * WGN + nw * CTW * 16 + c32;
+#pragma unroll
+        for (int c = 0; c < C32; ++c) store_val(p.y, o + c * 32, acc[rt][c][i], p.y_dtype);
+      }
+  }
 }
 
-// bm: rows per schedule tile.  Gate/up (two matrices) runs 64-row kernel
-// tiles (128 would spill registers), splitting 128-row schedule tiles.
+// Sx[row][g] = sum of the 128 activations of group g of the row (float32,
+// fixed order): 16 lanes per (row, group), 8 elements per lane.
+template <typename AT>
+__global__ __launch_bounds__(256) void row_group_sums_kernel(const AT* __restrict__ x, int64_t ldx, int64_t M,
+                                                             int64_t KT, float* __restrict__ out, int64_t ldo) {
+  using V = typename Act<AT>::vec;
+  const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+  const int part = threadIdx.x & 15;
+  const bool ok = g < M * KT;
+  const int64_t row = ok ? g / KT : 0, kt = ok ? g - row * KT : 0;
+  float s = 0.f;
+  if (ok) {
+    const V v = *reinterpret_cast<const V*>(x + row * ldx + kt * 128 + part * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)v[e];
+  }
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off, 64);
+  if (ok && part == 0) out[row * ldo + kt] = s;
+}
+
+static int launch_row_group_sums(const void* x, int x_bf16, int64_t ldx, int64_t M, int64_t K, float* out,
+                                 int64_t ldo, hipStream_t st) {
+  const int64_t KT = K / 128, blocks = cdiv(M * KT * 16, 256);
+  if (x_bf16)
+    hipLaunchKernelGGL(row_group_sums_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const __bf16*)x, ldx, M, KT, out, ldo);
+  else
+    hipLaunchKernelGGL(row_group_sums_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const _Float16*)x, ldx, M, KT, out, ldo);
+  return launch_status("row group sums");
+}
+
+// Columns per workgroup of the grouped kernel for one matrix of N columns.
+static int group_cols(int EPI, int64_t N) { return EPI == EPI_SILU ? 128 : (N % 256 == 0 ? 256 : 128); }
+
 template <int EPI>
-static int launch_group_gemm(W4GP p, int x_bf16, int s_bf16, int bm, int64_t tiles, hipStream_t st) {
-  const int kbm = EPI == EPI_SILU ? WG_BM_SMALL : bm;
-  p.tile_div = bm / kbm;
-  bm = kbm;
-  const dim3 grid((unsigned)(p.N / 128), (unsigned)(tiles * p.tile_div)), block(64 * WG_WAVES);
-#define CCQ_LAUNCH_GG(AT, ST)                                                                     \
-  do {                                                                                            \
-    if constexpr (EPI != EPI_SILU) {                                                              \
-      if (bm == WG_BM_LARGE) {                                                                    \
-        hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, WG_BM_LARGE>), grid, block, 0, st, p); \
-        break;                                                                                    \
-      }                                                                                           \
-    }                                                                                             \
-    hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, WG_BM_SMALL>), grid, block, 0, st, p);  \
+static int launch_group_gemm(const W4GP& p, int x_bf16, int s_bf16, int64_t tiles, hipStream_t st) {
+  const int wgn = group_cols(EPI, p.N);
+  const dim3 grid((unsigned)(tiles * (p.N / wgn))), block(512);
+#define CCQ_LAUNCH_GG(AT, ST)                                                                  \
+  do {                                                                                         \
+    if (wgn == 256)                                                                            \
+      hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, (EPI == EPI_SILU ? 2 : 4)>), grid, \
+                         block, 0, st, p);                                                     \
+    else                                                                                       \
+      hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, 2>), grid, block, 0, st, p);      \
   } while (0)
   if (x_bf16) {
     if (s_bf16)
@@ -739,9 +941,6 @@ static int launch_group_gemm(W4GP p, int x_bf16, int s_bf16, int bm, int64_t til
   return launch_status("w4 grouped gemm");
 }
 
-// Tile rows of the grouped kernel for n assignments over E experts (each
-// tile streams its expert's weights, so a tile should hold all of them).
-static int group_tile_rows(int64_t n, int64_t E) { return n >= 32 * E ? WG_BM_LARGE : WG_BM_SMALL; }
 // The grouped kernel replaces the 16-row decode kernel once the average
 // expert receives at least 16 rows (and the shape suits it: group 128,
 // N a multiple of 128).
@@ -816,9 +1015,19 @@ extern "C" int ccq_awq_pack_sz(const int32_t* qzeros, const void* scales, int sc
   return launch_status("ccq_awq_pack_sz");
 }
 
+namespace {
+// The dense GEMM switches to the grouped kernel for prefill-sized M.
+bool gemm_grouped(int64_t M, int64_t N, int64_t G) { return M > 64 && G == 128 && N % 128 == 0; }
+}  // namespace
+
+extern "C" size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N, int64_t group_size) {
+  if (M <= 0 || K <= 0 || K % 128 || !gemm_grouped(M, N, group_size)) return 0;
+  return align256((size_t)M * (size_t)(K / 128) * 4);
+}
+
 extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, const uint32_t* sz, int scale_dtype,
                            void* y, int y_dtype, int64_t M, int64_t K, int64_t N, int64_t group_size,
-                           void* stream) {
+                           void* workspace, size_t workspace_bytes, void* stream) {
   CCQ_REQUIRE(M >= 0 && K >= 0 && N >= 0, "ccq_w4_gemm: negative shape");
   CCQ_REQUIRE(K % 128 == 0 && N % 16 == 0, "ccq_w4_gemm: need K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
               (long long)K, (long long)N);
@@ -826,22 +1035,35 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_w4_gemm: x_dtype must be f16|bf16");
   CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_w4_gemm: scale_dtype must be f16|bf16");
   CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_w4_gemm: bad y_dtype");
-  CCQ_REQUIRE(M > 64 || cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
   CCQ_REQUIRE(K <= (1 << 20) && N / 16 <= 0x7fffffff, "ccq_w4_gemm: K=%lld or N=%lld too large", (long long)K,
               (long long)N);
+  const bool grouped = gemm_grouped(M, N, group_size);
+  CCQ_REQUIRE(grouped || cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
   if (M == 0 || N == 0) return 0;
   CCQ_REQUIRE(K > 0, "ccq_w4_gemm: K == 0");
   CCQ_REQUIRE(x && w_tiled && sz && y, "ccq_w4_gemm: null pointer");
   CCQ_REQUIRE(aligned(x, 16) && aligned(w_tiled, 16) && aligned(sz, 16),
               "ccq_w4_gemm: x, w_tiled and sz must be 16-byte aligned");
-  if (M > 64 && group_size == 128 && N % 128 == 0) {
-    // prefill-sized: tiles of 64/128 rows stream the weight once per tile
-    const int bm = M >= WG_BM_LARGE ? WG_BM_LARGE : WG_BM_SMALL;
-    CCQ_REQUIRE(cdiv(M, bm) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
+  if (grouped) {
+    // prefill-sized: 128-row tiles stream the weight once per tile
+    const size_t need = ccq_w4_gemm_workspace_size(M, K, N, group_size);
+    CCQ_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 256),
+                "ccq_w4_gemm: workspace of %zu bytes (256-byte aligned) needed for M=%lld, %zu given", need,
+                (long long)M, workspace_bytes);
+    CCQ_REQUIRE(M * K * 2 < (int64_t)1 << 32, "ccq_w4_gemm: activations of %lld x %lld exceed 4 GiB",
+                (long long)M, (long long)K);
+    CCQ_REQUIRE(cdiv(M, GG_BM) * (N / 128) <= 0x7fffffff, "ccq_w4_gemm: M=%lld too large", (long long)M);
+    hipStream_t st = as_stream(stream);
+    float* sx = (float*)workspace;
+    int rc = launch_row_group_sums(x, x_dtype == CCQ_BF16, K, M, K, sx, K / 128, st);
+    if (rc) return rc;
     W4GP g = {};
     g.x = x;
     g.ldx = K;
+    g.sx = sx;
+    g.ldsx = K / 128;
     g.row_div = 1;
+    g.tiles = (int)cdiv(M, GG_BM);
     g.w0 = (const uint32_t*)w_tiled;
     g.sz0 = sz;
     g.y = y;
@@ -852,9 +1074,8 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
     g.K = (int)K;
     g.KT = (int)(K / 128);
     g.szw = (int)sz_words_per_column(K, group_size);
-    CCQ_REQUIRE(cdiv(M, bm) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
-    return launch_group_gemm<EPI_STORE>(g, x_dtype == CCQ_BF16, scale_dtype == CCQ_BF16, bm, cdiv(M, bm),
-                                        as_stream(stream));
+    g.nib_mask = 0x000F000Fu;
+    return launch_group_gemm<EPI_STORE>(g, x_dtype == CCQ_BF16, scale_dtype == CCQ_BF16, g.tiles, st);
   }
   const int64_t tiles = cdiv(M, 16);
   const SkinnyPlan pl = plan_skinny(K, N, group_size, 1, gemm_nb(M));
@@ -912,16 +1133,16 @@ int check_expert_ptrs(const ccq_w4_experts* ex, bool gate_up, const char* name) 
 // and the per-assignment down rows.
 struct MoeLayout {
   int64_t n, max_tiles;
-  int tile_m;       // rows per schedule tile: 16 (decode kernel) or 64/128 (grouped kernel)
+  int tile_m;       // rows per schedule tile: 16 (decode kernel) or 128 (grouped kernel)
   bool grouped;
-  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, total;
+  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, off_sx, off_sxh, total;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes) {
   MoeLayout L;
   L.n = T * k;
   L.grouped = use_group_gemm(L.n, ex->num_experts, ex->group_size, ex->inter, ex->hidden);
-  L.tile_m = L.grouped ? group_tile_rows(L.n, ex->num_experts) : 16;
+  L.tile_m = L.grouped ? GG_BM : 16;
   L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, L.tile_m);
   size_t o = 0;
   L.off_sorted = o;
@@ -936,6 +1157,13 @@ MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes
   o += align256((size_t)L.n * ex->inter * x_bytes);
   L.off_rows = o;
   o += align256((size_t)L.n * ex->hidden * 4);
+  L.off_sx = o;   // grouped: group sums of x rows and of the intermediate rows
+  L.off_sxh = o;
+  if (L.grouped) {
+    o += align256((size_t)T * (ex->hidden / 128) * 4);
+    L.off_sxh = o;
+    o += align256((size_t)L.n * (ex->inter / 128) * 4);
+  }
   L.total = o;
   return L;
 }
@@ -1074,9 +1302,17 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
   if (rc) return rc;
   if (L.grouped) {
     const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
+    CCQ_REQUIRE(T * H * 2 < (int64_t)1 << 32 && L.n * I * 2 < (int64_t)1 << 32,
+                "ccq_moe_w4_ffn: activations exceed 4 GiB");
+    float* sx = (float*)(ws + L.off_sx);
+    float* sxh = (float*)(ws + L.off_sxh);
+    rc = launch_row_group_sums(x, x_dtype == CCQ_BF16, H, T, H, sx, H / 128, st);
+    if (rc) return rc;
     W4GP g = {};
     g.x = x;
     g.ldx = H;
+    g.sx = sx;
+    g.ldsx = H / 128;
     g.rows = sorted;
     g.row_div = (int)k;
     g.tile_expert = tile_expert;
@@ -1091,14 +1327,19 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
     g.y = inter;
     g.ldy = I;
     g.y_dtype = x_dtype;
+    g.sxo = sxh;
+    g.ldsxo = I / 128;
     g.N = (int)I;
     g.K = (int)H;
     g.KT = (int)(H / 128);
-    rc = launch_group_gemm<EPI_SILU>(g, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.tile_m, L.max_tiles, st);
+    g.nib_mask = 0x000F000Fu;
+    rc = launch_group_gemm<EPI_SILU>(g, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.max_tiles, st);
     if (rc) return rc;
     W4GP d = {};
     d.x = inter;
     d.ldx = I;
+    d.sx = sxh;
+    d.ldsx = I / 128;
     d.rows = sorted;
     d.row_div = 1;
     d.tile_expert = tile_expert;
@@ -1114,7 +1355,8 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
     d.N = (int)H;
     d.K = (int)I;
     d.KT = (int)(I / 128);
-    rc = launch_group_gemm<EPI_ROWS>(d, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.tile_m, L.max_tiles, st);
+    d.nib_mask = 0x000F000Fu;
+    rc = launch_group_gemm<EPI_ROWS>(d, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.max_tiles, st);
     if (rc) return rc;
   } else {
     rc = run_gate_up(x, x_dtype, k, sorted, tile_expert, meta, L.max_tiles, inter, ex, st);

@@ -116,17 +116,25 @@ int64_t ccq_awq_sz_words(int64_t K, int64_t group_size);
 int ccq_awq_pack_sz(const int32_t* qzeros, const void* scales, int scale_dtype,
                     uint32_t* sz, int64_t K, int64_t N, int64_t group_size, void* stream);
 
+/* Workspace bytes ccq_w4_gemm needs for these sizes: 0 for the decode
+ * kernel (M <= 64, or group_size != 128, or N % 128 != 0), else the
+ * per-row group sums of x, M * K/128 floats (256-byte rounded). */
+size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N, int64_t group_size);
+
 /* y [M, N] = x [M, K] @ dequant(W) with fp32 accumulation.
  * x_dtype CCQ_F16 | CCQ_BF16; scale_dtype (of the scales packed in sz)
  * CCQ_F16 | CCQ_BF16; y_dtype CCQ_F16 | CCQ_BF16 | CCQ_F32.  w_tiled from
  * ccq_awq_repack, sz from ccq_awq_pack_sz.  group_size in {32, 64, 128}.
- * x, w_tiled and sz must be 16-byte aligned.  M <= 16 rows per weight pass
- * (decode); larger M re-reads the weight once per 16 rows.  No workspace.
+ * x, w_tiled and sz must be 16-byte aligned.  M <= 64: decode kernel (one
+ * weight pass per 16 rows, no workspace); larger M with group 128 and
+ * N % 128 == 0: the grouped MFMA kernel over 128-row tiles, which needs
+ * ccq_w4_gemm_workspace_size bytes (256-byte aligned) of workspace.
  * Replaces WeightOnlyMethod.apply (quant/weight_only.py:37-54) for AWQ. */
 int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled,
                 const uint32_t* sz, int scale_dtype,
                 void* y, int y_dtype, int64_t M, int64_t K, int64_t N,
-                int64_t group_size, void* stream);
+                int64_t group_size, void* workspace, size_t workspace_bytes,
+                void* stream);
 
 /* ------------------------------------------------------------------------
  * Routing and token grouping

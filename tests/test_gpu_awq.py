@@ -90,6 +90,14 @@ def test_gemm_prefill_grouped_kernel(gpu, M, xdt):
     assert _gemm_case(gpu, M, 768, 384, 128, xdt, xdt, seed=M + 1) <= TOL
 
 
+@pytest.mark.parametrize("M,K,N", [(200, 384, 512), (130, 256, 256), (300, 640, 384), (97, 1024, 768)])
+def test_gemm_prefill_grouped_shapes(gpu, M, K, N):
+    """Grouped kernel with 256-column blocks (N % 256 == 0) and 128-column
+    blocks, odd and even numbers of k-tiles."""
+    assert _gemm_case(gpu, M, K, N, 128, torch.bfloat16, torch.float32, seed=M + K) <= TIGHT
+    assert _gemm_case(gpu, M, K, N, 128, torch.float16, torch.float32, seed=M + N) <= TIGHT
+
+
 @pytest.mark.parametrize("G", [32, 64])
 def test_gemm_parity_groups(gpu, G):
     assert _gemm_case(gpu, 3, 384, 160, G, torch.float16, torch.float32, seed=G) <= TIGHT

@@ -55,18 +55,24 @@ def test_w4_gemm_rejects_bad_shapes(lib):
     from ccut._lib import CCQ_BF16, CCQ_EINVAL, CCQ_F16, last_error
 
     p = ctypes.c_void_p(16)  # never dereferenced: validation comes first
-    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 1, 100, 64, 128, None)
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 1, 100, 64, 128, None, 0, None)
     assert rc == CCQ_EINVAL and "K % 128" in last_error()
-    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 96, None)
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 96, None, 0, None)
     assert rc == CCQ_EINVAL and "group_size" in last_error()
-    rc = lib.ccq_w4_gemm(p, 7, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
+    rc = lib.ccq_w4_gemm(p, 7, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0, None)
     assert rc == CCQ_EINVAL and "x_dtype" in last_error()
-    rc = lib.ccq_w4_gemm(None, CCQ_BF16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
+    rc = lib.ccq_w4_gemm(None, CCQ_BF16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0, None)
     assert rc == CCQ_EINVAL and "null" in last_error()
-    rc = lib.ccq_w4_gemm(ctypes.c_void_p(18), CCQ_BF16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None)
+    rc = lib.ccq_w4_gemm(ctypes.c_void_p(18), CCQ_BF16, p, p, CCQ_F16, p, CCQ_F16, 1, 256, 64, 128, None, 0, None)
     assert rc == CCQ_EINVAL and "aligned" in last_error()
     # M == 0 is an empty product: success without a launch
-    assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None) == 0
+    assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None, 0, None) == 0
+    # prefill-sized M needs the group-sum workspace
+    assert lib.ccq_w4_gemm_workspace_size(64, 256, 128, 128) == 0
+    assert lib.ccq_w4_gemm_workspace_size(65, 256, 128, 128) == 768
+    assert lib.ccq_w4_gemm_workspace_size(200, 256, 128, 64) == 0
+    rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 65, 256, 128, 128, None, 0, None)
+    assert rc == CCQ_EINVAL and "workspace" in last_error()
 
 
 def test_routing_rejects_bad_args(lib):
