@@ -121,11 +121,21 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // completion is counted by vmcnt.  Issued as inline assembly so that the
 // compiler adds no waits of its own for the LDS it writes: the pipelines
 // below order these copies with explicit wait_vmcnt + barrier.
+// The compiler's hazard recognizer does not look into inline assembly, so
+// the s_nop 4 provides the wait states the load needs after the instructions
+// the compiler places right before it: a VALU write of the base SGPRs
+// (v_readfirstlane, 5 wait states before a VMEM read of them) and the SALU
+// write of M0 (1 wait state before an LDS DMA).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t u = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u), hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }
 
 // Wait until at most N vector-memory operations of this wave are in flight.

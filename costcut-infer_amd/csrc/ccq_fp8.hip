@@ -27,8 +27,8 @@ namespace ccq {
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
                  int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st);
-int launch_combine(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y, int y_dtype,
-                   int64_t T, int64_t k, int64_t H, hipStream_t st);
+int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
+                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st);
 
 constexpr float kFp8Max = 448.0f;
 constexpr float kAmaxFloor = 1e-12f;
@@ -664,5 +664,5 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   // down runs 64-row tiles (two resident workgroups per CU; see DEPTH)
   rc = launch_fp8_gemm<F8_ROWS>(d, L.bm, F8_BM_SMALL, L.max_tiles, st);
   if (rc) return rc;
-  return launch_combine(rows, weights, ids, ex->num_experts, y, y_dtype, T, k, H, st);
+  return launch_combine(rows, CCQ_F32, weights, ids, ex->num_experts, y, y_dtype, T, k, H, st);
 }

@@ -320,13 +320,14 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
 
 // y[t, h] = sum_s w[t, s] * rows[t*k + s, h], slot order, float32.  Slots
 // whose id is outside [0, E) (dropped by the schedule) contribute nothing.
-// Four columns per thread (16-byte loads) when H % 4 == 0.
-template <int YT, bool VEC>
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ rows,
+// rows are float32 (RT = CCQ_F32) or bf16 (RT = CCQ_BF16); with VEC each
+// thread takes 16 bytes of a row (4 or 8 columns).
+template <int YT, int RT, bool VEC>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ rows,
                                                           const float* __restrict__ wts,
                                                           const int64_t* __restrict__ ids, int64_t E,
                                                           void* __restrict__ y, int64_t T, int k, int64_t H) {
-  constexpr int CW = VEC ? 4 : 1;
+  constexpr int CW = VEC ? (RT == CCQ_F32 ? 4 : 8) : 1;
   const int64_t t = blockIdx.y;
   const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * CW;
   if (h >= H) return;
@@ -340,13 +341,28 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
       if (e < 0 || e >= E) continue;
     }
     const float wv = wts[a];
-    if (VEC) {
-      const f32x4 r = *reinterpret_cast<const f32x4*>(rows + a * H + h);
+    float r[CW];
+    if constexpr (RT == CCQ_F32) {
+      const float* rp = reinterpret_cast<const float*>(rows) + a * H + h;
+      if constexpr (VEC) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(rp);
 #pragma unroll
-      for (int c = 0; c < CW; ++c) acc[c] = fmaf(wv, r[c], acc[c]);
+        for (int c = 0; c < CW; ++c) r[c] = v[c];
+      } else {
+        r[0] = rp[0];
+      }
     } else {
-      acc[0] = fmaf(wv, rows[a * H + h], acc[0]);
+      const uint16_t* rp = reinterpret_cast<const uint16_t*>(rows) + a * H + h;
+      if constexpr (VEC) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(rp);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) r[c] = bf16_bits_to_f32((v[c >> 1] >> (16 * (c & 1))) & 0xFFFFu);
+      } else {
+        r[0] = bf16_bits_to_f32(rp[0]);
+      }
     }
+#pragma unroll
+    for (int c = 0; c < CW; ++c) acc[c] = fmaf(wv, r[c], acc[c]);
   }
 #pragma unroll
   for (int c = 0; c < CW; ++c) {
@@ -360,28 +376,36 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   }
 }
 
-template <bool VEC>
-static void launch_combine_v(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y,
+template <int RT, bool VEC>
+static void launch_combine_v(const void* rows, const float* wts, const int64_t* ids, int64_t E, void* y,
                              int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st) {
-  const int64_t cols = VEC ? H / 4 : H;
+  const int64_t cols = VEC ? H / (RT == CCQ_F32 ? 4 : 8) : H;
   dim3 grid((unsigned)cdiv(cols, 256), (unsigned)T);
   if (y_dtype == CCQ_F32)
-    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F32, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F32, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
                        (int)k, H);
   else if (y_dtype == CCQ_BF16)
-    hipLaunchKernelGGL((moe_combine_kernel<CCQ_BF16, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+    hipLaunchKernelGGL((moe_combine_kernel<CCQ_BF16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
                        (int)k, H);
   else
-    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F16, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
                        (int)k, H);
 }
 
-int launch_combine(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y, int y_dtype,
-                   int64_t T, int64_t k, int64_t H, hipStream_t st) {
-  if (H % 4 == 0 && aligned(rows, 16))
-    launch_combine_v<true>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
-  else
-    launch_combine_v<false>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+// rows_dtype CCQ_F32 or CCQ_BF16.
+int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
+                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st) {
+  if (rows_dtype == CCQ_BF16) {
+    if (H % 8 == 0 && aligned(rows, 16))
+      launch_combine_v<CCQ_BF16, true>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+    else
+      launch_combine_v<CCQ_BF16, false>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+  } else {
+    if (H % 4 == 0 && aligned(rows, 16))
+      launch_combine_v<CCQ_F32, true>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+    else
+      launch_combine_v<CCQ_F32, false>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+  }
   return launch_status("moe_combine");
 }
 
@@ -446,5 +470,5 @@ extern "C" int ccq_moe_combine(const float* rows, const float* weights, void* y,
   CCQ_REQUIRE(T <= 65535, "ccq_moe_combine: T=%lld > 65535", (long long)T);
   if (T == 0 || H == 0) return 0;
   CCQ_REQUIRE(rows && weights && y, "ccq_moe_combine: null pointer");
-  return launch_combine(rows, weights, nullptr, 0, y, y_dtype, T, k, H, as_stream(stream));
+  return launch_combine(rows, CCQ_F32, weights, nullptr, 0, y, y_dtype, T, k, H, as_stream(stream));
 }

@@ -35,8 +35,8 @@ namespace ccq {
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
                  int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st);
-int launch_combine(const float* rows, const float* wts, const int64_t* ids, int64_t E, void* y, int y_dtype,
-                   int64_t T, int64_t k, int64_t H, hipStream_t st);
+int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
+                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st);
 
 // shift of column 8c + j inside an AWQ word: 4 * AWQ_REVERSE_ORDER[j]
 __device__ __forceinline__ int awq_shift(int j) { return 4 * ((j >> 1) + 4 * (j & 1)); }
@@ -588,7 +588,8 @@ constexpr int GG_SZ_OFF = GG_B_OFF + GG_B_BYTES;
 constexpr int GG_SX_OFF = GG_SZ_OFF + GG_SZ_BYTES;
 constexpr int GG_STAGE = GG_SX_OFF + GG_SX_BYTES;
 constexpr int GG_STAGES = 3;
-static_assert(GG_STAGES * GG_STAGE + GG_BM * 4 <= 160 * 1024, "LDS budget of one workgroup");
+constexpr int GG_RID = GG_BM + 64;  // row ids of one item + copies of its expert id
+static_assert(GG_STAGES * GG_STAGE + 3 * GG_RID * 4 + 4 * GG_BM * 4 <= 160 * 1024, "LDS budget of one workgroup");
 
 template <int N>
 __device__ __forceinline__ void wait_stage(int n) {
@@ -625,85 +626,112 @@ template <typename AT, typename ST, int EPI, int CTW>
 __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
   using V = typename Act<AT>::vec;
   constexpr int NQ = EPI == EPI_SILU ? 2 : 1;
-  constexpr int WGN = 64 * CTW;      // columns per matrix per workgroup
+  constexpr int WGN = 64 * CTW;      // columns per matrix per item
   constexpr int TPM = WGN / 16;      // 16-column weight tiles per matrix per k-tile
   constexpr int NBT = NQ * TPM;      // weight tiles per k-tile
   constexpr int BPW = NBT / 8;       // weight tiles each wave copies
   constexpr int NSZ = NQ * WGN;      // scale/zero words per k-tile
   constexpr int C32 = CTW * NQ / 2;  // 32-column MFMA tiles per wave
   constexpr int CQ = C32 / NQ;       // ... per matrix
-  static_assert(NBT % 8 == 0 && NBT <= 16 && NSZ <= 256 && NSZ % 64 == 0 && C32 >= 1, "tile shape");
+  static_assert(NBT % 8 == 0 && NBT <= 16 && NSZ <= 256 && NSZ % 64 == 0 && C32 >= 1 && BPW <= 2, "tile shape");
   __shared__ __align__(16) char smem[GG_STAGES * GG_STAGE];
-  __shared__ int Rid[GG_BM];
+  __shared__ __align__(16) int Rid[3][GG_RID];  // row ids (+ expert id copies) of items j, j+1, j+2
+  __shared__ __align__(16) float part[4 * GG_BM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int mw = wave >> 2, nw = wave & 3;
   const int nblk = p.N / WGN;
-  const int items = (p.meta != nullptr ? p.meta[0] : p.tiles) * nblk;
-  if ((int)blockIdx.x >= items) return;
-  const int item = xcd_remap(blockIdx.x, items);
-  const int tile = item / nblk, nb = item - tile * nblk;
-  const int ex = p.tile_expert != nullptr ? p.tile_expert[tile] : 0;
-  if (tid < GG_BM) {
-    int rid;
-    if (p.rows != nullptr) {
-      rid = p.rows[tile * GG_BM + tid];
-    } else {
-      rid = tile * GG_BM + tid;
-      if (rid >= p.M) rid = -1;
-    }
-    Rid[tid] = rid;
-  }
-  const int nvalid = __syncthreads_count(tid < GG_BM && Rid[tid] >= 0);
-  if (nvalid == 0) return;
-  const int rid0 = Rid[0];
+  const int ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
+  // Static schedule: workgroup b runs on XCD b % 8 (nx workgroups per XCD).
+  // Row tiles are dealt to the XCDs round-robin (tile t to XCD t % 8), so an
+  // expert with many tiles is spread over all of them, and all column blocks
+  // of a tile stay on one XCD, sharing its activations in that L2.  Within
+  // an XCD, workgroup wx takes every nx-th of the XCD's items (tile-major).
+  const int xcd = blockIdx.x & 7, wx = blockIdx.x >> 3;
+  const int nx = ((int)gridDim.x - xcd + 7) >> 3;
+  const int items_x = (ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0) * nblk;
+  if (wx >= items_x) return;
+  const int nmine = (items_x - wx + nx - 1) / nx;
+  const int KT = p.KT;
+  const int total = nmine * KT;  // k-steps of this workgroup
 
-  // ---- copy plan of this wave (per k-tile) ----
-  // activations: rows 16*wave + 4*i + (lane >> 4), i = 0..3; the lane takes
-  // piece (lane & 15) ^ (row & 15), which lands at position lane & 15
-  uint32_t aoff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * wave + 4 * i + (lane >> 4);
-    const int rid = Rid[row] >= 0 ? Rid[row] : rid0;
-    const int piece = (lane & 15) ^ (4 * i + (lane >> 4));
-    aoff[i] = (uint32_t)((int64_t)(rid / p.row_div) * p.ldx * 2 + piece * 16);
+  // ---- row ids: rows of item j go to Rid[j % 3], copied (DMA) at the first
+  // k-step of item j - 2; Rid[.][GG_BM..] holds the item's expert ----
+  auto tile_of = [&](int j) { return xcd + 8 * ((wx + j * nx) / nblk); };
+  auto fetch_rows = [&](int j) {  // waves 5..7
+    if (j >= nmine) return;
+    const int tile = tile_of(j);
+    const uint32_t dst = lds_addr(&Rid[j % 3][0]);
+    if (wave >= 6) dma4(p.rows + (int64_t)tile * GG_BM, (wave - 6) * 256 + lane * 4, dst + (wave - 6) * 256);
+    if (wave == 5 && p.tile_expert != nullptr) dma4(p.tile_expert + tile, 0u, dst + GG_BM * 4);
+  };
+  // prologue: items 0 and 1 with plain loads
+  for (int j = 0; j < 2 && j < nmine; ++j) {
+    const int tile = tile_of(j);
+    if (tid < GG_BM) Rid[j][tid] = p.rows[(int64_t)tile * GG_BM + tid];
+    if (tid == GG_BM) Rid[j][GG_BM] = p.tile_expert != nullptr ? p.tile_expert[tile] : 0;
   }
-  const char* bsrc[BPW];
-#pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-    const int b = wave * BPW + j, q = b / TPM, nt = nb * TPM + (b - q * TPM);
-    bsrc[j] = reinterpret_cast<const char*>((q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + (int64_t)nt * p.KT * 256);
-  }
+  __syncthreads();
+
+  // ---- per-item copy plan of this wave ----
+  struct Plan {
+    uint32_t aoff[4];
+    const char* bsrc[BPW];
+    const char* zsrc;
+    uint32_t zoff, soff;
+    int nvalid, nb;
+  };
   const bool has_sz = wave < NSZ / 64;
-  uint32_t zoff = 0;
-  const char* zsrc = nullptr;
-  if (has_sz) {
-    const int q = (64 * wave) / WGN, col = nb * WGN + (64 * wave - q * WGN) + lane;
-    zoff = (uint32_t)((int64_t)col * p.szw * 4);
-    zsrc = reinterpret_cast<const char*>((q == 0 ? p.sz0 : p.sz1) + (int64_t)ex * p.sz_es);
-  }
   const bool has_sx = wave == 4 || wave == 5;
-  uint32_t soff = 0;
-  if (has_sx) {
-    const int row = 64 * (wave - 4) + lane;
-    const int rid = Rid[row] >= 0 ? Rid[row] : rid0;
-    soff = (uint32_t)((int64_t)(rid / p.row_div) * p.ldsx * 4);
-  }
   const int ncopy = 4 + BPW + (has_sz ? 1 : 0) + (has_sx ? 1 : 0);
+  auto make_plan = [&](int j, Plan& P) {
+    const int li = wx + j * nx;
+    P.nb = li % nblk;
+    const int* R = Rid[j % 3];
+    const int ex = p.tile_expert != nullptr ? __builtin_amdgcn_readfirstlane(R[GG_BM]) : 0;
+    // valid rows form a prefix of the tile
+    P.nvalid = (int)(__popcll(__ballot(R[lane] >= 0)) + __popcll(__ballot(R[64 + lane] >= 0)));
+    const int rid0 = R[0];
+    // activations: rows 16*wave + 4*i + (lane >> 4); the lane takes piece
+    // (lane & 15) ^ (row & 15), which lands at position lane & 15
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * wave + 4 * i + (lane >> 4);
+      const int rid = R[row] >= 0 ? R[row] : rid0;
+      const int piece = (lane & 15) ^ (4 * i + (lane >> 4));
+      P.aoff[i] = (uint32_t)((int64_t)(rid / p.row_div) * p.ldx * 2 + piece * 16);
+    }
+#pragma unroll
+    for (int b2 = 0; b2 < BPW; ++b2) {
+      const int b = wave * BPW + b2, q = b / TPM, nt = P.nb * TPM + (b - q * TPM);
+      P.bsrc[b2] = reinterpret_cast<const char*>((q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + (int64_t)nt * KT * 256);
+    }
+    P.zsrc = nullptr;
+    P.zoff = 0;
+    if (has_sz) {
+      const int q = (64 * wave) / WGN, col = P.nb * WGN + (64 * wave - q * WGN) + lane;
+      P.zoff = (uint32_t)((int64_t)col * p.szw * 4);
+      P.zsrc = reinterpret_cast<const char*>((q == 0 ? p.sz0 : p.sz1) + (int64_t)ex * p.sz_es);
+    }
+    P.soff = 0;
+    if (has_sx) {
+      const int row = 64 * (wave - 4) + lane;
+      const int rid = R[row] >= 0 ? R[row] : rid0;
+      P.soff = (uint32_t)((int64_t)(rid / p.row_div) * p.ldsx * 4);
+    }
+  };
   const uint32_t lds0 = lds_addr(smem);
-
-  auto issue = [&](int kt, int slot) {
+  auto issue = [&](const Plan& P, int kt, int slot) {
     const uint32_t st = lds0 + slot * GG_STAGE;
     const char* xb = reinterpret_cast<const char*>(p.x) + (int64_t)kt * 256;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(xb, aoff[i], st + (16 * wave + 4 * i) * 256);
+    for (int i = 0; i < 4; ++i) dma16(xb, P.aoff[i], st + (16 * wave + 4 * i) * 256);
 #pragma unroll
-    for (int j = 0; j < BPW; ++j)
-      dma16(bsrc[j] + (int64_t)kt * 1024, lane * 16, st + GG_B_OFF + (wave * BPW + j) * 1024);
-    if (has_sz) dma4(zsrc + kt * 4, zoff, st + GG_SZ_OFF + wave * 256);
-    if (has_sx) dma4(p.sx + kt, soff, st + GG_SX_OFF + (wave - 4) * 256);
+    for (int b2 = 0; b2 < BPW; ++b2)
+      dma16(P.bsrc[b2] + (int64_t)kt * 1024, lane * 16, st + GG_B_OFF + (wave * BPW + b2) * 1024);
+    if (has_sz) dma4(P.zsrc + kt * 4, P.zoff, st + GG_SZ_OFF + wave * 256);
+    if (has_sx) dma4(p.sx + kt, P.soff, st + GG_SX_OFF + (wave - 4) * 256);
   };
 
   // ---- MFMA side: v_mfma_f32_32x32x16; the wave owns rows mw*64 + 32*rt
@@ -726,7 +754,6 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
     for (int pp = 0; pp < 2; ++pp) bdoff[c][pp] = GG_B_OFF + t16 * 1024 + (16 * (2 * pp + h) + (c32 & 15)) * 16;
     zdoff[c] = GG_SZ_OFF + (q * WGN + nw * CTW * 16 + cc * 32 + c32) * 4;
   }
-  const bool active = mw * 64 < nvalid;
   // Waves of the second row half (sharing SIMDs with the first) fold a
   // k-tile's products at the start of the next one, so the two waves of a
   // SIMD are not in their VALU-only phase at the same time.
@@ -753,7 +780,7 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
   }
   const uint32_t mask_s = p.nib_mask;
   uint32_t magic_v = Act<AT>::kMagic2;
-  asm volatile("v_mov_b32 %0, %0" : "+v"(magic_v));  // keep the magic in a VGPR
+  asm volatile("v_mov_b32 %0, %0" : "+v"(magic_v));  // keep the magic in a VGPR (far from any MFMA)
 
   auto fold = [&](const float (&s)[C32]) {
 #pragma unroll
@@ -798,7 +825,7 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
     if (!late) fold(sc);
 #pragma unroll
     for (int c = 0; c < C32; ++c) scp[c] = sc[c];
-    if ((kt & 1) == 1 || kt + 1 == p.KT) {
+    if ((kt & 1) == 1 || kt + 1 == KT) {
       if (late) fold(scp);  // the window's products go in before its correction
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
@@ -812,79 +839,105 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
     }
   };
 
-  // ---- pipeline: ring of 3 k-tiles, loads two k-tiles ahead ----
-  const int KT = p.KT;
-  issue(0, 0);
-  if (KT > 1) issue(1, 1);
-  for (int kt0 = 0; kt0 < KT; kt0 += GG_STAGES) {
-#pragma unroll
-    for (int s = 0; s < GG_STAGES; ++s) {
-      const int kt = kt0 + s;
-      if (kt >= KT) break;
-      if (kt + 1 < KT)
-        wait_stage<7>(ncopy);
-      else
-        wait_vmcnt<0>();
-      lds_barrier();
-      if (kt + 2 < KT) issue(kt + 2, (s + 2) % GG_STAGES);
-      if (active) compute(s, kt);
-    }
-  }
-
-  // ---- epilogue: register i of tile (rt, c) = row mw*64 + 32*rt + 8*(i/4) +
-  // 4*h + i%4 of column c32 of the tile ----
+  // ---- epilogue of item j: register i of tile (rt, c) = row mw*64 + 32*rt +
+  // 8*(i/4) + 4*h + i%4 of column c32 of the tile ----
   auto row_of = [&](int rt, int i) { return mw * 64 + 32 * rt + 8 * (i >> 2) + 4 * h + (i & 3); };
-  if constexpr (EPI == EPI_SILU) {
-    float rs[32];
-    const int64_t col = nb * WGN + nw * CTW * 16 + c32;
+  auto epilogue = [&](int j, const Plan& P) {
+    const int* R = Rid[j % 3];
+    if constexpr (EPI == EPI_SILU) {
+      float rs[32];
+      const int64_t col = P.nb * WGN + nw * CTW * 16 + c32;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = row_of(rt, i);
-        float sum = 0.f;
-        if (row < nvalid) {
-          const float g = acc[rt][0][i], u = acc[rt][1][i];
-          const float hv = g * __frcp_rn(1.0f + __expf(-g)) * u;
-          const uint32_t hb = p.y_dtype == CCQ_BF16 ? f32_to_bf16_bits(hv) : f32_to_f16_bits(hv);
-          reinterpret_cast<uint16_t*>(p.y)[(int64_t)Rid[row] * p.ldy + col] = (uint16_t)hb;
-          sum = p.y_dtype == CCQ_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+        for (int i = 0; i < 16; ++i) {
+          const int row = row_of(rt, i);
+          float sum = 0.f;
+          if (row < P.nvalid) {
+            const float g = acc[rt][0][i], u = acc[rt][1][i];
+            const float hv = g * __frcp_rn(1.0f + __expf(-g)) * u;
+            const uint32_t hb = p.y_dtype == CCQ_BF16 ? f32_to_bf16_bits(hv) : f32_to_f16_bits(hv);
+            reinterpret_cast<uint16_t*>(p.y)[(int64_t)R[row] * p.ldy + col] = (uint16_t)hb;
+            sum = p.y_dtype == CCQ_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+          }
+          rs[rt * 16 + i] = sum;
         }
-        rs[rt * 16 + i] = sum;
+      if (p.sxo != nullptr) {
+        // group sums of the stored rows over this item's 128 columns: 32 per
+        // wave by butterfly, then the 4 column waves through LDS
+        const float part_sum = half_wave_row_sums(rs, c32);
+        part[nw * GG_BM + row_of(c32 >> 4, c32 & 15)] = part_sum;
+        lds_barrier();
+        if (tid < P.nvalid)
+          p.sxo[(int64_t)R[tid] * p.ldsxo + P.nb] =
+              ((part[tid] + part[GG_BM + tid]) + part[2 * GG_BM + tid]) + part[3 * GG_BM + tid];
       }
-    if (p.sxo != nullptr) {
-      // group sums of the stored rows over this block's 128 columns: 32 per
-      // wave by butterfly, then the 4 column waves through LDS
-      const float part_sum = half_wave_row_sums(rs, c32);
-      float* part = reinterpret_cast<float*>(smem);  // [4 column waves][128 rows]
-      lds_barrier();
-      part[nw * GG_BM + row_of(c32 >> 4, c32 & 15)] = part_sum;
-      lds_barrier();
-      if (tid < nvalid)
-        p.sxo[(int64_t)Rid[tid] * p.ldsxo + nb] =
-            ((part[tid] + part[GG_BM + tid]) + part[2 * GG_BM + tid]) + part[3 * GG_BM + tid];
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int row = row_of(rt, i);
+          if (row >= P.nvalid) continue;
+          const int64_t o = (int64_t)R[row] * p.ldy + P.nb * WGN + nw * CTW * 16 + c32;
+#pragma unroll
+          for (int c = 0; c < C32; ++c) store_val(p.y, o + c * 32, acc[rt][c][i], p.y_dtype);
+        }
     }
-  } else {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = row_of(rt, i);
-        if (row >= nvalid) continue;
-        const int64_t o = (int64_t)Rid[row] * p.ldy + nb * WGN + nw * CTW * 16 + c32;
-#pragma unroll
-        for (int c = 0; c < C32; ++c) store_val(p.y, o + c * 32, acc[rt][c][i], p.y_dtype);
-      }
+      for (int c = 0; c < C32; ++c) acc[rt][c] = f32x16{};
+  };
+
+  // ---- pipeline over all k-steps of all items of this workgroup: a ring of
+  // 3 k-tiles, loads two k-steps ahead (across item boundaries) ----
+  Plan cur, nxt;
+  make_plan(0, cur);
+  if (nmine > 1) make_plan(1, nxt);
+  issue(cur, 0, 0);
+  if (total > 1) issue(KT > 1 ? cur : nxt, KT > 1 ? 1 : 0, 1);
+  // the ring slot is a run-time index: the ring lives in LDS only
+  int j = 0, kt = 0, slot = 0;
+  for (int g = 0; g < total; ++g) {
+    if (g + 1 < total)
+      wait_stage<7>(ncopy);
+    else
+      wait_vmcnt<0>();
+    lds_barrier();
+    if (kt == 0 && j + 2 < nmine) fetch_rows(j + 2);
+    if (kt == KT - 2 && j + 1 < nmine) make_plan(j + 1, nxt);
+    const bool last = kt + 1 == KT;
+    const int slot2 = slot == 0 ? 2 : slot - 1;  // (slot + 2) % 3
+    if (!last && g + 2 < total) issue(kt + 2 < KT ? cur : nxt, kt + 2 < KT ? kt + 2 : kt + 2 - KT, slot2);
+    if (mw * 64 < cur.nvalid) compute(slot, kt);
+    if (last) {
+      epilogue(j, cur);
+      // the next item's second k-step is issued after the stores, so the
+      // wait of the next k-step does not hold it back
+      if (g + 2 < total) issue(nxt, 1, slot2);
+      cur = nxt;
+      ++j;
+      kt = 0;
+    } else {
+      ++kt;
+    }
+    slot = slot == 2 ? 0 : slot + 1;
   }
 }
 
 // Sx[row][g] = sum of the 128 activations of group g of the row (float32,
-// fixed order): 16 lanes per (row, group), 8 elements per lane.
+// fixed order): 16 lanes per (row, group), 8 elements per lane.  With
+// rows_out, also the row ids of a dense schedule: rows_out[i] = i < M ? i : -1
+// for i < nrows_out.
 template <typename AT>
 __global__ __launch_bounds__(256) void row_group_sums_kernel(const AT* __restrict__ x, int64_t ldx, int64_t M,
-                                                             int64_t KT, float* __restrict__ out, int64_t ldo) {
+                                                             int64_t KT, float* __restrict__ out, int64_t ldo,
+                                                             int32_t* __restrict__ rows_out, int64_t nrows_out) {
   using V = typename Act<AT>::vec;
-  const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+  const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (rows_out != nullptr && gt < nrows_out) rows_out[gt] = gt < M ? (int32_t)gt : -1;
+  const int64_t g = gt >> 4;
   const int part = threadIdx.x & 15;
   const bool ok = g < M * KT;
   const int64_t row = ok ? g / KT : 0, kt = ok ? g - row * KT : 0;
@@ -900,24 +953,41 @@ __global__ __launch_bounds__(256) void row_group_sums_kernel(const AT* __restric
 }
 
 static int launch_row_group_sums(const void* x, int x_bf16, int64_t ldx, int64_t M, int64_t K, float* out,
-                                 int64_t ldo, hipStream_t st) {
-  const int64_t KT = K / 128, blocks = cdiv(M * KT * 16, 256);
+                                 int64_t ldo, hipStream_t st, int32_t* rows_out = nullptr, int64_t nrows_out = 0) {
+  const int64_t KT = K / 128, threads = M * KT * 16 > nrows_out ? M * KT * 16 : nrows_out;
+  const int64_t blocks = cdiv(threads, 256);
   if (x_bf16)
     hipLaunchKernelGGL(row_group_sums_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const __bf16*)x, ldx, M, KT, out, ldo);
+                       (const __bf16*)x, ldx, M, KT, out, ldo, rows_out, nrows_out);
   else
     hipLaunchKernelGGL(row_group_sums_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const _Float16*)x, ldx, M, KT, out, ldo);
+                       (const _Float16*)x, ldx, M, KT, out, ldo, rows_out, nrows_out);
   return launch_status("row group sums");
 }
 
 // Columns per workgroup of the grouped kernel for one matrix of N columns.
 static int group_cols(int EPI, int64_t N) { return EPI == EPI_SILU ? 128 : (N % 256 == 0 ? 256 : 128); }
 
+// Compute units of the current device (one persistent workgroup each).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n < 8 ? 8 : n;  // the grouped kernel's schedule needs a workgroup on each of the 8 XCDs
+  }
+  return cus[dev];
+}
+
+// tiles = schedule tiles the grid is sized for (the kernel reads the actual
+// number from meta); one persistent workgroup per compute unit at most.
 template <int EPI>
 static int launch_group_gemm(const W4GP& p, int x_bf16, int s_bf16, int64_t tiles, hipStream_t st) {
   const int wgn = group_cols(EPI, p.N);
-  const dim3 grid((unsigned)(tiles * (p.N / wgn))), block(512);
+  const int64_t items = tiles * (p.N / wgn), cus = device_cus();
+  const dim3 grid((unsigned)(items < cus ? items : cus)), block(512);
 #define CCQ_LAUNCH_GG(AT, ST)                                                                  \
   do {                                                                                         \
     if (wgn == 256)                                                                            \
@@ -943,9 +1013,10 @@ static int launch_group_gemm(const W4GP& p, int x_bf16, int s_bf16, int64_t tile
 
 // The grouped kernel replaces the 16-row decode kernel once the average
 // expert receives at least 16 rows (and the shape suits it: group 128,
-// N a multiple of 128).
+// N a multiple of 128, and at least 2 k-tiles on both matrices, as hidden
+// and inter are each the N of one matrix and the K of the other).
 static bool use_group_gemm(int64_t n, int64_t E, int64_t G, int64_t N1, int64_t N2) {
-  return n >= 16 * E && G == 128 && N1 % 128 == 0 && N2 % 128 == 0;
+  return n >= 16 * E && G == 128 && N1 % 128 == 0 && N2 % 128 == 0 && N1 >= 256 && N2 >= 256;
 }
 
 
@@ -1017,12 +1088,15 @@ extern "C" int ccq_awq_pack_sz(const int32_t* qzeros, const void* scales, int sc
 
 namespace {
 // The dense GEMM switches to the grouped kernel for prefill-sized M.
-bool gemm_grouped(int64_t M, int64_t N, int64_t G) { return M > 64 && G == 128 && N % 128 == 0; }
+bool gemm_grouped(int64_t M, int64_t K, int64_t N, int64_t G) {
+  return M > 64 && G == 128 && N % 128 == 0 && K >= 256;
+}
 }  // namespace
 
 extern "C" size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N, int64_t group_size) {
-  if (M <= 0 || K <= 0 || K % 128 || !gemm_grouped(M, N, group_size)) return 0;
-  return align256((size_t)M * (size_t)(K / 128) * 4);
+  if (M <= 0 || K <= 0 || K % 128 || !gemm_grouped(M, K, N, group_size)) return 0;
+  // row group sums, then the row ids of the 128-row tiles
+  return align256((size_t)M * (size_t)(K / 128) * 4) + align256((size_t)cdiv(M, GG_BM) * GG_BM * 4);
 }
 
 extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, const uint32_t* sz, int scale_dtype,
@@ -1037,7 +1111,7 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
   CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_w4_gemm: bad y_dtype");
   CCQ_REQUIRE(K <= (1 << 20) && N / 16 <= 0x7fffffff, "ccq_w4_gemm: K=%lld or N=%lld too large", (long long)K,
               (long long)N);
-  const bool grouped = gemm_grouped(M, N, group_size);
+  const bool grouped = gemm_grouped(M, K, N, group_size);
   CCQ_REQUIRE(grouped || cdiv(M, 16) <= 65535, "ccq_w4_gemm: M=%lld too large", (long long)M);
   if (M == 0 || N == 0) return 0;
   CCQ_REQUIRE(K > 0, "ccq_w4_gemm: K == 0");
@@ -1055,13 +1129,16 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
     CCQ_REQUIRE(cdiv(M, GG_BM) * (N / 128) <= 0x7fffffff, "ccq_w4_gemm: M=%lld too large", (long long)M);
     hipStream_t st = as_stream(stream);
     float* sx = (float*)workspace;
-    int rc = launch_row_group_sums(x, x_dtype == CCQ_BF16, K, M, K, sx, K / 128, st);
+    int32_t* rows = (int32_t*)((char*)workspace + align256((size_t)M * (size_t)(K / 128) * 4));
+    const int64_t tiles = cdiv(M, GG_BM);
+    int rc = launch_row_group_sums(x, x_dtype == CCQ_BF16, K, M, K, sx, K / 128, st, rows, tiles * GG_BM);
     if (rc) return rc;
     W4GP g = {};
     g.x = x;
     g.ldx = K;
     g.sx = sx;
     g.ldsx = K / 128;
+    g.rows = rows;
     g.row_div = 1;
     g.tiles = (int)cdiv(M, GG_BM);
     g.w0 = (const uint32_t*)w_tiled;
@@ -1351,7 +1428,7 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
     d.sz_es = H * d.szw;
     d.y = rows;
     d.ldy = H;
-    d.y_dtype = CCQ_F32;
+    d.y_dtype = CCQ_BF16;
     d.N = (int)H;
     d.K = (int)I;
     d.KT = (int)(I / 128);
@@ -1364,5 +1441,8 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
     rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
     if (rc) return rc;
   }
-  return launch_combine(rows, weights, ids, ex->num_experts, y, y_dtype, T, k, ex->hidden, st);
+  // the grouped path stores the down rows as bf16 (half the traffic of the
+  // row write and of the combine's read)
+  return launch_combine(rows, L.grouped ? CCQ_BF16 : CCQ_F32, weights, ids, ex->num_experts, y, y_dtype, T, k,
+                        ex->hidden, st);
 }

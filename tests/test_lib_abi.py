@@ -69,7 +69,7 @@ def test_w4_gemm_rejects_bad_shapes(lib):
     assert lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 0, 256, 64, 128, None, 0, None) == 0
     # prefill-sized M needs the group-sum workspace
     assert lib.ccq_w4_gemm_workspace_size(64, 256, 128, 128) == 0
-    assert lib.ccq_w4_gemm_workspace_size(65, 256, 128, 128) == 768
+    assert lib.ccq_w4_gemm_workspace_size(65, 256, 128, 128) == 768 + 512  # group sums + row ids
     assert lib.ccq_w4_gemm_workspace_size(200, 256, 128, 64) == 0
     rc = lib.ccq_w4_gemm(p, CCQ_F16, p, p, CCQ_F16, p, CCQ_F16, 65, 256, 128, 128, None, 0, None)
     assert rc == CCQ_EINVAL and "workspace" in last_error()
