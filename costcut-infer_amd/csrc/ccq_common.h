@@ -161,4 +161,38 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
   return x * q + (x < r ? x : r) + (b >> 3);
 }
 
+// Wait for this wave's copies of one k-step: n (wave-uniform) = copies the
+// wave issues per k-step, N = the largest such count in the kernel.
+template <int N>
+__device__ __forceinline__ void wait_stage(int n) {
+  if constexpr (N > 0) {
+    if (n == N) {
+      wait_vmcnt<N>();
+      return;
+    }
+    wait_stage<N - 1>(n);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+// Row reductions (sum, or max with MAX) over the 32 lanes of each half-wave
+// for 32 values per lane, value r of a lane belonging to row r: a butterfly
+// that halves the list at every step, so lane l ends with row l & 31.
+template <bool MAX>
+__device__ __forceinline__ float half_wave_row_reduce(float (&v)[32], int c32) {
+#pragma unroll
+  for (int m = 1, n = 32; m < 32; m <<= 1, n >>= 1) {
+    const bool up = (c32 & m) != 0;
+#pragma unroll
+    for (int j = 0; j < n / 2; ++j) {
+      const float keep = up ? v[2 * j + 1] : v[2 * j];
+      const float send = up ? v[2 * j] : v[2 * j + 1];
+      const float other = __shfl_xor(send, m, 64);
+      v[j] = MAX ? fmaxf(keep, other) : keep + other;
+    }
+  }
+  return v[0];
+}
+
 }  // namespace ccq

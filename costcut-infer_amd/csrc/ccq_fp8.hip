@@ -1,24 +1,23 @@
 // FP8 e4m3fn with 128x128 block weight scales and per-token-per-128 dynamic
 // activation scales on gfx950: activation quantization, weight re-pack, the
-// block-scaled grouped GEMM on v_mfma_f32_16x16x128_f8f6f4, and the MoE
+// block-scaled grouped GEMM on v_mfma_f32_32x32x64_f8f6f4, and the MoE
 // expert FFN built on it.
 //
 // Format (public DeepSeek-V3-style block FP8): weights w [N, K] e4m3fn bytes
 // (row = output channel) with s_w [N/128, K/128] float32,
 // W[n, k] = fp8(w[n, k]) * s_w[n/128, k/128]; activations x [T, K] quantized
 // per token per 128 channels: s_a = max(amax, 1e-12) / 448 (float32),
-// q = RNE(x / s_a) saturated to +-448.  One 16x16x128 MFMA covers exactly one
+// q = RNE(x / s_a) saturated to +-448.  Two 32x32x64 MFMAs cover one
 // 128-wide K block, so each block's product is scaled once on the
 // accumulator: acc += (s_a[row, kb] * s_w[nb, kb]) * mfma(q_a, q_w).
 //
 // Weight tile layout: tile (nt, kb) = 16 output channels x 128 K bytes =
-// 2 KiB at byte (nt*KB + kb)*2048 (each wave streams one contiguous run of
-// its 16 channels); inside, [half h][lane l][16 bytes] with
-// bytes k = kb*128 + 32*(l >> 4) + 16*h + e of channel nt*16 + (l & 15).  A
-// lane's 32 operand bytes (channel l & 15, K bytes 32*(l >> 4) .. +32) come
-// from two wave-wide 16-byte loads, each a contiguous 1 KiB transfer.  The
-// activation A operand uses the same K mapping (row l & 15, K bytes
-// 32*(l >> 4) .. +32), so every K index meets its partner.
+// 2 KiB at byte (nt*KB + kb)*2048; inside, [half h][lane l][16 bytes] with
+// bytes k = kb*128 + 32*(l >> 4) + 16*h + e of channel nt*16 + (l & 15).
+// Each half is one contiguous 1 KiB copy.  The 32x32x64 B operand of lane
+// (h', c) = (l >> 5, l & 31) at K step s (bytes 64s + 32h' .. +32) is the
+// two halves of the slot of lane 16*(2s + h') + (c & 15) in 16-column tile
+// c >> 4; the A operand (row c, same K bytes) reads the activation tile.
 #include "ccq_common.h"
 
 #include <math.h>
@@ -100,6 +99,20 @@ __global__ void fp8_unpack_kernel(const uint8_t* __restrict__ tiled, uint8_t* __
 }
 
 // ------------------------------------------------------ grouped GEMM --
+// Persistent grouped GEMM on v_mfma_f32_32x32x64_f8f6f4, the FP8 form of the
+// int4 kernel in ccq_w4.hip: one workgroup of 8 waves per compute unit walks
+// a list of (128-row tile, column block) items; per 128-wide K block it
+// copies from HBM straight into LDS (global_load_lds) the activation tile
+// (128 rows x 128 bytes, rows gathered by row id), the weight tiles, the
+// rows' activation scales and the block's weight scales, in a ring of three
+// K blocks that runs on across items (loads two K blocks ahead).  Waves form
+// a 2 (rows) x 4 (columns) grid, each owning 64 rows x 2 tiles of 32
+// columns (gate and up for F8_SILU_Q).  Per K block and tile the two MFMAs
+// (K = 64 each) give the block's product t and
+//     acc += (s_a[row, kb] * s_w[block, kb]) * t.
+// Activation rows keep their 16-byte pieces swizzled by row (piece p of row
+// r at position p ^ f8_swz(r)), so the operand reads of 16 consecutive rows
+// hit 16 different bank groups.
 enum { F8_STORE = 0, F8_ROWS = 1, F8_SILU_Q = 2 };
 
 struct Fp8GP {
@@ -107,17 +120,17 @@ struct Fp8GP {
   int64_t lda;
   const float* sa;             // their scales [*, K/128]
   int64_t ldsa;
-  const int32_t* rows;         // per tile 64 row ids (-1 = padding); null = dense rows
+  const int32_t* rows;         // per tile 128 row ids (-1 = padding, at the end); null = dense rows
   int row_div;                 // activation row = row id / row_div
   const int32_t* tile_expert;  // null = one weight
-  const int32_t* meta;         // meta[0] = valid tiles; null = all
-  int tile_div;                // kernel tiles per schedule tile (schedule rows / BM)
+  const int32_t* meta;         // meta[0] = valid tiles; null = tiles
+  int tiles;
   const uint8_t* w0;           // tiled weights (gate for F8_SILU_Q)
   const float* sw0;            // block scales [N/128, K/128]
   const uint8_t* w1;           // up weights for F8_SILU_Q
   const float* sw1;
   int64_t w_es, sw_es;         // per-expert strides (bytes, floats)
-  void* y;                     // F8_STORE: [M, N] y_dtype; F8_ROWS: float [row id, N]
+  void* y;                     // F8_STORE: [M, N] y_dtype; F8_ROWS: [row id, N] y_dtype
   int64_t ldy;
   int y_dtype;
   uint8_t* qy;                 // F8_SILU_Q: e4m3fn [row id, N] and scales [row id, N/128]
@@ -126,259 +139,335 @@ struct Fp8GP {
   int M, N, K, KB;
 };
 
-constexpr int F8_BM_SMALL = 64;   // rows per tile (decode-sized groups)
-constexpr int F8_BM_LARGE = 128;  // rows per tile when experts receive many tokens
-constexpr int F8_BN = 128;        // output channels per workgroup (one scale block)
-constexpr int F8_ALD = 128 + 16;  // LDS row stride of the A tile (bytes)
+constexpr int F8_BM = 128;
+constexpr int F8_A_BYTES = F8_BM * 128;   // 128 rows x 128 e4m3 bytes
+constexpr int F8_B_BYTES = 16 * 2048;     // up to 16 weight tiles of 16 columns
+constexpr int F8_B_OFF = F8_A_BYTES;
+constexpr int F8_SA_OFF = F8_B_OFF + F8_B_BYTES;
+constexpr int F8_SW_OFF = F8_SA_OFF + F8_BM * 4;  // 2 x 64 copies of a block scale
+constexpr int F8_STAGE = F8_SW_OFF + 2 * 256;
+constexpr int F8_STAGES = 3;
+constexpr int F8_RID = F8_BM + 64;
+static_assert(F8_STAGES * F8_STAGE + 3 * F8_RID * 4 + 5 * F8_BM * 4 <= 160 * 1024, "LDS budget of one workgroup");
 
-__device__ __forceinline__ f32x4 mfma_f8(const i32x8& a, const i32x8& b, f32x4 c) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+__device__ __forceinline__ int f8_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+
+__device__ __forceinline__ f32x16 mfma_f8_32(const i32x8& a, const i32x8& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-// Workgroup = 8 waves on one BM-row tile x 128 output channels (blockIdx.x =
-// channel block, blockIdx.y = tile).  Wave w owns channels [16w, 16w+16)
-// (one 16-channel MFMA column; F8_SILU_Q: the same channels of gate and
-// up).  Per 128-wide K block: the A tile (BM x 128 bytes) and its row scales
-// go through LDS (double-buffered), the wave's weight tiles go straight to
-// registers; BM/16 (or 2*BM/16) MFMAs per wave.  Each tile streams its
-// expert's whole weight, so the tile height is chosen to hold all of an
-// expert's tokens whenever that is affordable (128 for prefill).
-constexpr int F8_WAVES = 8;
-
-template <int EPI, int BM>
+template <int EPI, int CTW>
 __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
-  constexpr int NQ = EPI == F8_SILU_Q ? 2 : 1;  // weight matrices
-  constexpr int NC = NQ;                        // 16-channel B tiles per wave
-  constexpr int RT = BM / 16;                   // 16-row MFMA tiles
-  constexpr int AP = BM * 8 / (64 * F8_WAVES);  // 16-byte A pieces per thread
-  __shared__ __align__(16) uint8_t As[2][BM * F8_ALD];
-  __shared__ __align__(16) float Ss[2][BM];
-  __shared__ int Rid[BM];
-  __shared__ float Red[F8_WAVES][BM];
+  constexpr int NQ = EPI == F8_SILU_Q ? 2 : 1;
+  constexpr int WGN = 64 * CTW;      // columns per matrix per item
+  constexpr int TPM = WGN / 16;      // 16-column weight tiles per matrix
+  constexpr int NBT = NQ * TPM;      // weight tiles per K block
+  constexpr int BPW = NBT / 4;       // 1 KiB weight copies per wave (2 per tile)
+  constexpr int C32 = CTW * NQ / 2;  // 32-column MFMA tiles per wave
+  constexpr int CQ = C32 / NQ;
+  constexpr int NSW = WGN == 256 || NQ == 2 ? 2 : 1;  // block scales per K block
+  static_assert(NBT % 4 == 0 && NBT <= 16 && C32 >= 1 && C32 <= 2, "tile shape");
+  __shared__ __align__(16) char smem[F8_STAGES * F8_STAGE];
+  __shared__ __align__(16) int Rid[3][F8_RID];
+  __shared__ __align__(16) float part[4 * F8_BM];
+  __shared__ __align__(16) float amax_s[F8_BM];
+
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nb = blockIdx.x, tile = blockIdx.y;
-  if (p.meta != nullptr && tile >= p.meta[0] * p.tile_div) return;
-  const int ex = p.tile_expert ? p.tile_expert[tile / p.tile_div] : 0;
-  if (tid < BM) {
-    int rid;
-    if (p.rows) {
-      rid = p.rows[tile * BM + tid];
+  const int mw = wave >> 2, nw = wave & 3;
+  const int nblk = p.N / WGN;
+  const int ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
+  // static schedule (as in the int4 kernel): row tiles dealt to XCDs
+  // round-robin, all column blocks of a tile on one XCD
+  const int xcd = blockIdx.x & 7, wx = blockIdx.x >> 3;
+  const int nx = ((int)gridDim.x - xcd + 7) >> 3;
+  const int items_x = (ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0) * nblk;
+  if (wx >= items_x) return;
+  const int nmine = (items_x - wx + nx - 1) / nx;
+  const int KB = p.KB;
+  const int total = nmine * KB;
+
+  auto tile_of = [&](int j) { return xcd + 8 * ((wx + j * nx) / nblk); };
+  // row ids of item j into Rid[j % 3] (+ expert id copies): DMA from the
+  // schedule, or the rows of a dense tile; called two items ahead
+  auto fetch_rows = [&](int j) {
+    if (j >= nmine) return;
+    const int tile = tile_of(j);
+    if (p.rows != nullptr) {
+      const uint32_t dst = lds_addr(&Rid[j % 3][0]);
+      if (wave >= 6) dma4(p.rows + (int64_t)tile * F8_BM, (wave - 6) * 256 + lane * 4, dst + (wave - 6) * 256);
+      if (wave == 5 && p.tile_expert != nullptr) dma4(p.tile_expert + tile, 0u, dst + F8_BM * 4);
+    } else if (wave >= 6) {
+      const int r = (wave - 6) * 64 + lane, rid = tile * F8_BM + r;
+      Rid[j % 3][r] = rid < p.M ? rid : -1;
+    }
+  };
+  for (int j = 0; j < 2 && j < nmine; ++j) {
+    const int tile = tile_of(j);
+    if (tid < F8_BM) {
+      const int rid = tile * F8_BM + tid;
+      Rid[j][tid] = p.rows != nullptr ? p.rows[(int64_t)tile * F8_BM + tid] : (rid < p.M ? rid : -1);
+    }
+    if (tid == F8_BM) Rid[j][F8_BM] = p.tile_expert != nullptr ? p.tile_expert[tile] : 0;
+  }
+  __syncthreads();
+
+  // ---- per-item copy plan of this wave ----
+  struct Plan {
+    uint32_t aoff[2];
+    const uint8_t* bsrc[BPW];
+    uint32_t soff;
+    const float* swsrc;
+    int nvalid, nb;
+  };
+  const bool has_sa = wave == 4 || wave == 5;
+  const bool has_sw = wave >= 6 && wave - 6 < NSW;
+  const int ncopy = 2 + BPW + (has_sa ? 1 : 0) + (has_sw ? 1 : 0);
+  auto make_plan = [&](int j, Plan& P) {
+    const int li = wx + j * nx;
+    P.nb = li % nblk;
+    const int* R = Rid[j % 3];
+    const int ex = p.tile_expert != nullptr ? __builtin_amdgcn_readfirstlane(R[F8_BM]) : 0;
+    P.nvalid = (int)(__popcll(__ballot(R[lane] >= 0)) + __popcll(__ballot(R[64 + lane] >= 0)));
+    const int rid0 = R[0];
+    // activations: rows 16*wave + 8*i + (lane >> 3); the lane takes piece
+    // (lane & 7) ^ f8_swz(row), which lands at position lane & 7
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = 16 * wave + 8 * i + (lane >> 3);
+      const int rid = R[row] >= 0 ? R[row] : rid0;
+      const int piece = (lane & 7) ^ f8_swz(row);
+      P.aoff[i] = (uint32_t)((int64_t)(rid / p.row_div) * p.lda + piece * 16);
+    }
+    // weights: copy b of the wave = half (b & 1) of tile b >> 1
+#pragma unroll
+    for (int b2 = 0; b2 < BPW; ++b2) {
+      const int b = wave * BPW + b2, t = b >> 1, q = t / TPM, nt = P.nb * TPM + (t - q * TPM);
+      P.bsrc[b2] = (q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + (int64_t)nt * KB * 2048 + (b & 1) * 1024;
+    }
+    P.soff = 0;
+    if (has_sa) {
+      const int row = 64 * (wave - 4) + lane;
+      const int rid = R[row] >= 0 ? R[row] : rid0;
+      P.soff = (uint32_t)((int64_t)(rid / p.row_div) * p.ldsa * 4);
+    }
+    P.swsrc = nullptr;
+    if (has_sw) {
+      // SILU: gate (wave 6) and up (wave 7) of block nb; 256-column items:
+      // blocks 2nb and 2nb+1
+      const int q = NQ == 2 ? wave - 6 : 0;
+      const int blk = NQ == 2 ? P.nb : P.nb * (WGN / 128) + (wave - 6);
+      P.swsrc = (q == 0 ? p.sw0 : p.sw1) + (int64_t)ex * p.sw_es + (int64_t)blk * KB;
+    }
+  };
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](const Plan& P, int kb, int slot) {
+    const uint32_t st = lds0 + slot * F8_STAGE;
+    const uint8_t* ab = p.a + (int64_t)kb * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(ab, P.aoff[i], st + (16 * wave + 8 * i) * 128);
+#pragma unroll
+    for (int b2 = 0; b2 < BPW; ++b2) {
+      const int b = wave * BPW + b2;
+      dma16(P.bsrc[b2] + (int64_t)kb * 2048, lane * 16, st + F8_B_OFF + (b >> 1) * 2048 + (b & 1) * 1024);
+    }
+    if (has_sa) dma4(p.sa + kb, P.soff, st + F8_SA_OFF + (wave - 4) * 256);
+    if (has_sw) dma4(P.swsrc + kb, 0u, st + F8_SW_OFF + (wave - 6) * 256);
+  };
+
+  // ---- MFMA side: lane (h, c32) = (lane >> 5, lane & 31) ----
+  const int c32 = lane & 31, h = lane >> 5;
+  const int fsw = f8_swz(c32);
+  // A operand of k-step s (K = 64): row c32 of the 32-row tile, bytes
+  // 64s + 32h .. +32 = pieces 4s + 2h and 4s + 2h + 1
+  uint32_t adoff[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) adoff[s][e] = (mw * 64 + c32) * 128 + (((4 * s + 2 * h + e) ^ fsw) * 16);
+  // B operand: column c32 of the tile = column c32 & 15 of 16-column weight
+  // tile (c32 >> 4); bytes 64s + 32h .. +32 are the two halves of the slot of
+  // lane 16 * (2s + h) + (c32 & 15)
+  uint32_t bdoff[C32][2];
+  int swq[C32];
+#pragma unroll
+  for (int c = 0; c < C32; ++c) {
+    const int q = c / CQ, cc = c - q * CQ;
+    const int t16 = q * TPM + nw * CTW + 2 * cc + (c32 >> 4);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) bdoff[c][s] = F8_B_OFF + t16 * 2048 + (16 * (2 * s + h) + (c32 & 15)) * 16;
+    swq[c] = NQ == 2 ? q : (WGN == 256 ? nw >> 1 : 0);
+  }
+
+  f32x16 acc[2][C32];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int c = 0; c < C32; ++c) acc[rt][c] = f32x16{};
+
+  auto compute = [&](int slot) {
+    const char* S = smem + slot * F8_STAGE;
+    float swv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) swv[q] = *reinterpret_cast<const float*>(S + F8_SW_OFF + q * 256);
+    f32x16 t[2][C32];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      i32x8 a[2], b[C32];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(S + rt * 32 * 128 + adoff[s][0]);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(S + rt * 32 * 128 + adoff[s][1]);
+        a[rt] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int c = 0; c < C32; ++c) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(S + bdoff[c][s]);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(S + bdoff[c][s] + 1024);
+        b[c] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int c = 0; c < C32; ++c)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) t[rt][c] = mfma_f8_32(a[rt], b[c], s == 0 ? f32x16{} : t[rt][c]);
+    }
+    // acc += (s_a[row] * s_w[block]) * t; register i of tile rt holds row
+    // mw*64 + 32*rt + 8*(i/4) + 4*h + i%4
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 sa = *reinterpret_cast<const f32x4*>(S + F8_SA_OFF + (mw * 64 + 32 * rt + 8 * g + 4 * h) * 4);
+#pragma unroll
+        for (int c = 0; c < C32; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[rt][c][4 * g + e] = fmaf(sa[e] * swv[swq[c]], t[rt][c][4 * g + e], acc[rt][c][4 * g + e]);
+      }
+  };
+
+  auto row_of = [&](int rt, int i) { return mw * 64 + 32 * rt + 8 * (i >> 2) + 4 * h + (i & 3); };
+  auto epilogue = [&](int j, const Plan& P) {
+    const int* R = Rid[j % 3];
+    if constexpr (EPI == F8_SILU_Q) {
+      // h = silu(g) * u held in bf16, then e4m3 per row per 128-column block
+      // (this item's columns): scale = max(amax, 1e-12) / 448
+      float hv[32], am[32];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float g = acc[rt][0][i], u = acc[rt][1][i];
+          const float v = g * __frcp_rn(1.0f + __expf(-g)) * u;
+          hv[rt * 16 + i] = bf16_bits_to_f32(f32_to_bf16_bits(v));
+          am[rt * 16 + i] = fabsf(hv[rt * 16 + i]);
+        }
+      const float wmax = half_wave_row_reduce<true>(am, c32);
+      part[nw * F8_BM + row_of(c32 >> 4, c32 & 15)] = wmax;
+      lds_barrier();
+      if (tid < F8_BM)
+        amax_s[tid] = fmaxf(fmaxf(part[tid], part[F8_BM + tid]), fmaxf(part[2 * F8_BM + tid], part[3 * F8_BM + tid]));
+      lds_barrier();
+      const int64_t col = (int64_t)P.nb * WGN + nw * CTW * 16 + c32;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 amx = *reinterpret_cast<const f32x4*>(&amax_s[mw * 64 + 32 * rt + 8 * g + 4 * h]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = row_of(rt, 4 * g + e);
+            if (row < P.nvalid) {
+              const float sc = fmaxf(amx[e], kAmaxFloor) / kFp8Max;
+              p.qy[(int64_t)R[row] * p.ldqy + col] = (uint8_t)f32_to_fp8_rne(hv[rt * 16 + 4 * g + e] / sc);
+            }
+          }
+        }
+      if (tid < P.nvalid) p.sy[(int64_t)R[tid] * p.ldsy + P.nb] = fmaxf(amax_s[tid], kAmaxFloor) / kFp8Max;
     } else {
-      rid = tile * BM + tid;
-      if (rid >= p.M) rid = -1;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int row = row_of(rt, i);
+          if (row >= P.nvalid) continue;
+          const int64_t o = (int64_t)R[row] * p.ldy + P.nb * WGN + nw * CTW * 16 + c32;
+#pragma unroll
+          for (int c = 0; c < C32; ++c) {
+            const float v = acc[rt][c][i];
+            if (p.y_dtype == CCQ_F32)
+              reinterpret_cast<float*>(p.y)[o + c * 32] = v;
+            else if (p.y_dtype == CCQ_BF16)
+              reinterpret_cast<uint16_t*>(p.y)[o + c * 32] = (uint16_t)f32_to_bf16_bits(v);
+            else
+              reinterpret_cast<uint16_t*>(p.y)[o + c * 32] = (uint16_t)f32_to_f16_bits(v);
+          }
+        }
     }
-    Rid[tid] = rid;
-  }
-  // a tile of padding only (the tail of an expert's last schedule tile)
-  if (!__syncthreads_or(tid < BM && Rid[tid] >= 0)) return;
-
-  // A staging: BM rows x 8 pieces of 16 bytes, AP pieces per thread
-  // (piece i = tid + 512*j: row = i / 8, part = i % 8)
-  const uint8_t* asrc[AP];
-  bool aval[AP];
 #pragma unroll
-  for (int j = 0; j < AP; ++j) {
-    const int i = tid + 64 * F8_WAVES * j, row = i >> 3, part = i & 7;
-    aval[j] = Rid[row] >= 0;
-    asrc[j] = p.a + (int64_t)(aval[j] ? Rid[row] / p.row_div : 0) * p.lda + 16 * part;
-  }
-  const float* ssrc = nullptr;
-  bool sval = false;
-  if (tid < BM) {
-    const int rid = Rid[tid];
-    sval = rid >= 0;
-    ssrc = p.sa + (int64_t)(sval ? rid / p.row_div : 0) * p.ldsa;
-  }
-  // A for a K block: AP 16-byte pieces per thread (+ one row scale for
-  // threads < BM), held in registers until written to LDS
-  struct AStage {
-    u32x4 v[AP];
-    float s;
-  };
-  auto load_a = [&](AStage& st, int kb) {
+    for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int j = 0; j < AP; ++j) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(asrc[j] + (int64_t)kb * 128);
-      st.v[j] = aval[j] ? v : u32x4{0u, 0u, 0u, 0u};
-    }
-    if (tid < BM) st.s = sval ? ssrc[kb] : 0.f;
-  };
-  auto store_a = [&](const AStage& st, int buf) {
-#pragma unroll
-    for (int j = 0; j < AP; ++j) {
-      const int i = tid + 64 * F8_WAVES * j, row = i >> 3, part = i & 7;
-      *reinterpret_cast<u32x4*>(&As[buf][row * F8_ALD + 16 * part]) = st.v[j];
-    }
-    if (tid < BM) Ss[buf][tid] = st.s;
-  };
-  // weight tile of this wave: channel tile nt = nb*8 + wave, per matrix
-  const uint8_t* wsrc[NC];
-#pragma unroll
-  for (int q = 0; q < NQ; ++q)
-    wsrc[q] = (q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + ((int64_t)(nb * 8 + wave) * p.KB) * 2048 + lane * 16;
-  const float* swb[NQ];
-#pragma unroll
-  for (int q = 0; q < NQ; ++q) swb[q] = (q == 0 ? p.sw0 : p.sw1) + (int64_t)ex * p.sw_es + (int64_t)nb * p.KB;
-
-  auto load_b = [&](i32x8 (&b)[NC], int kb) {
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const uint8_t* src = wsrc[c] + (int64_t)kb * 2048;
-      const u32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-      const u32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 1024));
-      b[c] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-    }
+      for (int c = 0; c < C32; ++c) acc[rt][c] = f32x16{};
   };
 
-  f32x4 acc[RT][NC];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int r = lane & 15, kq = lane >> 4;
-  auto compute = [&](int buf, const i32x8 (&b)[NC], int kb) {
-    float sw[NQ];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) sw[q] = swb[q][kb];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const uint8_t* ap = &As[buf][(rt * 16 + r) * F8_ALD + 32 * kq];
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(ap);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(ap + 16);
-      const i32x8 a = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      const f32x4 sr = *reinterpret_cast<const f32x4*>(&Ss[buf][rt * 16 + 4 * kq]);
-      f32x4 t[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) t[c] = mfma_f8(a, b[c], f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const float s = sw[c];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[rt][c][i] = fmaf(sr[i] * s, t[c][i], acc[rt][c][i]);
-      }
-      // keep one row tile's products live at a time (the scheduler would
-      // otherwise hoist every MFMA of the block and run out of registers)
-      __builtin_amdgcn_sched_barrier(0);
+  // ---- pipeline over all K blocks of all items of this workgroup ----
+  Plan cur, nxt;
+  make_plan(0, cur);
+  if (nmine > 1) make_plan(1, nxt);
+  issue(cur, 0, 0);
+  if (total > 1) issue(cur, 1, 1);  // KB >= 2
+  int j = 0, kb = 0, slot = 0;
+  for (int g = 0; g < total; ++g) {
+    if (g + 1 < total)
+      wait_stage<7>(ncopy);
+    else
+      wait_vmcnt<0>();
+    lds_barrier();
+    if (kb == 0 && j + 2 < nmine) fetch_rows(j + 2);
+    if (kb == KB - 2 && j + 1 < nmine) make_plan(j + 1, nxt);
+    const bool last = kb + 1 == KB;
+    const int slot2 = slot == 0 ? 2 : slot - 1;  // (slot + 2) % 3
+    if (!last && g + 2 < total) issue(kb + 2 < KB ? cur : nxt, kb + 2 < KB ? kb + 2 : kb + 2 - KB, slot2);
+    if (mw * 64 < cur.nvalid) compute(slot);
+    if (last) {
+      epilogue(j, cur);
+      if (g + 2 < total) issue(nxt, 1, slot2);
+      cur = nxt;
+      ++j;
+      kb = 0;
+    } else {
+      ++kb;
     }
-  };
-
-  // software pipeline: step kb computes block kb from LDS buffer kb & 1 and
-  // a weight register slot, then writes A(kb+1) to LDS; the loads of block
-  // kb+DEPTH (A first, then weights) are issued at its start.  Waits retire
-  // loads in issue order, so writing A(kb+1) only waits for loads issued up
-  // to A(kb+1) itself and the later weights stay in flight.  DEPTH is 2, or
-  // 1 where the registers of a third stage would cost a workgroup per CU
-  // (measured: two resident workgroups hide each other's barrier stalls
-  // better than a deeper single-workgroup pipeline).
-  constexpr int DEPTH = (EPI == F8_SILU_Q && BM == F8_BM_LARGE) || EPI == F8_ROWS ? 1 : 2;
-  if constexpr (DEPTH == 2) {
-    AStage as0, as1, as2;
-    i32x8 b0[NC], b1[NC], b2[NC];
-    auto step = [&](int kb, AStage& a_next, AStage& a_far, const i32x8 (&bc)[NC], i32x8 (&bfar)[NC]) {
-      if (kb + 2 < p.KB) {
-        load_a(a_far, kb + 2);
-        load_b(bfar, kb + 2);
-      }
-      compute(kb & 1, bc, kb);
-      if (kb + 1 < p.KB) store_a(a_next, (kb + 1) & 1);
-      __syncthreads();
-    };
-    load_a(as0, 0);
-    load_b(b0, 0);
-    if (p.KB > 1) {
-      load_a(as1, 1);
-      load_b(b1, 1);
-    }
-    store_a(as0, 0);
-    __syncthreads();
-    for (int kb = 0; kb < p.KB; kb += 3) {
-      step(kb, as1, as2, b0, b2);
-      if (kb + 1 >= p.KB) break;
-      step(kb + 1, as2, as0, b1, b0);
-      if (kb + 2 >= p.KB) break;
-      step(kb + 2, as0, as1, b2, b1);
-    }
-  } else {
-    AStage as0, as1;
-    i32x8 b0[NC], b1[NC];
-    load_a(as0, 0);
-    load_b(b0, 0);
-    store_a(as0, 0);
-    __syncthreads();
-    for (int kb = 0; kb < p.KB; kb += 2) {
-      if (kb + 1 < p.KB) {
-        load_a(as1, kb + 1);
-        load_b(b1, kb + 1);
-      }
-      compute(0, b0, kb);
-      if (kb + 1 < p.KB) store_a(as1, 1);
-      __syncthreads();
-      if (kb + 1 >= p.KB) break;
-      if (kb + 2 < p.KB) {
-        load_a(as0, kb + 2);
-        load_b(b0, kb + 2);
-      }
-      compute(1, b1, kb + 1);
-      if (kb + 2 < p.KB) store_a(as0, 0);
-      __syncthreads();
-    }
+    slot = slot == 2 ? 0 : slot + 1;
   }
+}
 
-  // epilogue: lane holds rows rt*16 + 4*kq + i, channel c*16 + r of its wave
-  if constexpr (EPI == F8_SILU_Q) {
-    float h[RT][4];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float g = acc[rt][0][i], u = acc[rt][1][i];
-        // silu(g) * u in float64 stored float32 (kernels.py:219-231), then
-        // rounded to bf16: the intermediate is held in bf16
-        const double gd = (double)g;
-        const float hv = (float)((gd / (1.0 + exp(-gd))) * (double)u);
-        const float hb = bf16_bits_to_f32(f32_to_bf16_bits(hv));
-        h[rt][i] = hb;
-        float m = fabsf(hb);
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        if (r == 0) Red[wave][rt * 16 + 4 * kq + i] = m;
-      }
-    __syncthreads();
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = rt * 16 + 4 * kq + i;
-        const int rid = Rid[row];
-        if (rid < 0) continue;
-        float amax = Red[0][row];
-#pragma unroll
-        for (int w = 1; w < F8_WAVES; ++w) amax = fmaxf(amax, Red[w][row]);
-        const float sc = fmaxf(amax, kAmaxFloor) / kFp8Max;
-        const int64_t col = (int64_t)nb * F8_BN + 16 * wave + r;
-        p.qy[(int64_t)rid * p.ldqy + col] = (uint8_t)f32_to_fp8_rne(h[rt][i] / sc);
-        if (wave == 0 && r == 0) p.sy[(int64_t)rid * p.ldsy + nb] = sc;
-      }
-  } else {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rid = Rid[rt * 16 + 4 * kq + i];
-        if (rid < 0) continue;
-        const int64_t col = (int64_t)nb * F8_BN + 16 * wave + r;
-        const int64_t o = (int64_t)rid * p.ldy + col;
-        const float v = acc[rt][0][i];
-        if (EPI == F8_ROWS || p.y_dtype == CCQ_F32)
-          reinterpret_cast<float*>(p.y)[o] = v;
-        else if (p.y_dtype == CCQ_BF16)
-          reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)f32_to_bf16_bits(v);
-        else
-          reinterpret_cast<uint16_t*>(p.y)[o] = (uint16_t)f32_to_f16_bits(v);
-      }
+// Compute units of the current device (one persistent workgroup each; at
+// least 8 so that every XCD gets one).
+static int f8_device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n < 8 ? 8 : n;
   }
+  return cus[dev];
+}
+
+// tiles = 128-row schedule tiles the grid is sized for (the kernel reads the
+// actual number from meta when given).  K must hold at least 2 blocks.
+template <int EPI>
+static int launch_fp8_gemm(const Fp8GP& p, int64_t tiles, hipStream_t st) {
+  const int wgn = EPI == F8_SILU_Q ? 128 : (p.N % 256 == 0 ? 256 : 128);
+  const int64_t items = tiles * (p.N / wgn), cus = f8_device_cus();
+  const dim3 grid((unsigned)(items < cus ? items : cus)), block(512);
+  if (wgn == 256)
+    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, (EPI == F8_SILU_Q ? 2 : 4)>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, 2>), grid, block, 0, st, p);
+  return launch_status("fp8 gemm");
 }
 
 static int grid_of(int64_t n, int block) {
@@ -397,25 +486,6 @@ int launch_act_quant(const void* x, int x_dtype, int64_t ldx, int64_t rows, int6
   else
     hipLaunchKernelGGL(fp8_act_quant_kernel<CCQ_F32>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
   return launch_status("fp8 act quant");
-}
-
-// bm: rows per schedule tile; kernel_bm: rows per kernel tile (a divisor)
-template <int EPI>
-static int launch_fp8_gemm(Fp8GP p, int bm, int kernel_bm, int64_t tiles, hipStream_t st) {
-  p.tile_div = bm / kernel_bm;
-  const dim3 grid((unsigned)(p.N / F8_BN), (unsigned)(tiles * p.tile_div)), block(64 * F8_WAVES);
-  if (kernel_bm == F8_BM_LARGE)
-    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, F8_BM_LARGE>), grid, block, 0, st, p);
-  else
-    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, F8_BM_SMALL>), grid, block, 0, st, p);
-  return launch_status("fp8 gemm");
-}
-
-// Tile height of a grouped call: 128 rows once the average expert receives
-// at least 32 tokens (each tile re-streams its expert's weights, so a tile
-// should hold all of them), 64 below that.
-static int fp8_tile_rows(int64_t assignments, int64_t experts) {
-  return assignments >= 32 * experts ? F8_BM_LARGE : F8_BM_SMALL;
 }
 
 }  // namespace ccq
@@ -488,7 +558,11 @@ extern "C" int ccq_fp8_block_linear(const void* x, int x_dtype, const uint8_t* w
               (long long)K, (long long)N);
   CCQ_REQUIRE(x_dtype == CCQ_F32 || x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_fp8_block_linear: bad x_dtype");
   CCQ_REQUIRE(y_dtype == CCQ_F32 || y_dtype == CCQ_F16 || y_dtype == CCQ_BF16, "ccq_fp8_block_linear: bad y_dtype");
-  CCQ_REQUIRE(cdiv(M, F8_BM_SMALL) <= 65535 && N / F8_BN <= 65535, "ccq_fp8_block_linear: M or N too large");
+  CCQ_REQUIRE(cdiv(M, F8_BM) * (N / 128) <= 0x7fffffff, "ccq_fp8_block_linear: M or N too large");
+  CCQ_REQUIRE(K == 0 || K >= 256, "ccq_fp8_block_linear: K=%lld < 256 (the kernel pipelines two 128-blocks)",
+              (long long)K);
+  CCQ_REQUIRE(M * K < (int64_t)1 << 32, "ccq_fp8_block_linear: activations of %lld x %lld exceed 4 GiB",
+              (long long)M, (long long)K);
   if (M == 0 || N == 0) return 0;
   CCQ_REQUIRE(K > 0, "ccq_fp8_block_linear: K == 0");
   CCQ_REQUIRE(x && w_tiled && s_w && y, "ccq_fp8_block_linear: null pointer");
@@ -517,8 +591,8 @@ extern "C" int ccq_fp8_block_linear(const void* x, int x_dtype, const uint8_t* w
   p.N = (int)N;
   p.K = (int)K;
   p.KB = (int)(K / 128);
-  const int bm = M >= F8_BM_LARGE ? F8_BM_LARGE : F8_BM_SMALL;
-  return launch_fp8_gemm<F8_STORE>(p, bm, bm, cdiv(M, bm), st);
+  p.tiles = (int)cdiv(M, F8_BM);
+  return launch_fp8_gemm<F8_STORE>(p, p.tiles, st);
 }
 
 // ------------------------------------------------------------ MoE FP8 --
@@ -531,7 +605,10 @@ int check_fp8_experts(const ccq_fp8_experts* ex, const char* name) {
   CCQ_REQUIRE(ex->hidden > 0 && ex->inter > 0 && ex->hidden % 128 == 0 && ex->inter % 128 == 0,
               "%s: hidden=%lld and inter=%lld must be positive multiples of 128", name, (long long)ex->hidden,
               (long long)ex->inter);
-  CCQ_REQUIRE(ex->hidden / F8_BN <= 65535 && ex->inter / F8_BN <= 65535, "%s: hidden/inter too large", name);
+  CCQ_REQUIRE(ex->hidden <= (1 << 20) && ex->inter <= (1 << 20), "%s: hidden/inter too large", name);
+  CCQ_REQUIRE(ex->hidden >= 256 && ex->inter >= 256,
+              "%s: hidden=%lld and inter=%lld must be at least 256 (two 128-blocks)", name, (long long)ex->hidden,
+              (long long)ex->inter);
   CCQ_REQUIRE(ex->w_gate && ex->s_gate && ex->w_up && ex->s_up && ex->w_down && ex->s_down,
               "%s: null weight pointer", name);
   CCQ_REQUIRE(aligned(ex->w_gate, 16) && aligned(ex->w_up, 16) && aligned(ex->w_down, 16),
@@ -549,7 +626,7 @@ F8MoeLayout f8_moe_layout(int64_t T, int64_t k, const ccq_fp8_experts* ex) {
   F8MoeLayout L;
   const int64_t H = ex->hidden, I = ex->inter;
   L.n = T * k;
-  L.bm = fp8_tile_rows(L.n, ex->num_experts);
+  L.bm = F8_BM;
   L.max_tiles = ccq_moe_align_max_tiles(L.n, ex->num_experts, L.bm);
   size_t o = 0;
   L.off_sorted = o;
@@ -595,7 +672,8 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   if (T == 0) return 0;
   CCQ_REQUIRE(x && ids && weights && y, "ccq_moe_fp8_ffn: null pointer");
   const F8MoeLayout L = f8_moe_layout(T, k, ex);
-  CCQ_REQUIRE(L.max_tiles * 2 <= 65535, "ccq_moe_fp8_ffn: too many tiles");
+  CCQ_REQUIRE(T * ex->hidden < (int64_t)1 << 32 && L.n * ex->inter < (int64_t)1 << 32,
+              "ccq_moe_fp8_ffn: activations exceed 4 GiB");
   CCQ_REQUIRE(workspace && workspace_bytes >= L.total && aligned(workspace, 256),
               "ccq_moe_fp8_ffn: workspace of %zu bytes (256-byte aligned) needed, %zu given", L.total,
               workspace_bytes);
@@ -610,7 +688,7 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   float* sx = (float*)(ws + L.off_sx);
   uint8_t* qh = (uint8_t*)(ws + L.off_qh);
   float* sh = (float*)(ws + L.off_sh);
-  float* rows = (float*)(ws + L.off_rows);
+  void* rows = ws + L.off_rows;
 
   rc = launch_align(ids, L.n, ex->num_experts, L.bm, sorted, te, meta, counts, st);
   if (rc) return rc;
@@ -639,7 +717,7 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   g.N = (int)I;
   g.K = (int)H;
   g.KB = (int)(H / 128);
-  rc = launch_fp8_gemm<F8_SILU_Q>(g, L.bm, L.bm, L.max_tiles, st);
+  rc = launch_fp8_gemm<F8_SILU_Q>(g, L.max_tiles, st);
   if (rc) return rc;
 
   Fp8GP d = {};
@@ -657,12 +735,11 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   d.sw_es = (H / 128) * (I / 128);
   d.y = rows;
   d.ldy = H;
-  d.y_dtype = CCQ_F32;
+  d.y_dtype = CCQ_BF16;  // bf16 rows: half the traffic of the row write and of the combine
   d.N = (int)H;
   d.K = (int)I;
   d.KB = (int)(I / 128);
-  // down runs 64-row tiles (two resident workgroups per CU; see DEPTH)
-  rc = launch_fp8_gemm<F8_ROWS>(d, L.bm, F8_BM_SMALL, L.max_tiles, st);
+  rc = launch_fp8_gemm<F8_ROWS>(d, L.max_tiles, st);
   if (rc) return rc;
-  return launch_combine(rows, CCQ_F32, weights, ids, ex->num_experts, y, y_dtype, T, k, H, st);
+  return launch_combine(rows, CCQ_BF16, weights, ids, ex->num_experts, y, y_dtype, T, k, H, st);
 }

@@ -591,36 +591,7 @@ constexpr int GG_STAGES = 3;
 constexpr int GG_RID = GG_BM + 64;  // row ids of one item + copies of its expert id
 static_assert(GG_STAGES * GG_STAGE + 3 * GG_RID * 4 + 4 * GG_BM * 4 <= 160 * 1024, "LDS budget of one workgroup");
 
-template <int N>
-__device__ __forceinline__ void wait_stage(int n) {
-  // n (wave-uniform) = copies this wave issues per k-tile, N = the largest
-  if constexpr (N > 0) {
-    if (n == N) {
-      wait_vmcnt<N>();
-      return;
-    }
-    wait_stage<N - 1>(n);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
 
-// Row sums over the 32 lanes of each half-wave for 32 values per lane
-// (value r of a lane belongs to row r): a butterfly that halves the list at
-// every step, so lane l ends with the sum for row l & 31.
-__device__ __forceinline__ float half_wave_row_sums(float (&v)[32], int c32) {
-#pragma unroll
-  for (int m = 1, n = 32; m < 32; m <<= 1, n >>= 1) {
-    const bool up = (c32 & m) != 0;
-#pragma unroll
-    for (int j = 0; j < n / 2; ++j) {
-      const float keep = up ? v[2 * j + 1] : v[2 * j];
-      const float send = up ? v[2 * j] : v[2 * j + 1];
-      v[j] = keep + __shfl_xor(send, m, 64);
-    }
-  }
-  return v[0];
-}
 
 template <typename AT, typename ST, int EPI, int CTW>
 __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
@@ -865,7 +836,7 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
       if (p.sxo != nullptr) {
         // group sums of the stored rows over this item's 128 columns: 32 per
         // wave by butterfly, then the 4 column waves through LDS
-        const float part_sum = half_wave_row_sums(rs, c32);
+        const float part_sum = half_wave_row_reduce<false>(rs, c32);
         part[nw * GG_BM + row_of(c32 >> 4, c32 & 15)] = part_sum;
         lds_barrier();
         if (tid < P.nvalid)
