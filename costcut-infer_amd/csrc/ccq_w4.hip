@@ -31,6 +31,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace ccq {
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
@@ -532,6 +534,303 @@ static int gemm_nb(int64_t M) { return M <= 4 ? 1 : (M <= 8 ? 2 : 4); }
 
 static bool valid_group(int64_t G) { return G == 32 || G == 64 || G == 128; }
 
+// ------------------------------------------------ decode streaming GEMM --
+// For up to 16 rows per weight (decode; MoE experts receiving a few tokens):
+// pure weight streaming.  One persistent workgroup of 8 waves per compute
+// unit takes a contiguous range of jobs; a job is one 16-row tile times NQ
+// "quads" of 16 output columns over all of K: the gate and the up columns of
+// one 16-column block for EPI_SILU, two adjacent 16-column blocks otherwise
+// (NQ = 2), or one block (NQ = 1, K up to 4096).  The 8 waves split K (wave w
+// takes k-tiles w, w + 8, ...).  Each wave streams its own weight tiles
+// (1 KiB per 128 K x 16 columns, one 16-byte slice per lane) and one
+// scale/zero word per lane straight into registers, WS_DEPTH jobs ahead, so
+// the weight stream needs no LDS and no barrier: with 8 waves that is
+// WS_DEPTH x 34 KiB in flight per compute unit.  The tile's activation
+// fragments and their group sums (one MFMA against a ones operand) stay in
+// registers; the fragments of a second tile in the range wait in LDS.  The
+// waves' partial sums go through LDS and are added in a fixed order, two jobs
+// per barrier (waves 0..3 add the first, 4..7 the second).  The schedule
+// (valid tiles, experts, row ids) is read with scalar loads.
+struct W4SP {
+  const void* x;
+  int64_t ldx;
+  const int32_t* rows;         // per tile 16 row ids (-1 = padding); null = dense rows
+  int row_div;                 // activation row = row id / row_div
+  const int32_t* tile_expert;  // expert of each tile; set exactly when rows is
+  const int32_t* meta;         // meta[0] = valid tiles; null = tiles
+  int tiles;
+  const uint32_t* w0;
+  const uint32_t* sz0;
+  const uint32_t* w1;          // up projection (EPI_SILU)
+  const uint32_t* sz1;
+  int64_t w_es, sz_es;         // per-expert strides (words)
+  void* y;
+  int64_t ldy;
+  int y_dtype;
+  int M, N, K, KT, szw;
+  uint32_t nib_mask;           // 0x000F000F (a run-time value, see dq_b3)
+};
+
+constexpr int WS_DEPTH = 2;  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
+
+// Quads per job of the streaming kernel for a stage of N columns and K rows
+// (0: the kernel does not take it).  EPI_SILU always pairs gate and up; two
+// quads keep K <= 2048 (two k-tiles per wave), one quad K <= 4096.
+static int stream_nq(int EPI, int64_t N, int64_t K, int64_t G) {
+  if (G != 128 || K % 128 != 0 || N % 16 != 0) return 0;
+  const int64_t KT = K / 128;
+  const bool two = EPI == EPI_SILU || N % 32 == 0;
+  if (two && KT <= 16) return 2;
+  if (EPI != EPI_SILU && KT <= 32) return 1;
+  return 0;
+}
+
+template <typename AT, typename ST, int EPI, int MT, int NQ>
+__global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
+  using V = typename Act<AT>::vec;
+  constexpr int D = WS_DEPTH;
+  static_assert(EPI != EPI_SILU || NQ == 2, "gate and up quads");
+  static_assert(MT * NQ <= 4, "one scale/zero word per lane covers a wave's share of a job");
+  static_assert(D % 2 == 0, "jobs are reduced in pairs");
+  constexpr int XB = MT == 2 ? 8 * MT * 4 * 64 : 1;  // second tile's fragments (MT = 4 runs one tile)
+  __shared__ __align__(16) f32x4 part[2][2][NQ][8][64];
+  __shared__ __align__(16) V xb[XB];
+  __shared__ int Rid[2][16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int NJ = p.N / (EPI == EPI_SILU ? 16 : 16 * NQ), KT = p.KT, szw = p.szw;  // jobs per tile
+  const int ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
+  const int J = ntiles * NJ;
+  const int lo = (int)((int64_t)blockIdx.x * J / gridDim.x), hi = (int)((int64_t)(blockIdx.x + 1) * J / gridDim.x);
+  if (lo >= hi) return;
+  const int n = hi - lo;
+  const int tA = lo / NJ, ntl = (hi - 1) / NJ - tA + 1;  // the range covers 1 or 2 tiles
+  const int tB = ntl > 1 ? tA + 1 : tA;
+
+  // ---- experts and row ids of the range's tiles: scalar loads, issued
+  // together; lane r16 keeps row r16 ----
+  const int r16 = lane & 15, kq = lane >> 4;
+  int exA = 0, exB = 0, rid[2];
+  if (p.rows != nullptr) {  // expert schedule (rows and tile_expert both set)
+    const int32_t* ra = p.rows + (int64_t)tA * 16;
+    const int32_t* rb = p.rows + (int64_t)tB * 16;
+    exA = p.tile_expert[tA];
+    exB = p.tile_expert[tB];
+    int va = -1, vb = -1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int sa = ra[r], sb = rb[r];
+      va = r16 == r ? sa : va;
+      vb = r16 == r ? sb : vb;
+    }
+    rid[0] = va;
+    rid[1] = vb;
+  } else {  // dense rows of one weight
+    rid[0] = tA * 16 + r16 < p.M ? tA * 16 + r16 : -1;
+    rid[1] = tB * 16 + r16 < p.M ? tB * 16 + r16 : -1;
+  }
+  if (wave == 0 && lane < 32) Rid[kq][r16] = kq == 0 ? rid[0] : rid[1];  // read after the first barrier
+  const int nvalid0 = (int)__popcll(__ballot(lane < 16 && rid[0] >= 0));
+  const int nvalid1 = (int)__popcll(__ballot(lane < 16 && rid[1] >= 0));
+
+  // ---- activation fragments (issued before the weights, so that waiting
+  // for them does not wait for the weight stream): a padding row reads the
+  // tile's first row, and k-tiles past K repeat the last one (padding rows
+  // are never stored, and those k-tiles get a zero scale) ----
+  V a[MT][4], b[MT][4];
+  {
+    const int rA = rid[0] >= 0 ? rid[0] : __shfl(rid[0], 0, 64);
+    const int rB = rid[1] >= 0 ? rid[1] : __shfl(rid[1], 0, 64);
+    const AT* xa = reinterpret_cast<const AT*>(p.x) + (int64_t)(rA / p.row_div) * p.ldx + 8 * kq;
+    const AT* xbp = reinterpret_cast<const AT*>(p.x) + (int64_t)(rB / p.row_div) * p.ldx + 8 * kq;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int kt = min(wave + 8 * m, KT - 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a[m][j] = *reinterpret_cast<const V*>(xa + kt * 128 + 32 * j);
+        if constexpr (MT == 2) b[m][j] = *reinterpret_cast<const V*>(xbp + kt * 128 + 32 * j);
+      }
+    }
+  }
+
+  // ---- the weight stream: a wave's share of one job is MT x NQ tiles (16 B
+  // per lane) and the scale/zero words of its k-tiles for the 16 columns of
+  // each quad (lane l: column l & 15, (m, q) pair l >> 4).  Every load is
+  // issued unconditionally, so that the compiler's count of loads in flight
+  // stays exact and each wait leaves the later jobs' loads in flight: a slot
+  // past the end of the range reads the first KiB of the weights (and the
+  // first words of the scales) instead, the same lines for every workgroup,
+  // which stay in L2 ----
+  const int zmq = (lane >> 4) < MT * NQ ? lane >> 4 : 0;
+  const int zq = zmq % NQ, zkt = min(wave + 8 * (zmq / NQ), KT - 1);
+  auto load = [&](int i, u32x4 (&w)[MT][NQ], uint32_t& z) {
+    const bool real = i < n;
+    const int job = lo + (real ? i : 0);
+    const int tl = job / NJ, nj = job - tl * NJ, e_x = tl == tA ? exA : exB;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int kt = min(wave + 8 * m, KT - 1);
+      const bool live = real && wave + 8 * m < KT;  // k-tiles past K: the hot line too
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const uint32_t* base = EPI == EPI_SILU && q == 1 ? p.w1 : p.w0;
+        int64_t off = (int64_t)e_x * p.w_es +
+                      ((int64_t)(EPI == EPI_SILU ? nj : nj * NQ + q) * KT + kt) * 256;
+        off = live ? off : 0;
+        // the select stays on the offset (the compiler would otherwise load
+        // from both addresses and select the data); the base keeps the
+        // pointer in the global address space
+        asm volatile("" : "+s"(off));
+        w[m][q] = *(reinterpret_cast<const u32x4*>(base + off) + lane);  // plain loads: faster than nontemporal here
+      }
+    }
+    const uint32_t* zbase = EPI == EPI_SILU && zq == 1 ? p.sz1 : p.sz0;
+    int64_t zoff = (int64_t)e_x * p.sz_es + ((int64_t)(EPI == EPI_SILU ? nj : nj * NQ + zq) * 16 + r16) * szw + zkt;
+    zoff = real ? zoff : lane;
+    asm volatile("" : "+v"(zoff));
+    z = zbase[zoff];
+  };
+  u32x4 wv[D][MT][NQ];
+  uint32_t zv[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, wv[d], zv[d]);
+
+  // park the second tile's fragments in LDS, group sums of the first
+  if constexpr (MT == 2) {
+    if (ntl > 1) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xb[((wave * MT + m) * 4 + j) * 64 + lane] = b[m][j];
+    }
+  }
+  const V ones = __builtin_bit_cast(V, u32x4{Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2, Act<AT>::kOne2});
+  f32x4 sx[MT];
+  auto group_sums = [&]() {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      sx[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sx[m] = mfma16(a[m][j], ones, sx[m]);
+    }
+  };
+  group_sums();
+
+  const uint32_t mask_s = p.nib_mask;
+  uint32_t magic_v = Act<AT>::kMagic2;
+  asm volatile("v_mov_b32 %0, %0" : "+v"(magic_v));  // keep the magic in a VGPR (far from any MFMA)
+
+  // this wave's share of a job's product (lane: rows 4*kq + i of column r16
+  // of each quad), the MT x NQ MFMA chains interleaved, into LDS
+  auto compute = [&](const u32x4 (&w)[MT][NQ], uint32_t z, int pp, int jj) {
+    f32x4 t[MT][NQ];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) t[m][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) t[m][q] = mfma16(a[m][j], dq_b3<AT>(w[m][q][j], mask_s, magic_v), t[m][q]);
+    f32x4 acc[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const bool live = wave + 8 * m < KT;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const uint32_t zz = (uint32_t)__shfl((int)z, (m * NQ + q) * 16 + r16, 64);
+        const float s = live ? sz_scale<ST>(zz) : 0.f, c = Act<AT>::kMagic + (float)(zz >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[q][i] = fmaf(s, fmaf(-c, sx[m][i], t[m][q][i]), acc[q][i]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) part[pp][jj][q][wave][lane] = acc[q];
+  };
+
+  // sum of the 8 waves' partials of one job (fixed order) and the store;
+  // thread u of the half-workgroup holds row 4*(l/16) + i4 of column l%16
+  auto reduce = [&](int job, int pp, int jj) {
+    const int tl = job / NJ, nj = job - tl * NJ, ts = tl == tA ? 0 : 1;
+    const int u = tid & 255, l = u >> 2, i4 = u & 3, row = 4 * (l >> 4) + i4;
+    if (row >= (ts == 0 ? nvalid0 : nvalid1)) return;
+    float pv[NQ][8];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int w = 0; w < 8; ++w) pv[q][w] = reinterpret_cast<const float*>(&part[pp][jj][q][w][l])[i4];
+    float v[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      float s = pv[q][0];
+#pragma unroll
+      for (int w = 1; w < 8; ++w) s += pv[q][w];
+      v[q] = s;
+    }
+    const int64_t o = (int64_t)Rid[ts][row] * p.ldy + (l & 15);
+    if constexpr (EPI == EPI_SILU) {
+      const float g = v[0], up = v[1];
+      store_val(p.y, o + nj * 16, g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * up, p.y_dtype);
+    } else {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) store_val(p.y, o + (nj * NQ + q) * 16, v[q], p.y_dtype);
+    }
+  };
+
+  // ---- the range's jobs: job i uses register set i % D, and its slot is
+  // refilled with job i + D right after; a barrier after every pair.  Whole
+  // blocks of D jobs first (loads without conditions), then the rest ----
+  const int iB = ntl > 1 ? (tA + 1) * NJ - lo : n;  // first job of the second tile
+  auto enter = [&](int i) {
+    if constexpr (MT == 2) {
+      if (i == iB) {  // the range moves on to its second tile
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[m][j] = xb[((wave * MT + m) * 4 + j) * 64 + lane];
+        group_sums();
+      }
+    }
+  };
+  auto pair_done = [&](int i) {  // jobs i - 1 and i are in LDS
+    lds_barrier();
+    const int jj = wave >> 2;
+    if (i - 1 + jj < n) reduce(lo + i - 1 + jj, (i >> 1) & 1, jj);
+  };
+  const int nfull = n / D * D;
+  for (int g = 0; g < nfull; g += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int i = g + d;
+      enter(i);
+      compute(wv[d], zv[d], (i >> 1) & 1, i & 1);
+      load(i + D, wv[d], zv[d]);
+      if (d & 1) pair_done(i);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int i = nfull + d;
+    if (i < n) {
+      enter(i);
+      compute(wv[d], zv[d], (i >> 1) & 1, i & 1);
+    }
+    if ((d & 1) && i - 1 < n) pair_done(i);
+  }
+}
+
+// Launch of the streaming kernel; tiles = 16-row tiles the grid is sized for
+// (at most one workgroup per compute unit, at most one tile change per range;
+// K > 2048 only for a single tile).
+template <int EPI>
+static int launch_stream(const W4SP& p, int nq, int x_bf16, int s_bf16, int64_t tiles, hipStream_t st);
+
 // ------------------------------------------------ prefill grouped GEMM --
 // For tiles with many rows (prefill; experts receiving tens to thousands of
 // tokens).  A workgroup of 8 waves computes a 128-row tile against 128
@@ -952,6 +1251,39 @@ static int device_cus() {
   return cus[dev];
 }
 
+template <typename AT, typename ST, int EPI>
+static void launch_stream_t(const W4SP& p, int nq, dim3 grid, hipStream_t st) {
+  const dim3 block(512);
+  const bool mt4 = p.KT > 16;
+  if (nq == 2)  // two quads: K <= 2048, two k-tiles per wave
+    hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
+  else if constexpr (EPI != EPI_SILU) {
+    if (mt4)
+      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 4, 1>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 1>), grid, block, 0, st, p);
+  }
+}
+
+template <int EPI>
+static int launch_stream(const W4SP& p, int nq, int x_bf16, int s_bf16, int64_t tiles, hipStream_t st) {
+  if (p.KT > 16 && (tiles != 1 || p.meta != nullptr)) return arg_error("w4 stream gemm: K > 2048 needs a single row tile");
+  const int64_t jobs = tiles * (p.N / (EPI == EPI_SILU ? 16 : 16 * nq)), cus = device_cus();
+  const dim3 grid((unsigned)(jobs < cus ? jobs : cus));
+  if (x_bf16) {
+    if (s_bf16)
+      launch_stream_t<__bf16, __bf16, EPI>(p, nq, grid, st);
+    else
+      launch_stream_t<__bf16, _Float16, EPI>(p, nq, grid, st);
+  } else {
+    if (s_bf16)
+      launch_stream_t<_Float16, __bf16, EPI>(p, nq, grid, st);
+    else
+      launch_stream_t<_Float16, _Float16, EPI>(p, nq, grid, st);
+  }
+  return launch_status("w4 stream gemm");
+}
+
 // tiles = schedule tiles the grid is sized for (the kernel reads the actual
 // number from meta); one persistent workgroup per compute unit at most.
 template <int EPI>
@@ -1125,6 +1457,28 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
     g.nib_mask = 0x000F000Fu;
     return launch_group_gemm<EPI_STORE>(g, x_dtype == CCQ_BF16, scale_dtype == CCQ_BF16, g.tiles, st);
   }
+  const int64_t szw_d = sz_words_per_column(K, group_size);
+  const int nq = stream_nq(EPI_STORE, N, K, group_size);
+  if (M <= 16 && nq > 0) {
+    // decode: one 16-row tile, weights streamed once
+    W4SP w = {};
+    w.x = x;
+    w.ldx = K;
+    w.row_div = 1;
+    w.tiles = 1;
+    w.w0 = (const uint32_t*)w_tiled;
+    w.sz0 = sz;
+    w.y = y;
+    w.ldy = N;
+    w.y_dtype = y_dtype;
+    w.M = (int)M;
+    w.N = (int)N;
+    w.K = (int)K;
+    w.KT = (int)(K / 128);
+    w.szw = (int)szw_d;
+    w.nib_mask = 0x000F000Fu;
+    return launch_stream<EPI_STORE>(w, nq, x_dtype == CCQ_BF16, scale_dtype == CCQ_BF16, 1, as_stream(stream));
+  }
   const int64_t tiles = cdiv(M, 16);
   const SkinnyPlan pl = plan_skinny(K, N, group_size, 1, gemm_nb(M));
   SkinnyP p = {};
@@ -1216,6 +1570,33 @@ MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes
   return L;
 }
 
+// The streaming kernel's parameters for a decode stage set up as SkinnyP.
+W4SP stream_params(const SkinnyP& p) {
+  W4SP w = {};
+  w.x = p.x;
+  w.ldx = p.ldx;
+  w.rows = p.rows;
+  w.row_div = p.row_div;
+  w.tile_expert = p.tile_expert;
+  w.meta = p.meta;
+  w.w0 = p.w0;
+  w.sz0 = p.sz0;
+  w.w1 = p.w1;
+  w.sz1 = p.sz1;
+  w.w_es = p.w_es;
+  w.sz_es = p.sz_es;
+  w.y = p.y;
+  w.ldy = p.ldy;
+  w.y_dtype = p.y_dtype;
+  w.M = p.M;
+  w.N = p.N;
+  w.K = p.K;
+  w.KT = p.KT;
+  w.szw = p.szw;
+  w.nib_mask = 0x000F000Fu;
+  return w;
+}
+
 SkinnyP grouped_params(const int32_t* sorted_ids, const int32_t* tile_expert, const int32_t* meta,
                        const ccq_w4_experts* ex) {
   SkinnyP p = {};
@@ -1245,6 +1626,11 @@ int run_gate_up(const void* x, int x_dtype, int64_t k, const int32_t* sorted_ids
   p.N = (int)I;
   p.K = (int)H;
   p.KT = (int)(H / 128);
+  const int nq = stream_nq(EPI_SILU, I, H, G);
+  if (nq > 0 && max_tiles <= device_cus()) {
+    const W4SP w = stream_params(p);
+    return launch_stream<EPI_SILU>(w, nq, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, max_tiles, st);
+  }
   const SkinnyPlan pl = plan_skinny(H, I, G, 2, 1);
   launch_skinny<EPI_SILU>(p, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
   return launch_status("moe_w4 gate_up");
@@ -1268,6 +1654,11 @@ int run_down(const void* inter, int x_dtype, const int32_t* sorted_ids, const in
   d.N = (int)H;
   d.K = (int)I;
   d.KT = (int)(I / 128);
+  const int nq = stream_nq(EPI_ROWS, H, I, G);
+  if (nq > 0 && max_tiles <= device_cus()) {
+    const W4SP w = stream_params(d);
+    return launch_stream<EPI_ROWS>(w, nq, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, max_tiles, st);
+  }
   const SkinnyPlan pl = plan_skinny(I, H, G, 1, 1);
   launch_skinny<EPI_ROWS>(d, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, pl, max_tiles, st, (int)G);
   return launch_status("moe_w4 down");
