@@ -431,7 +431,7 @@ def main():
                    "tokens": args.tokens, "experts": E, "top_k": TOPK, "hidden": HID, "inter": INTER,
                    "group": GROUP, "hip_graph": True},
         "frac_hbm_peak": round(head["GBps"] * 1e9 / PEAK_HBM, 4),
-        "roofline": {"bound": "hbm", "kernel": "w4_skinny_kernel<bf16,NB=1,G=128,SiLU> (MoE gate/up)",
+        "roofline": {"bound": "hbm", "kernel": "w4_stream_kernel<bf16,bf16,SiLU,MT=2,NQ=2> (MoE gate/up)",
                      "achieved": round(gu["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": round(gu["GBps"] * 1e9 / PEAK_HBM, 4), "avg_us": round(gu["avg_us"], 3),
                      "traffic": None},

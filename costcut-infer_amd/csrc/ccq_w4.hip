@@ -835,14 +835,16 @@ static int launch_stream(const W4SP& p, int nq, int x_bf16, int s_bf16, int64_t 
 // For tiles with many rows (prefill; experts receiving tens to thousands of
 // tokens).  A workgroup of 8 waves computes a 128-row tile against 128
 // columns of gate and of up (EPI_SILU) or 128 / 256 columns of one matrix.
-// The waves form a 2 (rows) x 4 (columns) grid, each owning 64 rows x 4
-// MFMA column tiles of 16, so every activation fragment read from LDS feeds
-// 4 MFMAs and every dequantized weight fragment 4 more.  Group size 128 is
-// one k-tile; per k-tile
-//     acc += s * (sum_k x * (MAGIC + q) - (MAGIC + z) * Sx)
+// The waves form a 2 (rows) x 4 (columns) grid, each owning 64 rows (two
+// 32-row tiles) x C32 tiles of 32 columns on v_mfma_f32_32x32x16, so every
+// activation fragment read from LDS feeds C32 MFMAs and every dequantized
+// weight fragment two.  Group size 128 is one k-tile; per k-tile
+//     acc += s * sum_k x * (MAGIC + q)  -  Sx * s * (MAGIC + z)
 // where Sx is the sum of the row's 128 activations of that group, computed
 // beforehand (row_group_sums_kernel for a layer input, the gate/up epilogue
-// for the intermediate rows).
+// for the intermediate rows).  The second term is a rank-1 update per
+// k-tile; two k-tiles' worth go in as one v_mfma_f32_32x32x2f32 (rows' -Sx
+// against columns' s * (MAGIC + z)) instead of a VALU FMA per element.
 //
 // Per k-tile the workgroup copies from HBM straight into LDS
 // (global_load_lds, no registers): the activation tile (128 rows x 256 B,

@@ -117,18 +117,21 @@ int ccq_awq_pack_sz(const int32_t* qzeros, const void* scales, int scale_dtype,
                     uint32_t* sz, int64_t K, int64_t N, int64_t group_size, void* stream);
 
 /* Workspace bytes ccq_w4_gemm needs for these sizes: 0 for the decode
- * kernel (M <= 64, or group_size != 128, or N % 128 != 0), else the
- * per-row group sums of x, M * K/128 floats (256-byte rounded). */
+ * kernels (M <= 64, or group_size != 128, or N % 128 != 0, or K < 256),
+ * else the per-row group sums of x (M * K/128 floats) and the row ids of
+ * the 128-row tiles, each 256-byte rounded. */
 size_t ccq_w4_gemm_workspace_size(int64_t M, int64_t K, int64_t N, int64_t group_size);
 
 /* y [M, N] = x [M, K] @ dequant(W) with fp32 accumulation.
  * x_dtype CCQ_F16 | CCQ_BF16; scale_dtype (of the scales packed in sz)
  * CCQ_F16 | CCQ_BF16; y_dtype CCQ_F16 | CCQ_BF16 | CCQ_F32.  w_tiled from
  * ccq_awq_repack, sz from ccq_awq_pack_sz.  group_size in {32, 64, 128}.
- * x, w_tiled and sz must be 16-byte aligned.  M <= 64: decode kernel (one
- * weight pass per 16 rows, no workspace); larger M with group 128 and
- * N % 128 == 0: the grouped MFMA kernel over 128-row tiles, which needs
- * ccq_w4_gemm_workspace_size bytes (256-byte aligned) of workspace.
+ * x, w_tiled and sz must be 16-byte aligned.  M <= 16 with group 128 and
+ * K <= 4096: the persistent streaming kernel (weights read once); other
+ * M <= 64: one workgroup per 16-row tile and column block (one weight pass
+ * per 16 rows); no workspace for either.  Larger M with group 128,
+ * N % 128 == 0 and K >= 256: the grouped MFMA kernel over 128-row tiles,
+ * which needs ccq_w4_gemm_workspace_size bytes (256-byte aligned).
  * Replaces WeightOnlyMethod.apply (quant/weight_only.py:37-54) for AWQ. */
 int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled,
                 const uint32_t* sz, int scale_dtype,
@@ -248,7 +251,8 @@ int ccq_fp8_block_unpack(const uint8_t* tiled, uint8_t* w, int64_t N, int64_t K,
 size_t ccq_fp8_block_linear_workspace_size(int64_t M, int64_t K);
 
 /* y [M, N] = dequant(act_quant(x)) @ W^T with fp32 accumulation;
- * K % 128 == 0, N % 128 == 0, w_tiled from ccq_fp8_block_repack. */
+ * K % 128 == 0 and K >= 256 (or K == 0), N % 128 == 0, w_tiled from
+ * ccq_fp8_block_repack. */
 int ccq_fp8_block_linear(const void* x, int x_dtype, const uint8_t* w_tiled,
                          const float* s_w, void* y, int y_dtype, int64_t M, int64_t K,
                          int64_t N, void* workspace, size_t workspace_bytes,
@@ -270,7 +274,8 @@ size_t ccq_moe_fp8_workspace_size(int64_t T, int64_t k, const ccq_fp8_experts* e
 /* Full MoE FFN on FP8 block experts: x [T, H] is quantized per token per
  * 128; gate/up + SiLU*up with the intermediate rounded to bf16 and
  * re-quantized per row per 128; down; weighted combine in slot order.
- * Tokens are grouped by expert into 64-row tiles (ccq_moe_align).
+ * Tokens are grouped by expert into 128-row tiles (ccq_moe_align);
+ * hidden and inter must be multiples of 128 and at least 256.
  * Replaces expert_ffn + moe_combine (blocks/moe.py:122-174) for FP8
  * experts, as called by moe_forward (models/generic.py:348-378). */
 int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights,
