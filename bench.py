@@ -163,7 +163,7 @@ def bench_moe(T: int, steps: int, warmup: int, dev):
 
     def step(i):
         l = layers[i % LAYERS]
-        ys[i % LAYERS].copy_(moe.moe_forward_w4(x, l.logits, l.experts, TOPK, True))
+        moe.moe_forward_w4(x, l.logits, l.experts, TOPK, True, out=ys[i % LAYERS])
 
     for i in range(warmup):
         step(i)

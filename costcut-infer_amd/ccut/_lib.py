@@ -79,6 +79,8 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_moe_w4_workspace_size": (_sz, [_i64, _i64, ctypes.POINTER(ccq_w4_experts)]),
     "ccq_moe_w4_ffn": (_int, [_vp, _int, _vp, _vp, _vp, _int, _i64, _i64,
                               ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
+    "ccq_moe_w4_forward": (_int, [_vp, _int, _vp, _i64, _i64, _int, _vp, _vp, _vp, _int,
+                                  ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
     "ccq_fp8_act_quant": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "ccq_fp8_block_repack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ccq_fp8_block_unpack": (_int, [_vp, _vp, _i64, _i64, _vp]),

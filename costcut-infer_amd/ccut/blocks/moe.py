@@ -282,13 +282,35 @@ def moe_ffn_w4(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, expert
 
 
 def moe_forward_w4(x: torch.Tensor, router_logits: torch.Tensor, experts: W4Experts, top_k: int,
-                   norm_topk_prob: bool = True, out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """Routed MoE layer on AWQ experts: ``topk_softmax`` then the fused FFN
-    (the compute of ``ExpertPipeline.step``, reference
+                   norm_topk_prob: bool = True, out_dtype: torch.dtype | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed MoE layer on AWQ experts: ``topk_softmax`` routing, expert
+    grouping, gate/up + SiLU, down and the weighted combine in one call of
+    ``ccq_moe_w4_forward`` (the compute of ``ExpertPipeline.step``, reference
     ``experts/pipeline.py:145-179``, and ``moe_forward``,
-    ``models/generic.py:361-378``)."""
-    w, ids = topk_softmax(router_logits, top_k, norm_topk_prob)
-    return moe_ffn_w4(x, ids, w, experts, out_dtype)
+    ``models/generic.py:361-378``).  Decode batches are routed inside the
+    gate/up kernel.  ``out``: optional [T, H] tensor to write (its dtype
+    wins over ``out_dtype``)."""
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"activations must be float16 or bfloat16, got {x.dtype}")
+    x = x.contiguous()
+    T, H = x.shape
+    if H != experts.hidden:
+        raise ValueError(f"x has {H} features, experts expect {experts.hidden}")
+    lg = _dev.to_device(router_logits, torch.float32).contiguous()
+    if lg.dim() != 2 or lg.shape[0] != T or lg.shape[1] != experts.num_experts:
+        raise ValueError(f"router logits must be [{T}, {experts.num_experts}], got {tuple(lg.shape)}")
+    if out is None:
+        out = torch.empty((T, H), dtype=out_dtype or x.dtype, device=x.device)
+    elif out.shape != (T, H) or not out.is_contiguous() or out.device != x.device:
+        raise ValueError(f"out must be a contiguous [{T}, {H}] tensor on {x.device}")
+    desc = experts.descriptor()
+    nbytes = lib().ccq_moe_w4_workspace_size(T, top_k, desc)
+    ws = _dev.workspace("moe_w4", nbytes, x.device)
+    mode = _MODE_TOPK_THEN_SOFTMAX if norm_topk_prob else _MODE_SOFTMAX_ALL
+    call("ccq_moe_w4_forward", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], lg.data_ptr(), T, top_k, mode, None, None,
+         out.data_ptr(), _dev.DTYPE_CODE[out.dtype], desc, ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -6,6 +6,7 @@
 // token grouping reference python/ccut/blocks/moe.py:163-173,
 //               python/ccut/models/generic.py:366-378
 #include "ccq_common.h"
+#include "ccq_topk.h"
 
 #include <math.h>
 
@@ -14,34 +15,7 @@ namespace ccq {
 constexpr int kMaxE = 1024;      // experts per row held in registers (16 per lane)
 constexpr int kMaxK = 16;
 
-// numpy's pairwise float32 summation of n <= 16 values, value j held by lane
-// j (other lanes hold 0): below 8 a plain running sum in index order;
-// otherwise 8 partial sums r[j] = a[j] (+ a[8+j] when n == 16) combined as
-// ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) -- float addition is commutative, so
-// the xor-shuffle tree forms exactly those sums -- then the tail in order.
-// The result is returned in every lane.
-__device__ float np_pairwise_sum16(float a, int n, int lane) {
-  if (n < 8) {
-    float res = 0.f;  // numpy starts from -0.0; identical for these (positive) inputs
-    for (int i = 0; i < n; ++i) res += __shfl(a, i, 64);
-    return res;
-  }
-  const int whole = n - (n % 8);  // 8 or 16
-  const float hi = __shfl(a, (lane + 8) & 63, 64);
-  float r = a + ((lane < 8 && 8 + lane < whole) ? hi : 0.f);
-  r += __shfl_xor(r, 1, 64);
-  r += __shfl_xor(r, 2, 64);
-  r += __shfl_xor(r, 4, 64);
-  float res = __shfl(r, 0, 64);
-  for (int i = whole; i < n; ++i) res += __shfl(a, i, 64);
-  return res;
-}
-
-// One wave per token row.  Lane l holds columns l, l+64, ... (PER values,
-// PER = ceil(E / 64) rounded up to 1, 2, 4 or 16); after selection pass j,
-// lane j holds slot j.  The code stays compact (a run-time loop over the k
-// passes, no per-slot arrays): the kernel runs on a handful of CUs, where a
-// large body costs more in cold instruction fetches than it saves.
+// One wave per token row (topk_row), 4 rows per workgroup.
 template <int PER>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restrict__ logits,
                                                            float* __restrict__ weights,
@@ -50,91 +24,12 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;
-  const float* lr = logits + row * E;
-  float v[PER];
-  bool used[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    int c = lane + 64 * i;
-    v[i] = c < E ? lr[c] : -INFINITY;
-    used[i] = c >= E;  // out-of-range slots never selectable
-  }
-  if (mode == 0) {
-    // p = exp(x - max) / max(sum, 1e-30) in float32 (blocks/moe.py:80-81)
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (!used[i]) m = fmaxf(m, v[i]);
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (!used[i]) {
-        v[i] = expf(v[i] - m);
-        s += v[i];
-      }
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-    const float d = fmaxf(s, 1e-30f);
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (!used[i]) v[i] = v[i] / d;
-  }
-  // k passes of "first value strictly greater than the running best" with the
-  // best starting at -1e30 (ties -> lowest column; NaN never picked).
-  float my_v = 0.f;
-  int my_i = 0;
-  for (int j = 0; j < k; ++j) {
-    float bv = -1.0e30f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      int c = lane + 64 * i;
-      if (!used[i] && v[i] > bv) {  // per lane columns are increasing
-        bv = v[i];
-        bi = c;
-      }
-    }
-    for (int off = 32; off >= 1; off >>= 1) {
-      float ov = __shfl_xor(bv, off, 64);
-      int oi = __shfl_xor(bi, off, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (bi == 0x7fffffff) {  // nothing > -1e30: reference stores (-1e30, -1)
-      bi = -1;                // and its used[-1] = 1 marks the last column
-      bv = -1.0e30f;
-    }
-    const int mark = bi >= 0 ? bi : E - 1;
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (lane + 64 * i == mark) used[i] = true;
-    if (lane == j) {
-      my_v = bv;
-      my_i = bi;
-    }
-  }
-  const bool mine = lane < k;
-  float w = my_v;  // modes 0 and 3: the selected values themselves
-  if (mode == 1) {
-    // v = vals - vals.max(); exp; / max(exp.sum(), 1e-30)  (blocks/moe.py:86-88)
-    float m = mine ? my_v : -INFINITY;
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    const float e = mine ? expf(my_v - m) : 0.f;
-    const float d = fmaxf(np_pairwise_sum16(e, k, lane), 1e-30f);
-    w = e / d;
-  } else if (mode == 2) {
-    // route_experts norm_topk=0: exp(v)/sum(exp(v)) with a float64 running sum
-    // (blocks/moe.py:114-118)
-    const float e = mine ? expf(my_v) : 0.f;
-    double s = 0.0;
-    for (int j = 0; j < k; ++j) s += (double)__shfl(e, j, 64);
-    w = s > 0.0 ? (float)((double)e / s) : 0.f;
-  }
-  if (mine) {
+  float w;
+  int id;
+  topk_row<PER>(logits + row * E, E, k, mode, w, id);
+  if (lane < k) {
     weights[row * k + lane] = w;
-    ids[row * k + lane] = my_i;
+    ids[row * k + lane] = id;
   }
 }
 

@@ -28,6 +28,7 @@
 // from one extra MFMA against a ones operand, already in the accumulator
 // layout.
 #include "ccq_common.h"
+#include "ccq_topk.h"
 
 #include <math.h>
 
@@ -569,7 +570,165 @@ struct W4SP {
   int y_dtype;
   int M, N, K, KT, szw;
   uint32_t nib_mask;           // 0x000F000F (a run-time value, see dq_b3)
+  // routing on the fly (EPI_SILU only): non-null logits [rT, rE] replace
+  // rows / tile_expert / meta; every workgroup routes the rT tokens itself
+  // and workgroup 0 writes the routing and the schedule for the next kernels
+  const float* logits;
+  int rT, rE, rk, rmode;
+  int64_t* ids_out;            // [rT, rk]
+  float* wts_out;              // [rT, rk]
+  int32_t* sched_rows;         // [tiles * 16], as ccq_moe_align's sorted_ids
+  int32_t* sched_tile_expert;  // [tiles]
+  int32_t* sched_meta;         // [2]
+  int32_t* sched_counts;       // [rE]
 };
+
+// ---- routing of a decode batch inside a workgroup ----
+// Top-k of every token (one wave per token, the routing kernel's own code,
+// on logits staged in LDS) and the expert schedule of ccq_moe_align with
+// 16-row tiles: experts in first-appearance order, each expert's
+// assignments ascending, tiles padded with -1.  Assignments are handled in
+// 64-lane chunks (one wave each): ballots over the expert id bits give each
+// assignment its rank among equal ids in the chunk, per-chunk counts give
+// the offsets across chunks.  Limits: RT_MAXN assignments, RT_MAXE experts,
+// RT_MAXLG logits.
+constexpr int RT_MAXN = 256;
+constexpr int RT_MAXE = 256;
+constexpr int RT_MAXLG = 4096;
+constexpr int RT_CHUNKS = RT_MAXN / 64;
+constexpr int RT_MAXTILES = RT_MAXN / 16 + RT_MAXN;  // ccq_moe_align_max_tiles(RT_MAXN, .., 16) at most
+struct RouteSmem {
+  float lg[RT_MAXLG];
+  int sid[RT_MAXN];  // expert of each assignment, -1 = dropped
+  int cnt[RT_MAXE], first[RT_MAXE], base[RT_MAXE], inv[RT_MAXE];
+  int ccnt[RT_CHUNKS][RT_MAXE];  // per-chunk counts
+  int nflags[RT_CHUNKS];
+  int sorted[RT_MAXTILES * 16];
+  int tile_expert[RT_MAXTILES];
+  int ntiles, nactive;
+};
+
+__device__ __forceinline__ int pad16(int c) { return (c + 15) & ~15; }
+
+// Lanes of the wave whose key equals this lane's (0 for invalid lanes).
+__device__ __forceinline__ uint64_t equal_keys(int key, bool valid, int nbits) {
+  uint64_t same = __ballot(valid);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t bal = __ballot(valid && bit);
+    same &= bit ? bal : ~bal;
+  }
+  return valid ? same : 0ull;
+}
+
+// Whole workgroup (blockDim.x = 512); ends with the schedule in rs and a
+// barrier.
+__device__ void route_decode(const W4SP& p, RouteSmem& rs) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int T = p.rT, E = p.rE, k = p.rk, n = T * k;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int e = tid; e < E; e += blockDim.x) {
+    rs.cnt[e] = 0;
+    rs.first[e] = 0x7fffffff;
+  }
+  for (int i = tid; i < RT_CHUNKS * RT_MAXE; i += blockDim.x) (&rs.ccnt[0][0])[i] = 0;
+  for (int i = tid; i < T * E; i += blockDim.x) rs.lg[i] = p.logits[i];
+  __syncthreads();
+  for (int t = wave; t < T; t += nw) {
+    float w;
+    int id;
+    const float* lr = rs.lg + t * E;
+    if (E <= 64)
+      topk_row<1>(lr, E, k, p.rmode, w, id);
+    else if (E <= 128)
+      topk_row<2>(lr, E, k, p.rmode, w, id);
+    else
+      topk_row<4>(lr, E, k, p.rmode, w, id);
+    if (lane < k) {
+      const int a = t * k + lane;
+      rs.sid[a] = id >= 0 && id < E ? id : -1;
+      if (blockIdx.x == 0) {
+        p.ids_out[a] = id;
+        p.wts_out[a] = w;
+      }
+    }
+  }
+  __syncthreads();
+  // chunk c = wave (c < RT_CHUNKS): assignment a = 64 c + lane
+  const bool chunk = wave < RT_CHUNKS && wave * 64 < n;
+  const int a = wave * 64 + lane;
+  const int e = chunk && a < n ? rs.sid[a] : -1;
+  const bool valid = e >= 0;
+  uint64_t same = 0;
+  int rnk = 0;
+  if (chunk) {
+    same = equal_keys(e, valid, nbits);
+    const uint64_t lower = same & ((1ull << lane) - 1ull);
+    rnk = __popcll(lower);
+    if (valid && lower == 0) {  // the lowest lane of each id in the chunk
+      rs.ccnt[wave][e] = __popcll(same);
+      atomicAdd(&rs.cnt[e], __popcll(same));
+      atomicMin(&rs.first[e], a);
+    }
+  }
+  __syncthreads();
+  // experts in first-appearance order: a flag at each expert's first assignment
+  const bool flag = valid && rs.first[e] == a;
+  const uint64_t fl = __ballot(flag);
+  if (chunk && lane == 0) rs.nflags[wave] = __popcll(fl);
+  __syncthreads();
+  if (chunk && flag) {
+    int before = 0;
+    for (int c = 0; c < wave; ++c) before += rs.nflags[c];
+    rs.inv[before + __popcll(fl & ((1ull << lane) - 1ull))] = e;
+  }
+  if (tid == 0) {
+    int na = 0;
+    for (int c = 0; c < RT_CHUNKS && c * 64 < n; ++c) na += rs.nflags[c];
+    rs.nactive = na;
+  }
+  __syncthreads();
+  if (wave == 0) {  // padded bases in first-appearance order
+    const int na = rs.nactive;
+    int carry = 0;
+    for (int r0 = 0; r0 < na; r0 += 64) {
+      const int r = r0 + lane;
+      const int pd = r < na ? pad16(rs.cnt[rs.inv[r]]) : 0;
+      int incl = pd;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      if (r < na) rs.base[rs.inv[r]] = carry + incl - pd;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) rs.ntiles = carry / 16;
+  }
+  __syncthreads();
+  if (valid) {
+    int off = rs.base[e] + rnk;
+    for (int c = 0; c < wave; ++c) off += rs.ccnt[c][e];
+    rs.sorted[off] = a;
+  }
+  for (int r = tid; r < rs.nactive; r += blockDim.x) {  // padding and tile -> expert
+    const int ex = rs.inv[r];
+    const int b = rs.base[ex], c = rs.cnt[ex], pd = pad16(c);
+    for (int j = c; j < pd; ++j) rs.sorted[b + j] = -1;
+    for (int t = b / 16; t < (b + pd) / 16; ++t) rs.tile_expert[t] = ex;
+  }
+  __syncthreads();
+  if (blockIdx.x == 0) {  // the schedule of the down and combine kernels
+    const int nt = rs.ntiles;
+    for (int i = tid; i < nt * 16; i += blockDim.x) p.sched_rows[i] = rs.sorted[i];
+    for (int i = tid; i < nt; i += blockDim.x) p.sched_tile_expert[i] = rs.tile_expert[i];
+    for (int x = tid; x < E; x += blockDim.x) p.sched_counts[x] = rs.cnt[x];
+    if (tid == 0) {
+      p.sched_meta[0] = nt;
+      p.sched_meta[1] = rs.nactive;
+    }
+  }
+}
 
 constexpr int WS_DEPTH = 2;  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
 
@@ -600,7 +759,21 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int NJ = p.N / (EPI == EPI_SILU ? 16 : 16 * NQ), KT = p.KT, szw = p.szw;  // jobs per tile
-  const int ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
+  // the routing scratch lives in the partial-sum buffer, unused until the
+  // first job
+  RouteSmem& rs = *reinterpret_cast<RouteSmem*>(&part[0][0][0][0][0]);
+  bool routed = false;
+  int ntiles;
+  if constexpr (EPI == EPI_SILU) {
+    static_assert(sizeof(RouteSmem) <= sizeof(part), "routing scratch");
+    routed = p.logits != nullptr;
+  }
+  if (routed) {
+    route_decode(p, rs);
+    ntiles = __builtin_amdgcn_readfirstlane(rs.ntiles);
+  } else {
+    ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
+  }
   const int J = ntiles * NJ;
   const int lo = (int)((int64_t)blockIdx.x * J / gridDim.x), hi = (int)((int64_t)(blockIdx.x + 1) * J / gridDim.x);
   if (lo >= hi) return;
@@ -612,7 +785,13 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // together; lane r16 keeps row r16 ----
   const int r16 = lane & 15, kq = lane >> 4;
   int exA = 0, exB = 0, rid[2];
-  if (p.rows != nullptr) {  // expert schedule (rows and tile_expert both set)
+  if (routed) {  // the schedule routed above, in LDS
+    exA = __builtin_amdgcn_readfirstlane(rs.tile_expert[tA]);
+    exB = __builtin_amdgcn_readfirstlane(rs.tile_expert[tB]);
+    rid[0] = rs.sorted[tA * 16 + r16];
+    rid[1] = rs.sorted[tB * 16 + r16];
+    lds_barrier();  // every wave has read it before the first job reuses the space
+  } else if (p.rows != nullptr) {  // expert schedule (rows and tile_expert both set)
     const int32_t* ra = p.rows + (int64_t)tA * 16;
     const int32_t* rb = p.rows + (int64_t)tB * 16;
     exA = p.tile_expert[tA];
@@ -724,34 +903,52 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
 
   // this wave's share of a job's product (lane: rows 4*kq + i of column r16
   // of each quad), the MT x NQ MFMA chains interleaved, into LDS
-  auto compute = [&](const u32x4 (&w)[MT][NQ], uint32_t z, int pp, int jj) {
+  // MM = this wave's live k-tiles (wave + 8 m < K/128): the MFMAs of the
+  // others are skipped (their loads still run, on the hot line), which frees
+  // the SIMD for the partner wave when K/128 is not a multiple of 8
+  auto compute_mm = [&](auto mm_tag, const u32x4 (&w)[MT][NQ], uint32_t z, int pp, int jj) {
+    constexpr int MM = decltype(mm_tag)::value;
     f32x4 t[MT][NQ];
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MM; ++m)
 #pragma unroll
       for (int q = 0; q < NQ; ++q) t[m][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
+      for (int m = 0; m < MM; ++m)
 #pragma unroll
         for (int q = 0; q < NQ; ++q) t[m][q] = mfma16(a[m][j], dq_b3<AT>(w[m][q][j], mask_s, magic_v), t[m][q]);
     f32x4 acc[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const bool live = wave + 8 * m < KT;
+    for (int m = 0; m < MM; ++m) {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         const uint32_t zz = (uint32_t)__shfl((int)z, (m * NQ + q) * 16 + r16, 64);
-        const float s = live ? sz_scale<ST>(zz) : 0.f, c = Act<AT>::kMagic + (float)(zz >> 16);
+        const float s = sz_scale<ST>(zz), c = Act<AT>::kMagic + (float)(zz >> 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[q][i] = fmaf(s, fmaf(-c, sx[m][i], t[m][q][i]), acc[q][i]);
       }
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) part[pp][jj][q][wave][lane] = acc[q];
+  };
+  const int mlive = min(MT, max(0, (KT - wave + 7) / 8));  // wave-uniform
+  auto compute = [&](const u32x4 (&w)[MT][NQ], uint32_t z, int pp, int jj) {
+    if (mlive == MT)
+      compute_mm(std::integral_constant<int, MT>{}, w, z, pp, jj);
+    else if (mlive == 1)
+      compute_mm(std::integral_constant<int, 1>{}, w, z, pp, jj);
+    else if (mlive == 0)
+      compute_mm(std::integral_constant<int, 0>{}, w, z, pp, jj);
+    else if constexpr (MT == 4) {
+      if (mlive == 2)
+        compute_mm(std::integral_constant<int, 2>{}, w, z, pp, jj);
+      else
+        compute_mm(std::integral_constant<int, 3>{}, w, z, pp, jj);
+    }
   };
 
   // sum of the 8 waves' partials of one job (fixed order) and the store;
@@ -1539,7 +1736,8 @@ struct MoeLayout {
   int64_t n, max_tiles;
   int tile_m;       // rows per schedule tile: 16 (decode kernel) or 128 (grouped kernel)
   bool grouped;
-  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, off_sx, off_sxh, total;
+  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, off_sx, off_sxh, off_ids, off_wts,
+      total;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes) {
@@ -1568,6 +1766,10 @@ MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes
     L.off_sxh = o;
     o += align256((size_t)L.n * (ex->inter / 128) * 4);
   }
+  L.off_ids = o;  // routing of ccq_moe_w4_forward when the caller keeps none
+  o += align256((size_t)L.n * 8);
+  L.off_wts = o;
+  o += align256((size_t)L.n * 4);
   L.total = o;
   return L;
 }
@@ -1809,4 +2011,89 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
   // row write and of the combine's read)
   return launch_combine(rows, L.grouped ? CCQ_BF16 : CCQ_F32, weights, ids, ex->num_experts, y, y_dtype, T, k,
                         ex->hidden, st);
+}
+
+// Whether a decode batch routes inside the gate/up kernel: the streaming
+// kernels take both stages and the batch fits the in-workgroup router.
+static bool fused_route(const MoeLayout& L, const ccq_w4_experts* ex, int64_t k) {
+  const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
+  return !L.grouped && L.n <= RT_MAXN && ex->num_experts <= RT_MAXE && k <= 16 &&
+         L.n / k * ex->num_experts <= RT_MAXLG &&
+         stream_nq(EPI_SILU, I, H, G) > 0 && stream_nq(EPI_ROWS, H, I, G) > 0 && L.max_tiles <= device_cus() &&
+         L.max_tiles <= RT_MAXTILES;
+}
+
+extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k, int mode,
+                                  int64_t* ids_out, float* weights_out, void* y, int y_dtype,
+                                  const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_experts(ex, "ccq_moe_w4_forward");
+  if (rc) return rc;
+  CCQ_REQUIRE(T >= 0 && k >= 1 && k <= 16 && k <= ex->num_experts, "ccq_moe_w4_forward: bad T=%lld / k=%lld",
+              (long long)T, (long long)k);
+  CCQ_REQUIRE(mode >= 0 && mode <= 3, "ccq_moe_w4_forward: mode=%d not in {0,1,2,3}", mode);
+  CCQ_REQUIRE(T * k <= 65536 && T <= 65535, "ccq_moe_w4_forward: T=%lld too large", (long long)T);
+  CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_moe_w4_forward: x_dtype must be f16|bf16");
+  CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_moe_w4_forward: bad y_dtype");
+  if (T == 0) return 0;
+  CCQ_REQUIRE(x && logits && y, "ccq_moe_w4_forward: null pointer");
+  rc = check_expert_ptrs(ex, true, "ccq_moe_w4_forward");
+  if (rc) return rc;
+  rc = check_expert_ptrs(ex, false, "ccq_moe_w4_forward");
+  if (rc) return rc;
+  CCQ_REQUIRE(aligned(x, 16), "ccq_moe_w4_forward: x must be 16-byte aligned");
+  const MoeLayout L = moe_layout(T, k, ex, 2);
+  CCQ_REQUIRE(workspace && workspace_bytes >= L.total && aligned(workspace, 256),
+              "ccq_moe_w4_forward: workspace of %zu bytes (256-byte aligned) needed, %zu given", L.total,
+              workspace_bytes);
+  hipStream_t st = as_stream(stream);
+  char* ws = (char*)workspace;
+  int64_t* ids = ids_out != nullptr ? ids_out : (int64_t*)(ws + L.off_ids);
+  float* wts = weights_out != nullptr ? weights_out : (float*)(ws + L.off_wts);
+  if (!fused_route(L, ex, k)) {  // separate routing kernel, then the FFN
+    rc = ccq_topk_softmax(logits, wts, ids, T, ex->num_experts, k, mode, stream);
+    if (rc) return rc;
+    return ccq_moe_w4_ffn(x, x_dtype, ids, wts, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream);
+  }
+  const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
+  int32_t* sorted = (int32_t*)(ws + L.off_sorted);
+  int32_t* tile_expert = (int32_t*)(ws + L.off_tile_expert);
+  int32_t* meta = (int32_t*)(ws + L.off_meta);
+  int32_t* counts = (int32_t*)(ws + L.off_counts);
+  void* inter = ws + L.off_inter;
+  float* rows = (float*)(ws + L.off_rows);
+  // gate/up + SiLU with the routing done inside its workgroups
+  W4SP w = {};
+  w.x = x;
+  w.ldx = H;
+  w.row_div = (int)k;
+  w.w0 = (const uint32_t*)ex->w_gate;
+  w.sz0 = ex->sz_gate;
+  w.w1 = (const uint32_t*)ex->w_up;
+  w.sz1 = ex->sz_up;
+  w.szw = (int)sz_words_per_column(H, G);
+  w.w_es = H * I / 8;
+  w.sz_es = I * w.szw;
+  w.y = inter;
+  w.ldy = I;
+  w.y_dtype = x_dtype;
+  w.N = (int)I;
+  w.K = (int)H;
+  w.KT = (int)(H / 128);
+  w.nib_mask = 0x000F000Fu;
+  w.logits = logits;
+  w.rT = (int)T;
+  w.rE = (int)ex->num_experts;
+  w.rk = (int)k;
+  w.rmode = mode;
+  w.ids_out = ids;
+  w.wts_out = wts;
+  w.sched_rows = sorted;
+  w.sched_tile_expert = tile_expert;
+  w.sched_meta = meta;
+  w.sched_counts = counts;
+  rc = launch_stream<EPI_SILU>(w, 2, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.max_tiles, st);
+  if (rc) return rc;
+  rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
+  if (rc) return rc;
+  return launch_combine(rows, CCQ_F32, wts, ids, ex->num_experts, y, y_dtype, T, k, H, st);
 }

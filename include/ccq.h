@@ -221,6 +221,20 @@ int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* 
                    const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* The MoE layer from router logits: routing (ccq_topk_softmax, mode as
+ * there) + ccq_moe_w4_ffn in one call.  logits [T, E] f32 with
+ * E = ex->num_experts; ids_out [T, k] int64 and weights_out [T, k] f32
+ * receive the routing (either may be null: the workspace keeps it);
+ * workspace as ccq_moe_w4_ffn.  Decode batches (T*k <= 256, E <= 256, T*E <= 4096,
+ * k <= 16) route inside the gate/up kernel's workgroups (three launches in
+ * all); larger ones run the routing kernel and ccq_moe_w4_ffn.  Same results
+ * either way.  Replaces moe_forward (models/generic.py:348-378): topk_softmax
+ * + expert grouping + expert_ffn + combine. */
+int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
+                       int mode, int64_t* ids_out, float* weights_out, void* y, int y_dtype,
+                       const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 
 /* ------------------------------------------------------------------------
  * FP8 e4m3fn with 128x128 block weight scales (w [N, K] bytes, row = output

@@ -73,8 +73,8 @@ def test_moe_w4_decode_config(gpu, T):
 
 @pytest.mark.parametrize("T,k,E", [(64, 2, 8), (200, 2, 8), (96, 4, 6)])
 def test_moe_w4_grouped_prefill(gpu, T, k, E):
-    """Experts averaging >= 16 rows take the grouped prefill kernel (64-row
-    tiles below 32 rows per expert, 128-row above)."""
+    """Experts averaging >= 16 rows take the grouped prefill kernel
+    (128-row tiles)."""
     assert _run(gpu, E=E, H=256, I=384, G=128, T=T, k=k, seed=T + E) <= TOL
 
 
@@ -82,6 +82,53 @@ def test_moe_w4_prefill_skewed_router(gpu):
     """Skewed router (per-expert bias N(0, 2)): hot experts span many tiles,
     cold ones get a few rows; hidden 2048, inter 768, 32 experts, top-8."""
     assert _run(gpu, E=32, H=2048, I=768, G=128, T=160, k=8, seed=5, skew=2.0, ydt=torch.bfloat16) <= TOL
+
+
+@pytest.mark.parametrize("E,H,I,T,k,norm", [(8, 256, 384, 3, 2, True), (4, 256, 384, 40, 2, True),
+                                             (8, 256, 384, 16, 2, False), (64, 2048, 1408, 1, 6, True),
+                                             (64, 2048, 1408, 16, 6, True), (8, 256, 384, 200, 2, True)])
+def test_moe_w4_forward_matches_routed_ffn(gpu, E, H, I, T, k, norm):
+    """ccq_moe_w4_forward from router logits -- routed inside the gate/up
+    kernel's workgroups for decode batches (T*k <= 256), by the routing
+    kernel otherwise -- gives routing ids and weights bit-identical to
+    ccq_topk_softmax and an output bit-identical to ccq_moe_w4_ffn on that
+    routing (same kernels, same summation order).  E=4, T=40 puts more than
+    16 rows on experts (several tiles each); T=200 takes the unfused path."""
+    import ctypes
+
+    from ccut import _dev, _lib
+    from ccut.blocks import moe
+
+    G = 128
+    gate, up, down = _experts(E, H, I, G, seed=E + T)
+    dev = lambda t: tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(dev(gate), dev(up), dev(down), group_size=G)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16).to(gpu)
+    lg = torch.randn((T, E), generator=g).to(gpu)
+    w_ref, ids_ref = moe.topk_softmax(lg, k, norm)
+    y_ref = moe.moe_ffn_w4(x, ids_ref, w_ref, ex, out_dtype=torch.bfloat16)
+
+    lib = _lib.lib()
+    desc = ex.descriptor()
+    nbytes = lib.ccq_moe_w4_workspace_size(T, k, desc)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    ids = torch.full((T, k), -7, dtype=torch.int64, device=gpu)
+    w = torch.full((T, k), -7.0, dtype=torch.float32, device=gpu)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
+    rc = lib.ccq_moe_w4_forward(ctypes.c_void_p(x.data_ptr()), _lib.CCQ_BF16, ctypes.c_void_p(lg.data_ptr()), T, k,
+                                1 if norm else 0, ctypes.c_void_p(ids.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                                ctypes.c_void_p(y.data_ptr()), _lib.CCQ_BF16, ctypes.byref(desc),
+                                ctypes.c_void_p(ws.data_ptr()), nbytes, ctypes.c_void_p(_dev.stream_ptr(gpu)))
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids_ref)
+    assert torch.equal(w, w_ref)
+    assert torch.equal(y, y_ref)
+    # and through the Python front end, into a caller's output tensor
+    out = torch.empty_like(y)
+    assert moe.moe_forward_w4(x, lg, ex, k, norm, out=out) is out
+    assert torch.equal(out, y_ref)
 
 
 def test_moe_combine_api_with_expert_fn(gpu):
