@@ -25,7 +25,9 @@
 namespace ccq {
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
-                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st);
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch = nullptr,
+                 size_t scratch_bytes = 0);
+size_t align_scratch_bytes(int64_t n, int64_t E);
 int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
                    int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st);
 
@@ -619,7 +621,7 @@ int check_fp8_experts(const ccq_fp8_experts* ex, const char* name) {
 struct F8MoeLayout {
   int64_t n, max_tiles;
   int bm;
-  size_t off_sorted, off_te, off_meta, off_counts, off_qx, off_sx, off_qh, off_sh, off_rows, total;
+  size_t off_sorted, off_te, off_meta, off_counts, off_qx, off_sx, off_qh, off_sh, off_rows, off_align, total;
 };
 
 F8MoeLayout f8_moe_layout(int64_t T, int64_t k, const ccq_fp8_experts* ex) {
@@ -647,6 +649,8 @@ F8MoeLayout f8_moe_layout(int64_t T, int64_t k, const ccq_fp8_experts* ex) {
   o += a256((size_t)L.n * (I / 128) * 4);
   L.off_rows = o;
   o += a256((size_t)L.n * H * 4);
+  L.off_align = o;  // per-chunk tables of the schedule of large batches
+  o += a256(align_scratch_bytes(L.n, ex->num_experts));
   L.total = o;
   return L;
 }
@@ -690,7 +694,8 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   float* sh = (float*)(ws + L.off_sh);
   void* rows = ws + L.off_rows;
 
-  rc = launch_align(ids, L.n, ex->num_experts, L.bm, sorted, te, meta, counts, st);
+  rc = launch_align(ids, L.n, ex->num_experts, L.bm, sorted, te, meta, counts, st, ws + L.off_align,
+                    L.total - L.off_align);
   if (rc) return rc;
   rc = launch_act_quant(x, x_dtype, H, T, H, qx, H, sx, H / 128, st);
   if (rc) return rc;

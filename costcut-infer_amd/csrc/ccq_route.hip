@@ -304,11 +304,211 @@ int launch_combine(const void* rows, int rows_dtype, const float* wts, const int
   return launch_status("moe_combine");
 }
 
+// ----------------------------------------------------------------------------
+// moe_align for large batches, over many workgroups: the same schedule as
+// moe_align_kernel.  The assignments are cut into chunks of kChunk; a chunk
+// is one workgroup of 4 waves, wave w owning the contiguous quarter
+// [w*kChunk/4, (w+1)*kChunk/4) in 64-lane steps, so "chunk, wave, step,
+// lane" order is the global order.
+//  1. align_chunk_count: per chunk and expert, the count and the first index;
+//  2. align_plan (one workgroup): totals, expert order by first appearance,
+//     padded bases, meta / counts / tile_expert and the padding entries;
+//  3. align_chunk_scatter: each assignment's slot = base + the counts of
+//     the earlier chunks + offset of its wave in the chunk + rank among
+//     equal ids before it.
+// The scratch holds two [chunks][E] tables.
+// ----------------------------------------------------------------------------
+constexpr int kChunk = 1024;
+
+// Chunk id-match ranks of one 64-lane step: lanes with equal expert ids.
+__device__ __forceinline__ uint64_t step_match(const int64_t* ids, int a, int n, int E, int nbits, int& e) {
+  const int64_t v = a < n ? ids[a] : -1;
+  e = (v >= 0 && v < E) ? (int)v : -1;
+  return match_key(e, e >= 0, nbits);
+}
+
+__global__ __launch_bounds__(256) void align_chunk_count_kernel(const int64_t* __restrict__ ids, int n, int E,
+                                                                int32_t* __restrict__ ccnt,
+                                                                int32_t* __restrict__ cfirst) {
+  __shared__ int cnt[kMaxE], first[kMaxE];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = blockIdx.x;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int e = tid; e < E; e += 256) {
+    cnt[e] = 0;
+    first[e] = 0x7fffffff;
+  }
+  __syncthreads();
+  const int q0 = c * kChunk + w * (kChunk / 4);
+  for (int s = 0; s < kChunk / 4; s += 64) {
+    const int a = q0 + s + lane;
+    int e;
+    const uint64_t same = step_match(ids, a, n, E, nbits, e);
+    if (e >= 0 && (same & ((1ull << lane) - 1ull)) == 0) {  // lowest lane of its id
+      atomicAdd(&cnt[e], __popcll(same));
+      atomicMin(&first[e], a);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) {
+    ccnt[(int64_t)c * E + e] = cnt[e];
+    cfirst[(int64_t)c * E + e] = first[e];
+  }
+}
+
+__global__ __launch_bounds__(1024) void align_plan_kernel(int E, int nchunks, int tile_m,
+                                                          const int32_t* __restrict__ ccnt,
+                                                          int32_t* __restrict__ cfirst, int32_t* __restrict__ sorted_ids,
+                                                          int32_t* __restrict__ tile_expert, int32_t* __restrict__ meta,
+                                                          int32_t* __restrict__ counts_out) {
+  __shared__ int cnt[kMaxE], base[kMaxE], inv[kMaxE];
+  __shared__ __align__(16) int key[kMaxE];  // first appearance, INT_MAX for unused experts
+  __shared__ int nactive;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int e = tid; e < E; e += 1024) {  // loads only, 16 chunks in flight
+    int run = 0, f = 0x7fffffff;
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+      int x[16], y[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const bool in = c0 + u < nchunks;
+        x[u] = in ? ccnt[(int64_t)(c0 + u) * E + e] : 0;
+        y[u] = in ? cfirst[(int64_t)(c0 + u) * E + e] : 0x7fffffff;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        run += x[u];
+        f = min(f, y[u]);
+      }
+    }
+    cnt[e] = run;
+    key[e] = run > 0 ? f : 0x7fffffff;
+    counts_out[e] = run;
+  }
+  for (int e = E + tid; e < ((E + 3) & ~3); e += 1024) key[e] = 0x7fffffff;  // whole 16-byte reads below
+  __syncthreads();
+  // order of first appearance: the number of used experts that appear
+  // earlier (first appearances are distinct), four keys per LDS read
+  for (int e = tid; e < E; e += 1024) {
+    const int f = key[e];
+    if (f != 0x7fffffff) {
+      int r = 0;
+      for (int e2 = 0; e2 < E; e2 += 4) {
+        const int4 k4 = *reinterpret_cast<const int4*>(&key[e2]);
+        r += (k4.x < f) + (k4.y < f) + (k4.z < f) + (k4.w < f);
+      }
+      inv[r] = e;
+    }
+  }
+  if (w == 0) {
+    int na = 0;
+    for (int e = lane; e < E; e += 64) na += key[e] != 0x7fffffff ? 1 : 0;
+    for (int off = 32; off >= 1; off >>= 1) na += __shfl_xor(na, off, 64);
+    if (lane == 0) nactive = na;
+  }
+  __syncthreads();
+  const int na = nactive;
+  if (w == 0) {  // padded bases in rank order
+    int carry = 0;
+    for (int r0 = 0; r0 < na; r0 += 64) {
+      const int r = r0 + lane;
+      int p = 0;
+      if (r < na) p = (int)cdiv(cnt[inv[r]], tile_m) * tile_m;
+      int incl = p;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      if (r < na) base[inv[r]] = carry + incl - p;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) {
+      meta[0] = carry / tile_m;
+      meta[1] = na;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) cfirst[e] = cnt[e] > 0 ? base[e] : 0;  // row 0 of the table: the bases
+  for (int r = w; r < na; r += 16) {  // padding and tile -> expert: one wave per expert
+    const int e = inv[r];
+    const int b = base[e], c = cnt[e];
+    const int p = (int)cdiv(c, tile_m) * tile_m;
+    for (int j = c + lane; j < p; j += 64) sorted_ids[b + j] = -1;
+    for (int t = b / tile_m + lane; t < (b + p) / tile_m; t += 64) tile_expert[t] = e;
+  }
+}
+
+__global__ __launch_bounds__(256) void align_chunk_scatter_kernel(const int64_t* __restrict__ ids, int n, int E,
+                                                                  const int32_t* __restrict__ ccnt,
+                                                                  const int32_t* __restrict__ base,
+                                                                  int32_t* __restrict__ sorted_ids) {
+  __shared__ int woff[4][kMaxE];  // per wave: ids counted so far (then: offset of the wave's quarter)
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = blockIdx.x;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int i = tid; i < 4 * E; i += 256) woff[i / E][i % E] = 0;
+  __syncthreads();
+  const int q0 = c * kChunk + w * (kChunk / 4);
+  for (int s = 0; s < kChunk / 4; s += 64) {  // per-wave counts of the quarter
+    const int a = q0 + s + lane;
+    int e;
+    const uint64_t same = step_match(ids, a, n, E, nbits, e);
+    if (e >= 0 && (same & ((1ull << lane) - 1ull)) == 0) woff[w][e] += __popcll(same);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) {  // base + earlier chunks' counts, then the 4 quarters
+    int run = base[e];
+    for (int c0 = 0; c0 < c; c0 += 16) {
+      int x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = c0 + u < c ? ccnt[(int64_t)(c0 + u) * E + e] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) run += x[u];
+    }
+    for (int q = 0; q < 4; ++q) {
+      const int x = woff[q][e];
+      woff[q][e] = run;
+      run += x;
+    }
+  }
+  __syncthreads();
+  for (int s = 0; s < kChunk / 4; s += 64) {
+    const int a = q0 + s + lane;
+    int e;
+    const uint64_t same = step_match(ids, a, n, E, nbits, e);
+    const int r = __popcll(same & ((1ull << lane) - 1ull));
+    int off = 0;
+    if (e >= 0) off = woff[w][e];
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0) {
+      sorted_ids[off + r] = a;
+      if (r == 0) woff[w][e] = off + __popcll(same);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+size_t align_scratch_bytes(int64_t n, int64_t E) { return (size_t)2 * cdiv(n, kChunk) * E * 4; }
+
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
-                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
-                     tile_expert, meta, counts);
-  return launch_status("moe_align");
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
+                 size_t scratch_bytes) {
+  const int64_t nchunks = cdiv(n, kChunk);
+  // below ~6K assignments one workgroup is faster than three launches
+  if (scratch == nullptr || n <= 3 * kChunk || scratch_bytes < align_scratch_bytes(n, E)) {
+    hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
+                       tile_expert, meta, counts);
+    return launch_status("moe_align");
+  }
+  int32_t* ccnt = (int32_t*)scratch;
+  int32_t* cfirst = ccnt + nchunks * E;
+  hipLaunchKernelGGL(align_chunk_count_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
+                     cfirst);
+  hipLaunchKernelGGL(align_plan_kernel, dim3(1), dim3(1024), 0, st, (int)E, (int)nchunks, (int)tile_m, ccnt, cfirst,
+                     sorted_ids, tile_expert, meta, counts);
+  hipLaunchKernelGGL(align_chunk_scatter_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
+                     cfirst, sorted_ids);
+  return launch_status("moe_align (chunked)");
 }
 
 }  // namespace ccq
@@ -355,7 +555,7 @@ extern "C" int ccq_moe_align(const int64_t* ids, int64_t num_assignments, int64_
   CCQ_REQUIRE(meta && counts && (num_assignments == 0 || (ids && sorted_ids && tile_expert)),
               "ccq_moe_align: null pointer");
   return launch_align(ids, num_assignments, num_experts, tile_m, sorted_ids, tile_expert, meta, counts,
-                      as_stream(stream));
+                      as_stream(stream), nullptr, 0);
 }
 
 extern "C" int ccq_moe_combine(const float* rows, const float* weights, void* y, int y_dtype, int64_t T, int64_t k,

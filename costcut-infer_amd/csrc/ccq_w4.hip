@@ -37,7 +37,9 @@
 namespace ccq {
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
-                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st);
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch = nullptr,
+                 size_t scratch_bytes = 0);
+size_t align_scratch_bytes(int64_t n, int64_t E);
 int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
                    int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st);
 
@@ -903,9 +905,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
 
   // this wave's share of a job's product (lane: rows 4*kq + i of column r16
   // of each quad), the MT x NQ MFMA chains interleaved, into LDS
-  // MM = this wave's live k-tiles (wave + 8 m < K/128): the MFMAs of the
-  // others are skipped (their loads still run, on the hot line), which frees
-  // the SIMD for the partner wave when K/128 is not a multiple of 8
+  // the first MM of the wave's MT k-tiles, those past K/128 with a zero
+  // scale (their loads read the hot line)
   auto compute_mm = [&](auto mm_tag, const u32x4 (&w)[MT][NQ], uint32_t z, int pp, int jj) {
     constexpr int MM = decltype(mm_tag)::value;
     f32x4 t[MT][NQ];
@@ -924,10 +925,11 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     for (int q = 0; q < NQ; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
+      const bool live = wave + 8 * m < KT;
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         const uint32_t zz = (uint32_t)__shfl((int)z, (m * NQ + q) * 16 + r16, 64);
-        const float s = sz_scale<ST>(zz), c = Act<AT>::kMagic + (float)(zz >> 16);
+        const float s = live ? sz_scale<ST>(zz) : 0.f, c = Act<AT>::kMagic + (float)(zz >> 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[q][i] = fmaf(s, fmaf(-c, sx[m][i], t[m][q][i]), acc[q][i]);
       }
@@ -935,20 +937,15 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) part[pp][jj][q][wave][lane] = acc[q];
   };
-  const int mlive = min(MT, max(0, (KT - wave + 7) / 8));  // wave-uniform
+  // a wave whose second k-tile lies past K (K/128 not a multiple of 8, two
+  // k-tiles per wave) skips its MFMAs, which frees the SIMD for the partner
+  // wave
+  const bool one_live = MT == 2 && wave + 8 >= KT;  // wave-uniform
   auto compute = [&](const u32x4 (&w)[MT][NQ], uint32_t z, int pp, int jj) {
-    if (mlive == MT)
-      compute_mm(std::integral_constant<int, MT>{}, w, z, pp, jj);
-    else if (mlive == 1)
+    if (one_live)
       compute_mm(std::integral_constant<int, 1>{}, w, z, pp, jj);
-    else if (mlive == 0)
-      compute_mm(std::integral_constant<int, 0>{}, w, z, pp, jj);
-    else if constexpr (MT == 4) {
-      if (mlive == 2)
-        compute_mm(std::integral_constant<int, 2>{}, w, z, pp, jj);
-      else
-        compute_mm(std::integral_constant<int, 3>{}, w, z, pp, jj);
-    }
+    else
+      compute_mm(std::integral_constant<int, MT>{}, w, z, pp, jj);
   };
 
   // sum of the 8 waves' partials of one job (fixed order) and the store;
@@ -1737,7 +1734,7 @@ struct MoeLayout {
   int tile_m;       // rows per schedule tile: 16 (decode kernel) or 128 (grouped kernel)
   bool grouped;
   size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, off_sx, off_sxh, off_ids, off_wts,
-      total;
+      off_align, total;
 };
 
 MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes) {
@@ -1770,6 +1767,8 @@ MoeLayout moe_layout(int64_t T, int64_t k, const ccq_w4_experts* ex, int x_bytes
   o += align256((size_t)L.n * 8);
   L.off_wts = o;
   o += align256((size_t)L.n * 4);
+  L.off_align = o;  // per-chunk tables of the schedule of large batches
+  o += align256(align_scratch_bytes(L.n, ex->num_experts));
   L.total = o;
   return L;
 }
@@ -1941,7 +1940,8 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
   float* rows = (float*)(ws + L.off_rows);
 
   CCQ_REQUIRE(L.max_tiles * 2 <= 65535, "ccq_moe_w4_ffn: too many tiles");
-  rc = launch_align(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st);
+  rc = launch_align(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st, ws + L.off_align,
+                    L.total - L.off_align);
   if (rc) return rc;
   if (L.grouped) {
     const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;

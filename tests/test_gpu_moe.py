@@ -131,6 +131,62 @@ def test_moe_w4_forward_matches_routed_ffn(gpu, E, H, I, T, k, norm):
     assert torch.equal(out, y_ref)
 
 
+def test_moe_w4_large_batch_schedule_matches_align(gpu):
+    """8192 assignments (T=1024, top-8, skewed router): the FFN builds its
+    expert schedule over many workgroups (per-chunk counts, plan, scatter);
+    the schedule it leaves at the head of its workspace is bit-identical to
+    the single-workgroup ccq_moe_align on the same ids, and the output
+    matches the oracle."""
+    import ctypes
+
+    from ccut import _dev, _lib
+    from ccut.blocks import moe
+
+    E, H, I, G, T, k = 32, 256, 256, 128, 1024, 8
+    gate, up, down = _experts(E, H, I, G, seed=11)
+    dev = lambda t: tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(dev(gate), dev(up), dev(down), group_size=G)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    lg = torch.randn((T, E), generator=g) + torch.randn((1, E), generator=g) * 2.0
+    w, ids = moe.topk_softmax(lg.to(gpu), k, True)
+    lib = _lib.lib()
+    desc = ex.descriptor()
+    nbytes = lib.ccq_moe_w4_workspace_size(T, k, desc)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    y = torch.empty((T, H), dtype=torch.float32, device=gpu)
+    xd = x.to(gpu)
+    rc = lib.ccq_moe_w4_ffn(ctypes.c_void_p(xd.data_ptr()), _lib.CCQ_BF16, ctypes.c_void_p(ids.data_ptr()),
+                            ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(y.data_ptr()), _lib.CCQ_F32, T, k,
+                            ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), nbytes,
+                            ctypes.c_void_p(_dev.stream_ptr(gpu)))
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    ref = moe.moe_align(ids, E, 128)  # single workgroup
+    nt = int(ref.meta[0].item())
+    mt = lib.ccq_moe_align_max_tiles(T * k, E, 128)
+    a256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    o_te = a256(mt * 128 * 4)
+    o_meta = o_te + a256(mt * 4)
+    o_cnt = o_meta + 256
+    i32 = lambda o, n: ws[o:o + 4 * n].view(torch.int32)  # noqa: E731
+    assert torch.equal(i32(0, nt * 128), ref.sorted_ids[:nt * 128])
+    assert torch.equal(i32(o_te, nt), ref.tile_expert[:nt])
+    assert torch.equal(i32(o_meta, 2), ref.meta[:2])
+    assert torch.equal(i32(o_cnt, E), ref.counts)
+
+    w0, ids0 = omoe.topk_softmax(lg.numpy(), k)
+    cache = {}
+
+    def lookup(e):
+        if e not in cache:
+            cache[e] = tuple(oawq.dequant(t[0][e], t[1][e], t[2][e], G) for t in (gate, up, down))
+        return cache[e]
+
+    r = omoe.moe_combine(x.float().numpy(), ids0, w0, lookup)
+    assert np.abs(y.cpu().numpy() - r).max() <= TOL * np.abs(r).max()
+
+
 def test_moe_combine_api_with_expert_fn(gpu):
     """moe_combine(x, ids, w, w_lookup=...) with float32 experts, numpy I/O."""
     from ccut.blocks import moe
