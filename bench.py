@@ -49,6 +49,12 @@ PEAK_BF16 = 2.5166e15      # dense bf16 MFMA FLOP/s
 PEAK_FP8 = 5.0332e15       # dense fp8 MFMA FLOP/s
 
 E, TOPK, HID, INTER, GROUP = 64, 6, 2048, 1408, 128
+# HBM bytes / algorithmic bytes of one decode gate/up launch, from rocprofv3
+# FETCH_SIZE (x 2.000) + WRITE_SIZE (x 1.000) on the torch-free driver
+# (47 routed experts: 145.23 MB moved for 141.16 MB algorithmic), the factors
+# calibrated on a 64 MiB streaming read and write; counters cannot be taken
+# inside this process, so the bench scales its own algorithmic bytes by it
+GATE_UP_TRAFFIC_RATIO = 1.029
 LAYERS = 4
 METRIC = "int4 MoE decode GB/s (% HBM peak) + FP8/int4 prefill TFLOP/s (% MFMA peak)"
 
@@ -431,10 +437,11 @@ def main():
                    "tokens": args.tokens, "experts": E, "top_k": TOPK, "hidden": HID, "inter": INTER,
                    "group": GROUP, "hip_graph": True},
         "frac_hbm_peak": round(head["GBps"] * 1e9 / PEAK_HBM, 4),
-        "roofline": {"bound": "hbm", "kernel": "w4_stream_kernel<bf16,bf16,SiLU,MT=2,NQ=2> (MoE gate/up)",
+        "roofline": {"bound": "hbm", "kernel": "w4_stream_kernel<bf16,f16,SiLU,MT=2,NQ=2> (MoE gate/up)",
                      "achieved": round(gu["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": round(gu["GBps"] * 1e9 / PEAK_HBM, 4), "avg_us": round(gu["avg_us"], 3),
-                     "traffic": None},
+                     "algorithmic_bytes": round(gu["bytes"]),
+                     "traffic": round(gu["bytes"] * GATE_UP_TRAFFIC_RATIO)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

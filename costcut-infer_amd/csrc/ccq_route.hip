@@ -495,7 +495,7 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
                  size_t scratch_bytes) {
   const int64_t nchunks = cdiv(n, kChunk);
   // below ~6K assignments one workgroup is faster than three launches
-  if (scratch == nullptr || n <= 3 * kChunk || scratch_bytes < align_scratch_bytes(n, E)) {
+  if (scratch == nullptr || n <= 6 * kChunk || scratch_bytes < align_scratch_bytes(n, E)) {
     hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
                        tile_expert, meta, counts);
     return launch_status("moe_align");

@@ -746,7 +746,7 @@ static int stream_nq(int EPI, int64_t N, int64_t K, int64_t G) {
   return 0;
 }
 
-template <typename AT, typename ST, int EPI, int MT, int NQ>
+template <typename AT, typename ST, int EPI, int MT, int NQ, bool ROUTE = false>
 __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   using V = typename Act<AT>::vec;
   constexpr int D = WS_DEPTH;
@@ -764,13 +764,10 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // the routing scratch lives in the partial-sum buffer, unused until the
   // first job
   RouteSmem& rs = *reinterpret_cast<RouteSmem*>(&part[0][0][0][0][0]);
-  bool routed = false;
+  static_assert(!ROUTE || (EPI == EPI_SILU && sizeof(RouteSmem) <= sizeof(part)), "routing in gate/up only");
+  constexpr bool routed = ROUTE;  // p.logits is set exactly for this instance
   int ntiles;
-  if constexpr (EPI == EPI_SILU) {
-    static_assert(sizeof(RouteSmem) <= sizeof(part), "routing scratch");
-    routed = p.logits != nullptr;
-  }
-  if (routed) {
+  if constexpr (routed) {
     route_decode(p, rs);
     ntiles = __builtin_amdgcn_readfirstlane(rs.ntiles);
   } else {
@@ -787,7 +784,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // together; lane r16 keeps row r16 ----
   const int r16 = lane & 15, kq = lane >> 4;
   int exA = 0, exB = 0, rid[2];
-  if (routed) {  // the schedule routed above, in LDS
+  if constexpr (routed) {  // the schedule routed above, in LDS
     exA = __builtin_amdgcn_readfirstlane(rs.tile_expert[tA]);
     exB = __builtin_amdgcn_readfirstlane(rs.tile_expert[tB]);
     rid[0] = rs.sorted[tA * 16 + r16];
@@ -1451,7 +1448,12 @@ template <typename AT, typename ST, int EPI>
 static void launch_stream_t(const W4SP& p, int nq, dim3 grid, hipStream_t st) {
   const dim3 block(512);
   const bool mt4 = p.KT > 16;
-  if (nq == 2)  // two quads: K <= 2048, two k-tiles per wave
+  if constexpr (EPI == EPI_SILU) {
+    if (p.logits != nullptr)  // routing inside the workgroups
+      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 2, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
+  } else if (nq == 2)  // two quads: K <= 2048, two k-tiles per wave
     hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
   else if constexpr (EPI != EPI_SILU) {
     if (mt4)
