@@ -39,7 +39,7 @@ __all__ = [
     "moe_forward_fp8",
 ]
 
-_MODE_SOFTMAX_ALL, _MODE_TOPK_THEN_SOFTMAX, _MODE_RAW_EXP, _MODE_PLAIN = 0, 1, 2, 3
+_MODE_SOFTMAX_ALL, _MODE_TOPK_THEN_SOFTMAX, _MODE_RAW_EXP, _MODE_PLAIN, _MODE_ROUTE_NORM = 0, 1, 2, 3, 4
 
 
 def _route(logits, k: int, mode: int):
@@ -75,7 +75,7 @@ def route_experts(gate_logits, top_k: int, norm_topk: int):
     """Fused top-k + softmax (reference ``moe.py:92-119``); ``norm_topk=0``
     normalises exp of the raw selected logits (it disagrees with
     ``topk_softmax(norm_topk_prob=False)`` as in the reference)."""
-    return _route(gate_logits, top_k, _MODE_TOPK_THEN_SOFTMAX if norm_topk else _MODE_RAW_EXP)
+    return _route(gate_logits, top_k, _MODE_ROUTE_NORM if norm_topk else _MODE_RAW_EXP)
 
 
 def expert_ffn(x, w_gate, w_up, w_down):

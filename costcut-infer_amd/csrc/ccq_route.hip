@@ -521,7 +521,7 @@ extern "C" int ccq_topk_softmax(const float* logits, float* weights, int64_t* id
   CCQ_REQUIRE(E >= 1 && E <= kMaxE, "ccq_topk_softmax: E=%lld outside [1, %d]", (long long)E, kMaxE);
   CCQ_REQUIRE(k >= 1 && k <= kMaxK && k <= E, "ccq_topk_softmax: k=%lld outside [1, min(%d, E)]", (long long)k,
               kMaxK);
-  CCQ_REQUIRE(mode >= 0 && mode <= 3, "ccq_topk_softmax: mode=%d not in {0,1,2,3}", mode);
+  CCQ_REQUIRE(mode >= 0 && mode <= 4, "ccq_topk_softmax: mode=%d not in {0,1,2,3,4}", mode);
   if (T == 0) return 0;
   CCQ_REQUIRE(logits && weights && ids, "ccq_topk_softmax: null pointer");
   CCQ_REQUIRE(T <= (int64_t)4 * 0x7fffffff, "ccq_topk_softmax: T too large");

@@ -67,6 +67,10 @@ __device__ inline float np_pairwise_sum16(float a, int n) {
   return res;
 }
 
+// numpy's maximum(a, b) for a constant b: NaN in a propagates (fmaxf would
+// return b).
+__device__ __forceinline__ float np_maximum(float a, float b) { return a != a ? a : fmaxf(a, b); }
+
 // Routing of one token row by one wave.  Lane l holds columns l, l+64, ...
 // (PER values, PER = ceil(E / 64) rounded up to 1, 2, 4 or 16); after
 // selection pass j, lane j holds slot j; on return lanes j < k hold the
@@ -100,16 +104,58 @@ __device__ __forceinline__ void topk_row(const float* __restrict__ lr, int E, in
         s += v[i];
       }
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-    const float d = fmaxf(s, 1e-30f);
+    const float d = np_maximum(s, 1e-30f);
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       if (!used[i]) v[i] = v[i] / d;
   }
   // k passes of "first value strictly greater than the running best" with the
-  // best starting at -1e30 (ties -> lowest column; NaN never picked): each
-  // lane's best, the wave maximum, then the lowest column holding it.
+  // best starting at -1e30 (ties -> lowest column; NaN never picked) select
+  // the values > -1e30 in descending order, ties to the lowest column, and
+  // fill the slots left over with (-1e30, -1).
   float my_v = 0.f;
   int my_i = 0;
+  if constexpr (PER == 1) {
+    // One column per lane: the same selection without k passes.  Eligible
+    // values map to integer keys in the same order (-0 keyed as +0, since
+    // the passes treat them as equal); ballots over the key bits find the
+    // k-th largest key, the lanes above it and the lowest-column lanes equal
+    // to it are the selection, and each selected lane's slot is the number
+    // of selected lanes before it in (value desc, column asc) order.
+    // Eligible keys are >= 1 (0 would be the NaN bit pattern 0xFFFFFFFF),
+    // the others are 0, so every test against a threshold >= 1 below
+    // excludes them.
+    const bool elig = !used[0] && v[0] > -1.0e30f;
+    const uint32_t u = __float_as_uint(v[0] == 0.f ? 0.f : v[0]);
+    const uint32_t key = elig ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+    const int ne = (int)__popcll(__ballot(elig));
+    const int kk = ne < k ? ne : k;
+    uint32_t th = 0;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t t = th | (1u << b);
+      if ((int)__popcll(__ballot(key >= t)) >= kk) th = t;
+    }
+    uint64_t sel = __ballot(key > th);
+    uint64_t eq = __ballot(key == th);
+    for (int need = kk - (int)__popcll(sel); need > 0; --need) {
+      const uint64_t low = eq & (~eq + 1ull);
+      sel |= low;
+      eq ^= low;
+    }
+    if (kk == 0) sel = 0;
+    my_v = -1.0e30f;  // slots past the selection: (-1e30, -1)
+    my_i = -1;
+    for (uint64_t m = sel; m != 0; m &= m - 1) {
+      const int L = (int)__builtin_ctzll(m);
+      const uint32_t kL = (uint32_t)__builtin_amdgcn_readlane((int)key, L);
+      const int slot = (int)__popcll(sel & __ballot(key > kL)) +
+                       (int)__popcll(sel & __ballot(key == kL) & ((1ull << L) - 1ull));
+      if (lane == slot) {
+        my_v = lane_f(v[0], L);
+        my_i = L;
+      }
+    }
+  } else {
   for (int j = 0; j < k; ++j) {
     float bv = -1.0e30f;
     int bi = 0x7fffffff;
@@ -142,18 +188,23 @@ __device__ __forceinline__ void topk_row(const float* __restrict__ lr, int E, in
       my_i = bi;
     }
   }
+  }
   const bool mine = lane < k;
   float w = my_v;  // modes 0 and 3: the selected values themselves
   if (mode == 1) {
     // v = vals - vals.max(); exp; / max(exp.sum(), 1e-30)  (blocks/moe.py:86-88)
     const float m = wave_max(mine ? my_v : -INFINITY);
     const float e = mine ? expf(my_v - m) : 0.f;
-    const float d = fmaxf(np_pairwise_sum16(e, k), 1e-30f);
+    const float d = np_maximum(np_pairwise_sum16(e, k), 1e-30f);
     w = e / d;
-  } else if (mode == 2) {
-    // route_experts norm_topk=0: exp(v)/sum(exp(v)) with a float64 running sum
-    // (blocks/moe.py:114-118)
-    const float e = mine ? expf(my_v) : 0.f;
+  } else if (mode == 2 || mode == 4) {
+    // route_experts: exp(v - m) (norm_topk=1, m the largest selected value)
+    // or exp(v) (norm_topk=0) over a float64 running sum, weights 0 when
+    // the sum is not > 0 (blocks/moe.py:104-118).  The reference's m is a
+    // float64 starting at -1e30, above the float32 slot filler -1e30f: a row
+    // with nothing selected has exp(v - m) = 0 in every slot, so weights 0.
+    const float m = mode == 4 ? wave_max(mine ? my_v : -1.0e30f) : 0.f;
+    const float e = mine && (mode == 2 || m > -1.0e30f) ? expf(my_v - m) : 0.f;
     double s = 0.0;
     for (int j = 0; j < k; ++j) s += (double)lane_f(e, j);
     w = s > 0.0 ? (float)((double)e / s) : 0.f;

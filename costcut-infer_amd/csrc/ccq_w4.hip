@@ -2032,7 +2032,7 @@ extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logit
   if (rc) return rc;
   CCQ_REQUIRE(T >= 0 && k >= 1 && k <= 16 && k <= ex->num_experts, "ccq_moe_w4_forward: bad T=%lld / k=%lld",
               (long long)T, (long long)k);
-  CCQ_REQUIRE(mode >= 0 && mode <= 3, "ccq_moe_w4_forward: mode=%d not in {0,1,2,3}", mode);
+  CCQ_REQUIRE(mode >= 0 && mode <= 4, "ccq_moe_w4_forward: mode=%d not in {0,1,2,3,4}", mode);
   CCQ_REQUIRE(T * k <= 65536 && T <= 65535, "ccq_moe_w4_forward: T=%lld too large", (long long)T);
   CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_moe_w4_forward: x_dtype must be f16|bf16");
   CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_moe_w4_forward: bad y_dtype");

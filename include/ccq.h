@@ -149,8 +149,13 @@ int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled,
  * over all E then top-k of the probabilities (norm_topk_prob=False,
  * blocks/moe.py:79-83); mode 2: exp(v)/sum(exp(v)) over the k raw logits
  * (route_experts norm_topk=0, blocks/moe.py:113-118); mode 3: plain top-k,
- * weights = the selected logits (topk, blocks/moe.py:46-68).  Selection is
- * topk (blocks/moe.py:46-68): strict '>', ties to the lowest index.
+ * weights = the selected logits (topk, blocks/moe.py:46-68); mode 4:
+ * exp(v - max)/sum over the k (route_experts norm_topk=1,
+ * blocks/moe.py:100-112).  Modes 0 and 1 divide by numpy's
+ * maximum(sum, 1e-30), which keeps a NaN sum (a NaN or +inf logit makes the
+ * row NaN); modes 2 and 4 sum in float64 and give 0 when the sum is not
+ * > 0.  Selection is topk (blocks/moe.py:46-68): strict '>', ties to the
+ * lowest index.
  * E <= 1024, 1 <= k <= 16, k <= E. */
 int ccq_topk_softmax(const float* logits, float* weights, int64_t* ids,
                      int64_t T, int64_t E, int64_t k, int mode, void* stream);

@@ -69,7 +69,10 @@ def route_experts(gate_logits: np.ndarray, top_k: int, norm_topk: int) -> tuple[
     ``norm_topk=1``: softmax over the k selected logits with the max
     subtracted.  ``norm_topk=0``: ``exp(v)/sum(exp(v))`` over the k selected
     raw logits (no max subtraction) -- this disagrees with
-    ``topk_softmax(norm_topk_prob=False)``, as in the reference.
+    ``topk_softmax(norm_topk_prob=False)``, as in the reference.  The running
+    maximum is a float64 starting at -1e30, above the float32 slot filler
+    -1e30f, so a row with nothing selectable gets weights 0 (``s > 0`` fails),
+    where ``topk_softmax`` gives 1/k.
     """
     vals, idx = topk(np.asarray(gate_logits, dtype=np.float32), top_k)
     rows = vals.shape[0]

@@ -50,6 +50,48 @@ def test_topk_nan_rows_and_sentinel(gpu):
     assert np.array_equal(v, v0)
 
 
+@pytest.mark.parametrize("E,k", [(64, 8), (64, 16), (40, 6), (64, 1), (96, 8)])
+def test_topk_edge_cases_all_modes(gpu, E, k):
+    """Heavy ties, +0 next to -0, exact -1e30 and NaN (never selected), rows
+    with fewer selectable values than k (slots filled with -1e30 / -1), and
+    NaN / +inf logits, which numpy's softmax turns into NaN rows and the
+    route_experts loop into zero weights.  E <= 64 is the one column per lane
+    selection, E = 96 two columns per lane."""
+    from ccut.blocks import moe
+
+    rng = np.random.default_rng(E + k)
+    x = rng.integers(-2, 3, size=(96, E)).astype(np.float32)
+    x[x == 0] = np.where(rng.random(np.count_nonzero(x == 0)) < 0.5, -0.0, 0.0)
+    x[rng.random(x.shape) < 0.05] = -1e30
+    x[rng.random(x.shape) < 0.05] = np.nan
+    x[5, :] = -1e30
+    x[6, : E - 3] = np.nan
+    x[7, :] = -0.0
+    x[7, 9] = 0.0
+    x[8:12] = np.where(np.isnan(x[8:12]), 1.0, x[8:12])  # rows 8-11: no NaN
+    x[9, 3] = np.inf
+    x[10, [2, 30]] = np.inf
+    x[11, :] = rng.integers(-2, 3, size=E)
+    x[11, 17] = -np.inf
+    v, i = moe.topk(x, k)
+    v0, i0 = omoe.topk(x, k)
+    assert np.array_equal(i, i0)
+    assert np.array_equal(v.view(np.uint32), v0.view(np.uint32))  # -0 stays -0
+    for norm in (True, False):
+        w, ids = moe.topk_softmax(x, k, norm)
+        w0, ids0 = omoe.topk_softmax(x, k, norm)
+        assert np.array_equal(ids, ids0)
+        assert np.allclose(w, w0, atol=1e-6, rtol=1e-6, equal_nan=True)
+    assert np.isnan(omoe.topk_softmax(x, k, True)[0][9]).all()  # the +inf row
+    assert (omoe.topk_softmax(x, k, False)[1][9] == -1).all()  # NaN probabilities
+    for norm in (0, 1):
+        w, ids = moe.route_experts(x, k, norm)
+        w0, ids0 = omoe.route_experts(x, k, norm)
+        assert np.array_equal(ids, ids0)
+        assert np.allclose(w, w0, atol=1e-6, rtol=1e-6, equal_nan=True)
+    assert (omoe.route_experts(x, k, 1)[0][9] == 0).all()
+
+
 def test_route_experts_modes(gpu):
     from ccut.blocks import moe
 

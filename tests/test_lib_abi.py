@@ -127,7 +127,7 @@ def test_moe_w4_descriptor_validation(lib):
     ex.inter = 1408
     assert lib.ccq_moe_w4_workspace_size(16, 6, ctypes.byref(ex)) > 0
     # the layer from logits: routing mode and k are checked before any launch
-    assert lib.ccq_moe_w4_forward(p, 2, p, 16, 6, 4, None, None, p, 2, ctypes.byref(ex), p, 1 << 30,
+    assert lib.ccq_moe_w4_forward(p, 2, p, 16, 6, 5, None, None, p, 2, ctypes.byref(ex), p, 1 << 30,
                                   None) == CCQ_EINVAL
     assert "mode" in last_error()
     assert lib.ccq_moe_w4_forward(p, 2, p, 16, 17, 1, None, None, p, 2, ctypes.byref(ex), p, 1 << 30,

@@ -74,6 +74,31 @@ def test_route_experts_modes():
     assert np.allclose(w0, np.exp(sel) / np.exp(sel).sum(1, keepdims=True), atol=1e-6)
 
 
+def test_routing_special_rows_closed_forms():
+    """Rows where numpy's float32 softmax and the float64 route_experts loop
+    part ways (IEEE arithmetic fixes every value here)."""
+    k = 3
+    assert float(np.float32(-1e30)) < -1e30  # the slot filler sits below the loop's start
+    empty = np.full((1, 5), -1e30, np.float32)  # nothing selectable
+    w, i = moe.topk_softmax(empty, k, True)
+    assert (i == -1).all() and np.allclose(w, 1.0 / k)  # exp(0) / k
+    w, i = moe.route_experts(empty, k, 1)
+    assert (w == 0).all()  # exp(-1e30f - (-1e30)) underflows: sum 0 -> weights 0
+    w, i = moe.route_experts(empty, k, 0)
+    assert (w == 0).all()
+    inf_row = np.array([[1.0, np.inf, 0.5, 2.0, -1.0]], np.float32)
+    with np.errstate(invalid="ignore"):
+        w, i = moe.topk_softmax(inf_row, k, True)
+        assert list(i[0]) == [1, 3, 0] and np.isnan(w).all()  # inf - inf in the max shift
+        w, i = moe.route_experts(inf_row, k, 1)
+        assert (w == 0).all()  # NaN sum is not > 0
+        w, i = moe.route_experts(inf_row, k, 0)
+        assert np.isnan(w[0, 0]) and (w[0, 1:] == 0).all()  # inf / inf, finite / inf
+        nan_row = np.array([[1.0, np.nan, 0.5, 2.0, -1.0]], np.float32)
+        w, i = moe.topk_softmax(nan_row, k, False)
+        assert (i == -1).all()  # every probability NaN: nothing selectable
+
+
 def test_expert_order_and_align_contract():
     ids = np.array([[3, 1], [1, 0], [2, 3], [3, 1]])
     order = moe.expert_order(ids)
