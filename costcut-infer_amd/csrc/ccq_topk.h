@@ -47,6 +47,18 @@ __device__ __forceinline__ int wave_min(int v) {
   return min(min(a, b), min(c, d));
 }
 
+// The maximum over the wave of unsigned keys, in every lane (max with 0 as
+// the DPP fill value folds each move into the max instruction).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x124>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x128>((int)v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+
 // numpy's pairwise float32 summation of n <= 16 values, value j held by lane
 // j: below 8 a plain running sum in index order; otherwise 8 partial sums
 // r[j] = a[j] (+ a[8+j] when n == 16) combined as
@@ -71,109 +83,99 @@ __device__ inline float np_pairwise_sum16(float a, int n) {
 // return b).
 __device__ __forceinline__ float np_maximum(float a, float b) { return a != a ? a : fmaxf(a, b); }
 
-// Routing of one token row by one wave.  Lane l holds columns l, l+64, ...
-// (PER values, PER = ceil(E / 64) rounded up to 1, 2, 4 or 16); after
-// selection pass j, lane j holds slot j; on return lanes j < k hold the
-// weight and expert id of slot j.  The code stays compact (a run-time loop
-// over the k passes, no per-slot arrays): it runs on a handful of CUs, where
-// a large body costs more in cold instruction fetches than it saves.
-template <int PER>
-__device__ __forceinline__ void topk_row(const float* __restrict__ lr, int E, int k, int mode, float& w_out,
-                                         int& id_out) {
+// Routing of R token rows by one wave, row r at lr + r * stride.  Lane l
+// holds columns l, l+64, ... (PER values, PER = ceil(E / 64) rounded up to
+// 1, 2, 4 or 16); on return lanes j < k hold the weight and expert id of
+// slot j of each row.  The R rows run interleaved (R > 1 only with one
+// column per lane): each step below is a chain of cross-lane operations,
+// and independent rows fill each other's latency.
+template <int PER, int R>
+__device__ __forceinline__ void topk_rows(const float* __restrict__ lr, int64_t stride, int E, int k, int mode,
+                                          float (&w_out)[R], int (&id_out)[R]) {
+  static_assert(R == 1 || PER == 1, "several rows per wave with one column per lane only");
   const int lane = lane_id();
-  float v[PER];
+  float v[R][PER];
   bool used[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    int c = lane + 64 * i;
-    v[i] = c < E ? lr[c] : -INFINITY;
-    used[i] = c >= E;  // out-of-range slots never selectable
-  }
+  for (int i = 0; i < PER; ++i) used[i] = lane + 64 * i >= E;  // out-of-range slots never selectable
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[r][i] = used[i] ? -INFINITY : lr[r * stride + lane + 64 * i];
   if (mode == 0) {
-    // p = exp(x - max) / max(sum, 1e-30) in float32 (blocks/moe.py:80-81)
-    float m = -INFINITY;
+    // p = exp(x - max) / maximum(sum, 1e-30) in float32 (blocks/moe.py:80-81)
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (!used[i]) m = fmaxf(m, v[i]);
-    m = wave_max(m);
-    float s = 0.f;
+    for (int r = 0; r < R; ++r) {
+      float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (!used[i]) {
-        v[i] = expf(v[i] - m);
-        s += v[i];
-      }
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-    const float d = np_maximum(s, 1e-30f);
+      for (int i = 0; i < PER; ++i)
+        if (!used[i]) m = fmaxf(m, v[r][i]);
+      m = wave_max(m);
+      float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (!used[i]) v[i] = v[i] / d;
+      for (int i = 0; i < PER; ++i)
+        if (!used[i]) {
+          v[r][i] = expf(v[r][i] - m);
+          s += v[r][i];
+        }
+      for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+      const float d = np_maximum(s, 1e-30f);
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if (!used[i]) v[r][i] = v[r][i] / d;
+    }
   }
   // k passes of "first value strictly greater than the running best" with the
   // best starting at -1e30 (ties -> lowest column; NaN never picked) select
   // the values > -1e30 in descending order, ties to the lowest column, and
   // fill the slots left over with (-1e30, -1).
-  float my_v = 0.f;
-  int my_i = 0;
+  float my_v[R];
+  int my_i[R];
   if constexpr (PER == 1) {
-    // One column per lane: the same selection without k passes.  Eligible
-    // values map to integer keys in the same order (-0 keyed as +0, since
-    // the passes treat them as equal); ballots over the key bits find the
-    // k-th largest key, the lanes above it and the lowest-column lanes equal
-    // to it are the selection, and each selected lane's slot is the number
-    // of selected lanes before it in (value desc, column asc) order.
-    // Eligible keys are >= 1 (0 would be the NaN bit pattern 0xFFFFFFFF),
-    // the others are 0, so every test against a threshold >= 1 below
-    // excludes them.
-    const bool elig = !used[0] && v[0] > -1.0e30f;
-    const uint32_t u = __float_as_uint(v[0] == 0.f ? 0.f : v[0]);
-    const uint32_t key = elig ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
-    const int ne = (int)__popcll(__ballot(elig));
-    const int kk = ne < k ? ne : k;
-    uint32_t th = 0;
-    for (int b = 31; b >= 0; --b) {
-      const uint32_t t = th | (1u << b);
-      if ((int)__popcll(__ballot(key >= t)) >= kk) th = t;
+    // One column per lane: the same k passes on integer keys.  Eligible
+    // values map to keys >= 1 in the same order (-0 keyed as +0, since the
+    // float passes treat them as equal), the others to 0; a pass takes the
+    // wave's largest key (DPP steps that fold into the max instructions),
+    // the lowest lane holding it, and clears that lane.  A pass that finds
+    // only zeros (nothing > -1e30 left) stores (-1e30, -1), as do all later
+    // ones.
+    uint32_t cur[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool elig = !used[0] && v[r][0] > -1.0e30f;
+      const uint32_t u = __float_as_uint(v[r][0] == 0.f ? 0.f : v[r][0]);
+      cur[r] = elig ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+      my_v[r] = -1.0e30f;
+      my_i[r] = -1;
     }
-    uint64_t sel = __ballot(key > th);
-    uint64_t eq = __ballot(key == th);
-    for (int need = kk - (int)__popcll(sel); need > 0; --need) {
-      const uint64_t low = eq & (~eq + 1ull);
-      sel |= low;
-      eq ^= low;
-    }
-    if (kk == 0) sel = 0;
-    my_v = -1.0e30f;  // slots past the selection: (-1e30, -1)
-    my_i = -1;
-    for (uint64_t m = sel; m != 0; m &= m - 1) {
-      const int L = (int)__builtin_ctzll(m);
-      const uint32_t kL = (uint32_t)__builtin_amdgcn_readlane((int)key, L);
-      const int slot = (int)__popcll(sel & __ballot(key > kL)) +
-                       (int)__popcll(sel & __ballot(key == kL) & ((1ull << L) - 1ull));
-      if (lane == slot) {
-        my_v = lane_f(v[0], L);
-        my_i = L;
+    for (int j = 0; j < k; ++j) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t m = wave_max_u32(cur[r]);
+        const uint64_t eq = __ballot(cur[r] == m);
+        const int L = m != 0u ? (int)__builtin_ctzll(eq) : -1;
+        const float vL = lane_f(v[r][0], L & 63);
+        my_v[r] = lane == j && L >= 0 ? vL : my_v[r];
+        my_i[r] = lane == j ? L : my_i[r];
+        cur[r] = lane == L ? 0u : cur[r];
       }
     }
   } else {
+    const int r = 0;
   for (int j = 0; j < k; ++j) {
     float bv = -1.0e30f;
     int bi = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       int c = lane + 64 * i;
-      if (!used[i] && v[i] > bv) {  // per lane columns are increasing
-        bv = v[i];
+      if (!used[i] && v[r][i] > bv) {  // per lane columns are increasing
+        bv = v[r][i];
         bi = c;
       }
     }
     const float m = wave_max(bv);
     if (m > -1.0e30f) {
-      if constexpr (PER == 1) {
-        bi = (int)__builtin_ctzll(__ballot(bv == m));  // column = lane
-      } else {
-        bi = wave_min(bv == m ? bi : 0x7fffffff);
-      }
+      bi = wave_min(bv == m ? bi : 0x7fffffff);
       bv = lane_f(bv, bi & 63);  // the value at that column (+0 and -0 compare equal)
     } else {  // nothing > -1e30: reference stores (-1e30, -1)
       bi = -1;  // and its used[-1] = 1 marks the last column
@@ -184,33 +186,49 @@ __device__ __forceinline__ void topk_row(const float* __restrict__ lr, int E, in
     for (int i = 0; i < PER; ++i)
       if (lane + 64 * i == mark) used[i] = true;
     if (lane == j) {
-      my_v = bv;
-      my_i = bi;
+      my_v[r] = bv;
+      my_i[r] = bi;
     }
   }
   }
   const bool mine = lane < k;
-  float w = my_v;  // modes 0 and 3: the selected values themselves
-  if (mode == 1) {
-    // v = vals - vals.max(); exp; / max(exp.sum(), 1e-30)  (blocks/moe.py:86-88)
-    const float m = wave_max(mine ? my_v : -INFINITY);
-    const float e = mine ? expf(my_v - m) : 0.f;
-    const float d = np_maximum(np_pairwise_sum16(e, k), 1e-30f);
-    w = e / d;
-  } else if (mode == 2 || mode == 4) {
-    // route_experts: exp(v - m) (norm_topk=1, m the largest selected value)
-    // or exp(v) (norm_topk=0) over a float64 running sum, weights 0 when
-    // the sum is not > 0 (blocks/moe.py:104-118).  The reference's m is a
-    // float64 starting at -1e30, above the float32 slot filler -1e30f: a row
-    // with nothing selected has exp(v - m) = 0 in every slot, so weights 0.
-    const float m = mode == 4 ? wave_max(mine ? my_v : -1.0e30f) : 0.f;
-    const float e = mine && (mode == 2 || m > -1.0e30f) ? expf(my_v - m) : 0.f;
-    double s = 0.0;
-    for (int j = 0; j < k; ++j) s += (double)lane_f(e, j);
-    w = s > 0.0 ? (float)((double)e / s) : 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float w = my_v[r];  // modes 0 and 3: the selected values themselves
+    if (mode == 1) {
+      // v = vals - vals.max(); exp; / maximum(exp.sum(), 1e-30)  (blocks/moe.py:86-88);
+      // the slots hold the values in descending order (fillers -1e30 last),
+      // so the maximum is slot 0's
+      const float m = lane_f(my_v[r], 0);
+      const float e = mine ? expf(my_v[r] - m) : 0.f;
+      const float d = np_maximum(np_pairwise_sum16(e, k), 1e-30f);
+      w = e / d;
+    } else if (mode == 2 || mode == 4) {
+      // route_experts: exp(v - m) (norm_topk=1, m the largest selected value)
+      // or exp(v) (norm_topk=0) over a float64 running sum, weights 0 when
+      // the sum is not > 0 (blocks/moe.py:104-118).  The reference's m is a
+      // float64 starting at -1e30, above the float32 slot filler -1e30f: a
+      // row with nothing selected has exp(v - m) = 0 in every slot, so
+      // weights 0.
+      const float m = mode == 4 ? lane_f(my_v[r], 0) : 0.f;
+      const float e = mine && (mode == 2 || m > -1.0e30f) ? expf(my_v[r] - m) : 0.f;
+      double s = 0.0;
+      for (int j = 0; j < k; ++j) s += (double)lane_f(e, j);
+      w = s > 0.0 ? (float)((double)e / s) : 0.f;
+    }
+    w_out[r] = w;
+    id_out[r] = my_i[r];
   }
-  w_out = w;
-  id_out = my_i;
+}
+
+template <int PER>
+__device__ __forceinline__ void topk_row(const float* __restrict__ lr, int E, int k, int mode, float& w_out,
+                                         int& id_out) {
+  float w[1];
+  int id[1];
+  topk_rows<PER, 1>(lr, 0, E, k, mode, w, id);
+  w_out = w[0];
+  id_out = id[0];
 }
 
 }  // namespace ccq

@@ -637,16 +637,7 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
   for (int i = tid; i < RT_CHUNKS * RT_MAXE; i += blockDim.x) (&rs.ccnt[0][0])[i] = 0;
   for (int i = tid; i < T * E; i += blockDim.x) rs.lg[i] = p.logits[i];
   __syncthreads();
-  for (int t = wave; t < T; t += nw) {
-    float w;
-    int id;
-    const float* lr = rs.lg + t * E;
-    if (E <= 64)
-      topk_row<1>(lr, E, k, p.rmode, w, id);
-    else if (E <= 128)
-      topk_row<2>(lr, E, k, p.rmode, w, id);
-    else
-      topk_row<4>(lr, E, k, p.rmode, w, id);
+  auto keep = [&](int t, float w, int id) {
     if (lane < k) {
       const int a = t * k + lane;
       rs.sid[a] = id >= 0 && id < E ? id : -1;
@@ -654,6 +645,27 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
         p.ids_out[a] = id;
         p.wts_out[a] = w;
       }
+    }
+  };
+  if (E <= 64) {  // tokens t and t + nw together (a lone last token runs twice)
+    for (int t = wave; t < T; t += 2 * nw) {
+      const int t2 = t + nw < T ? t + nw : t;
+      float w[2];
+      int id[2];
+      topk_rows<1, 2>(rs.lg + t * E, (int64_t)(t2 - t) * E, E, k, p.rmode, w, id);
+      keep(t, w[0], id[0]);
+      if (t2 != t) keep(t2, w[1], id[1]);
+    }
+  } else {
+    for (int t = wave; t < T; t += nw) {
+      float w;
+      int id;
+      const float* lr = rs.lg + t * E;
+      if (E <= 128)
+        topk_row<2>(lr, E, k, p.rmode, w, id);
+      else
+        topk_row<4>(lr, E, k, p.rmode, w, id);
+      keep(t, w, id);
     }
   }
   __syncthreads();

@@ -131,6 +131,45 @@ def test_moe_w4_forward_matches_routed_ffn(gpu, E, H, I, T, k, norm):
     assert torch.equal(out, y_ref)
 
 
+@pytest.mark.parametrize("T,k,ydt", [(1, 6, torch.bfloat16), (16, 6, torch.float32), (16, 6, torch.bfloat16),
+                                      (40, 4, torch.float16), (64, 6, torch.float32), (65, 6, torch.float32)])
+def test_moe_w4_layer_matches_stage_kernels(gpu, T, k, ydt):
+    """The layer calls (routing inside the gate/up kernel for moe_forward_w4)
+    give the same bits as the stage entry points run one by one: moe_align,
+    ccq_moe_w4_gate_up, ccq_moe_w4_down, ccq_moe_combine."""
+    from ccut import _dev
+    from ccut._lib import call
+    from ccut.blocks import moe
+
+    E, H, I, G = 64, 512, 256, 128
+    gate, up, down = _experts(E, H, I, G, 11 + T)
+    dev = lambda t: tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(dev(gate), dev(up), dev(down), group_size=G)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16).to(gpu)
+    lg = torch.randn((T, E), generator=g).to(gpu)
+    w, ids = moe.topk_softmax(lg, k, True)
+    y_ffn = moe.moe_ffn_w4(x, ids, w, ex, out_dtype=ydt)
+    y_fwd = moe.moe_forward_w4(x, lg, ex, top_k=k, out_dtype=ydt)
+    sch = moe.moe_align(ids, E, 16)
+    mt = sch.tile_expert.numel()
+    inter = torch.empty((T * k, I), dtype=x.dtype, device=gpu)
+    rows = torch.empty((T * k, H), dtype=torch.float32, device=gpu)
+    desc = ex.descriptor()
+    call("ccq_moe_w4_gate_up", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], k, sch.sorted_ids.data_ptr(),
+         sch.tile_expert.data_ptr(), sch.meta.data_ptr(), mt, inter.data_ptr(), desc, _dev.stream_ptr())
+    call("ccq_moe_w4_down", inter.data_ptr(), _dev.DTYPE_CODE[x.dtype], sch.sorted_ids.data_ptr(),
+         sch.tile_expert.data_ptr(), sch.meta.data_ptr(), mt, rows.data_ptr(), desc, _dev.stream_ptr())
+    y_st = torch.empty((T, H), dtype=ydt, device=gpu)
+    call("ccq_moe_combine", rows.data_ptr(), w.data_ptr(), y_st.data_ptr(), _dev.DTYPE_CODE[ydt], T, k, H,
+         _dev.stream_ptr())
+    torch.cuda.synchronize()
+    assert torch.equal(y_ffn, y_st)
+    assert torch.equal(y_fwd, y_st)
+    # a second layer call on the same workspace
+    assert torch.equal(moe.moe_forward_w4(x, lg, ex, top_k=k, out_dtype=ydt), y_st)
+
+
 def test_moe_w4_large_batch_schedule_matches_align(gpu):
     """8192 assignments (T=1024, top-8, skewed router): the FFN builds its
     expert schedule over many workgroups (per-chunk counts, plan, scatter);
