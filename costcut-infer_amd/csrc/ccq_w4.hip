@@ -586,14 +586,16 @@ struct W4SP {
 };
 
 // ---- routing of a decode batch inside a workgroup ----
-// Top-k of every token (one wave per token, the routing kernel's own code,
-// on logits staged in LDS) and the expert schedule of ccq_moe_align with
-// 16-row tiles: experts in first-appearance order, each expert's
-// assignments ascending, tiles padded with -1.  Assignments are handled in
-// 64-lane chunks (one wave each): ballots over the expert id bits give each
-// assignment its rank among equal ids in the chunk, per-chunk counts give
-// the offsets across chunks.  Limits: RT_MAXN assignments, RT_MAXE experts,
-// RT_MAXLG logits.
+// Top-k of every token (one wave per token, two tokens at once for E <= 64,
+// the routing kernel's own code, on logits staged in LDS) and the expert
+// schedule of ccq_moe_align with 16-row tiles: experts in first-appearance
+// order, each expert's assignments ascending, tiles padded with -1.  One
+// wave builds the schedule, lane l holding assignments l, 64 + l, ...
+// (chunks of 64): ballots over the expert id bits of each chunk give every
+// assignment the lanes holding the same expert, so its rank among them, its
+// expert's count and whether it is the expert's first appearance; a scan
+// over the first appearances gives the padded bases.  Limits: RT_MAXN
+// assignments, RT_MAXE experts, RT_MAXLG logits.
 constexpr int RT_MAXN = 256;
 constexpr int RT_MAXE = 256;
 constexpr int RT_MAXLG = 4096;
@@ -602,39 +604,23 @@ constexpr int RT_MAXTILES = RT_MAXN / 16 + RT_MAXN;  // ccq_moe_align_max_tiles(
 struct RouteSmem {
   float lg[RT_MAXLG];
   int sid[RT_MAXN];  // expert of each assignment, -1 = dropped
-  int cnt[RT_MAXE], first[RT_MAXE], base[RT_MAXE], inv[RT_MAXE];
-  int ccnt[RT_CHUNKS][RT_MAXE];  // per-chunk counts
-  int nflags[RT_CHUNKS];
+  int cnt[RT_MAXE], base[RT_MAXE];
   int sorted[RT_MAXTILES * 16];
   int tile_expert[RT_MAXTILES];
   int ntiles, nactive;
 };
 
 __device__ __forceinline__ int pad16(int c) { return (c + 15) & ~15; }
-
-// Lanes of the wave whose key equals this lane's (0 for invalid lanes).
-__device__ __forceinline__ uint64_t equal_keys(int key, bool valid, int nbits) {
-  uint64_t same = __ballot(valid);
-  for (int b = 0; b < nbits; ++b) {
-    const bool bit = (key >> b) & 1;
-    const uint64_t bal = __ballot(valid && bit);
-    same &= bit ? bal : ~bal;
-  }
-  return valid ? same : 0ull;
-}
+__device__ __forceinline__ int popc64(uint64_t m) { return (int)__popcll(m); }
 
 // Whole workgroup (blockDim.x = 512); ends with the schedule in rs and a
 // barrier.
 __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int T = p.rT, E = p.rE, k = p.rk, n = T * k;
-  int nbits = 1;
-  while ((1 << nbits) < E) ++nbits;
-  for (int e = tid; e < E; e += blockDim.x) {
-    rs.cnt[e] = 0;
-    rs.first[e] = 0x7fffffff;
-  }
-  for (int i = tid; i < RT_CHUNKS * RT_MAXE; i += blockDim.x) (&rs.ccnt[0][0])[i] = 0;
+  const int nslots = n + 15 * min(n, E);  // the padded schedule is at most this long
+  for (int e = tid; e < E; e += blockDim.x) rs.cnt[e] = 0;
+  for (int i = tid; i < nslots; i += blockDim.x) rs.sorted[i] = -1;
   for (int i = tid; i < T * E; i += blockDim.x) rs.lg[i] = p.logits[i];
   __syncthreads();
   auto keep = [&](int t, float w, int id) {
@@ -669,67 +655,72 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
     }
   }
   __syncthreads();
-  // chunk c = wave (c < RT_CHUNKS): assignment a = 64 c + lane
-  const bool chunk = wave < RT_CHUNKS && wave * 64 < n;
-  const int a = wave * 64 + lane;
-  const int e = chunk && a < n ? rs.sid[a] : -1;
-  const bool valid = e >= 0;
-  uint64_t same = 0;
-  int rnk = 0;
-  if (chunk) {
-    same = equal_keys(e, valid, nbits);
-    const uint64_t lower = same & ((1ull << lane) - 1ull);
-    rnk = __popcll(lower);
-    if (valid && lower == 0) {  // the lowest lane of each id in the chunk
-      rs.ccnt[wave][e] = __popcll(same);
-      atomicAdd(&rs.cnt[e], __popcll(same));
-      atomicMin(&rs.first[e], a);
+  if (wave == 0) {
+    int nbits = 1;
+    while ((1 << nbits) < E) ++nbits;  // <= 8
+    const int nch = (n + 63) / 64;     // <= RT_CHUNKS
+    const uint64_t lt = (1ull << lane) - 1ull;
+    int key[RT_CHUNKS], rank[RT_CHUNKS], cnt[RT_CHUNKS];
+    uint64_t vm[RT_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < RT_CHUNKS; ++c) {
+      const int a = 64 * c + lane;
+      key[c] = c < nch && a < n ? rs.sid[a] : -1;
+      vm[c] = __ballot(key[c] >= 0);
+      rank[c] = 0;
+      cnt[c] = 0;
     }
-  }
-  __syncthreads();
-  // experts in first-appearance order: a flag at each expert's first assignment
-  const bool flag = valid && rs.first[e] == a;
-  const uint64_t fl = __ballot(flag);
-  if (chunk && lane == 0) rs.nflags[wave] = __popcll(fl);
-  __syncthreads();
-  if (chunk && flag) {
-    int before = 0;
-    for (int c = 0; c < wave; ++c) before += rs.nflags[c];
-    rs.inv[before + __popcll(fl & ((1ull << lane) - 1ull))] = e;
-  }
-  if (tid == 0) {
-    int na = 0;
-    for (int c = 0; c < RT_CHUNKS && c * 64 < n; ++c) na += rs.nflags[c];
-    rs.nactive = na;
-  }
-  __syncthreads();
-  if (wave == 0) {  // padded bases in first-appearance order
-    const int na = rs.nactive;
-    int carry = 0;
-    for (int r0 = 0; r0 < na; r0 += 64) {
-      const int r = r0 + lane;
-      const int pd = r < na ? pad16(rs.cnt[rs.inv[r]]) : 0;
+    // lanes of chunk d with the expert of this lane's assignment in chunk c
+#pragma unroll
+    for (int d = 0; d < RT_CHUNKS; ++d) {
+      if (d >= nch) break;
+      uint64_t bd[8];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) bd[b] = b < nbits ? __ballot(key[d] >= 0 && ((key[d] >> b) & 1)) : 0ull;
+#pragma unroll
+      for (int c = 0; c < RT_CHUNKS; ++c) {
+        if (c >= nch) break;
+        uint64_t m = key[c] >= 0 ? vm[d] : 0ull;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+          if (b < nbits) m &= ((key[c] >> b) & 1) ? bd[b] : ~bd[b];
+        cnt[c] += popc64(m);
+        if (d < c) rank[c] += popc64(m);
+        if (d == c) rank[c] += popc64(m & lt);
+      }
+    }
+    // first appearances in assignment order: the experts' order, padded
+    // sizes and bases (exclusive scan carried across the chunks)
+    int carry = 0, nact = 0;
+#pragma unroll
+    for (int c = 0; c < RT_CHUNKS; ++c) {
+      if (c >= nch) break;
+      const bool first = key[c] >= 0 && rank[c] == 0;
+      const int pd = first ? pad16(cnt[c]) : 0;
       int incl = pd;
       for (int off = 1; off < 64; off <<= 1) {
         const int o = __shfl_up(incl, off, 64);
         if (lane >= off) incl += o;
       }
-      if (r < na) rs.base[rs.inv[r]] = carry + incl - pd;
+      if (first) {
+        const int bs = carry + incl - pd;
+        rs.base[key[c]] = bs;
+        rs.cnt[key[c]] = cnt[c];
+        for (int t = bs / 16; t < (bs + pd) / 16; ++t) rs.tile_expert[t] = key[c];
+      }
       carry += __shfl(incl, 63, 64);
+      nact += popc64(__ballot(first));
     }
-    if (lane == 0) rs.ntiles = carry / 16;
-  }
-  __syncthreads();
-  if (valid) {
-    int off = rs.base[e] + rnk;
-    for (int c = 0; c < wave; ++c) off += rs.ccnt[c][e];
-    rs.sorted[off] = a;
-  }
-  for (int r = tid; r < rs.nactive; r += blockDim.x) {  // padding and tile -> expert
-    const int ex = rs.inv[r];
-    const int b = rs.base[ex], c = rs.cnt[ex], pd = pad16(c);
-    for (int j = c; j < pd; ++j) rs.sorted[b + j] = -1;
-    for (int t = b / 16; t < (b + pd) / 16; ++t) rs.tile_expert[t] = ex;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the bases above, before this wave reads them
+#pragma unroll
+    for (int c = 0; c < RT_CHUNKS; ++c) {
+      if (c >= nch) break;
+      if (key[c] >= 0) rs.sorted[rs.base[key[c]] + rank[c]] = 64 * c + lane;
+    }
+    if (lane == 0) {
+      rs.ntiles = carry / 16;
+      rs.nactive = nact;
+    }
   }
   __syncthreads();
   if (blockIdx.x == 0) {  // the schedule of the down and combine kernels

@@ -226,6 +226,57 @@ def test_moe_w4_large_batch_schedule_matches_align(gpu):
     assert np.abs(y.cpu().numpy() - r).max() <= TOL * np.abs(r).max()
 
 
+@pytest.mark.parametrize("E,T,k,skew", [(64, 16, 6, 0.0), (64, 42, 6, 5.0), (128, 32, 8, 3.0), (256, 16, 8, 2.0),
+                                         (8, 1, 2, 0.0), (5, 7, 5, 0.0)])
+def test_moe_w4_routed_schedule_matches_align(gpu, E, T, k, skew):
+    """Decode batches routed inside the gate/up kernel: the routing equals
+    the oracle's topk_softmax, and the expert schedule the layer leaves at
+    the head of its workspace (16-row tiles) is bit-identical to
+    ccq_moe_align on the same ids: experts with several tiles (skewed
+    router), every chunk count up to 256 assignments, E up to 256."""
+    import ctypes
+
+    from ccut import _dev, _lib
+    from ccut.blocks import moe
+
+    H, I, G = 512, 256, 128
+    gate, up, down = _experts(E, H, I, G, seed=E + T)
+    dev = lambda t: tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(dev(gate), dev(up), dev(down), group_size=G)
+    g = torch.Generator().manual_seed(E * T)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16).to(gpu)
+    lg = torch.randn((T, E), generator=g) + torch.randn((1, E), generator=g) * skew
+    lgd = lg.to(gpu)
+    lib = _lib.lib()
+    desc = ex.descriptor()
+    nbytes = lib.ccq_moe_w4_workspace_size(T, k, desc)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    y = torch.empty((T, H), dtype=torch.float32, device=gpu)
+    ids = torch.empty((T, k), dtype=torch.int64, device=gpu)
+    w = torch.empty((T, k), dtype=torch.float32, device=gpu)
+    vp = ctypes.c_void_p
+    rc = lib.ccq_moe_w4_forward(vp(x.data_ptr()), _lib.CCQ_BF16, vp(lgd.data_ptr()), T, k, 1, vp(ids.data_ptr()),
+                                vp(w.data_ptr()), vp(y.data_ptr()), _lib.CCQ_F32, ctypes.byref(desc),
+                                vp(ws.data_ptr()), nbytes, vp(_dev.stream_ptr(gpu)))
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    w0, ids0 = omoe.topk_softmax(lg.numpy(), k)
+    assert np.array_equal(ids.cpu().numpy(), ids0)
+    assert np.allclose(w.cpu().numpy(), w0, atol=1e-6)
+    ref = moe.moe_align(ids, E, 16)
+    nt = int(ref.meta[0].item())
+    mt = lib.ccq_moe_align_max_tiles(T * k, E, 16)
+    a256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    o_te = a256(mt * 16 * 4)
+    o_meta = o_te + a256(mt * 4)
+    o_cnt = o_meta + 256
+    i32 = lambda o, n: ws[o:o + 4 * n].view(torch.int32)  # noqa: E731
+    assert torch.equal(i32(0, nt * 16), ref.sorted_ids[:nt * 16])
+    assert torch.equal(i32(o_te, nt), ref.tile_expert[:nt])
+    assert torch.equal(i32(o_meta, 2), ref.meta[:2])
+    assert torch.equal(i32(o_cnt, E), ref.counts)
+
+
 def test_moe_combine_api_with_expert_fn(gpu):
     """moe_combine(x, ids, w, w_lookup=...) with float32 experts, numpy I/O."""
     from ccut.blocks import moe
