@@ -1,0 +1,186 @@
+"""One MoE step as the reference's ``ExpertPipeline.step`` (reference
+``python/ccut/experts/pipeline.py:34-204``), same names, arguments and
+metrics, on the GPU operators of this package.
+
+A step: speculative prefetch from the route history, the router
+``x @ gate_w.T`` (a library float32 GEMM), ``topk_softmax``, prefetch of the
+routed experts, the experts' FFN with the weighted combine, the shared expert
+and the metrics.  The expert weights come from ``reader`` in one of two ways:
+
+* ``reader.experts(layer)`` returning a whole layer in device format
+  (``W4Experts`` or ``Fp8Experts``): one fused call (``moe_ffn_w4`` /
+  ``moe_ffn_fp8``); activations go to the int4 kernels as bfloat16.
+* otherwise ``reader.get(layer, eid, timeout)`` per routed expert returning
+  float32 ``(w_gate [hidden, inter], w_up [hidden, inter], w_down [inter,
+  hidden])``, as the reference's reader does: ``expert_ffn`` per expert and
+  ``moe_combine`` (reference ``pipeline.py:155-179``).  An expert whose read
+  raises ``TimeoutError`` is left out of the step (its assignments
+  contribute nothing, the other weights are not renormalised), as in the
+  reference (``:159-163``).
+
+``reader.prefetch(layer, ids)``, ``reader.stats()`` and ``reader.close()``
+are called when the reader has them.
+"""
+
+from __future__ import annotations
+
+import time
+from collections import deque
+from dataclasses import dataclass
+from typing import Iterable
+
+import numpy as np
+import torch
+
+from ccut import _dev
+from ccut.blocks import moe
+
+__all__ = ["PipelineMetrics", "ExpertPipeline", "RouteHistory"]
+
+
+@dataclass
+class PipelineMetrics:
+    """Timings of the step's stages (reference ``pipeline.py:34-63``)."""
+
+    compute_ns: int = 0
+    prefetch_ns: int = 0
+    overlap_ns: int = 0
+    steps: int = 0
+    speculative_correct: int = 0
+    speculative_total: int = 0
+    ring_hits: int = 0
+    ring_misses: int = 0
+    ring_evicted: int = 0
+
+    def overlap_ratio(self) -> float:
+        return self.overlap_ns / self.compute_ns if self.compute_ns > 0 else 0.0
+
+    def speculative_accept_rate(self) -> float:
+        return self.speculative_correct / self.speculative_total if self.speculative_total > 0 else 0.0
+
+    def to_dict(self) -> dict:
+        return {
+            "compute_ns": self.compute_ns,
+            "prefetch_ns": self.prefetch_ns,
+            "overlap_ns": self.overlap_ns,
+            "overlap_ratio": round(self.overlap_ratio(), 4),
+            "steps": self.steps,
+            "spec_accept_rate": round(self.speculative_accept_rate(), 4),
+            "ring_hits": self.ring_hits,
+            "ring_misses": self.ring_misses,
+        }
+
+
+class RouteHistory:
+    """Sliding window of routing decisions (reference ``pipeline.py:66-84``):
+    ``predict`` returns the experts seen most often in the window, most
+    frequent first (ties in first-seen order)."""
+
+    def __init__(self, window: int = 4):
+        self.window = window
+        self._hist: deque[set[int]] = deque(maxlen=window)
+
+    def record(self, topk_ids: Iterable[int]) -> None:
+        self._hist.append(set(int(x) for x in topk_ids))
+
+    def predict(self, top_k: int) -> list[int]:
+        if not self._hist:
+            return []
+        counts: dict[int, int] = {}
+        for step in self._hist:
+            for e in step:
+                counts[e] = counts.get(e, 0) + 1
+        return [e for e, _ in sorted(counts.items(), key=lambda kv: -kv[1])[:top_k]]
+
+
+class ExpertPipeline:
+    """Routing + expert FFN + combine + shared expert per step (reference
+    ``pipeline.py:87-208``)."""
+
+    def __init__(self, reader, num_workers: int = 2, speculative_window: int = 4, prefetch_steps_ahead: int = 2,
+                 metrics_enabled: bool = True):
+        self.reader = reader
+        self.num_workers = num_workers
+        self.prefetch_steps_ahead = prefetch_steps_ahead
+        self.metrics = PipelineMetrics() if metrics_enabled else None
+        self.history = RouteHistory(window=speculative_window)
+
+    def _prefetch(self, layer: int, ids: list[int]):
+        fn = getattr(self.reader, "prefetch", None)
+        return fn(layer, ids) if fn is not None else 0
+
+    def step(self, layer: int, x, gate_w, top_k: int = 8, norm_topk_prob: bool = True,
+             shared_projs: dict | None = None, shared_gate: float = 1.0):
+        """``y [T, hidden]`` float32 for ``x [T, hidden]``: numpy in, numpy
+        out; a device tensor in, a device tensor out."""
+        t0 = time.monotonic_ns()
+        if self.metrics and self.prefetch_steps_ahead > 0:  # speculative prefetch
+            pred = self.history.predict(top_k)
+            if pred:
+                self.metrics.speculative_total += 1
+                if self._prefetch(layer, pred):
+                    self.metrics.speculative_correct += 1
+        xd = _dev.to_device(x, torch.float32)
+        if xd.dim() != 2:
+            raise ValueError(f"x must be [T, hidden], got {tuple(xd.shape)}")
+        gw = _dev.to_device(gate_w, torch.float32)
+        logits = xd @ gw.T
+        weights, ids = moe.topk_softmax(logits, top_k, norm_topk_prob)
+        ids_h = ids.cpu().numpy()
+        self.history.record(ids_h[0])  # the first token's experts, as the reference records
+        flat_ids = ids_h.reshape(-1).tolist()
+        t_pf0 = time.monotonic_ns()
+        self._prefetch(layer, flat_ids)
+        t_c0 = time.monotonic_ns()
+        layer_experts = getattr(self.reader, "experts", None)
+        ex = layer_experts(layer) if layer_experts is not None else None
+        if isinstance(ex, moe.W4Experts):
+            out = moe.moe_ffn_w4(xd.to(torch.bfloat16), ids, weights, ex, out_dtype=torch.float32)
+        elif isinstance(ex, moe.Fp8Experts):
+            out = moe.moe_ffn_fp8(xd, ids, weights, ex, out_dtype=torch.float32)
+        elif ex is not None:
+            raise TypeError(f"reader.experts({layer}) returned {type(ex).__name__}, "
+                            "expected W4Experts or Fp8Experts")
+        else:
+            resolved: dict[int, tuple] = {}
+            for eid in sorted(set(e for e in flat_ids if e >= 0)):
+                try:
+                    resolved[eid] = self.reader.get(layer, int(eid), timeout=30.0)
+                except TimeoutError:
+                    continue  # left out of this step
+            ids_used = ids.clone()
+            for eid in set(e for e in flat_ids if e >= 0) - set(resolved):
+                ids_used[ids_used == eid] = -1
+            if resolved:
+                out = moe.moe_combine(xd, ids_used, weights, w_lookup=resolved.__getitem__)
+            else:
+                out = torch.zeros_like(xd)
+        torch.cuda.synchronize(xd.device)
+        t_c1 = time.monotonic_ns()
+        if shared_projs is not None and "gate_proj" in shared_projs:
+            s = shared_projs["gate_proj"].apply(x)
+            su = shared_projs["up_proj"].apply(x)
+            from ccut.quant import kernels as qk
+
+            inter = qk.silu_mul_fused(s, su, None)
+            s_out = shared_projs["down_proj"].apply(inter)
+            moe.shared_expert_add(out, s_out, shared_gate)
+        t1 = time.monotonic_ns()
+        if self.metrics is not None:
+            compute = t_c1 - t_c0
+            prefetch = t_pf0 - t0 + (t1 - t_c1)
+            self.metrics.compute_ns += compute
+            self.metrics.prefetch_ns += prefetch
+            self.metrics.overlap_ns += min(compute, prefetch)
+            self.metrics.steps += 1
+            stats = getattr(self.reader, "stats", None)
+            if stats is not None:
+                st = stats()
+                self.metrics.ring_hits = st.get("hits", 0)
+                self.metrics.ring_misses = st.get("misses", 0)
+        return _dev.to_host(out) if _dev.is_host(x) else out
+
+    def close(self) -> None:
+        close = getattr(self.reader, "close", None)
+        if close is not None:
+            close()

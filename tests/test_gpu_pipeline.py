@@ -1,0 +1,154 @@
+"""GPU parity of ExpertPipeline.step (reference python/ccut/experts/
+pipeline.py:123-204) against the oracle: router, topk_softmax, expert FFN,
+weighted combine, shared expert; the per-expert reader path (float32
+weights, timeouts drop an expert) and the fused int4 layer path."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq as oawq
+from oracle import moe as omoe
+
+pytestmark = pytest.mark.gpu
+
+
+class _Reader:
+    """Per-expert float32 weights, as the reference's ExpertReader.get."""
+
+    def __init__(self, W, slow=()):
+        self.W, self.slow = W, set(slow)
+        self.prefetched, self.gets = [], []
+
+    def prefetch(self, layer, ids):
+        self.prefetched.append(list(ids))
+        return len(ids)
+
+    def get(self, layer, eid, timeout=30.0):
+        self.gets.append(eid)
+        if eid in self.slow:
+            raise TimeoutError(f"expert {eid}")
+        return self.W[eid]
+
+    def stats(self):
+        return {"hits": 7, "misses": 2}
+
+
+class _Proj:
+    def __init__(self, w):
+        self.w = w
+
+    def apply(self, x):
+        if isinstance(x, torch.Tensor):  # device activations stay on the device
+            return x.float() @ torch.from_numpy(self.w).to(x.device).T
+        return (np.asarray(x, np.float32) @ self.w.T).astype(np.float32)
+
+
+def _case(seed, T=8, E=16, H=64, I=32):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gate_w = (rng.standard_normal((E, H)) * 0.2).astype(np.float32)
+    W = {e: tuple((rng.standard_normal(s) * 0.1).astype(np.float32) for s in ((H, I), (H, I), (I, H)))
+         for e in range(E)}
+    return x, gate_w, W
+
+
+def _logits(gpu, x, gate_w):
+    # the step's router GEMM, same operands on the same device
+    return (torch.from_numpy(x).to(gpu) @ torch.from_numpy(gate_w).to(gpu).T).cpu().numpy()
+
+
+def test_step_per_expert_reader_matches_oracle(gpu):
+    from ccut.experts import ExpertPipeline
+
+    x, gate_w, W = _case(1)
+    r = _Reader(W)
+    pipe = ExpertPipeline(r, num_workers=1, speculative_window=4, prefetch_steps_ahead=2)
+    y = pipe.step(3, x, gate_w, top_k=4, norm_topk_prob=True)
+    w0, ids0 = omoe.topk_softmax(_logits(gpu, x, gate_w), 4)
+    ref = omoe.moe_combine(x, ids0, w0, W.__getitem__)
+    assert isinstance(y, np.ndarray) and y.dtype == np.float32 and y.shape == x.shape
+    assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
+    assert sorted(r.gets) == sorted(set(ids0.reshape(-1).tolist()))
+    assert r.prefetched[-1] == ids0.reshape(-1).tolist()
+    # second step: the speculative prefetch from the route history, metrics
+    y2 = pipe.step(3, x, gate_w, top_k=4, norm_topk_prob=False)
+    w1, ids1 = omoe.topk_softmax(_logits(gpu, x, gate_w), 4, False)
+    ref2 = omoe.moe_combine(x, ids1, w1, W.__getitem__)
+    assert np.abs(y2 - ref2).max() <= 1e-4 * np.abs(ref2).max()
+    m = pipe.metrics
+    assert m.steps == 2 and m.speculative_total == 1 and m.speculative_correct == 1
+    assert m.compute_ns > 0 and (m.ring_hits, m.ring_misses) == (7, 2)
+    # prefetches: step 1's experts, then step 2's speculative guess (token 0's
+    # experts of step 1) and step 2's experts
+    assert len(r.prefetched) == 3 and set(r.prefetched[1]) == set(ids0[0].tolist())
+
+
+def test_step_timeout_leaves_expert_out(gpu):
+    from ccut.experts import ExpertPipeline
+
+    x, gate_w, W = _case(2)
+    w0, ids0 = omoe.topk_softmax(_logits(gpu, x, gate_w), 4)
+    slow = int(ids0[0, 0])
+    pipe = ExpertPipeline(_Reader(W, slow=[slow]), metrics_enabled=False)
+    y = pipe.step(0, x, gate_w, top_k=4)
+    zero = tuple(np.zeros_like(a) for a in W[slow])
+    ref = omoe.moe_combine(x, ids0, w0, lambda e: zero if e == slow else W[e])  # contributes nothing
+    assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
+    assert pipe.metrics is None
+
+
+def test_step_shared_expert_device_io(gpu):
+    from ccut.experts import ExpertPipeline
+
+    x, gate_w, W = _case(3)
+    rng = np.random.default_rng(30)
+    H, S = x.shape[1], 48
+    sp = {"gate_proj": _Proj((rng.standard_normal((S, H)) * 0.1).astype(np.float32)),
+          "up_proj": _Proj((rng.standard_normal((S, H)) * 0.1).astype(np.float32)),
+          "down_proj": _Proj((rng.standard_normal((H, S)) * 0.1).astype(np.float32))}
+    pipe = ExpertPipeline(_Reader(W))
+    y = pipe.step(1, torch.from_numpy(x).to(gpu), gate_w, top_k=2, shared_projs=sp, shared_gate=0.5)
+    assert isinstance(y, torch.Tensor) and y.is_cuda
+    w0, ids0 = omoe.topk_softmax(_logits(gpu, x, gate_w), 2)
+    ref = omoe.moe_combine(x, ids0, w0, W.__getitem__)
+    s, su = sp["gate_proj"].apply(x), sp["up_proj"].apply(x)
+    inter = (s / (1.0 + np.exp(-s.astype(np.float64))) * su).astype(np.float32)
+    ref = ref + np.float32(0.5) * sp["down_proj"].apply(inter)
+    yh = y.cpu().numpy()
+    assert np.abs(yh - ref).max() <= 1e-4 * np.abs(ref).max()
+
+
+def test_step_fused_int4_layer(gpu):
+    """reader.experts(layer) hands the whole layer over in device format: one
+    fused call, bfloat16 activations, max|dy| <= 2e-2 max|y_ref|."""
+    from ccut.blocks import moe
+    from ccut.experts import ExpertPipeline
+
+    E, H, I, G, T, k = 16, 256, 128, 128, 8, 4
+    rng = np.random.default_rng(4)
+
+    def one(K, N):
+        q = rng.integers(0, 16, size=(E, K, N), dtype=np.uint8)
+        z = rng.integers(0, 16, size=(E, K // G, N), dtype=np.uint8)
+        s = (np.abs(rng.standard_normal((E, K // G, N))) * 0.01 + 1e-3).astype(np.float16)
+        return (np.stack([oawq.pack(q[e]) for e in range(E)]), np.stack([oawq.pack(z[e]) for e in range(E)]), s)
+
+    gate, up, down = one(H, I), one(H, I), one(I, H)
+    dev = lambda t: tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(dev(gate), dev(up), dev(down), group_size=G)
+
+    class _LayerReader:
+        def experts(self, layer):
+            return ex
+
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gate_w = (rng.standard_normal((E, H)) * 0.1).astype(np.float32)
+    y = ExpertPipeline(_LayerReader()).step(0, x, gate_w, top_k=k)
+    w0, ids0 = omoe.topk_softmax(_logits(gpu, x, gate_w), k)
+    lookup = lambda e: tuple(oawq.dequant(t[0][e], t[1][e], t[2][e], G) for t in (gate, up, down))  # noqa: E731
+    xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    ref = omoe.moe_combine(xb, ids0, w0, lookup)
+    assert np.abs(y - ref).max() <= 2e-2 * np.abs(ref).max()
