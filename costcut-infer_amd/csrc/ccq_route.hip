@@ -216,48 +216,62 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
 // y[t, h] = sum_s w[t, s] * rows[t*k + s, h], slot order, float32.  Slots
 // whose id is outside [0, E) (dropped by the schedule) contribute nothing.
 // rows are float32 (RT = CCQ_F32) or bf16 (RT = CCQ_BF16); with VEC each
-// thread takes 16 bytes of a row (4 or 8 columns).
+// thread takes 16 bytes of a row (4 or 8 columns).  The ids, weights and
+// rows of up to 16 slots are loaded before their FMAs (one memory round
+// trip per 16 slots, not one per slot); a dropped slot's row is read and
+// not used.
 template <int YT, int RT, bool VEC>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ rows,
                                                           const float* __restrict__ wts,
                                                           const int64_t* __restrict__ ids, int64_t E,
                                                           void* __restrict__ y, int64_t T, int k, int64_t H) {
   constexpr int CW = VEC ? (RT == CCQ_F32 ? 4 : 8) : 1;
+  constexpr int KMAX = 16;
   const int64_t t = blockIdx.y;
   const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * CW;
   if (h >= H) return;
   float acc[CW];
 #pragma unroll
   for (int c = 0; c < CW; ++c) acc[c] = 0.f;
-  for (int s = 0; s < k; ++s) {
-    const int64_t a = t * k + s;
-    if (ids) {
-      const int64_t e = ids[a];
-      if (e < 0 || e >= E) continue;
-    }
-    const float wv = wts[a];
-    float r[CW];
-    if constexpr (RT == CCQ_F32) {
-      const float* rp = reinterpret_cast<const float*>(rows) + a * H + h;
-      if constexpr (VEC) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(rp);
+  for (int s0 = 0; s0 < k; s0 += KMAX) {  // chunks of KMAX slots, in slot order
+    float wv[KMAX], r[KMAX][CW];
+    bool ok[KMAX];
 #pragma unroll
-        for (int c = 0; c < CW; ++c) r[c] = v[c];
-      } else {
-        r[0] = rp[0];
+    for (int j = 0; j < KMAX; ++j) {
+      if (s0 + j < k) {
+        const int64_t a = t * k + s0 + j;
+        ok[j] = true;
+        if (ids) {
+          const int64_t e = ids[a];
+          ok[j] = e >= 0 && e < E;
+        }
+        wv[j] = wts[a];
+        if constexpr (RT == CCQ_F32) {
+          const float* rp = reinterpret_cast<const float*>(rows) + a * H + h;
+          if constexpr (VEC) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(rp);
+#pragma unroll
+            for (int c = 0; c < CW; ++c) r[j][c] = v[c];
+          } else {
+            r[j][0] = rp[0];
+          }
+        } else {
+          const uint16_t* rp = reinterpret_cast<const uint16_t*>(rows) + a * H + h;
+          if constexpr (VEC) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(rp);
+#pragma unroll
+            for (int c = 0; c < CW; ++c) r[j][c] = bf16_bits_to_f32((v[c >> 1] >> (16 * (c & 1))) & 0xFFFFu);
+          } else {
+            r[j][0] = bf16_bits_to_f32(rp[0]);
+          }
+        }
       }
-    } else {
-      const uint16_t* rp = reinterpret_cast<const uint16_t*>(rows) + a * H + h;
-      if constexpr (VEC) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(rp);
-#pragma unroll
-        for (int c = 0; c < CW; ++c) r[c] = bf16_bits_to_f32((v[c >> 1] >> (16 * (c & 1))) & 0xFFFFu);
-      } else {
-        r[0] = bf16_bits_to_f32(rp[0]);
-      }
     }
 #pragma unroll
-    for (int c = 0; c < CW; ++c) acc[c] = fmaf(wv, r[c], acc[c]);
+    for (int j = 0; j < KMAX; ++j)
+      if (s0 + j < k && ok[j])
+#pragma unroll
+        for (int c = 0; c < CW; ++c) acc[c] = fmaf(wv[j], r[j][c], acc[c]);
   }
 #pragma unroll
   for (int c = 0; c < CW; ++c) {

@@ -155,12 +155,15 @@ def test_align_drops_invalid_ids_and_handles_duplicates(gpu):
     assert got["counts"].tolist() == [0, 2, 0, 4, 0]
 
 
-def test_combine_slot_order(gpu):
+@pytest.mark.parametrize("k,H", [(3, 70), (20, 128), (6, 2048)])
+def test_combine_slot_order(gpu, k, H):
+    """Slot-order float32 sums; k above 16 runs in chunks of 16 slots, H a
+    multiple of 4 on the 16-byte path."""
     from ccut._lib import call
     from ccut import _dev
 
-    rng = np.random.default_rng(9)
-    T, k, H = 5, 3, 70
+    rng = np.random.default_rng(9 + k)
+    T = 5
     rows = torch.from_numpy(rng.standard_normal((T * k, H)).astype(np.float32)).to(gpu)
     w = torch.from_numpy(rng.random((T, k)).astype(np.float32)).to(gpu)
     y = torch.empty((T, H), dtype=torch.float32, device=gpu)
