@@ -152,3 +152,31 @@ def test_step_fused_int4_layer(gpu):
     xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     ref = omoe.moe_combine(xb, ids0, w0, lookup)
     assert np.abs(y - ref).max() <= 2e-2 * np.abs(ref).max()
+
+
+def test_step_fused_fp8_layer(gpu):
+    """reader.experts(layer) returning FP8 128x128 block experts: one fused
+    call (float32 activations quantized per token per 128 channels inside)."""
+    from test_gpu_fp8_block import TOL as FP8_TOL, _fp8_weights, _moe_ref
+
+    from ccut.blocks import moe
+    from ccut.experts import ExpertPipeline
+
+    E, H, I, T, k = 8, 256, 256, 12, 2
+    rng = np.random.default_rng(5)
+    wg, sg = _fp8_weights(rng, E, I, H)
+    wu, su = _fp8_weights(rng, E, I, H)
+    wd, sd = _fp8_weights(rng, E, H, I)
+    dev = lambda a: torch.from_numpy(a).to(gpu)  # noqa: E731
+    ex = moe.Fp8Experts.from_block((dev(wg), dev(sg)), (dev(wu), dev(su)), (dev(wd), dev(sd)))
+
+    class _LayerReader:
+        def experts(self, layer):
+            return ex
+
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    gate_w = (rng.standard_normal((E, H)) * 0.1).astype(np.float32)
+    y = ExpertPipeline(_LayerReader()).step(2, x, gate_w, top_k=k)
+    w0, ids0 = omoe.topk_softmax(_logits(gpu, x, gate_w), k)
+    ref = _moe_ref(x, ids0, w0, wg, sg, wu, su, wd, sd)
+    assert np.abs(y - ref).max() <= FP8_TOL * np.abs(ref).max()
