@@ -1,0 +1,317 @@
+"""Expert weight reader over an expert index (reference
+``python/ccut/experts/reader.py:38-340``): per-layer rings of ready experts,
+background workers that fill them on ``prefetch``, ``get`` that waits for a
+fill and raises ``TimeoutError`` rather than returning stale weights.
+
+A slot holds one expert's ``(gate, up, down)`` as float32 device tensors,
+dequantized on the GPU from the checkpoint segments:
+
+* ``F8_E4M3`` / ``F8_E5M2`` weight ``[out, in]`` with an optional per-row
+  ``weight_scale`` (``[out]`` or ``[out, 1]``, BF16 / F16 / F32):
+  ``fp8_dequant_mat`` (``ccq_fp8_dequant``); E5M2 is decoded by torch;
+* ``BF16`` / ``F16`` / ``F32`` weight: converted to float32;
+* AWQ ``qweight`` / ``qzeros`` / ``scales`` (int32 ``[K, N/8]``, int32
+  ``[K/G, N/8]``, F16/BF16 ``[K/G, N]``): ``ccq_awq_dequant`` to
+  ``[K, N]``.
+
+The slots keep the checkpoint's orientation, as the reference's do
+(``[out, in]`` for the FP8 / float layouts, ``[in, out]`` for AWQ).
+
+``experts(layer)`` additionally packs a whole AWQ layer into the fused
+kernels' device format (``W4Experts``, built once per layer), which
+``ExpertPipeline`` uses instead of per-expert reads.
+"""
+
+from __future__ import annotations
+
+import os
+import threading
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from ccut import _dev
+from ccut.experts.index import ExpertEntry, ExpertIndex, read_header
+
+__all__ = ["ExpertReader", "ExpertRing", "RingFullError"]
+
+
+class RingFullError(RuntimeError):
+    """No slot can take another expert (reference ``reader.py:38-40``)."""
+
+
+class _Slot:
+    __slots__ = ("expert_id", "layer", "gate", "up", "down", "ready", "seq", "filling")
+
+    def __init__(self, layer: int):
+        self.expert_id, self.layer = -1, layer
+        self.gate = self.up = self.down = None
+        self.ready, self.seq, self.filling = False, 0, False
+
+
+class ExpertRing:
+    """Fixed slots of one layer, refilled round robin (reference ``reader.py:55-83``)."""
+
+    def __init__(self, layer: int, slots: int):
+        if slots < 1:
+            raise ValueError(f"ring needs at least one slot, got {slots}")
+        self.layer = layer
+        self.slots = [_Slot(layer) for _ in range(slots)]
+        self._next = 0
+
+    def find(self, expert_id: int) -> _Slot | None:
+        for s in self.slots:
+            if s.ready and s.expert_id == expert_id:
+                return s
+        return None
+
+    def take_slot(self) -> _Slot | None:
+        """The next slot in round-robin order that no worker is filling (None
+        when every slot is being filled)."""
+        for _ in range(len(self.slots)):
+            s = self.slots[self._next]
+            self._next = (self._next + 1) % len(self.slots)
+            if not s.filling:
+                return s
+        return None
+
+    def invalidate(self, expert_id: int) -> None:
+        for s in self.slots:
+            if s.expert_id == expert_id:
+                s.ready, s.expert_id = False, -1
+
+
+_FLOAT_DTYPES = {"BF16": torch.bfloat16, "F16": torch.float16, "F32": torch.float32}
+
+
+class ExpertReader:
+    def __init__(self, index: ExpertIndex, model_dir: str | Path, num_layers: int, ring_slots: int = 2,
+                 verify_crc: bool = False, num_workers: int = 2, device: torch.device | None = None):
+        self.index = index
+        self.model_dir = Path(model_dir)
+        self.device = device if device is not None else _dev.require_gpu()
+        self.rings = {l: ExpertRing(l, ring_slots) for l in range(num_layers)}
+        self._verify_crc = verify_crc  # accepted for signature parity; safetensors carries no checksums
+        self._fds: dict[str, tuple[int, int]] = {}  # shard -> (fd, data start)
+        self._cv = threading.Condition()
+        self._queue: list[tuple[int, int]] = []
+        self._pending: set[tuple[int, int]] = set()
+        self._failed: dict[tuple[int, int], str] = {}
+        self._seq = 0
+        self._stop = False
+        self._layers: dict[int, object] = {}
+        self._stats = {"reads": 0, "hits": 0, "misses": 0, "prefetches": 0, "stale": 0}
+        self._workers = [threading.Thread(target=self._worker, name=f"expert-prefetch-{w}", daemon=True)
+                         for w in range(max(1, num_workers))]
+        for t in self._workers:
+            t.start()
+
+    # ---- segment IO ----
+    def _shard_fd(self, shard: str) -> tuple[int, int]:
+        with self._cv:
+            got = self._fds.get(shard)
+            if got is None:
+                path = self.model_dir / shard
+                start, _ = read_header(path)
+                got = (os.open(path, os.O_RDONLY), start)
+                self._fds[shard] = got
+            return got
+
+    def _read(self, entry: ExpertEntry, key: str) -> tuple[np.ndarray, str, tuple[int, ...]]:
+        off, length, _, dtype = entry.segments[key]
+        fd, start = self._shard_fd(entry.shard)
+        raw = os.pread(fd, length, start + off)
+        if len(raw) != length:
+            raise OSError(f"{entry.shard}: short read of {key} ({len(raw)} of {length} bytes)")
+        return np.frombuffer(raw, dtype=np.uint8), dtype, tuple(entry.shapes.get(key, ()))
+
+    @staticmethod
+    def _pick(segs: dict, proj: str, suffixes: tuple[str, ...]) -> str | None:
+        for base in (f"{proj}_proj", proj):
+            for suf in suffixes:
+                if base + suf in segs:
+                    return base + suf
+        return None
+
+    def _dequant(self, entry: ExpertEntry, proj: str) -> torch.Tensor:
+        segs = entry.segments
+        qkey = self._pick(segs, proj, (".qweight",))
+        if qkey is not None:  # AWQ
+            from ccut.quant import awq
+
+            base = qkey[: -len(".qweight")]
+            qw, qz, sc = (self._device_tensor(entry, base + s) for s in (".qweight", ".qzeros", ".scales"))
+            K, N = qw.shape[0], qw.shape[1] * 8
+            return awq.dequant(qw, qz, sc, K // sc.shape[0]).float()
+        wkey = self._pick(segs, proj, (".weight", ""))
+        if wkey is None:
+            raise KeyError(f"no {proj} weight segment among {sorted(segs)}")
+        raw, dtype, shape = self._read(entry, wkey)
+        rows, cols = _shape_2d(int(entry.segments[wkey][2]), shape)
+        if dtype in ("F8_E4M3", "F8_E5M2"):
+            skey = self._pick(segs, proj, (".weight_scale", "_scale", ".weight_scale_inv"))
+            scale = (torch.ones(rows, dtype=torch.float32, device=self.device) if skey is None
+                     else self._device_tensor(entry, skey).float().reshape(-1))
+            if scale.numel() != rows:
+                raise ValueError(f"{proj}: {scale.numel()} scales for {rows} rows (per-row scales expected)")
+            w = torch.from_numpy(raw.copy()).to(self.device).reshape(rows, cols)
+            if dtype == "F8_E4M3":
+                from ccut.quant import kernels as qk
+
+                out = torch.empty((rows, cols), dtype=torch.float32, device=self.device)
+                return qk.fp8_dequant_mat(w, scale, out)
+            return w.view(torch.float8_e5m2).float() * scale[:, None]
+        if dtype in _FLOAT_DTYPES:
+            t = torch.from_numpy(raw.copy()).view(_FLOAT_DTYPES[dtype]).reshape(rows, cols)
+            return t.to(self.device).float()
+        raise NotImplementedError(f"expert segment dtype {dtype} is not supported")
+
+    def _device_tensor(self, entry: ExpertEntry, key: str) -> torch.Tensor:
+        raw, dtype, shape = self._read(entry, key)
+        tdt = {"I32": torch.int32, "U32": torch.int32, **_FLOAT_DTYPES}.get(dtype)
+        if tdt is None:
+            raise NotImplementedError(f"segment {key} of dtype {dtype}")
+        return torch.from_numpy(raw.copy()).view(tdt).reshape(shape or (-1,)).to(self.device)
+
+    # ---- slots ----
+    def _fill(self, layer: int, expert_id: int, slot: _Slot) -> None:
+        entry = self.index.entries[(layer, expert_id)]
+        g, u, d = (self._dequant(entry, p) for p in ("gate", "up", "down"))
+        torch.cuda.synchronize(self.device)
+        with self._cv:
+            self._seq += 1
+            slot.expert_id, slot.layer = expert_id, layer
+            slot.gate, slot.up, slot.down = g, u, d
+            slot.ready, slot.seq = True, self._seq
+            self._stats["reads"] += 1
+
+    def _worker(self) -> None:
+        while True:
+            with self._cv:
+                while not self._queue and not self._stop:
+                    self._cv.wait()
+                if self._stop:
+                    return
+                layer, eid = self._queue.pop(0)
+                ring = self.rings[layer]
+                if ring.find(eid) is not None:
+                    self._pending.discard((layer, eid))
+                    self._cv.notify_all()
+                    continue
+                slot = ring.take_slot()
+                if slot is None:  # every slot of the layer is being filled: wait for one
+                    self._queue.insert(0, (layer, eid))
+                    self._cv.wait(timeout=0.5)
+                    continue
+                slot.ready, slot.filling = False, True  # never handed out half written
+            try:
+                self._fill(layer, eid, slot)
+            except Exception as exc:  # the waiting get() times out; the reason is kept
+                with self._cv:
+                    slot.expert_id = -1
+                    self._failed[(layer, eid)] = repr(exc)
+            with self._cv:
+                slot.filling = False
+                self._pending.discard((layer, eid))
+                self._cv.notify_all()
+
+    def _enqueue(self, layer: int, eid: int) -> bool:
+        key = (layer, eid)
+        if key in self._pending or self._stop:
+            return False
+        if (layer, eid) not in self.index.entries:
+            self._failed[key] = "not in the expert index"
+            return False
+        self._queue.append(key)
+        self._pending.add(key)
+        self._stats["prefetches"] += 1
+        self._cv.notify_all()
+        return True
+
+    def prefetch(self, layer: int, expert_ids) -> int:
+        """Queue the experts that are neither ready nor queued; returns how many were queued."""
+        n = 0
+        with self._cv:
+            ring = self.rings[layer]
+            for eid in expert_ids:
+                if ring.find(int(eid)) is not None:
+                    self._stats["hits"] += 1
+                elif self._enqueue(layer, int(eid)):
+                    n += 1
+        return n
+
+    def get(self, layer: int, expert_id: int, timeout: float = 30.0):
+        """``(gate, up, down)`` float32 device tensors of a ready expert,
+        waiting for its fill; ``TimeoutError`` when it is not ready in time."""
+        deadline = time.monotonic() + timeout
+        with self._cv:
+            ring = self.rings[layer]
+            s = ring.find(expert_id)
+            if s is not None:
+                self._stats["hits"] += 1
+                return s.gate, s.up, s.down
+            self._stats["misses"] += 1
+            self._failed.pop((layer, expert_id), None)
+            self._enqueue(layer, expert_id)
+            while True:
+                s = ring.find(expert_id)
+                if s is not None:
+                    return s.gate, s.up, s.down
+                if (layer, expert_id) not in self._pending and (layer, expert_id) not in self._failed:
+                    # filled and already refilled for another expert before
+                    # this thread woke: queue it again
+                    self._enqueue(layer, expert_id)
+                left = deadline - time.monotonic()
+                if left <= 0:
+                    why = self._failed.get((layer, expert_id))
+                    raise TimeoutError(f"expert (layer={layer}, expert={expert_id}) not ready after {timeout}s"
+                                       + (f": {why}" if why else ""))
+                self._cv.wait(timeout=min(left, 0.5))
+
+    def experts(self, layer: int):
+        """The whole layer as ``W4Experts`` when its experts are AWQ
+        segments (built once), else None (per-expert reads)."""
+        if layer in self._layers:
+            return self._layers[layer]
+        e0 = self.index.get(layer, 0)
+        ex = None
+        if e0 is not None and self._pick(e0.segments, "gate", (".qweight",)) is not None:
+            from ccut.blocks import moe
+
+            def stack(proj):
+                parts = []
+                for eid in range(self.index.num_experts):
+                    entry = self.index.entries[(layer, eid)]
+                    base = self._pick(entry.segments, proj, (".qweight",))[: -len(".qweight")]
+                    parts.append([self._device_tensor(entry, base + s) for s in (".qweight", ".qzeros", ".scales")])
+                return tuple(torch.stack([p[i] for p in parts]) for i in range(3))
+
+            gate, up, down = stack("gate"), stack("up"), stack("down")
+            K = gate[0].shape[1]
+            ex = moe.W4Experts.from_awq(gate, up, down, group_size=K // gate[2].shape[1])
+        self._layers[layer] = ex
+        return ex
+
+    def stats(self) -> dict:
+        return dict(self._stats)
+
+    def close(self) -> None:
+        with self._cv:
+            self._stop = True
+            self._cv.notify_all()
+        for t in self._workers:
+            t.join(timeout=2.0)
+        for fd, _ in self._fds.values():
+            os.close(fd)
+        self._fds.clear()
+
+
+def _shape_2d(numel: int, shape: tuple[int, ...]) -> tuple[int, int]:
+    if len(shape) >= 2:
+        rows = 1
+        for s in shape[:-1]:
+            rows *= s
+        return rows, shape[-1]
+    raise ValueError(f"segment of {numel} elements has no 2-D shape {shape}")
