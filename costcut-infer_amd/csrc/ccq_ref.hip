@@ -164,9 +164,134 @@ static int grid_for(int64_t n, int block) {
   return (int)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
 }
 
+// |x| maximum of a row with numpy's NaN rule (any NaN gives NaN), over the
+// 256 threads of a workgroup; every thread gets the result.
+__device__ float row_amax_256(float m, bool nan, float* red) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    m = fmaxf(m, __shfl_xor(m, off, 64));
+    nan = __shfl_xor((int)nan, off, 64) != 0 || nan;
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = nan ? __builtin_nanf("") : m;
+  __syncthreads();
+  float a = red[0];
+  for (int i = 1; i < 4; ++i) a = (a != a || red[i] != red[i]) ? __builtin_nanf("") : fmaxf(a, red[i]);
+  __syncthreads();
+  return a;
+}
+
+// np.clip(q, -448, 448) keeps NaN
+__device__ __forceinline__ float clip448(float q) { return q != q ? q : fminf(fmaxf(q, -448.0f), 448.0f); }
+
+// Load-time quantization of a BF16 [rows, cols] weight to e4m3 codes, one
+// row per workgroup (quant/online.py:37-64): s = scale[r] when given, else
+// amax / 448 in float64 (0 -> 1); s <= 0 or NaN -> 1; code =
+// half-up(clip(w / float32(s), +-448)) with a float32 division, as numpy
+// divides a float32 row by a Python float.
+__global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const uint16_t* __restrict__ w,
+                                                             const float* __restrict__ scale,
+                                                             uint8_t* __restrict__ out, int64_t cols) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const uint16_t* row = w + r * cols;
+  float m = 0.f;
+  bool nan = false;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    const float v = __uint_as_float((uint32_t)row[c] << 16);
+    m = fmaxf(m, fabsf(v));
+    nan = nan || v != v;
+  }
+  double s;
+  if (scale != nullptr) {
+    s = (double)scale[r];
+  } else {
+    s = (double)row_amax_256(m, nan, red) / 448.0;
+    if (s == 0.0) s = 1.0;  // `amax / 448.0 or 1.0`: only 0.0 is falsy
+  }
+  if (!(s > 0.0)) s = 1.0;
+  const float s32 = (float)s;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    const float v = __uint_as_float((uint32_t)row[c] << 16);
+    out[r * cols + c] = (uint8_t)f32_to_fp8_halfup(clip448(v / s32));
+  }
+}
+
+// Per-token KV quantization (quant/kv.py:70-90): one row (side, head,
+// token) of `dim` float32 per workgroup; amax <= 0 -> codes and scale 0;
+// else s = amax / 448 (float64), codes = half-up(clip(x / float32(s))),
+// scale byte = half-up(float32(s)).  A NaN in the row gives NaN codes.
+__global__ __launch_bounds__(256) void kv_quant_fp8_kernel(const float* __restrict__ kv, uint8_t* __restrict__ out,
+                                                           uint8_t* __restrict__ scales, int64_t dim) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const float* row = kv + r * dim;
+  float m = 0.f;
+  bool nan = false;
+  for (int64_t c = threadIdx.x; c < dim; c += blockDim.x) {
+    const float v = row[c];
+    m = fmaxf(m, fabsf(v));
+    nan = nan || v != v;
+  }
+  const float amax = row_amax_256(m, nan, red);
+  if (amax <= 0.f) {
+    for (int64_t c = threadIdx.x; c < dim; c += blockDim.x) out[r * dim + c] = 0;
+    if (threadIdx.x == 0) scales[r] = 0;
+    return;
+  }
+  const float s32 = (float)((double)amax / 448.0);
+  for (int64_t c = threadIdx.x; c < dim; c += blockDim.x)
+    out[r * dim + c] = (uint8_t)f32_to_fp8_halfup(clip448(row[c] / s32));
+  if (threadIdx.x == 0) scales[r] = (uint8_t)f32_to_fp8_halfup(s32);
+}
+
+// KV read-back (quant/kv.py:93-101): out = decode(code) * decode(scale)
+// (float32 product) where the scale decodes to > 0, else 0.
+__global__ void kv_dequant_fp8_kernel(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
+                                      float* __restrict__ out, int64_t n, int64_t dim) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    const float sc = fp8_e4m3_to_f32(scales[i / dim]);
+    out[i] = sc > 0.f ? fp8_e4m3_to_f32(codes[i]) * sc : 0.f;
+  }
+}
+
 }  // namespace ccq
 
 using namespace ccq;
+
+extern "C" int ccq_quantize_rows_fp8(const uint16_t* w_bf16, const float* scale, uint8_t* out, int64_t rows,
+                                     int64_t cols, void* stream) {
+  CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_quantize_rows_fp8: negative shape");
+  CCQ_REQUIRE(rows <= 0x7fffffff, "ccq_quantize_rows_fp8: rows=%lld too large", (long long)rows);
+  if (rows == 0 || cols == 0) return 0;
+  CCQ_REQUIRE(w_bf16 && out, "ccq_quantize_rows_fp8: null pointer");
+  hipLaunchKernelGGL(quant_rows_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), w_bf16, scale,
+                     out, cols);
+  return launch_status("ccq_quantize_rows_fp8");
+}
+
+extern "C" int ccq_kv_quant_fp8(const float* kv, uint8_t* out, uint8_t* scales, int64_t rows, int64_t dim,
+                                void* stream) {
+  CCQ_REQUIRE(rows >= 0 && dim >= 0, "ccq_kv_quant_fp8: negative shape");
+  CCQ_REQUIRE(rows <= 0x7fffffff, "ccq_kv_quant_fp8: rows=%lld too large", (long long)rows);
+  if (rows == 0) return 0;
+  CCQ_REQUIRE(kv && out && scales, "ccq_kv_quant_fp8: null pointer");
+  hipLaunchKernelGGL(kv_quant_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), kv, out, scales,
+                     dim);
+  return launch_status("ccq_kv_quant_fp8");
+}
+
+extern "C" int ccq_kv_dequant_fp8(const uint8_t* codes, const uint8_t* scales, float* out, int64_t rows,
+                                  int64_t dim, void* stream) {
+  CCQ_REQUIRE(rows >= 0 && dim >= 0, "ccq_kv_dequant_fp8: negative shape");
+  if (rows == 0 || dim == 0) return 0;
+  CCQ_REQUIRE(codes && scales && out, "ccq_kv_dequant_fp8: null pointer");
+  const int64_t n = rows * dim;
+  hipLaunchKernelGGL(kv_dequant_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), codes, scales,
+                     out, n, dim);
+  return launch_status("ccq_kv_dequant_fp8");
+}
 
 extern "C" int ccq_fp8_to_f32(const uint8_t* code, float* out, int64_t n, void* stream) {
   CCQ_REQUIRE(n >= 0, "ccq_fp8_to_f32: n < 0");

@@ -55,6 +55,26 @@ int ccq_f32_to_fp8(const float* x, uint8_t* out, int64_t n, void* stream);
 
 /* out[r,c] = fp8(w[r,c]) * scale[r]   (w [rows,cols] e4m3fn, scale [rows]).
  * Replaces fp8_dequant_mat / fp8_dequant_row (quant/kernels.py:126-171). */
+/* Load-time FP8 quantization of a BF16 weight [rows, cols] (row-major
+ * bf16 bits) to e4m3 codes [rows, cols], per output row: scale[r] when
+ * scale is non-null, else amax(|row|)/448 (0 -> 1); scales <= 0 or NaN
+ * -> 1; code = the reference's half-up encoding of clip(w / s, +-448)
+ * (float32 division).  Replaces quantize_buffer_inplace
+ * (quant/online.py:37-64). */
+int ccq_quantize_rows_fp8(const uint16_t* w_bf16, const float* scale, uint8_t* out, int64_t rows,
+                          int64_t cols, void* stream);
+
+/* Per-token KV cache quantization: kv [rows, dim] f32 (rows = 2 * heads *
+ * seq) -> codes [rows, dim] e4m3 and one e4m3 scale byte per row:
+ * amax <= 0 -> zeros; else s = amax/448, codes = half-up(clip(x / s)),
+ * scale = half-up(s).  Replaces quantize_kv_token (quant/kv.py:70-90). */
+int ccq_kv_quant_fp8(const float* kv, uint8_t* out, uint8_t* scales, int64_t rows, int64_t dim, void* stream);
+
+/* KV read-back: out = fp8(code) * fp8(scale) (float32) where the scale
+ * decodes to > 0, else 0.  Replaces dequantize_kv_token (quant/kv.py:93-101). */
+int ccq_kv_dequant_fp8(const uint8_t* codes, const uint8_t* scales, float* out, int64_t rows, int64_t dim,
+                       void* stream);
+
 int ccq_fp8_dequant(const uint8_t* w, const float* scale, float* out,
                     int64_t rows, int64_t cols, void* stream);
 

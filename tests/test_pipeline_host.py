@@ -26,3 +26,23 @@ def test_metrics_ratios_and_dict():
     assert d["overlap_ratio"] == 0.25 and d["spec_accept_rate"] == 0.75
     assert set(d) == {"compute_ns", "prefetch_ns", "overlap_ns", "overlap_ratio", "steps", "spec_accept_rate",
                       "ring_hits", "ring_misses"}
+
+
+def test_kv_mode_and_bytes(tmp_path):
+    """reference python/ccut/quant/kv.py:37-67 (host logic)."""
+    import json
+
+    import pytest
+
+    from ccut.quant.kv import KVQuantMode, kv_bytes_per_token, resolve_kv_dtype
+
+    assert resolve_kv_dtype(None) == "bf16" and resolve_kv_dtype(None, "FP8") == "fp8"
+    (tmp_path / "config.json").write_text(json.dumps({"text_config": {"kv_cache_scheme": {"type": "fp8_e4m3"}}}))
+    assert resolve_kv_dtype(tmp_path) == KVQuantMode.FP8
+    (tmp_path / "config.json").write_text(json.dumps({"kv_cache_scheme": None}))
+    assert resolve_kv_dtype(tmp_path, "auto") == KVQuantMode.BF16
+    with pytest.raises(ValueError):
+        resolve_kv_dtype(tmp_path, "int8")
+    assert kv_bytes_per_token(4, 128, "bf16") == 2048 and kv_bytes_per_token(4, 128, "fp8") == 1032
+    with pytest.raises(ValueError):
+        kv_bytes_per_token(4, 128, "int4")
