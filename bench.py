@@ -272,6 +272,48 @@ def bench_gemm(M: int, K: int, N: int, dev, copies: int):
             "frac_hbm": nbytes / avg / PEAK_HBM, "TFLOPs": 2.0 * M * K * N / avg / 1e12}
 
 
+def bench_quantizers(dev):
+    """Load-time FP8 quantization of a BF16 weight [7168, 2048] and per-token
+    FP8 KV quantization / read-back of [2, 8, 4096, 128] float32, each over
+    distinct buffers (> 512 MiB in total).  Algorithmic bytes: 2 + 1 B per
+    weight element; 4 + 1 B per KV element (+ 1 B per row)."""
+    import torch
+
+    from ccut import _lib
+
+    lib = _lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = ctypes.c_void_p
+    g = torch.Generator(device=dev).manual_seed(3)
+    out = {}
+    R, C, copies = 7168, 2048, 20
+    ws = [(torch.randn((R, C), generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+    q = torch.empty((R, C), dtype=torch.uint8, device=dev)
+    launches = [lambda w=w: lib.ccq_quantize_rows_fp8(vp(w.data_ptr()), None, vp(q.data_ptr()), R, C, stream)
+                for w in ws]
+    _lib.check(launches[0](), "ccq_quantize_rows_fp8")
+    avg = device_time(launches, reps=2)
+    nb = R * C * 3
+    out["online_fp8_quant_7168x2048"] = {"avg_us": avg * 1e6, "bytes": nb, "GBps": nb / avg / 1e9,
+                                         "frac_hbm": nb / avg / PEAK_HBM}
+    del ws
+    rows, dim, copies = 2 * 8 * 4096, 128, 16
+    kvs = [torch.randn((rows, dim), generator=g, device=dev) for _ in range(copies)]
+    codes = [torch.empty((rows, dim), dtype=torch.uint8, device=dev) for _ in range(copies)]
+    scales = [torch.empty(rows, dtype=torch.uint8, device=dev) for _ in range(copies)]
+    back = torch.empty((rows, dim), dtype=torch.float32, device=dev)
+    lq = [lambda i=i: lib.ccq_kv_quant_fp8(vp(kvs[i].data_ptr()), vp(codes[i].data_ptr()), vp(scales[i].data_ptr()),
+                                           rows, dim, stream) for i in range(copies)]
+    ld = [lambda i=i: lib.ccq_kv_dequant_fp8(vp(codes[i].data_ptr()), vp(scales[i].data_ptr()), vp(back.data_ptr()),
+                                             rows, dim, stream) for i in range(copies)]
+    _lib.check(lq[0](), "ccq_kv_quant_fp8")
+    for name, launches in (("kv_fp8_quant_2x8x4096x128", lq), ("kv_fp8_dequant_2x8x4096x128", ld)):
+        avg = device_time(launches, reps=2)
+        nb = rows * dim * 5 + rows
+        out[name] = {"avg_us": avg * 1e6, "bytes": nb, "GBps": nb / avg / 1e9, "frac_hbm": nb / avg / PEAK_HBM}
+    return out
+
+
 def bench_int4_prefill(T: int, dev):
     """int4 (AWQ g128) MoE prefill layer: 128 experts, top-8 of a skewed
     router (logits N(0,1) + per-expert bias N(0,2)), hidden 2048, inter 768,
@@ -414,6 +456,9 @@ def main():
             extra[f"int4_moe_prefill_T{Tp}"] = r
             log(f"int4 MoE prefill T={Tp}: {r['us']:.1f} us, {r['TFLOPs']:.1f} TFLOP/s "
                 f"({r['frac_bf16_peak']:.3f} of bf16 peak), {r['GBps']:.0f} GB/s")
+        for name, r in bench_quantizers(dev).items():
+            extra[name] = r
+            log(f"{name}: {r['GBps']:.0f} GB/s = {r['frac_hbm']:.3f} of HBM peak ({r['avg_us']:.2f} us)")
         r = bench_fp8_prefill(dev)
         extra["fp8_moe_prefill_T2048"] = r
         log(f"fp8 block MoE prefill T=2048: {r['us']:.1f} us, {r['TFLOPs']:.1f} TFLOP/s ({r['frac_fp8_peak']:.3f} "

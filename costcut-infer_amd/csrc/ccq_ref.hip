@@ -256,6 +256,127 @@ __global__ void kv_dequant_fp8_kernel(const uint8_t* __restrict__ codes, const u
   }
 }
 
+// The same load-time quantization with 16-byte loads (cols % 8 == 0,
+// cols <= 2048 * VPT): each thread keeps its VPT x 8 values in registers
+// between the amax and the encode, and stores 8 codes at a time.
+template <int VPT>
+__global__ __launch_bounds__(256) void quant_rows_fp8_vec_kernel(const uint16_t* __restrict__ w,
+                                                                 const float* __restrict__ scale,
+                                                                 uint8_t* __restrict__ out, int64_t cols) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const u32x4* row = reinterpret_cast<const u32x4*>(w + r * cols);
+  const int nv = (int)(cols / 8);
+  float v[VPT][8];
+  float m = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int idx = (int)threadIdx.x + 256 * j;
+    if (idx < nv) {
+      const u32x4 q = row[idx];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t word = q[e >> 1];
+        v[j][e] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+        m = fmaxf(m, fabsf(v[j][e]));
+        nan = nan || v[j][e] != v[j][e];
+      }
+    }
+  }
+  double s;
+  if (scale != nullptr) {
+    s = (double)scale[r];
+  } else {
+    s = (double)row_amax_256(m, nan, red) / 448.0;
+    if (s == 0.0) s = 1.0;
+  }
+  if (!(s > 0.0)) s = 1.0;
+  const float s32 = (float)s;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int idx = (int)threadIdx.x + 256 * j;
+    if (idx < nv) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo |= f32_to_fp8_halfup(clip448(v[j][e] / s32)) << (8 * e);
+        hi |= f32_to_fp8_halfup(clip448(v[j][4 + e] / s32)) << (8 * e);
+      }
+      reinterpret_cast<uint2*>(out + r * cols)[idx] = make_uint2(lo, hi);
+    }
+  }
+}
+
+// KV rows of dim <= 4 * TPR floats (dim % 4 == 0): TPR threads per row,
+// 4 values each, the amax over the row's lanes by butterfly (TPR divides
+// 64, so a row never spans two waves).
+template <int TPR>
+__device__ __forceinline__ float group_amax(float m, bool nan) {
+#pragma unroll
+  for (int off = TPR / 2; off >= 1; off >>= 1) {
+    m = fmaxf(m, __shfl_xor(m, off, 64));
+    nan = __shfl_xor((int)nan, off, 64) != 0 || nan;
+  }
+  return nan ? __builtin_nanf("") : m;
+}
+
+template <int TPR>
+__global__ __launch_bounds__(256) void kv_quant_fp8_vec_kernel(const float* __restrict__ kv, uint8_t* __restrict__ out,
+                                                               uint8_t* __restrict__ scales, int64_t rows,
+                                                               int64_t dim) {
+  const int64_t r = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  const int l = threadIdx.x % TPR, c = 4 * l;
+  const bool ok = r < rows && c < dim;
+  f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (ok) x = *reinterpret_cast<const f32x4*>(kv + r * dim + c);
+  float m = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    m = fmaxf(m, fabsf(x[e]));
+    nan = nan || x[e] != x[e];
+  }
+  const float amax = group_amax<TPR>(m, nan);
+  if (r >= rows) return;
+  if (amax <= 0.f) {
+    if (ok) *reinterpret_cast<uint32_t*>(out + r * dim + c) = 0u;
+    if (l == 0) scales[r] = 0;
+    return;
+  }
+  const float s32 = (float)((double)amax / 448.0);
+  if (ok) {
+    uint32_t q = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q |= f32_to_fp8_halfup(clip448(x[e] / s32)) << (8 * e);
+    *reinterpret_cast<uint32_t*>(out + r * dim + c) = q;
+  }
+  if (l == 0) scales[r] = (uint8_t)f32_to_fp8_halfup(s32);
+}
+
+template <int TPR>
+__global__ __launch_bounds__(256) void kv_dequant_fp8_vec_kernel(const uint8_t* __restrict__ codes,
+                                                                 const uint8_t* __restrict__ scales,
+                                                                 float* __restrict__ out, int64_t rows, int64_t dim) {
+  const int64_t r = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  const int c = 4 * (threadIdx.x % TPR);
+  if (r >= rows || c >= dim) return;
+  const float sc = fp8_e4m3_to_f32(scales[r]);
+  const uint32_t q = *reinterpret_cast<const uint32_t*>(codes + r * dim + c);
+  f32x4 y;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = sc > 0.f ? fp8_e4m3_to_f32((q >> (8 * e)) & 0xffu) * sc : 0.f;
+  *reinterpret_cast<f32x4*>(out + r * dim + c) = y;
+}
+
+// threads per KV row for the vector kernels (0: the general kernels)
+static int kv_tpr(int64_t dim, const void* a, const void* b) {
+  if (dim % 4 != 0 || dim > 256 || !aligned(a, 16) || !aligned(b, 4)) return 0;
+  int t = 1;
+  while (4 * t < dim) t <<= 1;
+  return t;
+}
+
 }  // namespace ccq
 
 using namespace ccq;
@@ -266,8 +387,21 @@ extern "C" int ccq_quantize_rows_fp8(const uint16_t* w_bf16, const float* scale,
   CCQ_REQUIRE(rows <= 0x7fffffff, "ccq_quantize_rows_fp8: rows=%lld too large", (long long)rows);
   if (rows == 0 || cols == 0) return 0;
   CCQ_REQUIRE(w_bf16 && out, "ccq_quantize_rows_fp8: null pointer");
-  hipLaunchKernelGGL(quant_rows_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), w_bf16, scale,
-                     out, cols);
+  hipStream_t st = as_stream(stream);
+  const int64_t nv = cols / 8;
+  if (cols % 8 == 0 && nv <= 2048 && aligned(w_bf16, 16) && aligned(out, 8)) {
+    const dim3 g((unsigned)rows), b(256);
+    if (nv <= 256)
+      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<1>, g, b, 0, st, w_bf16, scale, out, cols);
+    else if (nv <= 512)
+      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<2>, g, b, 0, st, w_bf16, scale, out, cols);
+    else if (nv <= 1024)
+      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<4>, g, b, 0, st, w_bf16, scale, out, cols);
+    else
+      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<8>, g, b, 0, st, w_bf16, scale, out, cols);
+  } else {
+    hipLaunchKernelGGL(quant_rows_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, st, w_bf16, scale, out, cols);
+  }
   return launch_status("ccq_quantize_rows_fp8");
 }
 
@@ -277,19 +411,49 @@ extern "C" int ccq_kv_quant_fp8(const float* kv, uint8_t* out, uint8_t* scales, 
   CCQ_REQUIRE(rows <= 0x7fffffff, "ccq_kv_quant_fp8: rows=%lld too large", (long long)rows);
   if (rows == 0) return 0;
   CCQ_REQUIRE(kv && out && scales, "ccq_kv_quant_fp8: null pointer");
-  hipLaunchKernelGGL(kv_quant_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), kv, out, scales,
-                     dim);
+  hipStream_t st = as_stream(stream);
+  const int tpr = kv_tpr(dim, kv, out);
+#define CCQ_KVQ(T)                                                                                            \
+  hipLaunchKernelGGL(kv_quant_fp8_vec_kernel<T>, dim3((unsigned)cdiv(rows, 256 / T)), dim3(256), 0, st, kv, out, \
+                     scales, rows, dim)
+  switch (tpr) {
+    case 1: CCQ_KVQ(1); break;
+    case 2: CCQ_KVQ(2); break;
+    case 4: CCQ_KVQ(4); break;
+    case 8: CCQ_KVQ(8); break;
+    case 16: CCQ_KVQ(16); break;
+    case 32: CCQ_KVQ(32); break;
+    case 64: CCQ_KVQ(64); break;
+    default: hipLaunchKernelGGL(kv_quant_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, st, kv, out, scales, dim);
+  }
+#undef CCQ_KVQ
   return launch_status("ccq_kv_quant_fp8");
 }
 
 extern "C" int ccq_kv_dequant_fp8(const uint8_t* codes, const uint8_t* scales, float* out, int64_t rows,
                                   int64_t dim, void* stream) {
   CCQ_REQUIRE(rows >= 0 && dim >= 0, "ccq_kv_dequant_fp8: negative shape");
+  CCQ_REQUIRE(rows <= 0x7fffffff, "ccq_kv_dequant_fp8: rows=%lld too large", (long long)rows);
   if (rows == 0 || dim == 0) return 0;
   CCQ_REQUIRE(codes && scales && out, "ccq_kv_dequant_fp8: null pointer");
   const int64_t n = rows * dim;
-  hipLaunchKernelGGL(kv_dequant_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), codes, scales,
-                     out, n, dim);
+  hipStream_t st = as_stream(stream);
+  const int tpr = kv_tpr(dim, out, codes);
+#define CCQ_KVD(T)                                                                                          \
+  hipLaunchKernelGGL(kv_dequant_fp8_vec_kernel<T>, dim3((unsigned)cdiv(rows, 256 / T)), dim3(256), 0, st, codes, \
+                     scales, out, rows, dim)
+  switch (tpr) {
+    case 1: CCQ_KVD(1); break;
+    case 2: CCQ_KVD(2); break;
+    case 4: CCQ_KVD(4); break;
+    case 8: CCQ_KVD(8); break;
+    case 16: CCQ_KVD(16); break;
+    case 32: CCQ_KVD(32); break;
+    case 64: CCQ_KVD(64); break;
+    default:
+      hipLaunchKernelGGL(kv_dequant_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, codes, scales, out, n, dim);
+  }
+#undef CCQ_KVD
   return launch_status("ccq_kv_dequant_fp8");
 }
 

@@ -23,7 +23,7 @@ def _bf16_rows(rng, rows, cols):
     return u
 
 
-@pytest.mark.parametrize("cols", [64, 300, 2048])
+@pytest.mark.parametrize("cols", [64, 300, 2048, 4096, 8192])
 def test_quantize_buffer_bitexact(gpu, cols):
     from ccut.quant.online import quantize_buffer_inplace
 
@@ -38,7 +38,7 @@ def test_quantize_buffer_bitexact(gpu, cols):
     assert np.array_equal(dev_out.cpu().numpy(), ok.quantize_buffer(u.tobytes(), None, cols))
 
 
-@pytest.mark.parametrize("dim", [64, 128, 320])
+@pytest.mark.parametrize("dim", [8, 64, 128, 256, 320])
 def test_kv_quant_dequant_bitexact(gpu, dim):
     from ccut.quant.kv import dequantize_kv_token, quantize_kv_token
 
