@@ -47,6 +47,7 @@ for _p in (ROOT, ROOT / "costcut-infer_amd"):
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_BF16 = 2.5166e15      # dense bf16 MFMA FLOP/s
 PEAK_FP8 = 5.0332e15       # dense fp8 MFMA FLOP/s
+PEAK_INT8 = 5.0332e15      # dense int8 MFMA OP/s
 
 E, TOPK, HID, INTER, GROUP = 64, 6, 2048, 1408, 128
 # HBM bytes / algorithmic bytes of one decode gate/up launch, from rocprofv3
@@ -314,6 +315,46 @@ def bench_quantizers(dev):
     return out
 
 
+def bench_int8(M: int, K: int, N: int, dev, copies: int = 1):
+    """INT8 W8A8 linear y = x @ W.T: per-token activation quantization of x
+    [M, K] float32, then the int8 MFMA GEMM with its float32 epilogue (plus
+    the split-K reduction where K is split), device time per layer over
+    ``copies`` distinct weight matrices.  Algorithmic bytes: N*K weight bytes
+    + 4*M*K (x) + 4*M*N (y) + 4*N (scales); ops 2*M*N*K."""
+    import torch
+
+    from ccut import _lib
+
+    lib = _lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = ctypes.c_void_p
+    g = torch.Generator(device=dev).manual_seed(13)
+    ws = [torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8) for _ in range(copies)]
+    sc = torch.rand(N, generator=g, device=dev) * 0.01
+    x = torch.randn((M, K), generator=g, device=dev)
+    xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    xs = torch.empty(M, device=dev)
+    y = torch.empty((M, N), device=dev)
+    nws = int(lib.ccq_int8_linear_workspace_size(M, K, N))
+    wsp = torch.empty(max(nws, 256), dtype=torch.uint8, device=dev)
+
+    def layer(w):
+        _lib.check(lib.ccq_int8_act_quant(vp(x.data_ptr()), vp(xq.data_ptr()), vp(xs.data_ptr()), M, K, stream),
+                   "ccq_int8_act_quant")
+        _lib.check(lib.ccq_int8_linear(vp(xq.data_ptr()), vp(xs.data_ptr()), vp(w.data_ptr()), vp(sc.data_ptr()),
+                                       vp(y.data_ptr()), M, K, N, vp(wsp.data_ptr()), nws, stream),
+                   "ccq_int8_linear")
+
+    launches = [lambda w=w: layer(w) for w in ws]
+    launches[0]()
+    torch.cuda.synchronize()
+    avg = device_time(launches, reps=max(1, 24 // copies))
+    nb = N * K + 4 * M * K + 4 * M * N + 4 * N
+    ops = 2.0 * M * N * K
+    return {"avg_us": avg * 1e6, "bytes": nb, "GBps": nb / avg / 1e9, "frac_hbm": nb / avg / PEAK_HBM,
+            "TOPs": ops / avg / 1e12, "frac_int8_peak": ops / avg / PEAK_INT8, "splits_workspace_bytes": nws}
+
+
 def bench_int4_prefill(T: int, dev):
     """int4 (AWQ g128) MoE prefill layer: 128 experts, top-8 of a skewed
     router (logits N(0,1) + per-expert bias N(0,2)), hidden 2048, inter 768,
@@ -459,6 +500,11 @@ def main():
         for name, r in bench_quantizers(dev).items():
             extra[name] = r
             log(f"{name}: {r['GBps']:.0f} GB/s = {r['frac_hbm']:.3f} of HBM peak ({r['avg_us']:.2f} us)")
+        for M, copies in ((1, 6), (16, 6), (4096, 1)):
+            r = bench_int8(M, 4096, 14336, dev, copies=copies)
+            extra[f"int8_w8a8_k4096_n14336_m{M}"] = r
+            log(f"int8 w8a8 K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "
+                f"({r['frac_hbm']:.3f} of HBM peak), {r['TOPs']:.1f} TOP/s ({r['frac_int8_peak']:.3f} of int8 peak)")
         r = bench_fp8_prefill(dev)
         extra["fp8_moe_prefill_T2048"] = r
         log(f"fp8 block MoE prefill T=2048: {r['us']:.1f} us, {r['TFLOPs']:.1f} TFLOP/s ({r['frac_fp8_peak']:.3f} "

@@ -21,6 +21,7 @@ __all__ = [
     "fp8_dequant_row",
     "fp8_dequant_mat",
     "int4_dequant_row",
+    "int8_dequant_row",
     "silu_mul_fused",
     "group_broadcast_scale",
 ]
@@ -84,6 +85,23 @@ def int4_dequant_row(packed, scale, out):
                                                                   device=pd.device)
     call("ccq_int4_dequant", pd.data_ptr(), sd.data_ptr(), dst.data_ptr(), rows, cols, _dev.stream_ptr())
     return _finish(dst, packed, out)
+
+
+def int8_dequant_row(w, scale, out):
+    """``out[r, c] = w[r, c] * scale[r]`` for int8 ``w [out, in]`` and one
+    scale per output row (reference ``kernels.py:180-189``)."""
+    wd = _dev.to_device(w).view(torch.int8)
+    if wd.dim() != 2:
+        raise ValueError(f"int8_dequant_row: w must be [rows, cols], got {tuple(wd.shape)}")
+    rows, cols = wd.shape
+    sd = _dev.to_device(scale, torch.float32).reshape(-1)
+    if sd.numel() != rows:
+        raise ValueError(f"int8_dequant_row: scale has {sd.numel()} entries for {rows} rows")
+    dst = out if (isinstance(out, torch.Tensor) and out.is_cuda and out.is_contiguous()
+                  and out.dtype == torch.float32) else torch.empty((rows, cols), dtype=torch.float32,
+                                                                  device=wd.device)
+    call("ccq_int8_dequant", wd.data_ptr(), sd.data_ptr(), dst.data_ptr(), rows, cols, _dev.stream_ptr())
+    return _finish(dst, w, out)
 
 
 def silu_mul_fused(gate, up, out):

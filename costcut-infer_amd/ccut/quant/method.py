@@ -111,9 +111,14 @@ class LinearMethod(QuantizeMethodBase):
         if path == "w4a16":
             raise NotImplementedError(f"{path}: W4 weight-only is served by weight_only.WeightOnlyMethod")
         if path in ("w8a16", "w8a8"):
-            if self.key.weight_dtype not in (QuantDType.FP8_E4M3,):
-                raise ValueError(f"w8a16 on the GPU path supports fp8_e4m3 weights, not {self.key.weight_dtype}")
+            if self.key.weight_dtype not in (QuantDType.FP8_E4M3, QuantDType.INT8):
+                raise ValueError(f"w8a16 on the GPU path supports fp8_e4m3 and int8 weights, "
+                                 f"not {self.key.weight_dtype}")
             scale = scales.get(self.scale_name) if self.scale_name else None
+            if self.key.weight_dtype == QuantDType.INT8:
+                from ccut.quant.int8 import w8a16_linear
+
+                return w8a16_linear(weight_bytes, scale, x)
             if scale is None:
                 raise ValueError(f"FP8 layer is missing its scale tensor ({self.scale_name})")
             return fp8_linear_f32(weight_bytes, scale, x)
@@ -156,8 +161,12 @@ def make_method_for_spec(spec: LayerQuantSpec) -> QuantizeMethodBase:
         from ccut.quant.weight_only import WeightOnlyMethod
 
         return WeightOnlyMethod(spec)
-    if wd in (QuantDType.INT8, QuantDType.MXFP8, QuantDType.MXFP4, QuantDType.NVFP4):
+    if wd == QuantDType.INT8:
+        from ccut.quant.int8 import Int8LinearMethod
+
+        return Int8LinearMethod(spec)
+    if wd in (QuantDType.MXFP8, QuantDType.MXFP4, QuantDType.NVFP4):
         raise NotImplementedError(
             f"{spec.layer_name}: {wd} weights are outside the GPU quantized-expert path "
-            "(served formats: fp8_e4m3 per-channel / 128x128 block, int4 reference / AWQ)")
+            "(served formats: fp8_e4m3 per-channel / 128x128 block, int8 per-channel, int4 reference / AWQ)")
     return UnquantizedMethod(weight_dtype=wd)

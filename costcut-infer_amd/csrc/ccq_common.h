@@ -29,6 +29,11 @@ int launch_status(const char* what);           // hipGetLastError -> code
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// workgroups for a grid-stride loop over n items: at least 1, at most 65536
+inline int grid_for(int64_t n, int block) {
+  const int64_t g = cdiv(n, block);
+  return (int)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
+}
 __host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
 
 // ----------------------------------------------------------- vector types --

@@ -95,7 +95,9 @@ __global__ void int4_dequant_kernel(const uint8_t* __restrict__ packed, const fl
 // ----------------------------------------------------------------------------
 constexpr int kLinBB = 8;
 
-template <bool kFp8>
+// kFmt: 0 int4 (two codes per byte, scale per input column), 1 fp8 e4m3 or
+// 2 int8 (one code per byte, scale per output row)
+template <int kFmt>
 __global__ __launch_bounds__(256) void ref_linear_f32_kernel(const float* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              const float* __restrict__ scale,
@@ -106,15 +108,17 @@ __global__ __launch_bounds__(256) void ref_linear_f32_kernel(const float* __rest
   if (r >= out_f) return;
   const int64_t b0 = (int64_t)blockIdx.y * kLinBB;
   const int nb = (int)min<int64_t>(kLinBB, batch - b0);
-  const int64_t row_bytes = kFp8 ? in_f : in_f / 2;
+  constexpr bool kByte = kFmt != 0;
+  const int64_t row_bytes = kByte ? in_f : in_f / 2;
   const uint8_t* wr = w + r * row_bytes;
   float acc[kLinBB];
 #pragma unroll
   for (int b = 0; b < kLinBB; ++b) acc[b] = 0.f;
   for (int64_t byte = lane; byte < row_bytes; byte += 64) {
     uint32_t v = wr[byte];
-    if (kFp8) {
-      const float wv = fp8_e4m3_to_f32(v) * scale[r];  // W[r,c] as fp8_dequant_mat forms it
+    if (kByte) {
+      // W[r,c] as fp8_dequant_mat / int8_dequant_row form it
+      const float wv = (kFmt == 1 ? fp8_e4m3_to_f32(v) : (float)(int8_t)v) * scale[r];
       const int64_t c = byte;
 #pragma unroll
       for (int b = 0; b < kLinBB; ++b)
@@ -157,11 +161,6 @@ __global__ void zero_f32_kernel(float* __restrict__ y, int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) y[i] = 0.f;
-}
-
-static int grid_for(int64_t n, int block) {
-  int64_t g = cdiv(n, block);
-  return (int)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
 }
 
 // |x| maximum of a row with numpy's NaN rule (any NaN gives NaN), over the
@@ -502,10 +501,10 @@ extern "C" int ccq_int4_dequant(const uint8_t* packed, const float* scale, float
   return launch_status("ccq_int4_dequant");
 }
 
-static int ref_linear(bool fp8, const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
+static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
                       int64_t in_f, int64_t out_f, void* stream, const char* name) {
   CCQ_REQUIRE(batch >= 0 && in_f >= 0 && out_f >= 0, "%s: negative shape", name);
-  CCQ_REQUIRE(fp8 || in_f % 2 == 0, "%s: in_features=%lld must be even", name, (long long)in_f);
+  CCQ_REQUIRE(fmt != 0 || in_f % 2 == 0, "%s: in_features=%lld must be even", name, (long long)in_f);
   if (batch == 0 || out_f == 0) return 0;
   CCQ_REQUIRE(x && w && scale && y, "%s: null pointer", name);
   CCQ_REQUIRE(batch <= (int64_t)65535 * kLinBB, "%s: batch too large", name);
@@ -516,21 +515,30 @@ static int ref_linear(bool fp8, const float* x, const uint8_t* w, const float* s
                        batch * out_f);
     return launch_status(name);
   }
-  if (fp8)
-    hipLaunchKernelGGL(ref_linear_f32_kernel<true>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+  if (fmt == 1)
+    hipLaunchKernelGGL(ref_linear_f32_kernel<1>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+                       in_f, out_f);
+  else if (fmt == 2)
+    hipLaunchKernelGGL(ref_linear_f32_kernel<2>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
                        in_f, out_f);
   else
-    hipLaunchKernelGGL(ref_linear_f32_kernel<false>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+    hipLaunchKernelGGL(ref_linear_f32_kernel<0>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
                        in_f, out_f);
   return launch_status(name);
 }
 
 extern "C" int ccq_int4_linear_f32(const float* x, const uint8_t* packed, const float* scale, float* y,
                                    int64_t batch, int64_t in_features, int64_t out_features, void* stream) {
-  return ref_linear(false, x, packed, scale, y, batch, in_features, out_features, stream, "ccq_int4_linear_f32");
+  return ref_linear(0, x, packed, scale, y, batch, in_features, out_features, stream, "ccq_int4_linear_f32");
 }
 
 extern "C" int ccq_fp8_linear_f32(const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
                                   int64_t in_features, int64_t out_features, void* stream) {
-  return ref_linear(true, x, w, scale, y, batch, in_features, out_features, stream, "ccq_fp8_linear_f32");
+  return ref_linear(1, x, w, scale, y, batch, in_features, out_features, stream, "ccq_fp8_linear_f32");
+}
+
+extern "C" int ccq_int8_linear_f32(const float* x, const int8_t* w, const float* scale, float* y, int64_t batch,
+                                   int64_t in_features, int64_t out_features, void* stream) {
+  return ref_linear(2, x, reinterpret_cast<const uint8_t*>(w), scale, y, batch, in_features, out_features, stream,
+                    "ccq_int8_linear_f32");
 }

@@ -102,6 +102,39 @@ int ccq_fp8_linear_f32(const float* x, const uint8_t* w, const float* scale,
                        float* y, int64_t batch, int64_t in_features,
                        int64_t out_features, void* stream);
 
+/* y[b, r] = sum_c x[b,c] * (w[r,c] * scale[r]) in float32, w int8 [out, in],
+ * one scale per output row (the W8A16 path).  Replaces Int8LinearMethod.apply
+ * with compute_path "w8a16" (quant/int8.py:38-50) and LinearMethod.apply for
+ * int8 keys (quant/method.py:106-111,126-130). */
+int ccq_int8_linear_f32(const float* x, const int8_t* w, const float* scale,
+                        float* y, int64_t batch, int64_t in_features,
+                        int64_t out_features, void* stream);
+
+/* out[r, c] = w[r, c] * scale[r] (float32).  Replaces kernels.int8_dequant_row
+ * (quant/kernels.py:180-189). */
+int ccq_int8_dequant(const int8_t* w, const float* scale, float* out,
+                     int64_t rows, int64_t cols, void* stream);
+
+/* Per-token symmetric int8 activation quantization: amax = max|x[m,:]| (NaN
+ * if the row holds one), amax' = amax > 0 ? amax : 1, x_scale[m] = amax'/127,
+ * factor = 127/x_scale[m] (float32 divisions), xq = clamp(rint(x*factor),
+ * -127, 127), NaN -> 0.  x [M, K] f32.  Replaces _quantize_per_token
+ * (quant/int8.py:65-77). */
+int ccq_int8_act_quant(const float* x, int8_t* xq, float* x_scale,
+                       int64_t M, int64_t K, void* stream);
+
+/* Bytes of workspace ccq_int8_linear needs for this shape (0: none). */
+size_t ccq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t N);
+
+/* W8A8: acc[m,n] = sum_k xq[m,k] * w[n,k] exactly (int32; K < 131072),
+ * y[m,n] = (float(acc) * x_scale[m]) * w_scale[n] in float32.  xq [M, K],
+ * w [N, K] int8.  Replaces Int8LinearMethod._w8a8 after the activation
+ * quantization and _int8_matmul (quant/int8.py:52-62,80-100). */
+int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int8_t* w,
+                    const float* w_scale, float* y, int64_t M, int64_t K,
+                    int64_t N, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* ------------------------------------------------------------------------
  * AWQ int4 (qweight int32 [K, N/8] AWQ order, qzeros int32 [K/G, N/8],
  * scales f16|bf16 [K/G, N]; W[k,n] = (q - z) * s; y = x @ W)

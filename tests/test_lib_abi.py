@@ -157,3 +157,27 @@ def test_fp8_block_rejects_bad_args(lib):
     ex.inter = 2048
     assert lib.ccq_moe_fp8_workspace_size(16, 8, ctypes.byref(ex)) > 16 * 7168
     assert lib.ccq_moe_fp8_ffn(p, CCQ_BF16, p, p, p, CCQ_BF16, 16, 9, ctypes.byref(ex), p, 1 << 40, None) == CCQ_EINVAL
+
+
+def test_int8_rejects_bad_args(lib):
+    from ccut._lib import CCQ_EINVAL, last_error
+
+    p = ctypes.c_void_p(256)
+    assert lib.ccq_int8_linear(p, p, p, p, p, -1, 64, 64, None, 0, None) == CCQ_EINVAL
+    assert lib.ccq_int8_linear(p, p, p, p, p, 1, 1 << 17, 64, None, 0, None) == CCQ_EINVAL
+    assert "overflow" in last_error()
+    assert lib.ccq_int8_linear(None, p, p, p, p, 1, 64, 64, None, 0, None) == CCQ_EINVAL
+    assert lib.ccq_int8_linear(p, p, p, p, p, 0, 64, 64, None, 0, None) == 0  # empty: no launch
+    # decode shapes split K over workgroups and need the partial-sum workspace
+    need = lib.ccq_int8_linear_workspace_size(1, 4096, 4096)
+    assert need == 8 * 4096 * 4
+    assert lib.ccq_int8_linear_workspace_size(4096, 4096, 4096) == 0
+    assert lib.ccq_int8_linear_workspace_size(1, 100, 4096) == 0  # K % 16 != 0: no split
+    rc = lib.ccq_int8_linear(p, p, p, p, p, 1, 4096, 4096, None, 0, None)
+    assert rc == CCQ_EINVAL and "workspace" in last_error()
+    rc = lib.ccq_int8_linear(p, p, p, p, p, 1, 4096, 4096, p, need - 1, None)
+    assert rc == CCQ_EINVAL and "workspace" in last_error()
+    assert lib.ccq_int8_act_quant(p, p, p, -1, 8, None) == CCQ_EINVAL
+    assert lib.ccq_int8_act_quant(p, p, p, 0, 8, None) == 0
+    assert lib.ccq_int8_dequant(p, p, p, 3, -1, None) == CCQ_EINVAL
+    assert lib.ccq_int8_linear_f32(p, p, p, p, -2, 7, 4, None) == CCQ_EINVAL
