@@ -59,6 +59,58 @@ __global__ __launch_bounds__(256) void int8_act_quant_kernel(const float* __rest
   }
 }
 
+// The same for rows of K <= 1024 * VPT floats (K % 4 == 0, 16-byte aligned
+// rows): each thread loads its VPT float4 at once and keeps them in
+// registers for the quantization, one round of loads per row.
+template <int VPT>
+__global__ __launch_bounds__(256) void int8_act_quant_vec_kernel(const float* __restrict__ x,
+                                                                 int8_t* __restrict__ xq, float* __restrict__ xs,
+                                                                 int64_t K) {
+  __shared__ float red[4];
+  __shared__ int rnan[4];
+  const int64_t r = blockIdx.x;
+  const float4* row = reinterpret_cast<const float4*>(x + r * K);
+  const int n4 = (int)(K >> 2);
+  float4 v[VPT];
+  float m = 0.f;
+  int nan = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    v[i] = c < n4 ? row[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    m = fmaxf(fmaxf(m, fmaxf(fabsf(v[i].x), fabsf(v[i].y))), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+    nan |= (v[i].x != v[i].x) | (v[i].y != v[i].y) | (v[i].z != v[i].z) | (v[i].w != v[i].w);
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    m = fmaxf(m, __shfl_xor(m, off, 64));
+    nan |= __shfl_xor(nan, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    red[threadIdx.x >> 6] = m;
+    rnan[threadIdx.x >> 6] = nan;
+  }
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const bool anynan = (rnan[0] | rnan[1] | rnan[2] | rnan[3]) != 0;
+  const float a = (!anynan && amax > 0.f) ? amax : 1.0f;
+  const float scale = a / 127.0f;
+  const float factor = 127.0f / scale;
+  if (threadIdx.x == 0) xs[r] = scale;
+  auto q8 = [&](float f) -> uint32_t {
+    const float q = rintf(f * factor);
+    return q != q ? 0u : (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(q, -127.0f), 127.0f);
+  };
+  uint32_t* out = reinterpret_cast<uint32_t*>(xq + r * K);
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < n4) out[c] = q8(v[i].x) | (q8(v[i].y) << 8) | (q8(v[i].z) << 16) | (q8(v[i].w) << 24);
+  }
+}
+
 constexpr int I8_BT = 64;         // output tile
 constexpr int I8_KC = 64;         // K per LDS chunk
 constexpr int I8_LDS_STRIDE = 80; // bytes per staged row (64 + 16: 16-byte aligned, fewer bank conflicts)
@@ -117,6 +169,93 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(const int8_t* __restrict
   }
 }
 
+// Skinny GEMM for M <= 32 (decode): a workgroup owns 32 output columns and a
+// K range; its 4 waves take the range's 128-deep chunks in turn (adjacent
+// chunks of the same weight rows at once).  A chunk (32 rows x 128 B) is
+// read as 4 loads of 8 whole rows' 128 B each (lane l: row 8p + l/8, bytes
+// 16*(l%8)), SK_D chunks ahead of the MFMAs, and turned into MFMA layout
+// through the wave's own LDS tile.  MFMA step p uses bytes [16p, 16p+16)
+// of lane half h's 64-byte run, so lane half h covers k = k0 + 64h + 16p +
+// j in both operands: a fixed permutation of k, which leaves the integer
+// sums exact.  The activations (rows l%32 < M, L2-resident) are read in
+// MFMA layout directly.
+constexpr int SK_D = 4;          // chunks in flight per wave
+constexpr int SK_TROW = 144;     // bytes per LDS tile row (128 + 16)
+
+__global__ __launch_bounds__(256) void int8_gemm_skinny_kernel(const int8_t* __restrict__ xq,
+                                                               const float* __restrict__ xs,
+                                                               const int8_t* __restrict__ w,
+                                                               const float* __restrict__ ws, float* __restrict__ y,
+                                                               int32_t* __restrict__ part, int M, int N, int64_t K,
+                                                               int64_t kper) {
+  __shared__ __align__(16) int8_t tile[4][32 * SK_TROW];
+  __shared__ int32_t red[4][16][64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * 32;
+  const int64_t kb = (int64_t)blockIdx.y * kper, ke = kb + kper < K ? kb + kper : K;
+  const int nchunks = (int)cdiv(ke - kb, 128);
+  const int mine = nchunks > wave ? (nchunks - wave + 3) / 4 : 0;  // chunks wave, wave+4, ...
+  // Buffer loads: an offset at or past the buffer's size reads zeros without
+  // touching memory, which zeroes rows past N or M and k past the range
+  // with no branch around the loads (N*K and M*K < 2^31, checked by the host).
+  constexpr uint32_t kOut = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(N * K), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, (int)(M * K), 0x00020000);
+  const int lr = lane >> 3, lc = 16 * (lane & 7);  // load layout: row lr (+8p), byte lc of the chunk
+  uint32_t wrow[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) wrow[p] = n0 + 8 * p + lr < N ? (uint32_t)((n0 + 8 * p + lr) * K) : kOut;
+  const uint32_t xrow = r < M ? (uint32_t)(r * K) : kOut;
+  int8_t* tw = tile[wave];
+  i32x4v bq[SK_D][4], aq[SK_D][4];
+  auto load = [&](int c, i32x4v (&b)[4], i32x4v (&a)[4]) {
+    const uint32_t k0 = (uint32_t)(kb + (int64_t)(wave + 4 * c) * 128);
+    const bool okb = k0 + lc < (uint32_t)ke;  // ke is a multiple of 16
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      b[p] = __builtin_amdgcn_raw_buffer_load_b128(wr, okb ? wrow[p] + k0 + lc : kOut, 0, 0);
+      const uint32_t ka = k0 + 64 * h + 16 * p;
+      a[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, ka < (uint32_t)ke ? xrow + ka : kOut, 0, 0);
+    }
+  };
+  // Chunks past the wave's last one lie at k >= ke and load as zeros, so the
+  // prefetch and the MFMAs run unconditionally (a branch-free loop lets the
+  // compiler wait only for the oldest slot's loads).
+#pragma unroll
+  for (int d = 0; d < SK_D; ++d) load(d, bq[d], aq[d]);
+  i32x16 acc = i32x16{};
+  for (int c0 = 0; c0 < mine; c0 += SK_D) {
+#pragma unroll
+    for (int d = 0; d < SK_D; ++d) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) *reinterpret_cast<i32x4v*>(tw + (8 * p + lr) * SK_TROW + lc) = bq[d][p];
+      i32x4v bm[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) bm[p] = *reinterpret_cast<const i32x4v*>(tw + r * SK_TROW + 64 * h + 16 * p);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[d][p], bm[p], acc, 0, 0, 0);
+      load(c0 + d + SK_D, bq[d], aq[d]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) red[wave][i][lane] = acc[i];
+  __syncthreads();
+  // wave v finishes registers 4v .. 4v+3: rows 8v + 4h + (0..3)
+  const int col = n0 + r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = 4 * wave + q;
+    const int row = 8 * wave + 4 * h + q;
+    if (row >= M || col >= N) continue;
+    const int32_t a = red[0][i][lane] + red[1][i][lane] + red[2][i][lane] + red[3][i][lane];
+    if (gridDim.y == 1)
+      y[(int64_t)row * N + col] = ((float)a * xs[row]) * ws[col];
+    else
+      part[((int64_t)blockIdx.y * M + row) * N + col] = a;
+  }
+}
+
 __global__ void int8_splitk_epilogue_kernel(const int32_t* __restrict__ part, const float* __restrict__ xs,
                                             const float* __restrict__ ws, float* __restrict__ y, int M, int N,
                                             int splits) {
@@ -148,12 +287,23 @@ __global__ void int8_dequant_kernel(const int8_t* __restrict__ w, const float* _
   for (; i < rows * cols; i += stride) out[i] = (float)w[i] * scale[i / cols];
 }
 
-// K splits for an M x N problem: enough workgroups to cover the compute
-// units about twice, each split at least 512 deep
+constexpr int I8_SKINNY_M = 32;
+
+// K splits for an M x N problem.  Tiled kernel: enough workgroups to cover
+// the compute units about twice, each split at least 512 deep.  Skinny
+// kernel: up to 2048 waves (8 per compute unit), each split at least 512
+// deep (one chunk per wave).
+bool int8_skinny(int64_t M, int64_t K, int64_t N) { return M <= I8_SKINNY_M && N * K < ((int64_t)1 << 31); }
+
 int int8_splits(int64_t M, int64_t K, int64_t N) {
-  if (K % 16 != 0) return 1;
-  const int64_t tiles = cdiv(M, I8_BT) * cdiv(N, I8_BT);
+  if (K == 0 || K % 16 != 0) return 1;
   int64_t s = 1;
+  if (int8_skinny(M, K, N)) {
+    const int64_t waves = cdiv(N, 32) * 4;
+    while (waves * s * 2 <= 2048 && K / (2 * s) >= 512 && s < 64) s *= 2;
+    return (int)s;
+  }
+  const int64_t tiles = cdiv(M, I8_BT) * cdiv(N, I8_BT);
   while (tiles * s < 512 && K / (2 * s) >= 512 && s < 64) s *= 2;
   return (int)s;
 }
@@ -167,7 +317,25 @@ extern "C" int ccq_int8_act_quant(const float* x, int8_t* xq, float* x_scale, in
   CCQ_REQUIRE(M <= 0x7fffffff, "ccq_int8_act_quant: M=%lld too large", (long long)M);
   if (M == 0) return 0;
   CCQ_REQUIRE(x && xq && x_scale, "ccq_int8_act_quant: null pointer");
-  hipLaunchKernelGGL(int8_act_quant_kernel, dim3((unsigned)M), dim3(256), 0, as_stream(stream), x, xq, x_scale, K);
+  hipStream_t st = as_stream(stream);
+  const dim3 grid((unsigned)M), block(256);
+  if (K % 4 == 0 && K > 0 && aligned(x, 16) && aligned(xq, 4)) {
+    const int64_t n4 = K / 4;
+    if (n4 <= 256)
+      hipLaunchKernelGGL(int8_act_quant_vec_kernel<1>, grid, block, 0, st, x, xq, x_scale, K);
+    else if (n4 <= 512)
+      hipLaunchKernelGGL(int8_act_quant_vec_kernel<2>, grid, block, 0, st, x, xq, x_scale, K);
+    else if (n4 <= 1024)
+      hipLaunchKernelGGL(int8_act_quant_vec_kernel<4>, grid, block, 0, st, x, xq, x_scale, K);
+    else if (n4 <= 2048)
+      hipLaunchKernelGGL(int8_act_quant_vec_kernel<8>, grid, block, 0, st, x, xq, x_scale, K);
+    else if (n4 <= 4096)
+      hipLaunchKernelGGL(int8_act_quant_vec_kernel<16>, grid, block, 0, st, x, xq, x_scale, K);
+    else
+      hipLaunchKernelGGL(int8_act_quant_kernel, grid, block, 0, st, x, xq, x_scale, K);
+  } else {
+    hipLaunchKernelGGL(int8_act_quant_kernel, grid, block, 0, st, x, xq, x_scale, K);
+  }
   return launch_status("ccq_int8_act_quant");
 }
 
@@ -197,13 +365,23 @@ extern "C" int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int
   CCQ_REQUIRE(s == 1 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
               "ccq_int8_linear: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   CCQ_REQUIRE(cdiv(M, I8_BT) <= 65535, "ccq_int8_linear: M=%lld too large", (long long)M);
-  const int64_t kper = cdiv(cdiv(K, s), I8_KC) * I8_KC;
-  const dim3 grid((unsigned)cdiv(N, I8_BT), (unsigned)cdiv(M, I8_BT), (unsigned)cdiv(K, kper));
-  hipLaunchKernelGGL(int8_gemm_kernel, grid, dim3(256), 0, st, xq, x_scale, w, w_scale, y, (int32_t*)workspace,
-                     (int)M, (int)N, K, kper);
-  if (grid.z > 1)
+  int nsplit;
+  if (int8_skinny(M, K, N)) {
+    const int64_t kper = cdiv(cdiv(K, s), 16) * 16;
+    nsplit = (int)cdiv(K, kper);
+    CCQ_REQUIRE(cdiv(N, 32) <= 0x7fffffff, "ccq_int8_linear: N too large");
+    hipLaunchKernelGGL(int8_gemm_skinny_kernel, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0, st,
+                       xq, x_scale, w, w_scale, y, (int32_t*)workspace, (int)M, (int)N, K, kper);
+  } else {
+    const int64_t kper = cdiv(cdiv(K, s), I8_KC) * I8_KC;
+    const dim3 grid((unsigned)cdiv(N, I8_BT), (unsigned)cdiv(M, I8_BT), (unsigned)cdiv(K, kper));
+    nsplit = (int)grid.z;
+    hipLaunchKernelGGL(int8_gemm_kernel, grid, dim3(256), 0, st, xq, x_scale, w, w_scale, y, (int32_t*)workspace,
+                       (int)M, (int)N, K, kper);
+  }
+  if (nsplit > 1)
     hipLaunchKernelGGL(int8_splitk_epilogue_kernel, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
-                       (const int32_t*)workspace, x_scale, w_scale, y, (int)M, (int)N, (int)grid.z);
+                       (const int32_t*)workspace, x_scale, w_scale, y, (int)M, (int)N, nsplit);
   return launch_status("ccq_int8_linear");
 }
 
