@@ -22,6 +22,7 @@ __all__ = [
     "fp8_dequant_mat",
     "int4_dequant_row",
     "int8_dequant_row",
+    "mx_e8m0_to_float",
     "silu_mul_fused",
     "group_broadcast_scale",
 ]
@@ -102,6 +103,17 @@ def int8_dequant_row(w, scale, out):
                                                                   device=wd.device)
     call("ccq_int8_dequant", wd.data_ptr(), sd.data_ptr(), dst.data_ptr(), rows, cols, _dev.stream_ptr())
     return _finish(dst, w, out)
+
+
+def mx_e8m0_to_float(e8m0):
+    """E8M0 bytes -> float32 ``2^(e-127)``, 0 -> 0, 255 -> NaN (reference
+    ``kernels.py:240-256``)."""
+    from ccut.quant.mx import e8m0_bytes
+
+    e = e8m0_bytes(e8m0)
+    out = torch.empty(e.numel(), dtype=torch.float32, device=e.device)
+    call("ccq_e8m0_to_f32", e.data_ptr(), out.data_ptr(), e.numel(), _dev.stream_ptr())
+    return _finish(out, e8m0)
 
 
 def silu_mul_fused(gate, up, out):

@@ -166,7 +166,7 @@ def make_method_for_spec(spec: LayerQuantSpec) -> QuantizeMethodBase:
 
         return Int8LinearMethod(spec)
     if wd in (QuantDType.MXFP8, QuantDType.MXFP4, QuantDType.NVFP4):
-        raise NotImplementedError(
-            f"{spec.layer_name}: {wd} weights are outside the GPU quantized-expert path "
-            "(served formats: fp8_e4m3 per-channel / 128x128 block, int8 per-channel, int4 reference / AWQ)")
+        from ccut.quant.mx import MxLinearMethod
+
+        return MxLinearMethod(spec)
     return UnquantizedMethod(weight_dtype=wd)

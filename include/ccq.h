@@ -123,6 +123,28 @@ int ccq_int8_dequant(const int8_t* w, const float* scale, float* out,
 int ccq_int8_act_quant(const float* x, int8_t* xq, float* x_scale,
                        int64_t M, int64_t K, void* stream);
 
+/* E8M0 scale bytes -> float32: 2^(e-127), e = 0 -> 0, e = 255 -> NaN.
+ * Replaces kernels.mx_e8m0_to_float (quant/kernels.py:240-256). */
+int ccq_e8m0_to_f32(const uint8_t* e8m0, float* out, int64_t n, void* stream);
+
+/* MX weights [rows, cols] -> float32, groups of group_size columns per row
+ * with E8M0 scales [rows, ceil(cols / group_size)].  fmt 0 MXFP8 (e4m3fn
+ * bytes, scales required): W = fp8(w) * s.  fmt 1 MXFP4 / NVFP4 (two codes
+ * per byte, low nibble first; scales may be NULL): W = (lut[code] * s) *
+ * scale2, lut = {0, .5, 1, 1.5, -0, -.5, -1, -1.5} for codes & 7.  Replaces
+ * MxLinearMethod._dequant_mx / _dequant_mx4 (quant/mx.py:60-94, the NVFP4
+ * factor of :55-56). */
+int ccq_mx_dequant(const uint8_t* w, const uint8_t* scale_e8m0, float* out,
+                   int64_t rows, int64_t cols, int fmt, int group_size,
+                   float scale2, void* stream);
+
+/* y[b, r] = sum_c x[b,c] * W[r,c] in float32, W as ccq_mx_dequant forms it.
+ * Replaces MxLinearMethod.apply (quant/mx.py:37-58). */
+int ccq_mx_linear_f32(const float* x, const uint8_t* w, const uint8_t* scale_e8m0,
+                      float* y, int64_t batch, int64_t in_features,
+                      int64_t out_features, int fmt, int group_size,
+                      float scale2, void* stream);
+
 /* Bytes of workspace ccq_int8_linear needs for this shape (0: none). */
 size_t ccq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t N);
 

@@ -181,3 +181,15 @@ def test_int8_rejects_bad_args(lib):
     assert lib.ccq_int8_act_quant(p, p, p, 0, 8, None) == 0
     assert lib.ccq_int8_dequant(p, p, p, 3, -1, None) == CCQ_EINVAL
     assert lib.ccq_int8_linear_f32(p, p, p, p, -2, 7, 4, None) == CCQ_EINVAL
+
+
+def test_mx_rejects_bad_args(lib):
+    from ccut._lib import CCQ_EINVAL, last_error
+
+    p = ctypes.c_void_p(256)
+    assert lib.ccq_mx_dequant(p, p, p, 2, 64, 2, 32, 1.0, None) == CCQ_EINVAL and "fmt" in last_error()
+    assert lib.ccq_mx_dequant(p, None, p, 2, 64, 0, 32, 1.0, None) == CCQ_EINVAL and "scales" in last_error()
+    assert lib.ccq_mx_dequant(p, p, p, 2, 63, 1, 32, 1.0, None) == CCQ_EINVAL and "even" in last_error()
+    assert lib.ccq_mx_linear_f32(p, p, p, p, 1, 64, 8, 0, 0, 1.0, None) == CCQ_EINVAL and "group_size" in last_error()
+    assert lib.ccq_mx_linear_f32(p, p, None, p, 0, 64, 8, 1, 32, 1.0, None) == 0  # empty batch, no scales: ok
+    assert lib.ccq_e8m0_to_f32(p, p, -1, None) == CCQ_EINVAL
