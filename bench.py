@@ -355,6 +355,28 @@ def bench_int8(M: int, K: int, N: int, dev, copies: int = 1):
             "TOPs": ops / avg / 1e12, "frac_int8_peak": ops / avg / PEAK_INT8, "splits_workspace_bytes": nws}
 
 
+def bench_mx(fmt: str, M: int, K: int, N: int, dev, copies: int = 6):
+    """MX linear y = x @ W.T through ``ccut.quant.mx.mx_linear`` (the fused
+    dequant-linear up to 8 batch rows, dequant + float32 library GEMM above),
+    ``copies`` distinct weights.  Algorithmic bytes: weight codes + E8M0
+    scales (one per 32 columns) + 4*M*K (x) + 4*M*N (y)."""
+    import torch
+
+    from ccut.quant.mx import mx_linear
+
+    g = torch.Generator(device=dev).manual_seed(17)
+    row_bytes = K if fmt == "mxfp8" else K // 2
+    ws = [torch.randint(0, 255, (N, row_bytes), generator=g, device=dev, dtype=torch.uint8) for _ in range(copies)]
+    sc = torch.randint(120, 130, (N * K // 32,), generator=g, device=dev, dtype=torch.uint8)
+    x = torch.randn((M, K), generator=g, device=dev)
+    launches = [lambda w=w: mx_linear(w, sc, x, fmt, 32) for w in ws]
+    launches[0]()
+    torch.cuda.synchronize()
+    avg = device_time(launches, reps=max(1, 24 // copies))
+    nb = N * row_bytes + N * K // 32 + 4 * M * K + 4 * M * N
+    return {"avg_us": avg * 1e6, "bytes": nb, "GBps": nb / avg / 1e9, "frac_hbm": nb / avg / PEAK_HBM}
+
+
 def bench_int4_prefill(T: int, dev):
     """int4 (AWQ g128) MoE prefill layer: 128 experts, top-8 of a skewed
     router (logits N(0,1) + per-expert bias N(0,2)), hidden 2048, inter 768,
@@ -505,6 +527,11 @@ def main():
             extra[f"int8_w8a8_k4096_n14336_m{M}"] = r
             log(f"int8 w8a8 K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "
                 f"({r['frac_hbm']:.3f} of HBM peak), {r['TOPs']:.1f} TOP/s ({r['frac_int8_peak']:.3f} of int8 peak)")
+        for fmt, M in (("mxfp4", 1), ("mxfp8", 1), ("mxfp4", 16)):
+            r = bench_mx(fmt, M, 4096, 14336, dev)
+            extra[f"{fmt}_linear_k4096_n14336_m{M}"] = r
+            log(f"{fmt} linear K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "
+                f"({r['frac_hbm']:.3f} of HBM peak)")
         r = bench_fp8_prefill(dev)
         extra["fp8_moe_prefill_T2048"] = r
         log(f"fp8 block MoE prefill T=2048: {r['us']:.1f} us, {r['TFLOPs']:.1f} TFLOP/s ({r['frac_fp8_peak']:.3f} "
