@@ -168,6 +168,38 @@ __global__ __launch_bounds__(256) void mx_linear_f32_vec_kernel(const float* __r
         if (r0 + q < out_f) y[(b0 + b) * out_f + r0 + q] = acc[b][q];
 }
 
+// Dequant, vector form (cols % 32 == 0, G in {16, 32}, 16-byte aligned):
+// one thread per 16 weight bytes, float4 stores.
+template <bool kFp4, int G>
+__global__ void mx_dequant_vec_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ sc,
+                                      float* __restrict__ out, int64_t rows, int64_t cols, float s2) {
+  constexpr int VPU = kFp4 ? 32 : 16;
+  const int64_t upr = cols / VPU, gpr = cols / G;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < rows * upr; i += stride) {
+    const int64_t r = i / upr, u = i - r * upr, c0 = u * VPU;
+    const uint4 wb = *reinterpret_cast<const uint4*>(w + i * 16);
+    const float sg0 = sc ? e8m0_to_f32(sc[r * gpr + c0 / G]) : 1.f;
+    const float sg1 = sc ? e8m0_to_f32(sc[r * gpr + (c0 + VPU - 1) / G]) : 1.f;
+    const uint32_t words[4] = {wb.x, wb.y, wb.z, wb.w};
+    float4* o = reinterpret_cast<float4*>(out + r * cols + c0);
+#pragma unroll
+    for (int j4 = 0; j4 < VPU / 4; ++j4) {
+      float v[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int j = 4 * j4 + t;
+        const uint32_t word = words[kFp4 ? j / 8 : j / 4];
+        float x = kFp4 ? mx4_lut((word >> (4 * (j % 8))) & 15u) : fp8_e4m3_to_f32((word >> (8 * (j % 4))) & 255u);
+        if (sc) x = x * (j < G - (int)(c0 % G) ? sg0 : sg1);
+        v[t] = kFp4 ? x * s2 : x;
+      }
+      o[j4] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+}
+
 }  // namespace ccq
 
 using namespace ccq;
@@ -195,6 +227,22 @@ extern "C" int ccq_mx_dequant(const uint8_t* w, const uint8_t* scale_e8m0, float
   if (int rc = mx_check(fmt, rows, cols, group_size, scale_e8m0, "ccq_mx_dequant")) return rc;
   if (rows == 0 || cols == 0) return 0;
   CCQ_REQUIRE(w && out, "ccq_mx_dequant: null pointer");
+  if (cols % 32 == 0 && (group_size == 16 || group_size == 32) && aligned(w, 16) && aligned(out, 16)) {
+    const int64_t units = rows * (cols / (fmt == 1 ? 32 : 16));
+    const dim3 g(grid_for(units, 256));
+    hipStream_t st = as_stream(stream);
+    if (fmt == 1 && group_size == 32)
+      hipLaunchKernelGGL((mx_dequant_vec_kernel<true, 32>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols, scale2);
+    else if (fmt == 1)
+      hipLaunchKernelGGL((mx_dequant_vec_kernel<true, 16>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols, scale2);
+    else if (group_size == 32)
+      hipLaunchKernelGGL((mx_dequant_vec_kernel<false, 32>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols,
+                         scale2);
+    else
+      hipLaunchKernelGGL((mx_dequant_vec_kernel<false, 16>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols,
+                         scale2);
+    return launch_status("ccq_mx_dequant");
+  }
   const dim3 grid(grid_for(rows * cols, 256));
   if (fmt == 1)
     hipLaunchKernelGGL(mx_dequant_kernel<true>, grid, dim3(256), 0, as_stream(stream), w, scale_e8m0, out, rows,

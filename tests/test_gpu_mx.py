@@ -26,7 +26,7 @@ def test_e8m0_all_bytes(gpu):
     assert _same(kernels.mx_e8m0_to_float(e), omx.e8m0_to_float(e))
 
 
-@pytest.mark.parametrize("rows,cols,G", [(5, 64, 32), (7, 70, 32), (33, 4096, 32), (4, 48, 16)])
+@pytest.mark.parametrize("rows,cols,G", [(5, 64, 32), (7, 70, 32), (33, 4096, 32), (4, 48, 16), (6, 64, 16), (3, 96, 16)])
 def test_mx_dequant_bitexact(gpu, rows, cols, G):
     from ccut.quant.mx import mx_dequant
 
