@@ -316,9 +316,10 @@ def bench_quantizers(dev):
 
 
 def bench_int8(M: int, K: int, N: int, dev, copies: int = 1):
-    """INT8 W8A8 linear y = x @ W.T: per-token activation quantization of x
-    [M, K] float32, then the int8 MFMA GEMM with its float32 epilogue (plus
-    the split-K reduction where K is split), device time per layer over
+    """INT8 W8A8 linear y = x @ W.T through ``ccq_int8_w8a8_linear``:
+    per-token activation quantization of x [M, K] float32 (inside the GEMM up
+    to 4 rows), the int8 MFMA GEMM with its float32 epilogue (plus the
+    split-K reduction where K is split), device time per layer over
     ``copies`` distinct weight matrices.  Algorithmic bytes: N*K weight bytes
     + 4*M*K (x) + 4*M*N (y) + 4*N (scales); ops 2*M*N*K."""
     import torch
@@ -332,18 +333,15 @@ def bench_int8(M: int, K: int, N: int, dev, copies: int = 1):
     ws = [torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8) for _ in range(copies)]
     sc = torch.rand(N, generator=g, device=dev) * 0.01
     x = torch.randn((M, K), generator=g, device=dev)
-    xq = torch.empty((M, K), dtype=torch.int8, device=dev)
     xs = torch.empty(M, device=dev)
     y = torch.empty((M, N), device=dev)
-    nws = int(lib.ccq_int8_linear_workspace_size(M, K, N))
+    nws = int(lib.ccq_int8_w8a8_workspace_size(M, K, N))
     wsp = torch.empty(max(nws, 256), dtype=torch.uint8, device=dev)
 
     def layer(w):
-        _lib.check(lib.ccq_int8_act_quant(vp(x.data_ptr()), vp(xq.data_ptr()), vp(xs.data_ptr()), M, K, stream),
-                   "ccq_int8_act_quant")
-        _lib.check(lib.ccq_int8_linear(vp(xq.data_ptr()), vp(xs.data_ptr()), vp(w.data_ptr()), vp(sc.data_ptr()),
-                                       vp(y.data_ptr()), M, K, N, vp(wsp.data_ptr()), nws, stream),
-                   "ccq_int8_linear")
+        _lib.check(lib.ccq_int8_w8a8_linear(vp(x.data_ptr()), vp(xs.data_ptr()), vp(w.data_ptr()),
+                                            vp(sc.data_ptr()), vp(y.data_ptr()), M, K, N, vp(wsp.data_ptr()), nws,
+                                            stream), "ccq_int8_w8a8_linear")
 
     launches = [lambda w=w: layer(w) for w in ws]
     launches[0]()
@@ -352,7 +350,7 @@ def bench_int8(M: int, K: int, N: int, dev, copies: int = 1):
     nb = N * K + 4 * M * K + 4 * M * N + 4 * N
     ops = 2.0 * M * N * K
     return {"avg_us": avg * 1e6, "bytes": nb, "GBps": nb / avg / 1e9, "frac_hbm": nb / avg / PEAK_HBM,
-            "TOPs": ops / avg / 1e12, "frac_int8_peak": ops / avg / PEAK_INT8, "splits_workspace_bytes": nws}
+            "TOPs": ops / avg / 1e12, "frac_int8_peak": ops / avg / PEAK_INT8, "workspace_bytes": nws}
 
 
 def bench_mx(fmt: str, M: int, K: int, N: int, dev, copies: int = 6):

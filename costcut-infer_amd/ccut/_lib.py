@@ -70,6 +70,8 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_int8_act_quant": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "ccq_int8_linear_workspace_size": (_sz, [_i64, _i64, _i64]),
     "ccq_int8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "ccq_int8_w8a8_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "ccq_int8_w8a8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "ccq_e8m0_to_f32": (_int, [_vp, _vp, _i64, _vp]),
     "ccq_mx_dequant": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, ctypes.c_float, _vp]),
     "ccq_mx_linear_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp]),

@@ -77,13 +77,20 @@ def int8_linear(xq: torch.Tensor, x_scale: torch.Tensor, w: torch.Tensor, w_scal
 
 
 def w8a8_linear(weight_bytes, scale, x):
-    """The reference's ``Int8LinearMethod._w8a8`` on the GPU."""
+    """The reference's ``Int8LinearMethod._w8a8`` on the GPU: one call of
+    ``ccq_int8_w8a8_linear`` (the activation quantization fused into the GEMM
+    for up to 4 rows)."""
     xd = _dev.to_device(x, torch.float32)
     if xd.dim() != 2:
         raise ValueError(f"x must be [batch, in_features], got shape {tuple(xd.shape)}")
-    w, s = _weights(weight_bytes, scale, xd.shape[1])
-    xq, xs = quantize_per_token(xd)
-    y = int8_linear(xq, xs, w, s)
+    M, K = xd.shape
+    w, s = _weights(weight_bytes, scale, K)
+    xs = torch.empty((M,), dtype=torch.float32, device=xd.device)
+    y = torch.empty((M, w.shape[0]), dtype=torch.float32, device=xd.device)
+    nbytes = int(lib().ccq_int8_w8a8_workspace_size(M, K, w.shape[0]))
+    ws = _dev.workspace("int8_w8a8", nbytes, xd.device) if nbytes else None
+    call("ccq_int8_w8a8_linear", xd.data_ptr(), xs.data_ptr(), w.data_ptr(), s.data_ptr(), y.data_ptr(), M, K,
+         w.shape[0], ws.data_ptr() if ws is not None else None, nbytes, _dev.stream_ptr())
     return _dev.to_host(y) if _dev.is_host(x) else y
 
 

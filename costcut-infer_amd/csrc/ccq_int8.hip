@@ -182,7 +182,19 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(const int8_t* __restrict
 constexpr int SK_D = 4;          // chunks in flight per wave
 constexpr int SK_TROW = 144;     // bytes per LDS tile row (128 + 16)
 
+// kFused (M <= I8_FUSED_M): the activations come as float32; every
+// workgroup takes each row's amax over all of K (the rows are L2-resident;
+// the weight prefetch is already in flight), quantizes its own K range into
+// LDS exactly as int8_act_quant_vec_kernel does, and workgroup (0, 0)
+// stores the row scales to xs_out.  Otherwise xq / xs are the quantized
+// activations and their scales.
+constexpr int I8_FUSED_M = 4;
+constexpr int I8_FUSED_XA = 16384;  // LDS bytes for the quantized K range of all rows
+
+template <bool kFused>
 __global__ __launch_bounds__(256) void int8_gemm_skinny_kernel(const int8_t* __restrict__ xq,
+                                                               const float* __restrict__ xf,
+                                                               float* __restrict__ xs_out,
                                                                const float* __restrict__ xs,
                                                                const int8_t* __restrict__ w,
                                                                const float* __restrict__ ws, float* __restrict__ y,
@@ -190,6 +202,9 @@ __global__ __launch_bounds__(256) void int8_gemm_skinny_kernel(const int8_t* __r
                                                                int64_t kper) {
   __shared__ __align__(16) int8_t tile[4][32 * SK_TROW];
   __shared__ int32_t red[4][16][64];
+  __shared__ __align__(16) int8_t xa[kFused ? I8_FUSED_XA : 16];
+  __shared__ float xsl[I8_FUSED_M], pmax[4][I8_FUSED_M];
+  __shared__ int pnan[4][I8_FUSED_M];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 31, h = lane >> 5;
   const int n0 = blockIdx.x * 32;
@@ -201,41 +216,108 @@ __global__ __launch_bounds__(256) void int8_gemm_skinny_kernel(const int8_t* __r
   // with no branch around the loads (N*K and M*K < 2^31, checked by the host).
   constexpr uint32_t kOut = 0x80000000u;
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(N * K), 0x00020000);
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, (int)(M * K), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(kFused ? nullptr : xq), (short)0, kFused ? 0 : (int)(M * K), 0x00020000);
   const int lr = lane >> 3, lc = 16 * (lane & 7);  // load layout: row lr (+8p), byte lc of the chunk
   uint32_t wrow[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) wrow[p] = n0 + 8 * p + lr < N ? (uint32_t)((n0 + 8 * p + lr) * K) : kOut;
   const uint32_t xrow = r < M ? (uint32_t)(r * K) : kOut;
   int8_t* tw = tile[wave];
-  i32x4v bq[SK_D][4], aq[SK_D][4];
+  i32x4v bq[SK_D][4], aq[kFused ? 1 : SK_D][4];
   auto load = [&](int c, i32x4v (&b)[4], i32x4v (&a)[4]) {
     const uint32_t k0 = (uint32_t)(kb + (int64_t)(wave + 4 * c) * 128);
     const bool okb = k0 + lc < (uint32_t)ke;  // ke is a multiple of 16
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       b[p] = __builtin_amdgcn_raw_buffer_load_b128(wr, okb ? wrow[p] + k0 + lc : kOut, 0, 0);
-      const uint32_t ka = k0 + 64 * h + 16 * p;
-      a[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, ka < (uint32_t)ke ? xrow + ka : kOut, 0, 0);
+      if (!kFused) {
+        const uint32_t ka = k0 + 64 * h + 16 * p;
+        a[p] = __builtin_amdgcn_raw_buffer_load_b128(xr, ka < (uint32_t)ke ? xrow + ka : kOut, 0, 0);
+      }
     }
   };
   // Chunks past the wave's last one lie at k >= ke and load as zeros, so the
   // prefetch and the MFMAs run unconditionally (a branch-free loop lets the
   // compiler wait only for the oldest slot's loads).
 #pragma unroll
-  for (int d = 0; d < SK_D; ++d) load(d, bq[d], aq[d]);
+  for (int d = 0; d < SK_D; ++d) load(d, bq[d], aq[kFused ? 0 : d]);
+  const int kstride = (int)kper;  // bytes per row of xa
+  if constexpr (kFused) {
+    // row amax over all of K (NaN flagged apart, as numpy's max propagates it)
+    for (int m = 0; m < M; ++m) {
+      const float4* xr4 = reinterpret_cast<const float4*>(xf + (int64_t)m * K);
+      float mx = 0.f;
+      int nan = 0;
+#pragma unroll 4
+      for (int c = threadIdx.x; c < (int)(K >> 2); c += 256) {
+        const float4 v = xr4[c];
+        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+        nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+      }
+      for (int off = 32; off >= 1; off >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        nan |= __shfl_xor(nan, off, 64);
+      }
+      if (lane == 0) {
+        pmax[wave][m] = mx;
+        pnan[wave][m] = nan;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < M) {
+      const int m = threadIdx.x;
+      const float amax = fmaxf(fmaxf(pmax[0][m], pmax[1][m]), fmaxf(pmax[2][m], pmax[3][m]));
+      const bool anynan = (pnan[0][m] | pnan[1][m] | pnan[2][m] | pnan[3][m]) != 0;
+      const float a = (!anynan && amax > 0.f) ? amax : 1.0f;
+      const float scale = a / 127.0f;
+      xsl[m] = scale;
+      if (blockIdx.x == 0 && blockIdx.y == 0) xs_out[m] = scale;
+    }
+    __syncthreads();
+    // this workgroup's K range of every row, quantized into xa[m][k - kb]
+    const int kr4 = (int)((ke - kb) >> 2);
+    for (int m = 0; m < M; ++m) {
+      const float factor = 127.0f / xsl[m];
+      const float4* xr4 = reinterpret_cast<const float4*>(xf + (int64_t)m * K + kb);
+      uint32_t* xo = reinterpret_cast<uint32_t*>(xa + m * kstride);
+      auto q8 = [&](float f) -> uint32_t {
+        const float q = rintf(f * factor);
+        return q != q ? 0u : (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(q, -127.0f), 127.0f);
+      };
+      for (int c = threadIdx.x; c < kr4; c += 256) {
+        const float4 v = xr4[c];
+        xo[c] = q8(v.x) | (q8(v.y) << 8) | (q8(v.z) << 16) | (q8(v.w) << 24);
+      }
+    }
+    __syncthreads();
+  }
   i32x16 acc = i32x16{};
   for (int c0 = 0; c0 < mine; c0 += SK_D) {
 #pragma unroll
     for (int d = 0; d < SK_D; ++d) {
 #pragma unroll
       for (int p = 0; p < 4; ++p) *reinterpret_cast<i32x4v*>(tw + (8 * p + lr) * SK_TROW + lc) = bq[d][p];
-      i32x4v bm[4];
+      i32x4v bm[4], am[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) bm[p] = *reinterpret_cast<const i32x4v*>(tw + r * SK_TROW + 64 * h + 16 * p);
+      if constexpr (kFused) {
+        // k past the range multiplies zero weights: the offset is only kept
+        // inside this row's bytes
+        const int ka0 = (wave + 4 * (c0 + d)) * 128 + 64 * h;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[d][p], bm[p], acc, 0, 0, 0);
-      load(c0 + d + SK_D, bq[d], aq[d]);
+        for (int p = 0; p < 4; ++p) {
+          const int off = min(ka0 + 16 * p, kstride - 16);
+          const i32x4v v = *reinterpret_cast<const i32x4v*>(xa + (r < M ? r : 0) * kstride + off);
+          am[p] = r < M ? v : i32x4v{};
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) am[p] = aq[kFused ? 0 : d][p];
+      }
+#pragma unroll
+      for (int p = 0; p < 4; ++p) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(am[p], bm[p], acc, 0, 0, 0);
+      load(c0 + d + SK_D, bq[d], aq[kFused ? 0 : d]);
     }
   }
 #pragma unroll
@@ -250,7 +332,7 @@ __global__ __launch_bounds__(256) void int8_gemm_skinny_kernel(const int8_t* __r
     if (row >= M || col >= N) continue;
     const int32_t a = red[0][i][lane] + red[1][i][lane] + red[2][i][lane] + red[3][i][lane];
     if (gridDim.y == 1)
-      y[(int64_t)row * N + col] = ((float)a * xs[row]) * ws[col];
+      y[(int64_t)row * N + col] = ((float)a * (kFused ? xsl[row] : xs[row])) * ws[col];
     else
       part[((int64_t)blockIdx.y * M + row) * N + col] = a;
   }
@@ -370,8 +452,9 @@ extern "C" int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int
     const int64_t kper = cdiv(cdiv(K, s), 16) * 16;
     nsplit = (int)cdiv(K, kper);
     CCQ_REQUIRE(cdiv(N, 32) <= 0x7fffffff, "ccq_int8_linear: N too large");
-    hipLaunchKernelGGL(int8_gemm_skinny_kernel, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0, st,
-                       xq, x_scale, w, w_scale, y, (int32_t*)workspace, (int)M, (int)N, K, kper);
+    hipLaunchKernelGGL(int8_gemm_skinny_kernel<false>, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0,
+                       st, xq, (const float*)nullptr, (float*)nullptr, x_scale, w, w_scale, y, (int32_t*)workspace,
+                       (int)M, (int)N, K, kper);
   } else {
     const int64_t kper = cdiv(cdiv(K, s), I8_KC) * I8_KC;
     const dim3 grid((unsigned)cdiv(N, I8_BT), (unsigned)cdiv(M, I8_BT), (unsigned)cdiv(K, kper));
@@ -383,6 +466,54 @@ extern "C" int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int
     hipLaunchKernelGGL(int8_splitk_epilogue_kernel, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
                        (const int32_t*)workspace, x_scale, w_scale, y, (int)M, (int)N, nsplit);
   return launch_status("ccq_int8_linear");
+}
+
+static bool int8_fused_ok(int64_t M, int64_t K, int64_t N) {
+  if (M < 1 || M > I8_FUSED_M || K <= 0 || K % 16 != 0 || !int8_skinny(M, K, N)) return false;
+  const int64_t kper = cdiv(cdiv(K, int8_splits(M, K, N)), 16) * 16;
+  return M * kper <= I8_FUSED_XA;
+}
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+extern "C" size_t ccq_int8_w8a8_workspace_size(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  if (int8_fused_ok(M, K, N)) return ccq_int8_linear_workspace_size(M, K, N);
+  return align256((size_t)M * (size_t)K) + ccq_int8_linear_workspace_size(M, K, N);
+}
+
+extern "C" int ccq_int8_w8a8_linear(const float* x, float* x_scale, const int8_t* w, const float* w_scale, float* y,
+                                    int64_t M, int64_t K, int64_t N, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  CCQ_REQUIRE(M >= 0 && K >= 0 && N >= 0, "ccq_int8_w8a8_linear: negative shape");
+  CCQ_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff, "ccq_int8_w8a8_linear: M or N too large");
+  CCQ_REQUIRE(K < (1 << 17), "ccq_int8_w8a8_linear: K=%lld >= 131072 could overflow the int32 sums", (long long)K);
+  if (M == 0) return 0;
+  CCQ_REQUIRE(K > 0, "ccq_int8_w8a8_linear: K=0 (a per-token amax over no columns is undefined)");
+  CCQ_REQUIRE(x && x_scale && w_scale && y && (w || N == 0), "ccq_int8_w8a8_linear: null pointer");
+  const size_t need = ccq_int8_w8a8_workspace_size(M, K, N);
+  CCQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
+              "ccq_int8_w8a8_linear: workspace of %zu bytes (256-byte aligned) needed, %zu given", need,
+              workspace_bytes);
+  hipStream_t st = as_stream(stream);
+  if (N > 0 && int8_fused_ok(M, K, N) && aligned(x, 16) && aligned(w, 16)) {
+    const int s = int8_splits(M, K, N);
+    const int64_t kper = cdiv(cdiv(K, s), 16) * 16;
+    const int nsplit = (int)cdiv(K, kper);
+    hipLaunchKernelGGL(int8_gemm_skinny_kernel<true>, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0,
+                       st, (const int8_t*)nullptr, x, x_scale, (const float*)x_scale, w, w_scale, y,
+                       (int32_t*)workspace, (int)M, (int)N, K, kper);
+    if (nsplit > 1)
+      hipLaunchKernelGGL(int8_splitk_epilogue_kernel, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
+                         (const int32_t*)workspace, x_scale, w_scale, y, (int)M, (int)N, nsplit);
+    return launch_status("ccq_int8_w8a8_linear");
+  }
+  int8_t* xq = static_cast<int8_t*>(workspace);
+  if (int rc = ccq_int8_act_quant(x, xq, x_scale, M, K, stream)) return rc;
+  if (N == 0) return 0;
+  const size_t off = align256((size_t)M * (size_t)K);
+  return ccq_int8_linear(xq, x_scale, w, w_scale, y, M, K, N, static_cast<char*>(workspace) + off,
+                         workspace_bytes - off, stream);
 }
 
 extern "C" int ccq_int8_dequant(const int8_t* w, const float* scale, float* out, int64_t rows, int64_t cols,

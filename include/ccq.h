@@ -110,6 +110,19 @@ int ccq_int8_linear_f32(const float* x, const int8_t* w, const float* scale,
                         float* y, int64_t batch, int64_t in_features,
                         int64_t out_features, void* stream);
 
+/* Bytes of workspace ccq_int8_w8a8_linear needs for this shape (0: none). */
+size_t ccq_int8_w8a8_workspace_size(int64_t M, int64_t K, int64_t N);
+
+/* The whole W8A8 layer from float32 activations: x_scale[M] and y[M, N] as
+ * ccq_int8_act_quant followed by ccq_int8_linear give them, bit for bit.
+ * Up to 4 rows the activation quantization runs inside the GEMM (one
+ * launch); otherwise the quantized rows go to the workspace.  K > 0.
+ * Replaces Int8LinearMethod._w8a8 (quant/int8.py:52-62). */
+int ccq_int8_w8a8_linear(const float* x, float* x_scale, const int8_t* w,
+                         const float* w_scale, float* y, int64_t M, int64_t K,
+                         int64_t N, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
 /* out[r, c] = w[r, c] * scale[r] (float32).  Replaces kernels.int8_dequant_row
  * (quant/kernels.py:180-189). */
 int ccq_int8_dequant(const int8_t* w, const float* scale, float* out,

@@ -47,7 +47,8 @@ def test_act_quant_bitexact(gpu, M, K):
 
 # decode (K split over workgroups), prefill (one split), ragged tiles, K % 16 != 0
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (16, 7168, 2048), (3, 2048, 70), (130, 1024, 520),
-                                   (256, 4096, 1024), (65, 48, 1), (7, 100, 33), (2, 8, 3)])
+                                   (256, 4096, 1024), (65, 48, 1), (7, 100, 33), (2, 8, 3), (4, 7168, 2048),
+                                   (4, 16384, 64), (2, 4096, 14336), (5, 4096, 300)])
 def test_w8a8_linear_bitexact(gpu, M, K, N):
     from ccut.quant.int8 import w8a8_linear
 
@@ -115,3 +116,29 @@ def test_int8_dequant_row_bitexact(gpu):
     out = np.empty((37, 301), np.float32)
     kernels.int8_dequant_row(w, s, out)
     assert np.array_equal(out.view(np.uint32), oi8.dequant_row(w, s).view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (4, 7168, 2048), (3, 1024, 96), (4, 16384, 256)])
+def test_w8a8_fused_matches_two_kernels(gpu, M, K, N):
+    """ccq_int8_w8a8_linear (activation quantization inside the GEMM up to 4
+    rows) against ccq_int8_act_quant + ccq_int8_linear: scales and outputs
+    bit-identical, twice in a row on the shared workspace."""
+    from ccut import _dev
+    from ccut._lib import call, lib
+    from ccut.quant.int8 import int8_linear, quantize_per_token
+
+    rng = np.random.default_rng(M * 31 + K + N)
+    w = torch.from_numpy(rng.integers(-127, 128, (N, K)).astype(np.int8)).to(gpu)
+    s = torch.from_numpy((rng.random(N) * 0.02 + 1e-4).astype(np.float32)).to(gpu)
+    for rows in (M, max(1, M - 2)):
+        x = torch.from_numpy(_acts(rng, rows, K)).to(gpu)
+        xs = torch.empty(rows, device=gpu)
+        y = torch.empty((rows, N), device=gpu)
+        nb = int(lib().ccq_int8_w8a8_workspace_size(rows, K, N))
+        ws = _dev.workspace("int8_w8a8", nb, gpu) if nb else None
+        call("ccq_int8_w8a8_linear", x.data_ptr(), xs.data_ptr(), w.data_ptr(), s.data_ptr(), y.data_ptr(), rows, K,
+             N, ws.data_ptr() if ws is not None else None, nb, _dev.stream_ptr())
+        xq2, xs2 = quantize_per_token(x)
+        y2 = int8_linear(xq2, xs2, w, s)
+        assert np.array_equal(xs.cpu().numpy().view(np.uint32), xs2.cpu().numpy().view(np.uint32))
+        assert _same(y.cpu().numpy(), y2.cpu().numpy())

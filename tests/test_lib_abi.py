@@ -181,6 +181,15 @@ def test_int8_rejects_bad_args(lib):
     assert lib.ccq_int8_act_quant(p, p, p, 0, 8, None) == 0
     assert lib.ccq_int8_dequant(p, p, p, 3, -1, None) == CCQ_EINVAL
     assert lib.ccq_int8_linear_f32(p, p, p, p, -2, 7, 4, None) == CCQ_EINVAL
+    # the whole layer: fused up to 4 rows (workspace only for the K split),
+    # else the quantized rows (256-byte aligned) ahead of the split partials
+    assert lib.ccq_int8_w8a8_workspace_size(1, 4096, 14336) == 0
+    assert lib.ccq_int8_w8a8_workspace_size(1, 4096, 4096) == 4 * 4096 * 4
+    assert lib.ccq_int8_w8a8_workspace_size(16, 4096, 14336) == 16 * 4096
+    assert lib.ccq_int8_w8a8_workspace_size(5, 100, 7) == 512
+    assert lib.ccq_int8_w8a8_linear(p, p, p, p, p, 2, 0, 8, None, 0, None) == CCQ_EINVAL and "K=0" in last_error()
+    rc = lib.ccq_int8_w8a8_linear(p, p, p, p, p, 16, 4096, 14336, None, 0, None)
+    assert rc == CCQ_EINVAL and "workspace" in last_error()
 
 
 def test_mx_rejects_bad_args(lib):
