@@ -129,7 +129,8 @@ def moe_align(expert_ids, num_experts: int, tile_m: int = 16) -> Schedule:
     return sch
 
 
-def moe_combine(x, expert_ids, weights, expert_outputs=None, expert_fn=expert_ffn, w_lookup=None):
+def moe_combine(x, expert_ids, weights, expert_outputs=None, expert_fn=expert_ffn, w_lookup=None, *,
+                shared=None, shared_gate: float = 1.0):
     """``y[t] = sum_e w[t,e] * expert_e(x[t])`` with the tokens of each expert
     batched (reference ``moe.py:144-174``).  The grouping is computed on the
     GPU; ``expert_fn`` is called once per expert, in first-appearance order,
@@ -154,8 +155,20 @@ def moe_combine(x, expert_ids, weights, expert_outputs=None, expert_fn=expert_ff
         y = expert_fn(xd[a // k], wg, wu, wd)
         rows[a] = _dev.to_device(y, torch.float32)
     out = torch.empty((T, H), dtype=torch.float32, device=xd.device)
-    call("ccq_moe_combine", rows.data_ptr(), wts.data_ptr(), out.data_ptr(), 0, T, k, H, _dev.stream_ptr())
+    if shared is not None:
+        sd = _shared_rows(shared, T, H, xd.device)
+        call("ccq_moe_combine_shared", rows.data_ptr(), wts.data_ptr(), sd.data_ptr(), float(np.float32(shared_gate)),
+             out.data_ptr(), 0, T, k, H, _dev.stream_ptr())
+    else:
+        call("ccq_moe_combine", rows.data_ptr(), wts.data_ptr(), out.data_ptr(), 0, T, k, H, _dev.stream_ptr())
     return _dev.to_host(out) if _dev.is_host(x) else out
+
+
+def _shared_rows(shared, T: int, H: int, device) -> torch.Tensor:
+    sd = _dev.to_device(shared, torch.float32).contiguous()
+    if tuple(sd.shape) != (T, H):
+        raise ValueError(f"shared expert output must be [{T}, {H}], got {tuple(sd.shape)}")
+    return sd.to(device)
 
 
 def _experts_in_order(sch: dict) -> list[int]:
@@ -170,11 +183,24 @@ def _experts_in_order(sch: dict) -> list[int]:
 
 
 def shared_expert_add(y, shared_out, gate_value: float) -> None:
-    """``y += gate_value * shared_out`` in place (reference ``moe.py:177-179``)."""
+    """``y += gate_value * shared_out`` in place (reference ``moe.py:177-179``):
+    float32, the product rounded, then the add (``ccq_shared_expert_add``).
+    The MoE entry points can do this in their combine epilogue instead
+    (``moe_combine(..., shared=)``, ``moe_ffn_w4(..., shared=)``)."""
+    g = float(np.float32(gate_value))
+    if isinstance(y, torch.Tensor) and y.is_cuda and y.dtype == torch.float32 and y.is_contiguous():
+        sd = _dev.to_device(shared_out, torch.float32).contiguous().reshape(y.shape)
+        call("ccq_shared_expert_add", y.data_ptr(), sd.data_ptr(), g, y.numel(), _dev.stream_ptr(y.device))
+        return
     if isinstance(y, torch.Tensor):
-        y.add_(_dev.to_device(shared_out, y.dtype), alpha=float(gate_value))
-    else:
-        y += gate_value * shared_out
+        # other dtypes / layouts: the same float32 arithmetic on a float32 copy
+        yf = y.float().contiguous()
+        shared_expert_add(yf, shared_out, gate_value)
+        y.copy_(yf.reshape(y.shape))
+        return
+    yd = _dev.to_device(np.asarray(y, np.float32))
+    shared_expert_add(yd, shared_out, gate_value)
+    np.copyto(y, _dev.to_host(yd).reshape(np.shape(y)))
 
 
 # ---------------------------------------------------------------------------
@@ -259,9 +285,11 @@ class W4Experts:
 
 
 def moe_ffn_w4(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, experts: W4Experts,
-               out_dtype: torch.dtype | None = None) -> torch.Tensor:
+               out_dtype: torch.dtype | None = None, *, shared=None, shared_gate: float = 1.0) -> torch.Tensor:
     """Expert FFN + weighted combine for already-routed tokens (one call of
-    ``ccq_moe_w4_ffn``: align, gate/up + SiLU, down, combine)."""
+    ``ccq_moe_w4_ffn``: align, gate/up + SiLU, down, combine).  ``shared``
+    ([T, H] float32, the shared expert's output): ``shared_gate * shared``
+    is added in the combine's epilogue (``ccq_moe_w4_ffn_shared``)."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"activations must be float16 or bfloat16, got {x.dtype}")
     x = x.contiguous()
@@ -276,6 +304,12 @@ def moe_ffn_w4(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, expert
     ws = _dev.workspace("moe_w4", nbytes, x.device)
     ids = ids.to(torch.int64).contiguous()
     weights = weights.to(torch.float32).contiguous()
+    if shared is not None:
+        sd = _shared_rows(shared, T, H, x.device)
+        call("ccq_moe_w4_ffn_shared", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], ids.data_ptr(), weights.data_ptr(),
+             sd.data_ptr(), float(np.float32(shared_gate)), y.data_ptr(), _dev.DTYPE_CODE[out_dtype], T, k, desc,
+             ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
+        return y
     call("ccq_moe_w4_ffn", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], ids.data_ptr(), weights.data_ptr(),
          y.data_ptr(), _dev.DTYPE_CODE[out_dtype], T, k, desc, ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
     return y

@@ -131,11 +131,26 @@ class ExpertPipeline:
         flat_ids = ids_h.reshape(-1).tolist()
         t_pf0 = time.monotonic_ns()
         self._prefetch(layer, flat_ids)
+        # the shared expert first, so that its add rides in the combine's
+        # epilogue; its time counts as prefetch time, as in the reference
+        s_out, shared_ns = None, 0
+        if shared_projs is not None and "gate_proj" in shared_projs:
+            ts0 = time.monotonic_ns()
+            s = shared_projs["gate_proj"].apply(x)
+            su = shared_projs["up_proj"].apply(x)
+            from ccut.quant import kernels as qk
+
+            inter = qk.silu_mul_fused(s, su, None)
+            s_out = _dev.to_device(shared_projs["down_proj"].apply(inter), torch.float32).contiguous()
+            shared_ns = time.monotonic_ns() - ts0
         t_c0 = time.monotonic_ns()
         layer_experts = getattr(self.reader, "experts", None)
         ex = layer_experts(layer) if layer_experts is not None else None
+        shared_done = False
         if isinstance(ex, moe.W4Experts):
-            out = moe.moe_ffn_w4(xd.to(torch.bfloat16), ids, weights, ex, out_dtype=torch.float32)
+            out = moe.moe_ffn_w4(xd.to(torch.bfloat16), ids, weights, ex, out_dtype=torch.float32,
+                                 shared=s_out, shared_gate=shared_gate)
+            shared_done = True
         elif isinstance(ex, moe.Fp8Experts):
             out = moe.moe_ffn_fp8(xd, ids, weights, ex, out_dtype=torch.float32)
         elif ex is not None:
@@ -152,23 +167,19 @@ class ExpertPipeline:
             for eid in set(e for e in flat_ids if e >= 0) - set(resolved):
                 ids_used[ids_used == eid] = -1
             if resolved:
-                out = moe.moe_combine(xd, ids_used, weights, w_lookup=resolved.__getitem__)
+                out = moe.moe_combine(xd, ids_used, weights, w_lookup=resolved.__getitem__, shared=s_out,
+                                      shared_gate=shared_gate)
+                shared_done = True
             else:
                 out = torch.zeros_like(xd)
+        if s_out is not None and not shared_done:
+            moe.shared_expert_add(out, s_out, shared_gate)
         torch.cuda.synchronize(xd.device)
         t_c1 = time.monotonic_ns()
-        if shared_projs is not None and "gate_proj" in shared_projs:
-            s = shared_projs["gate_proj"].apply(x)
-            su = shared_projs["up_proj"].apply(x)
-            from ccut.quant import kernels as qk
-
-            inter = qk.silu_mul_fused(s, su, None)
-            s_out = shared_projs["down_proj"].apply(inter)
-            moe.shared_expert_add(out, s_out, shared_gate)
         t1 = time.monotonic_ns()
         if self.metrics is not None:
             compute = t_c1 - t_c0
-            prefetch = t_pf0 - t0 + (t1 - t_c1)
+            prefetch = t_pf0 - t0 + (t1 - t_c1) + shared_ns
             self.metrics.compute_ns += compute
             self.metrics.prefetch_ns += prefetch
             self.metrics.overlap_ns += min(compute, prefetch)

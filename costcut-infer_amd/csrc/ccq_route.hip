@@ -220,11 +220,15 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
 // rows of up to 16 slots are loaded before their FMAs (one memory round
 // trip per 16 slots, not one per slot); a dropped slot's row is read and
 // not used.
+// With shared (the shared expert's output [T, H] f32), the epilogue adds
+// shared_gate * shared[t, h] to the sum, as shared_expert_add does
+// (blocks/moe.py:177-179): the product rounded to float32, then the add.
 template <int YT, int RT, bool VEC>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ rows,
                                                           const float* __restrict__ wts,
                                                           const int64_t* __restrict__ ids, int64_t E,
-                                                          void* __restrict__ y, int64_t T, int k, int64_t H) {
+                                                          void* __restrict__ y, int64_t T, int k, int64_t H,
+                                                          const float* __restrict__ shared, float shared_gate) {
   constexpr int CW = VEC ? (RT == CCQ_F32 ? 4 : 8) : 1;
   constexpr int KMAX = 16;
   const int64_t t = blockIdx.y;
@@ -273,6 +277,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
 #pragma unroll
         for (int c = 0; c < CW; ++c) acc[c] = fmaf(wv[j], r[j][c], acc[c]);
   }
+  if (shared) {
+#pragma clang fp contract(off)  // the product rounds on its own, as numpy's does
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+      const float g = shared_gate * shared[t * H + h + c];
+      acc[c] = acc[c] + g;
+    }
+  }
 #pragma unroll
   for (int c = 0; c < CW; ++c) {
     const int64_t o = t * H + h + c;
@@ -287,33 +299,37 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
 
 template <int RT, bool VEC>
 static void launch_combine_v(const void* rows, const float* wts, const int64_t* ids, int64_t E, void* y,
-                             int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st) {
+                             int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared,
+                             float sg) {
   const int64_t cols = VEC ? H / (RT == CCQ_F32 ? 4 : 8) : H;
   dim3 grid((unsigned)cdiv(cols, 256), (unsigned)T);
   if (y_dtype == CCQ_F32)
     hipLaunchKernelGGL((moe_combine_kernel<CCQ_F32, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
-                       (int)k, H);
+                       (int)k, H, shared, sg);
   else if (y_dtype == CCQ_BF16)
     hipLaunchKernelGGL((moe_combine_kernel<CCQ_BF16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
-                       (int)k, H);
+                       (int)k, H, shared, sg);
   else
     hipLaunchKernelGGL((moe_combine_kernel<CCQ_F16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
-                       (int)k, H);
+                       (int)k, H, shared, sg);
 }
 
-// rows_dtype CCQ_F32 or CCQ_BF16.
+// rows_dtype CCQ_F32 or CCQ_BF16; shared optional (16-byte aligned for the
+// vector forms).
 int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
-                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st) {
+                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared,
+                   float shared_gate) {
+  const bool sh_ok = !shared || aligned(shared, 16);
   if (rows_dtype == CCQ_BF16) {
-    if (H % 8 == 0 && aligned(rows, 16))
-      launch_combine_v<CCQ_BF16, true>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+    if (H % 8 == 0 && aligned(rows, 16) && sh_ok)
+      launch_combine_v<CCQ_BF16, true>(rows, wts, ids, E, y, y_dtype, T, k, H, st, shared, shared_gate);
     else
-      launch_combine_v<CCQ_BF16, false>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+      launch_combine_v<CCQ_BF16, false>(rows, wts, ids, E, y, y_dtype, T, k, H, st, shared, shared_gate);
   } else {
-    if (H % 4 == 0 && aligned(rows, 16))
-      launch_combine_v<CCQ_F32, true>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+    if (H % 4 == 0 && aligned(rows, 16) && sh_ok)
+      launch_combine_v<CCQ_F32, true>(rows, wts, ids, E, y, y_dtype, T, k, H, st, shared, shared_gate);
     else
-      launch_combine_v<CCQ_F32, false>(rows, wts, ids, E, y, y_dtype, T, k, H, st);
+      launch_combine_v<CCQ_F32, false>(rows, wts, ids, E, y, y_dtype, T, k, H, st, shared, shared_gate);
   }
   return launch_status("moe_combine");
 }
@@ -579,5 +595,39 @@ extern "C" int ccq_moe_combine(const float* rows, const float* weights, void* y,
   CCQ_REQUIRE(T <= 65535, "ccq_moe_combine: T=%lld > 65535", (long long)T);
   if (T == 0 || H == 0) return 0;
   CCQ_REQUIRE(rows && weights && y, "ccq_moe_combine: null pointer");
-  return launch_combine(rows, CCQ_F32, weights, nullptr, 0, y, y_dtype, T, k, H, as_stream(stream));
+  return launch_combine(rows, CCQ_F32, weights, nullptr, 0, y, y_dtype, T, k, H, as_stream(stream), nullptr, 0.f);
+}
+
+extern "C" int ccq_moe_combine_shared(const float* rows, const float* weights, const float* shared,
+                                      float shared_gate, void* y, int y_dtype, int64_t T, int64_t k, int64_t H,
+                                      void* stream) {
+  CCQ_REQUIRE(T >= 0 && k >= 1 && H >= 0, "ccq_moe_combine_shared: bad shape");
+  CCQ_REQUIRE(y_dtype == CCQ_F32 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F16,
+              "ccq_moe_combine_shared: bad y_dtype");
+  CCQ_REQUIRE(T <= 65535, "ccq_moe_combine_shared: T=%lld > 65535", (long long)T);
+  if (T == 0 || H == 0) return 0;
+  CCQ_REQUIRE(rows && weights && shared && y, "ccq_moe_combine_shared: null pointer");
+  return launch_combine(rows, CCQ_F32, weights, nullptr, 0, y, y_dtype, T, k, H, as_stream(stream), shared,
+                        shared_gate);
+}
+
+// y += gate * shared (float32: the product rounded, then the add), in place
+__global__ void shared_add_kernel(float* __restrict__ y, const float* __restrict__ s, float g, int64_t n) {
+#pragma clang fp contract(off)  // no fused multiply-add
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    const float p = g * s[i];
+    y[i] = y[i] + p;
+  }
+}
+
+extern "C" int ccq_shared_expert_add(float* y, const float* shared, float shared_gate, int64_t n, void* stream) {
+  CCQ_REQUIRE(n >= 0, "ccq_shared_expert_add: negative size");
+  if (n == 0) return 0;
+  CCQ_REQUIRE(y && shared, "ccq_shared_expert_add: null pointer");
+  const int64_t g = cdiv(n, 256);
+  hipLaunchKernelGGL(shared_add_kernel, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(256), 0, as_stream(stream), y,
+                     shared, shared_gate, n);
+  return launch_status("ccq_shared_expert_add");
 }

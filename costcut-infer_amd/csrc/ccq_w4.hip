@@ -41,7 +41,8 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
                  size_t scratch_bytes = 0);
 size_t align_scratch_bytes(int64_t n, int64_t E);
 int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
-                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st);
+                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared = nullptr,
+                   float shared_gate = 0.f);
 
 // shift of column 8c + j inside an AWQ word: 4 * AWQ_REVERSE_ORDER[j]
 __device__ __forceinline__ int awq_shift(int j) { return 4 * ((j >> 1) + 4 * (j & 1)); }
@@ -1913,9 +1914,28 @@ extern "C" size_t ccq_moe_w4_workspace_size(int64_t T, int64_t k, const ccq_w4_e
   return moe_layout(T, k, ex, 2).total;
 }
 
+static int moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights, void* y, int y_dtype,
+                      int64_t T, int64_t k, const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
+                      void* stream, const float* shared, float shared_gate);
+
 extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights, void* y,
                               int y_dtype, int64_t T, int64_t k, const ccq_w4_experts* ex, void* workspace,
                               size_t workspace_bytes, void* stream) {
+  return moe_w4_ffn(x, x_dtype, ids, weights, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream, nullptr, 0.f);
+}
+
+extern "C" int ccq_moe_w4_ffn_shared(const void* x, int x_dtype, const int64_t* ids, const float* weights,
+                                     const float* shared, float shared_gate, void* y, int y_dtype, int64_t T,
+                                     int64_t k, const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  CCQ_REQUIRE(shared || T == 0, "ccq_moe_w4_ffn_shared: null shared");
+  return moe_w4_ffn(x, x_dtype, ids, weights, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream, shared,
+                    shared_gate);
+}
+
+static int moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights, void* y, int y_dtype,
+                      int64_t T, int64_t k, const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
+                      void* stream, const float* shared, float shared_gate) {
   int rc = check_experts(ex, "ccq_moe_w4_ffn");
   if (rc) return rc;
   CCQ_REQUIRE(T >= 0 && k >= 1 && k <= ex->num_experts, "ccq_moe_w4_ffn: bad T=%lld / k=%lld", (long long)T,
@@ -2015,7 +2035,7 @@ extern "C" int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, co
   // the grouped path stores the down rows as bf16 (half the traffic of the
   // row write and of the combine's read)
   return launch_combine(rows, L.grouped ? CCQ_BF16 : CCQ_F32, weights, ids, ex->num_experts, y, y_dtype, T, k,
-                        ex->hidden, st);
+                        ex->hidden, st, shared, shared_gate);
 }
 
 // Whether a decode batch routes inside the gate/up kernel: the streaming

@@ -269,6 +269,19 @@ int ccq_moe_align(const int64_t* ids, int64_t num_assignments, int64_t num_exper
 int ccq_moe_combine(const float* rows, const float* weights, void* y, int y_dtype,
                     int64_t T, int64_t k, int64_t H, void* stream);
 
+/* ccq_moe_combine with the shared expert's add in its epilogue:
+ * y[t, :] = sum (as above) + float32(shared_gate * shared[t, :]), shared
+ * [T, H] f32.  The combine of moe_combine followed by shared_expert_add
+ * (blocks/moe.py:172-179; experts/pipeline.py:181-190). */
+int ccq_moe_combine_shared(const float* rows, const float* weights, const float* shared,
+                           float shared_gate, void* y, int y_dtype, int64_t T, int64_t k,
+                           int64_t H, void* stream);
+
+/* y[i] += float32(shared_gate * shared[i]) in place, float32 (the product
+ * rounded, then the add).  Replaces shared_expert_add (blocks/moe.py:177-179). */
+int ccq_shared_expert_add(float* y, const float* shared, float shared_gate, int64_t n,
+                          void* stream);
+
 /* ------------------------------------------------------------------------
  * MoE expert FFN, AWQ int4 experts (gate/up [H -> I], down [I -> H])
  * Weights of all E experts are stacked: w_gate/w_up tiled [E][H*I/8] int32
@@ -313,6 +326,15 @@ int ccq_moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const float* 
                    void* y, int y_dtype, int64_t T, int64_t k,
                    const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
                    void* stream);
+
+/* ccq_moe_w4_ffn with the shared expert's output shared [T, H] f32 added in
+ * the combine's epilogue as ccq_moe_combine_shared does (the routed FFN,
+ * combine and shared_expert_add of ExpertPipeline.step,
+ * experts/pipeline.py:145-190, in one call). */
+int ccq_moe_w4_ffn_shared(const void* x, int x_dtype, const int64_t* ids, const float* weights,
+                          const float* shared, float shared_gate, void* y, int y_dtype,
+                          int64_t T, int64_t k, const ccq_w4_experts* ex, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* The MoE layer from router logits: routing (ccq_topk_softmax, mode as
  * there) + ccq_moe_w4_ffn in one call.  logits [T, E] f32 with
