@@ -94,7 +94,31 @@ __global__ __launch_bounds__(256) void mx_linear_f32_kernel(const float* __restr
 // aligned operands: a lane takes 16 weight bytes at a time (32 FP4 or 16
 // FP8 columns, inside one or two scale groups), each wave 4 weight rows that
 // share the activation loads, each workgroup 16 rows and up to 8 batch rows.
+// Decode: FP4 codes & 7 index, through one v_perm_b32 per 4 codes, the high
+// bytes of the table's values as f16 (0, .5, 1, 1.5 and their negatives
+// all have a zero low byte), then v_cvt_f32_f16; FP8 through the hardware
+// e4m3fn converter (v_cvt_pk_f32_fp8).  The E8M0 scale (a power of two, 0
+// or NaN) multiplies each group's partial sum once; NVFP4's second scale
+// multiplies the row's sum.  Both are exact rescalings of the terms, so only
+// the order of the float32 additions differs from x @ W.T.
 constexpr int kMxRPW = 4;
+
+typedef _Float16 mx_h2 __attribute__((ext_vector_type(2)));
+
+// columns 8w..8w+7 of one 32-bit word of FP4 codes, as float32
+__device__ __forceinline__ void mx4_word(uint32_t w, float (&v)[8]) {
+  constexpr uint32_t kLutLo = 0x3E3C3800u;  // f16 high bytes of 0, .5, 1, 1.5
+  constexpr uint32_t kLutHi = 0xBEBCB880u;  // and of -0, -.5, -1, -1.5
+  const uint32_t e = __builtin_amdgcn_perm(kLutHi, kLutLo, w & 0x07070707u);         // even columns
+  const uint32_t o = __builtin_amdgcn_perm(kLutHi, kLutLo, (w >> 4) & 0x07070707u);  // odd columns
+  const uint32_t sel[4] = {0x040C000Cu, 0x050C010Cu, 0x060C020Cu, 0x070C030Cu};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const mx_h2 hv = __builtin_bit_cast(mx_h2, __builtin_amdgcn_perm(o, e, sel[b]));
+    v[2 * b] = (float)hv.x;
+    v[2 * b + 1] = (float)hv.y;
+  }
+}
 
 template <bool kFp4, int G>
 __global__ __launch_bounds__(256) void mx_linear_f32_vec_kernel(const float* __restrict__ x,
@@ -102,7 +126,9 @@ __global__ __launch_bounds__(256) void mx_linear_f32_vec_kernel(const float* __r
                                                                 const uint8_t* __restrict__ sc,
                                                                 float* __restrict__ y, int64_t batch, int64_t in_f,
                                                                 int64_t out_f, float s2) {
-  constexpr int VPU = kFp4 ? 32 : 16;  // columns per 16-byte unit
+  constexpr int VPU = kFp4 ? 32 : 16;          // columns per 16-byte unit
+  constexpr int NG = (kFp4 && G == 16) ? 2 : 1;  // scale groups per unit
+  constexpr int GPU_ = VPU / NG;                // columns per group inside the unit
   const int lane = lane_id();
   const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kMxRPW;
   if (r0 >= out_f) return;
@@ -117,37 +143,50 @@ __global__ __launch_bounds__(256) void mx_linear_f32_vec_kernel(const float* __r
   for (int64_t u = lane; u < units; u += 64) {
     const int64_t c0 = u * VPU;
     uint4 wb[kMxRPW];
-    float sg[kMxRPW][2];
+    float sg[kMxRPW][NG];
 #pragma unroll
     for (int q = 0; q < kMxRPW; ++q) {
       const int64_t r = min<int64_t>(r0 + q, out_f - 1);
       wb[q] = *reinterpret_cast<const uint4*>(w + r * row_bytes + u * 16);
-      const uint8_t* srow = sc ? sc + r * gpr : nullptr;
-      sg[q][0] = srow ? e8m0_to_f32(srow[c0 / G]) : 1.f;
-      sg[q][1] = srow ? e8m0_to_f32(srow[(c0 + VPU - 1) / G]) : 1.f;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) sg[q][g] = sc ? e8m0_to_f32(sc[r * gpr + (c0 + g * GPU_) / G]) : 1.f;
     }
 #pragma unroll
     for (int q = 0; q < kMxRPW; ++q) {
       float wv[VPU];
       const uint32_t words[4] = {wb[q].x, wb[q].y, wb[q].z, wb[q].w};
 #pragma unroll
-      for (int j = 0; j < VPU; ++j) {
-        const uint32_t word = words[kFp4 ? j / 8 : j / 4];
-        float v = kFp4 ? mx4_lut((word >> (4 * (j % 8))) & 15u) : fp8_e4m3_to_f32((word >> (8 * (j % 4))) & 255u);
-        if (sc) v = v * sg[q][j < G - (int)(c0 % G) ? 0 : 1];
-        wv[j] = kFp4 ? v * s2 : v;
+      for (int t = 0; t < 4; ++t) {
+        if constexpr (kFp4) {
+          float v8[8];
+          mx4_word(words[t], v8);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) wv[8 * t + j] = v8[j];
+        } else {
+          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[t], false);
+          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[t], true);
+          wv[4 * t] = lo[0];
+          wv[4 * t + 1] = lo[1];
+          wv[4 * t + 2] = hi[0];
+          wv[4 * t + 3] = hi[1];
+        }
       }
 #pragma unroll
       for (int b = 0; b < kMxBB; ++b) {
         if (b < nb) {
           const float4* xr = reinterpret_cast<const float4*>(x + (b0 + b) * in_f + c0);
 #pragma unroll
-          for (int j4 = 0; j4 < VPU / 4; ++j4) {
-            const float4 xv = xr[j4];
-            acc[b][q] = fmaf(xv.x, wv[4 * j4], acc[b][q]);
-            acc[b][q] = fmaf(xv.y, wv[4 * j4 + 1], acc[b][q]);
-            acc[b][q] = fmaf(xv.z, wv[4 * j4 + 2], acc[b][q]);
-            acc[b][q] = fmaf(xv.w, wv[4 * j4 + 3], acc[b][q]);
+          for (int g = 0; g < NG; ++g) {
+            float part = 0.f;
+#pragma unroll
+            for (int j4 = g * GPU_ / 4; j4 < (g + 1) * GPU_ / 4; ++j4) {
+              const float4 xv = xr[j4];
+              part = fmaf(xv.x, wv[4 * j4], part);
+              part = fmaf(xv.y, wv[4 * j4 + 1], part);
+              part = fmaf(xv.z, wv[4 * j4 + 2], part);
+              part = fmaf(xv.w, wv[4 * j4 + 3], part);
+            }
+            acc[b][q] = fmaf(part, sg[q][g], acc[b][q]);
           }
         }
       }
@@ -159,7 +198,7 @@ __global__ __launch_bounds__(256) void mx_linear_f32_vec_kernel(const float* __r
     for (int q = 0; q < kMxRPW; ++q) {
       float v = acc[b][q];
       for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-      acc[b][q] = v;
+      acc[b][q] = kFp4 ? v * s2 : v;
     }
   if (lane == 0)
     for (int b = 0; b < nb; ++b)

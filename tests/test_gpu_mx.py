@@ -99,3 +99,36 @@ def test_mxfp8_requires_scales(gpu):
     m = make_method_for_spec(_spec("mxfp8_dynamic"))
     with pytest.raises(ValueError):
         m.apply(np.zeros((4, 64), np.uint8).tobytes(), {}, np.zeros((1, 64), np.float32))
+
+
+@pytest.mark.parametrize("fmt,G", [(0, 32), (0, 16), (1, 32), (1, 16)])
+def test_mx_linear_one_hot_is_exact(gpu, fmt, G):
+    """x = one-hot rows: every output is one weight exactly (the other terms
+    are zeros), so each code's decode and its group scale are checked bit
+    for bit through the fused kernel (all 256 e4m3fn codes but the NaNs, all
+    16 FP4 codes)."""
+    from ccut import _dev
+    from ccut._lib import call
+
+    K, N = 64, 8
+    rng = np.random.default_rng(fmt * 10 + G)
+    sc = rng.integers(100, 150, N * (K // G)).astype(np.uint8)
+    if fmt == 0:
+        codes = np.arange(N * K, dtype=np.int64).reshape(N, K) % 256
+        codes = np.where((codes & 0x7F) == 0x7F, 0x11, codes).astype(np.uint8)
+        w = omx.dequant_mxfp8(codes, sc, G)
+        raw = codes
+        s2 = 1.0
+    else:
+        nib = (np.arange(N * K).reshape(N, K) * 7) % 16
+        raw = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+        s2 = 0.75
+        w = omx.dequant_mxfp4(raw, sc, G, np.float32(s2))
+    x = np.eye(K, dtype=np.float32)
+    xd = torch.from_numpy(x).to(gpu)
+    rd = torch.from_numpy(np.ascontiguousarray(raw)).to(gpu)
+    sd = torch.from_numpy(sc).to(gpu)
+    y = torch.empty((K, N), device=gpu)
+    call("ccq_mx_linear_f32", xd.data_ptr(), rd.data_ptr(), sd.data_ptr(), y.data_ptr(), K, K, N, fmt, G, s2,
+         _dev.stream_ptr())
+    assert np.array_equal(y.cpu().numpy(), w.T)
