@@ -338,6 +338,109 @@ __global__ __launch_bounds__(256) void int8_gemm_skinny_kernel(const int8_t* __r
   }
 }
 
+// Prefill GEMM (M > 32): a workgroup owns a 128 x 128 output tile, wave
+// (wm, wn) the 64 x 64 block at (64 wm, 64 wn) as 2 x 2 MFMA blocks of 32 x
+// 32.  K runs in 128-deep chunks: the next chunk's 32 KB (128 rows of A and
+// of B, 128 B each: 8 loads of 16 B per thread) is loaded into registers
+// while the current one feeds 16 MFMAs per wave from one LDS buffer, then
+// stored to the other buffer; one barrier per chunk.  Buffer loads bounded by M*K and
+// N*K read rows past M or N and k past the range as zeros.
+constexpr int BG_T = 128;
+constexpr int BG_KC = 128;
+constexpr int BG_LS = BG_KC + 16;  // LDS bytes per staged row
+constexpr int BG_SEGS = BG_KC / 16;                 // 16-byte pieces per staged row
+constexpr int BG_PIECES = BG_T * BG_SEGS / 256;     // pieces per thread per operand
+
+__global__ __launch_bounds__(256) void int8_gemm_big_kernel(const int8_t* __restrict__ xq,
+                                                            const float* __restrict__ xs,
+                                                            const int8_t* __restrict__ w,
+                                                            const float* __restrict__ ws, float* __restrict__ y,
+                                                            int32_t* __restrict__ part, int M, int N, int64_t K,
+                                                            int64_t kper) {
+  __shared__ __align__(16) int8_t As[2][BG_T * BG_LS];
+  __shared__ __align__(16) int8_t Bs[2][BG_T * BG_LS];
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1, r = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.y * BG_T, n0 = blockIdx.x * BG_T;
+  const int64_t kb = (int64_t)blockIdx.z * kper, ke = kb + kper < K ? kb + kper : K;
+  constexpr uint32_t kOut = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, (int)(M * K), 0x00020000);
+  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(N * K), 0x00020000);
+  // staging: piece p of thread t is row (t + 256 p) / BG_SEGS, bytes 16 * ((t + 256 p) % BG_SEGS)
+  uint32_t arow[BG_PIECES], brow[BG_PIECES];
+  int prow[BG_PIECES], pseg[BG_PIECES];
+#pragma unroll
+  for (int p = 0; p < BG_PIECES; ++p) {
+    const int id = t + 256 * p;
+    prow[p] = id / BG_SEGS;
+    pseg[p] = 16 * (id % BG_SEGS);
+    arow[p] = m0 + prow[p] < M ? (uint32_t)((int64_t)(m0 + prow[p]) * K) : kOut;
+    brow[p] = n0 + prow[p] < N ? (uint32_t)((int64_t)(n0 + prow[p]) * K) : kOut;
+  }
+  i32x4v ra[BG_PIECES], rb[BG_PIECES];
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int p = 0; p < BG_PIECES; ++p) {
+      const uint32_t kk = (uint32_t)(k0 + pseg[p]);
+      const bool ok = kk < (uint32_t)ke;  // ke is a multiple of 16
+      ra[p] = __builtin_amdgcn_raw_buffer_load_b128(ar, ok ? arow[p] + kk : kOut, 0, 0);
+      rb[p] = __builtin_amdgcn_raw_buffer_load_b128(br, ok ? brow[p] + kk : kOut, 0, 0);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < BG_PIECES; ++p) {
+      *reinterpret_cast<i32x4v*>(&As[buf][prow[p] * BG_LS + pseg[p]]) = ra[p];
+      *reinterpret_cast<i32x4v*>(&Bs[buf][prow[p] * BG_LS + pseg[p]]) = rb[p];
+    }
+  };
+  gload(kb);
+  lstore(0);
+  __syncthreads();
+  i32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = i32x16{};
+  int buf = 0;
+  for (int64_t k0 = kb; k0 < ke; k0 += BG_KC) {
+    const bool more = k0 + BG_KC < ke;
+    if (more) gload(k0 + BG_KC);
+#pragma unroll
+    for (int s = 0; s < BG_KC / 32; ++s) {
+      i32x4v af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = *reinterpret_cast<const i32x4v*>(&As[buf][(wm * 64 + i * 32 + r) * BG_LS + 32 * s + 16 * h]);
+        bf[i] = *reinterpret_cast<const i32x4v*>(&Bs[buf][(wn * 64 + i * 32 + r) * BG_LS + 32 * s + 16 * h]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + j * 32 + r;
+      if (col >= N) continue;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (q / 4) + 4 * h + (q % 4);
+        if (row >= M) continue;
+        if (gridDim.z == 1)
+          y[(int64_t)row * N + col] = ((float)acc[i][j][q] * xs[row]) * ws[col];
+        else
+          part[((int64_t)blockIdx.z * M + row) * N + col] = acc[i][j][q];
+      }
+    }
+}
+
 __global__ void int8_splitk_epilogue_kernel(const int32_t* __restrict__ part, const float* __restrict__ xs,
                                             const float* __restrict__ ws, float* __restrict__ y, int M, int N,
                                             int splits) {
@@ -377,6 +480,11 @@ constexpr int I8_SKINNY_M = 32;
 // deep (one chunk per wave).
 bool int8_skinny(int64_t M, int64_t K, int64_t N) { return M <= I8_SKINNY_M && N * K < ((int64_t)1 << 31); }
 
+// the 128 x 128 prefill kernel: buffer offsets must fit 31 bits
+bool int8_big(int64_t M, int64_t K, int64_t N) {
+  return M > I8_SKINNY_M && M * K < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31);
+}
+
 int int8_splits(int64_t M, int64_t K, int64_t N) {
   if (K == 0 || K % 16 != 0) return 1;
   int64_t s = 1;
@@ -385,7 +493,8 @@ int int8_splits(int64_t M, int64_t K, int64_t N) {
     while (waves * s * 2 <= 2048 && K / (2 * s) >= 512 && s < 64) s *= 2;
     return (int)s;
   }
-  const int64_t tiles = cdiv(M, I8_BT) * cdiv(N, I8_BT);
+  const int64_t bt = int8_big(M, K, N) ? BG_T : I8_BT;
+  const int64_t tiles = cdiv(M, bt) * cdiv(N, bt);
   while (tiles * s < 512 && K / (2 * s) >= 512 && s < 64) s *= 2;
   return (int)s;
 }
@@ -455,6 +564,13 @@ extern "C" int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int
     hipLaunchKernelGGL(int8_gemm_skinny_kernel<false>, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0,
                        st, xq, (const float*)nullptr, (float*)nullptr, x_scale, w, w_scale, y, (int32_t*)workspace,
                        (int)M, (int)N, K, kper);
+  } else if (int8_big(M, K, N)) {
+    const int64_t kper = cdiv(cdiv(K, s), BG_KC) * BG_KC;
+    const dim3 grid((unsigned)cdiv(N, BG_T), (unsigned)cdiv(M, BG_T), (unsigned)cdiv(K, kper));
+    CCQ_REQUIRE(grid.y <= 65535, "ccq_int8_linear: M=%lld too large", (long long)M);
+    nsplit = (int)grid.z;
+    hipLaunchKernelGGL(int8_gemm_big_kernel, grid, dim3(256), 0, st, xq, x_scale, w, w_scale, y,
+                       (int32_t*)workspace, (int)M, (int)N, K, kper);
   } else {
     const int64_t kper = cdiv(cdiv(K, s), I8_KC) * I8_KC;
     const dim3 grid((unsigned)cdiv(N, I8_BT), (unsigned)cdiv(M, I8_BT), (unsigned)cdiv(K, kper));

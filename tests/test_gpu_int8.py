@@ -48,7 +48,8 @@ def test_act_quant_bitexact(gpu, M, K):
 # decode (K split over workgroups), prefill (one split), ragged tiles, K % 16 != 0
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (16, 7168, 2048), (3, 2048, 70), (130, 1024, 520),
                                    (256, 4096, 1024), (65, 48, 1), (7, 100, 33), (2, 8, 3), (4, 7168, 2048),
-                                   (4, 16384, 64), (2, 4096, 14336), (5, 4096, 300)])
+                                   (4, 16384, 64), (2, 4096, 14336), (5, 4096, 300), (40, 4096, 256),
+                                   (200, 2048, 130), (33, 64, 129)])
 def test_w8a8_linear_bitexact(gpu, M, K, N):
     from ccut.quant.int8 import w8a8_linear
 
