@@ -73,6 +73,9 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_int8_w8a8_workspace_size": (_sz, [_i64, _i64, _i64]),
     "ccq_int8_w8a8_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "ccq_e8m0_to_f32": (_int, [_vp, _vp, _i64, _vp]),
+    "ccq_nf4_dequant": (_int, [_vp, _vp, _vp, _int, _vp, _i64, _i64, _vp]),
+    "ccq_nf4_linear_f32": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
+    "ccq_int8_quantize_cols": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "ccq_moe_combine_shared": (_int, [_vp, _vp, _vp, ctypes.c_float, _vp, _int, _i64, _i64, _i64, _vp]),
     "ccq_shared_expert_add": (_int, [_vp, _vp, ctypes.c_float, _i64, _vp]),
     "ccq_moe_w4_ffn_shared": (_int, [_vp, _int, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _i64, _i64,

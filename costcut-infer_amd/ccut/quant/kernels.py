@@ -22,7 +22,9 @@ __all__ = [
     "fp8_dequant_mat",
     "int4_dequant_row",
     "int8_dequant_row",
+    "int8_quantize_row",
     "mx_e8m0_to_float",
+    "nf4_dequant_row",
     "silu_mul_fused",
     "group_broadcast_scale",
 ]
@@ -103,6 +105,43 @@ def int8_dequant_row(w, scale, out):
                                                                   device=wd.device)
     call("ccq_int8_dequant", wd.data_ptr(), sd.data_ptr(), dst.data_ptr(), rows, cols, _dev.stream_ptr())
     return _finish(dst, w, out)
+
+
+def int8_quantize_row(x, amax, out):
+    """Per-column int8 quantization ``q = clip(round(x * 127 / amax[c]),
+    -127, 127)`` (float64 arithmetic; 0 where amax is not > 0) of ``x [rows,
+    cols]`` (reference ``kernels.py:192-211``); fills and returns ``out``."""
+    xd = _dev.to_device(x, torch.float32)
+    if xd.dim() != 2:
+        raise ValueError(f"int8_quantize_row: x must be [rows, cols], got {tuple(xd.shape)}")
+    rows, cols = xd.shape
+    ad = _dev.to_device(amax, torch.float32).reshape(-1)
+    if ad.numel() != cols:
+        raise ValueError(f"int8_quantize_row: amax has {ad.numel()} entries for {cols} columns")
+    dst = out if (isinstance(out, torch.Tensor) and out.is_cuda and out.is_contiguous()
+                  and out.dtype == torch.int8) else torch.empty((rows, cols), dtype=torch.int8, device=xd.device)
+    call("ccq_int8_quantize_cols", xd.data_ptr(), ad.data_ptr(), dst.data_ptr(), rows, cols, _dev.stream_ptr())
+    return _finish(dst, x, out)
+
+
+def nf4_dequant_row(packed, scale, table, out):
+    """NF4 dequant: the int4 layout (low nibble first, one scale per input
+    column) with each code looked up in ``table`` (reference
+    ``kernels.py:305-322``; codes past the table give NaN)."""
+    pd = _dev.to_device(packed, torch.uint8)
+    sd = _dev.to_device(scale, torch.float32).reshape(-1)
+    tb = _dev.to_device(np.asarray(table, np.float32) if not isinstance(table, torch.Tensor) else table,
+                        torch.float32).reshape(-1)
+    rows, cols = pd.shape[0], sd.numel()
+    if cols % 2 or pd.shape[1] < cols // 2 or tb.numel() > 16:
+        raise ValueError(f"nf4_dequant_row: packed {tuple(pd.shape)}, {cols} scales, {tb.numel()} table entries")
+    pd = pd[:, : cols // 2].contiguous()
+    dst = out if (isinstance(out, torch.Tensor) and out.is_cuda and out.is_contiguous()
+                  and out.dtype == torch.float32) else torch.empty((rows, cols), dtype=torch.float32,
+                                                                  device=pd.device)
+    call("ccq_nf4_dequant", pd.data_ptr(), sd.data_ptr(), tb.data_ptr(), tb.numel(), dst.data_ptr(), rows, cols,
+         _dev.stream_ptr())
+    return _finish(dst, packed, out)
 
 
 def mx_e8m0_to_float(e8m0):

@@ -26,7 +26,36 @@ from ccut.quant import awq
 from ccut.quant.method import QuantizeMethodBase, _f32_input, _return
 from ccut.quant.spec import LayerQuantSpec, QuantDType
 
-__all__ = ["WeightOnlyMethod", "int4_linear_f32"]
+__all__ = ["WeightOnlyMethod", "int4_linear_f32", "nf4_linear_f32", "NF4_LUT"]
+
+# The reference's NF4 table (weight_only.py:18-21, kernels.py:299-302): eight
+# values, indexed by the 4-bit code; codes 8..15 fall past it (NaN here).
+NF4_LUT = np.array([-1.0, -0.6961928, -0.39238566, -0.08857854, 0.21522858, 0.51903564, 0.8228427, 1.1266499],
+                   dtype=np.float32)
+
+
+def nf4_linear_f32(weight_bytes, scale, x, table=NF4_LUT):
+    """``x @ nf4_dequant(W).T`` in float32 (reference ``weight_only.py:47-54``,
+    the NF4 branch): the int4 layout with the code looked up in ``table``."""
+    xd = _f32_input(x)
+    batch, in_f = xd.shape
+    if in_f % 2:
+        raise ValueError(f"nf4 weight-only needs an even in_features, got {in_f}")
+    raw = _dev.raw_u8(weight_bytes)
+    if raw.numel() % (in_f // 2):
+        raise ValueError(f"nf4 weight of {raw.numel()} bytes is not a multiple of in_features/2={in_f // 2}")
+    out_f = raw.numel() // (in_f // 2)
+    s = _dev.to_device(np.asarray(scale, dtype=np.float32) if not isinstance(scale, torch.Tensor) else scale,
+                       torch.float32).reshape(-1)
+    if s.numel() != in_f:
+        raise ValueError(f"nf4 scale has {s.numel()} entries, expected one per input column ({in_f})")
+    tb = _dev.to_device(np.asarray(table, np.float32)).reshape(-1)
+    if tb.numel() > 16:
+        raise ValueError(f"NF4 table has {tb.numel()} entries (at most 16)")
+    y = torch.empty((batch, out_f), dtype=torch.float32, device=xd.device)
+    call("ccq_nf4_linear_f32", xd.data_ptr(), raw.data_ptr(), s.data_ptr(), tb.data_ptr(), tb.numel(), y.data_ptr(),
+         batch, in_f, out_f, _dev.stream_ptr())
+    return _return(y, x)
 
 
 def int4_linear_f32(weight_bytes, scale, x):
@@ -110,4 +139,9 @@ class WeightOnlyMethod(QuantizeMethodBase):
             if scale is None:
                 raise ValueError(f"W4 layer is missing its scale tensor ({self.scale_name})")
             return int4_linear_f32(weight_bytes, scale, x)
-        raise NotImplementedError(f"weight-only {self.weight_dtype} is outside the GPU path (int4 and AWQ are served)")
+        if self.weight_dtype == QuantDType.NF4:
+            scale = scales.get(self.scale_name) if self.scale_name else None
+            if scale is None:
+                raise ValueError(f"W4 layer is missing its scale tensor ({self.scale_name})")
+            return nf4_linear_f32(weight_bytes, scale, x)
+        raise ValueError(f"weight-only does not support {self.weight_dtype}")

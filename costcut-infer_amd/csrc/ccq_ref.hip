@@ -72,6 +72,45 @@ __device__ __forceinline__ float nib_signed(uint32_t v) {
   return (float)(q >= 8 ? q - 16 : q);
 }
 
+// NF4 code -> value: table[code] for code < table_len; past the table NaN
+// (the reference indexes its 8-entry table with the 4-bit code unchecked,
+// kernels.py:299-322, an out-of-bounds read for codes 8..15)
+__device__ __forceinline__ float nf4_val(uint32_t v, const float* __restrict__ table, int table_len) {
+  const int q = (int)(v & 0xFu);
+  return q < table_len ? table[q] : __int_as_float(0x7fc00000);
+}
+
+__global__ void nf4_dequant_kernel(const uint8_t* __restrict__ packed, const float* __restrict__ scale,
+                                   const float* __restrict__ table, int table_len, float* __restrict__ out,
+                                   int64_t rows, int64_t cols) {
+  const int64_t half = cols / 2, n = rows * half;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    const int64_t r = i / half, j = i - r * half;
+    const uint32_t b = packed[i];
+    out[r * cols + 2 * j] = nf4_val(b, table, table_len) * scale[2 * j];
+    out[r * cols + 2 * j + 1] = nf4_val(b >> 4, table, table_len) * scale[2 * j + 1];
+  }
+}
+
+// int8_quantize_row (kernels.py:192-211): per column c, inv = 127 / amax[c]
+// in float64 (0 when amax[c] is not > 0), q = round-half-even(x * inv) in
+// float64, clamped to +-127.  The reference leaves NaN and +-inf products
+// undefined (numba fastmath, int() of a non-finite float); here NaN -> 0,
+// +-inf -> +-127.
+__global__ void int8_quantize_cols_kernel(const float* __restrict__ x, const float* __restrict__ amax,
+                                          int8_t* __restrict__ out, int64_t rows, int64_t cols) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < rows * cols; i += stride) {
+    const float a = amax[i % cols];
+    const double inv = a > 0.f ? 127.0 / (double)a : 0.0;
+    const double q = rint((double)x[i] * inv);
+    out[i] = q != q ? (int8_t)0 : (int8_t)(int)fmin(fmax(q, -127.0), 127.0);
+  }
+}
+
 // packed [rows, cols/2]: byte j -> columns 2j (low nibble), 2j+1 (high).
 __global__ void int4_dequant_kernel(const uint8_t* __restrict__ packed, const float* __restrict__ scale,
                                     float* __restrict__ out, int64_t rows, int64_t cols) {
@@ -95,20 +134,21 @@ __global__ void int4_dequant_kernel(const uint8_t* __restrict__ packed, const fl
 // ----------------------------------------------------------------------------
 constexpr int kLinBB = 8;
 
-// kFmt: 0 int4 (two codes per byte, scale per input column), 1 fp8 e4m3 or
-// 2 int8 (one code per byte, scale per output row)
+// kFmt: 0 int4 or 3 NF4 (two codes per byte, scale per input column), 1 fp8
+// e4m3 or 2 int8 (one code per byte, scale per output row)
 template <int kFmt>
 __global__ __launch_bounds__(256) void ref_linear_f32_kernel(const float* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              const float* __restrict__ scale,
                                                              float* __restrict__ y, int64_t batch,
-                                                             int64_t in_f, int64_t out_f) {
+                                                             int64_t in_f, int64_t out_f,
+                                                             const float* __restrict__ table, int table_len) {
   const int lane = lane_id();
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= out_f) return;
   const int64_t b0 = (int64_t)blockIdx.y * kLinBB;
   const int nb = (int)min<int64_t>(kLinBB, batch - b0);
-  constexpr bool kByte = kFmt != 0;
+  constexpr bool kByte = kFmt == 1 || kFmt == 2;
   const int64_t row_bytes = kByte ? in_f : in_f / 2;
   const uint8_t* wr = w + r * row_bytes;
   float acc[kLinBB];
@@ -125,8 +165,8 @@ __global__ __launch_bounds__(256) void ref_linear_f32_kernel(const float* __rest
         if (b < nb) acc[b] = fmaf(x[(b0 + b) * in_f + c], wv, acc[b]);
     } else {
       const int64_t c = 2 * byte;
-      float w0 = nib_signed(v) * scale[c];
-      float w1 = nib_signed(v >> 4) * scale[c + 1];
+      float w0 = (kFmt == 3 ? nf4_val(v, table, table_len) : nib_signed(v)) * scale[c];
+      float w1 = (kFmt == 3 ? nf4_val(v >> 4, table, table_len) : nib_signed(v >> 4)) * scale[c + 1];
 #pragma unroll
       for (int b = 0; b < kLinBB; ++b)
         if (b < nb) {
@@ -502,9 +542,10 @@ extern "C" int ccq_int4_dequant(const uint8_t* packed, const float* scale, float
 }
 
 static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
-                      int64_t in_f, int64_t out_f, void* stream, const char* name) {
+                      int64_t in_f, int64_t out_f, void* stream, const char* name, const float* table = nullptr,
+                      int table_len = 0) {
   CCQ_REQUIRE(batch >= 0 && in_f >= 0 && out_f >= 0, "%s: negative shape", name);
-  CCQ_REQUIRE(fmt != 0 || in_f % 2 == 0, "%s: in_features=%lld must be even", name, (long long)in_f);
+  CCQ_REQUIRE((fmt != 0 && fmt != 3) || in_f % 2 == 0, "%s: in_features=%lld must be even", name, (long long)in_f);
   if (batch == 0 || out_f == 0) return 0;
   CCQ_REQUIRE(x && w && scale && y, "%s: null pointer", name);
   CCQ_REQUIRE(batch <= (int64_t)65535 * kLinBB, "%s: batch too large", name);
@@ -517,13 +558,16 @@ static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* sc
   }
   if (fmt == 1)
     hipLaunchKernelGGL(ref_linear_f32_kernel<1>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
-                       in_f, out_f);
+                       in_f, out_f, table, table_len);
   else if (fmt == 2)
     hipLaunchKernelGGL(ref_linear_f32_kernel<2>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
-                       in_f, out_f);
+                       in_f, out_f, table, table_len);
+  else if (fmt == 3)
+    hipLaunchKernelGGL(ref_linear_f32_kernel<3>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+                       in_f, out_f, table, table_len);
   else
     hipLaunchKernelGGL(ref_linear_f32_kernel<0>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
-                       in_f, out_f);
+                       in_f, out_f, table, table_len);
   return launch_status(name);
 }
 
@@ -535,6 +579,37 @@ extern "C" int ccq_int4_linear_f32(const float* x, const uint8_t* packed, const 
 extern "C" int ccq_fp8_linear_f32(const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
                                   int64_t in_features, int64_t out_features, void* stream) {
   return ref_linear(1, x, w, scale, y, batch, in_features, out_features, stream, "ccq_fp8_linear_f32");
+}
+
+extern "C" int ccq_nf4_linear_f32(const float* x, const uint8_t* packed, const float* scale, const float* table,
+                                  int table_len, float* y, int64_t batch, int64_t in_features, int64_t out_features,
+                                  void* stream) {
+  CCQ_REQUIRE(table_len >= 0 && table_len <= 16, "ccq_nf4_linear_f32: table_len=%d outside [0, 16]", table_len);
+  CCQ_REQUIRE(table || table_len == 0, "ccq_nf4_linear_f32: null table");
+  return ref_linear(3, x, packed, scale, y, batch, in_features, out_features, stream, "ccq_nf4_linear_f32", table,
+                    table_len);
+}
+
+extern "C" int ccq_nf4_dequant(const uint8_t* packed, const float* scale, const float* table, int table_len,
+                               float* out, int64_t rows, int64_t cols, void* stream) {
+  CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_nf4_dequant: negative shape");
+  CCQ_REQUIRE(cols % 2 == 0, "ccq_nf4_dequant: cols=%lld must be even (2 nibbles per byte)", (long long)cols);
+  CCQ_REQUIRE(table_len >= 0 && table_len <= 16, "ccq_nf4_dequant: table_len=%d outside [0, 16]", table_len);
+  if (rows == 0 || cols == 0) return 0;
+  CCQ_REQUIRE(packed && scale && out && (table || table_len == 0), "ccq_nf4_dequant: null pointer");
+  hipLaunchKernelGGL(nf4_dequant_kernel, dim3(grid_for(rows * cols / 2, 256)), dim3(256), 0, as_stream(stream),
+                     packed, scale, table, table_len, out, rows, cols);
+  return launch_status("ccq_nf4_dequant");
+}
+
+extern "C" int ccq_int8_quantize_cols(const float* x, const float* amax, int8_t* out, int64_t rows, int64_t cols,
+                                      void* stream) {
+  CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_int8_quantize_cols: negative shape");
+  if (rows == 0 || cols == 0) return 0;
+  CCQ_REQUIRE(x && amax && out, "ccq_int8_quantize_cols: null pointer");
+  hipLaunchKernelGGL(int8_quantize_cols_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream),
+                     x, amax, out, rows, cols);
+  return launch_status("ccq_int8_quantize_cols");
 }
 
 extern "C" int ccq_int8_linear_f32(const float* x, const int8_t* w, const float* scale, float* y, int64_t batch,

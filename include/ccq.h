@@ -95,6 +95,25 @@ int ccq_int4_linear_f32(const float* x, const uint8_t* packed, const float* scal
                         float* y, int64_t batch, int64_t in_features,
                         int64_t out_features, void* stream);
 
+/* NF4: packed as ccq_int4_dequant (low nibble = even column, scale per input
+ * column), W[r,c] = table[code] * scale[c] for code < table_len, NaN past
+ * the table (the reference's 8-entry table is indexed by the 4-bit code
+ * unchecked).  table: table_len (<= 16) float32 on the device.  Replace
+ * kernels.nf4_dequant_row (quant/kernels.py:299-322) and WeightOnlyMethod.apply
+ * for NF4 (quant/weight_only.py:37-54). */
+int ccq_nf4_dequant(const uint8_t* packed, const float* scale, const float* table,
+                    int table_len, float* out, int64_t rows, int64_t cols, void* stream);
+int ccq_nf4_linear_f32(const float* x, const uint8_t* packed, const float* scale,
+                       const float* table, int table_len, float* y, int64_t batch,
+                       int64_t in_features, int64_t out_features, void* stream);
+
+/* Per-column int8 quantization of x [rows, cols] with a given amax [cols]:
+ * inv = 127 / amax (float64; 0 when amax is not > 0), q = round-half-even(
+ * x * inv) clamped to +-127 (NaN -> 0, +-inf -> +-127: undefined in the
+ * reference).  Replaces kernels.int8_quantize_row (quant/kernels.py:192-211). */
+int ccq_int8_quantize_cols(const float* x, const float* amax, int8_t* out,
+                           int64_t rows, int64_t cols, void* stream);
+
 /* y[b, r] = sum_c x[b,c] * fp8(w[r,c]) * scale[r] in float32.
  * Replaces LinearMethod.apply w8a16 / w8a8 (quant/method.py:100-140) and
  * Fp8LinearMethod.apply (quant/fp8.py:33). */

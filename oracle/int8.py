@@ -55,3 +55,17 @@ def dequant_row(w: np.ndarray, scale: np.ndarray) -> np.ndarray:
 def w8a16(w: np.ndarray, scale: np.ndarray, x: np.ndarray) -> np.ndarray:
     """x @ dequant_row(w, scale).T in float64, returned float32."""
     return (np.asarray(x, np.float64) @ dequant_row(w, scale).astype(np.float64).T).astype(np.float32)
+
+
+def quantize_cols(x: np.ndarray, amax: np.ndarray) -> np.ndarray:
+    """int8_quantize_row (reference python/ccut/quant/kernels.py:192-211):
+    per column inv = 127 / amax[c] in float64 (0 when amax[c] is not > 0),
+    q = round-half-even(float64(x) * inv) clamped to +-127.  NaN -> 0 and
+    +-inf -> +-127, which the reference leaves undefined (numba fastmath)."""
+    x = np.asarray(x, np.float32)
+    a = np.asarray(amax, np.float32).astype(np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        inv = np.where(a > 0, 127.0 / np.where(a > 0, a, 1.0), 0.0)
+        q = np.rint(x.astype(np.float64) * inv[None, :])
+    q = np.where(np.isnan(q), 0.0, np.clip(q, -127, 127))
+    return q.astype(np.int8)

@@ -164,3 +164,23 @@ def bf16_bits_to_float32(u16: np.ndarray) -> np.ndarray:
     """BF16 bits -> float32 by a 16-bit left shift.  Follows
     ``io_/safetensors_io.py:53-57``."""
     return (np.asarray(u16, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+NF4_TABLE = np.array([-1.0, -0.6961928, -0.39238566, -0.08857854, 0.21522858, 0.51903564, 0.8228427, 1.1266499],
+                     dtype=np.float32)
+
+
+def nf4_dequant_row(packed: np.ndarray, scale: np.ndarray, table: np.ndarray = NF4_TABLE) -> np.ndarray:
+    """nf4_dequant_row (reference python/ccut/quant/kernels.py:299-322): the
+    int4 layout, out[r, 2j] = table[lo] * scale[2j], out[r, 2j+1] =
+    table[hi] * scale[2j+1].  The reference indexes its 8-entry table with
+    the 4-bit code unchecked; codes past the table give NaN here."""
+    p = np.asarray(packed, np.uint8)
+    s = np.asarray(scale, np.float32)
+    cols = s.shape[0]
+    t = np.full(16, np.nan, np.float32)
+    t[: len(table)] = np.asarray(table, np.float32)
+    out = np.empty((p.shape[0], cols), np.float32)
+    out[:, 0::2] = t[p[:, : cols // 2] & 0x0F] * s[0::2]
+    out[:, 1::2] = t[(p[:, : cols // 2] >> 4) & 0x0F] * s[1::2]
+    return out

@@ -89,3 +89,22 @@ def test_w8a8_epilogue_order_and_dequant():
     d = oi8.dequant_row(w, s)
     assert d[1].tolist() == [5 / 8, -1 / 8, 127 / 8]
     assert d[0, 0] == np.float32(-127 * np.float64(np.float32(0.1)))
+
+
+def test_quantize_cols_closed_forms():
+    # amax 127: inv = 1, so q = round-half-even(x) exactly
+    x = np.array([[0.5, 1.5, 2.5, -0.5, -2.5, 200.0, -1e9, 3.49]], np.float32)
+    q = oi8.quantize_cols(x, np.full(8, 127.0, np.float32))
+    assert q[0].tolist() == [0, 2, 2, 0, -2, 127, -127, 3]
+    # amax not > 0 -> inv 0 -> codes 0; amax 254 -> inv 0.5
+    q = oi8.quantize_cols(np.array([[5.0, 3.0, 5.0]], np.float32), np.array([0.0, -1.0, 254.0], np.float32))
+    assert q[0].tolist() == [0, 0, 2]  # 5 * 0.5 = 2.5 -> 2 (half to even)
+    # brute force against a per-element float64 loop
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((4, 9)) * 3).astype(np.float32)
+    a = np.abs(x).max(axis=0).astype(np.float32)
+    q = oi8.quantize_cols(x, a)
+    for r in range(4):
+        for c in range(9):
+            v = round(float(x[r, c]) * (127.0 / float(a[c])))  # Python round: half to even
+            assert q[r, c] == max(-127, min(127, v))

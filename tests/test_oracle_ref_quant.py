@@ -143,3 +143,21 @@ def test_bf16_bits():
     x = np.array([1.0, -2.5, 3.140625], dtype=np.float32)
     u16 = (x.view(np.uint32) >> 16).astype(np.uint16)
     assert np.array_equal(rq.bf16_bits_to_float32(u16), x)
+
+
+def test_nf4_dequant_table_and_layout():
+    """Each code's value is the table entry times its column scale (low
+    nibble = even column); codes past the 8-entry table are NaN."""
+    from oracle.ref_quant import NF4_TABLE, nf4_dequant_row
+
+    packed = np.array([[0x10, 0x32, 0x54, 0x76, 0x98]], np.uint8)
+    scale = np.array([1, 2, 4, 8, 0.5, 0.25, 1, 1, 1, 1], np.float32)
+    out = nf4_dequant_row(packed, scale)
+    codes = [0, 1, 2, 3, 4, 5, 6, 7, 8, 9]
+    for c, code in enumerate(codes[:8]):
+        assert out[0, c] == np.float32(NF4_TABLE[code] * scale[c])
+    assert np.isnan(out[0, 8]) and np.isnan(out[0, 9])
+    # a 16-entry table makes every code valid
+    t16 = np.linspace(-1, 1, 16).astype(np.float32)
+    out16 = nf4_dequant_row(packed, scale, t16)
+    assert out16[0, 9] == np.float32(t16[9] * scale[9])
