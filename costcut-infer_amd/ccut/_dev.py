@@ -4,6 +4,8 @@ computation runs in libccq_hip.so."""
 
 from __future__ import annotations
 
+import warnings
+
 import numpy as np
 import torch
 
@@ -33,7 +35,10 @@ def to_device(a, dtype: torch.dtype | None = None) -> torch.Tensor:
     if isinstance(a, (bytes, bytearray, memoryview)):
         a = np.frombuffer(a, dtype=np.uint8)
     if isinstance(a, np.ndarray):
-        t = torch.from_numpy(np.ascontiguousarray(a))
+        with warnings.catch_warnings():
+            # read-only arrays (np.frombuffer over weight bytes) are only read here: uploaded, never written
+            warnings.filterwarnings("ignore", message="The given NumPy array is not writable")
+            t = torch.from_numpy(np.ascontiguousarray(a))
     elif isinstance(a, torch.Tensor):
         t = a
     else:
