@@ -151,41 +151,46 @@ __global__ __launch_bounds__(256) void mx_linear_f32_vec_kernel(const float* __r
 #pragma unroll
       for (int g = 0; g < NG; ++g) sg[q][g] = sc ? e8m0_to_f32(sc[r * gpr + (c0 + g * GPU_) / G]) : 1.f;
     }
+    // activations once per unit and batch row, shared by the 4 weight rows
+    // (the rows' codes are decoded per batch row: a few VALU per value)
 #pragma unroll
-    for (int q = 0; q < kMxRPW; ++q) {
-      float wv[VPU];
-      const uint32_t words[4] = {wb[q].x, wb[q].y, wb[q].z, wb[q].w};
+    for (int b = 0; b < kMxBB; ++b) {
+      if (b < nb) {
+        const float4* xr = reinterpret_cast<const float4*>(x + (b0 + b) * in_f + c0);
+        float xv[VPU];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if constexpr (kFp4) {
-          float v8[8];
-          mx4_word(words[t], v8);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) wv[8 * t + j] = v8[j];
-        } else {
-          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[t], false);
-          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[t], true);
-          wv[4 * t] = lo[0];
-          wv[4 * t + 1] = lo[1];
-          wv[4 * t + 2] = hi[0];
-          wv[4 * t + 3] = hi[1];
+        for (int j4 = 0; j4 < VPU / 4; ++j4) {
+          const float4 v4 = xr[j4];
+          xv[4 * j4] = v4.x;
+          xv[4 * j4 + 1] = v4.y;
+          xv[4 * j4 + 2] = v4.z;
+          xv[4 * j4 + 3] = v4.w;
         }
-      }
 #pragma unroll
-      for (int b = 0; b < kMxBB; ++b) {
-        if (b < nb) {
-          const float4* xr = reinterpret_cast<const float4*>(x + (b0 + b) * in_f + c0);
+        for (int q = 0; q < kMxRPW; ++q) {
+          float wv[VPU];
+          const uint32_t words[4] = {wb[q].x, wb[q].y, wb[q].z, wb[q].w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            if constexpr (kFp4) {
+              float v8[8];
+              mx4_word(words[t], v8);
+#pragma unroll
+              for (int j = 0; j < 8; ++j) wv[8 * t + j] = v8[j];
+            } else {
+              const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[t], false);
+              const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[t], true);
+              wv[4 * t] = lo[0];
+              wv[4 * t + 1] = lo[1];
+              wv[4 * t + 2] = hi[0];
+              wv[4 * t + 3] = hi[1];
+            }
+          }
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
             float part = 0.f;
 #pragma unroll
-            for (int j4 = g * GPU_ / 4; j4 < (g + 1) * GPU_ / 4; ++j4) {
-              const float4 xv = xr[j4];
-              part = fmaf(xv.x, wv[4 * j4], part);
-              part = fmaf(xv.y, wv[4 * j4 + 1], part);
-              part = fmaf(xv.z, wv[4 * j4 + 2], part);
-              part = fmaf(xv.w, wv[4 * j4 + 3], part);
-            }
+            for (int j = g * GPU_; j < (g + 1) * GPU_; ++j) part = fmaf(xv[j], wv[j], part);
             acc[b][q] = fmaf(part, sg[q][g], acc[b][q]);
           }
         }
