@@ -80,6 +80,8 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_shared_expert_add": (_int, [_vp, _vp, ctypes.c_float, _i64, _vp]),
     "ccq_moe_w4_ffn_shared": (_int, [_vp, _int, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _i64, _i64,
                                      ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
+    "ccq_moe_fp8_ffn_shared": (_int, [_vp, _int, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _i64, _i64,
+                                      ctypes.POINTER(ccq_fp8_experts), _vp, _sz, _vp]),
     "ccq_mx_dequant": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, ctypes.c_float, _vp]),
     "ccq_mx_linear_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp]),
     "ccq_awq_dequant": (_int, [_vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),

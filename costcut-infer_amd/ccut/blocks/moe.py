@@ -408,9 +408,10 @@ class Fp8Experts:
 
 
 def moe_ffn_fp8(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, experts: Fp8Experts,
-                out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                out_dtype: torch.dtype | None = None, *, shared=None, shared_gate: float = 1.0) -> torch.Tensor:
     """Expert FFN + weighted combine for already-routed tokens on FP8 block
-    experts (one call of ``ccq_moe_fp8_ffn``)."""
+    experts (one call of ``ccq_moe_fp8_ffn``); ``shared`` as in
+    :func:`moe_ffn_w4` (``ccq_moe_fp8_ffn_shared``)."""
     if x.dtype not in _dev.DTYPE_CODE:
         raise ValueError(f"activations must be float32, float16 or bfloat16, got {x.dtype}")
     x = x.contiguous()
@@ -425,6 +426,12 @@ def moe_ffn_fp8(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, exper
     ws = _dev.workspace("moe_fp8", nbytes, x.device)
     ids = ids.to(torch.int64).contiguous()
     weights = weights.to(torch.float32).contiguous()
+    if shared is not None:
+        sd = _shared_rows(shared, T, H, x.device)
+        call("ccq_moe_fp8_ffn_shared", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], ids.data_ptr(), weights.data_ptr(),
+             sd.data_ptr(), float(np.float32(shared_gate)), y.data_ptr(), _dev.DTYPE_CODE[out_dtype], T, k, desc,
+             ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
+        return y
     call("ccq_moe_fp8_ffn", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], ids.data_ptr(), weights.data_ptr(),
          y.data_ptr(), _dev.DTYPE_CODE[out_dtype], T, k, desc, ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
     return y

@@ -152,7 +152,9 @@ class ExpertPipeline:
                                  shared=s_out, shared_gate=shared_gate)
             shared_done = True
         elif isinstance(ex, moe.Fp8Experts):
-            out = moe.moe_ffn_fp8(xd, ids, weights, ex, out_dtype=torch.float32)
+            out = moe.moe_ffn_fp8(xd, ids, weights, ex, out_dtype=torch.float32, shared=s_out,
+                                  shared_gate=shared_gate)
+            shared_done = True
         elif ex is not None:
             raise TypeError(f"reader.experts({layer}) returned {type(ex).__name__}, "
                             "expected W4Experts or Fp8Experts")

@@ -663,9 +663,29 @@ extern "C" size_t ccq_moe_fp8_workspace_size(int64_t T, int64_t k, const ccq_fp8
   return f8_moe_layout(T, k, ex).total;
 }
 
+static int moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights, void* y, int y_dtype,
+                       int64_t T, int64_t k, const ccq_fp8_experts* ex, void* workspace, size_t workspace_bytes,
+                       void* stream, const float* shared, float shared_gate);
+
 extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights, void* y,
                                int y_dtype, int64_t T, int64_t k, const ccq_fp8_experts* ex, void* workspace,
                                size_t workspace_bytes, void* stream) {
+  return moe_fp8_ffn(x, x_dtype, ids, weights, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream, nullptr,
+                     0.f);
+}
+
+extern "C" int ccq_moe_fp8_ffn_shared(const void* x, int x_dtype, const int64_t* ids, const float* weights,
+                                      const float* shared, float shared_gate, void* y, int y_dtype, int64_t T,
+                                      int64_t k, const ccq_fp8_experts* ex, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  CCQ_REQUIRE(shared || T == 0, "ccq_moe_fp8_ffn_shared: null shared");
+  return moe_fp8_ffn(x, x_dtype, ids, weights, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream, shared,
+                     shared_gate);
+}
+
+static int moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const float* weights, void* y, int y_dtype,
+                       int64_t T, int64_t k, const ccq_fp8_experts* ex, void* workspace, size_t workspace_bytes,
+                       void* stream, const float* shared, float shared_gate) {
   int rc = check_fp8_experts(ex, "ccq_moe_fp8_ffn");
   if (rc) return rc;
   CCQ_REQUIRE(T >= 0 && k >= 1 && k <= ex->num_experts, "ccq_moe_fp8_ffn: bad T=%lld / k=%lld", (long long)T,
@@ -747,5 +767,6 @@ extern "C" int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, c
   d.KB = (int)(I / 128);
   rc = launch_fp8_gemm<F8_ROWS>(d, L.max_tiles, st);
   if (rc) return rc;
-  return launch_combine(rows, CCQ_BF16, weights, ids, ex->num_experts, y, y_dtype, T, k, H, st);
+  return launch_combine(rows, CCQ_BF16, weights, ids, ex->num_experts, y, y_dtype, T, k, H, st, shared,
+                        shared_gate);
 }

@@ -431,6 +431,13 @@ int ccq_moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const float*
                     const ccq_fp8_experts* ex, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* ccq_moe_fp8_ffn with the shared expert's output shared [T, H] f32 added
+ * in the combine's epilogue, as ccq_moe_w4_ffn_shared does. */
+int ccq_moe_fp8_ffn_shared(const void* x, int x_dtype, const int64_t* ids, const float* weights,
+                           const float* shared, float shared_gate, void* y, int y_dtype,
+                           int64_t T, int64_t k, const ccq_fp8_experts* ex, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

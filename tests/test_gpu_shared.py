@@ -71,3 +71,27 @@ def test_moe_ffn_w4_shared_epilogue(gpu):
     moe.shared_expert_add(y0, sh, 1.25)
     y1 = moe.moe_ffn_w4(x, ids, w, ex, out_dtype=torch.float32, shared=sh, shared_gate=1.25)
     assert np.array_equal(y1.cpu().numpy(), y0.cpu().numpy())
+
+
+def test_moe_ffn_fp8_shared_epilogue(gpu):
+    from ccut.blocks import moe
+
+    E, H, I, T, k = 8, 256, 384, 20, 2
+    rng = np.random.default_rng(21)
+
+    def fp8w(N, K):
+        v = np.clip(rng.standard_normal((E, N, K)) * 0.02, -448, 448).astype(np.float32)
+        w = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).to(gpu)
+        s = torch.from_numpy((np.abs(rng.standard_normal((E, N // 128, K // 128))) * 0.01 + 1e-3)
+                             .astype(np.float32)).to(gpu)
+        return w, s
+
+    ex = moe.Fp8Experts.from_block(fp8w(I, H), fp8w(I, H), fp8w(H, I))
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(gpu).to(torch.bfloat16)
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).to(gpu)
+    w, ids = moe.topk_softmax(lg, k, True)
+    sh = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(gpu)
+    y0 = moe.moe_ffn_fp8(x, ids, w, ex, out_dtype=torch.float32)
+    moe.shared_expert_add(y0, sh, 0.8)
+    y1 = moe.moe_ffn_fp8(x, ids, w, ex, out_dtype=torch.float32, shared=sh, shared_gate=0.8)
+    assert np.array_equal(y1.cpu().numpy(), y0.cpu().numpy())
