@@ -21,6 +21,7 @@ LIB_PATH = Path(os.environ.get("CCQ_LIB", Path(__file__).resolve().parent / "_li
 
 CCQ_F32, CCQ_F16, CCQ_BF16 = 0, 1, 2
 CCQ_EINVAL, CCQ_EUNSUPPORTED, CCQ_EWORKSPACE = -1, -2, -3
+CCQ_MOE_W4_NOALLOC_BYTES = 32 << 20  # the per-GPU scratch array of ccq_moe_w4_forward_noalloc
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -103,6 +104,8 @@ SIGNATURES: dict[str, tuple] = {
                               ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
     "ccq_moe_w4_forward": (_int, [_vp, _int, _vp, _i64, _i64, _int, _vp, _vp, _vp, _int,
                                   ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
+    "ccq_moe_w4_forward_noalloc": (_int, [_vp, _int, _vp, _i64, _i64, _int, _vp, _vp, _vp, _int,
+                                          ctypes.POINTER(ccq_w4_experts), _vp]),
     "ccq_fp8_act_quant": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "ccq_fp8_block_repack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ccq_fp8_block_unpack": (_int, [_vp, _vp, _i64, _i64, _vp]),

@@ -32,6 +32,7 @@
 
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 namespace ccq {
@@ -2121,4 +2122,70 @@ extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logit
   rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
   if (rc) return rc;
   return launch_combine(rows, CCQ_F32, wts, ids, ex->num_experts, y, y_dtype, T, k, H, st);
+}
+
+// ---------------------------------------------------------------------------
+// ccq_moe_w4_forward without a caller workspace.  The schedule, intermediate
+// and down rows go to `scratch`, a file-scope device array: every GPU the
+// library runs on holds its own copy (CCQ_MOE_W4_NOALLOC_BYTES) until the
+// process ends.  Its device address is looked up once per device with that
+// device current; the array's name is only a host-side stand-in and is never
+// passed to a kernel.  Nothing here allocates, and nothing in the workspace
+// needs initial contents (every kernel writes what it later reads), so no
+// clear is issued.  Calls that overlap in time on one GPU share the array
+// and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[CCQ_MOE_W4_NOALLOC_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of `scratch` on the current device.
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("ccq_moe_w4_forward_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  CCQ_REQUIRE(dev >= 0 && dev < kScratchDevices, "ccq_moe_w4_forward_noalloc: device %d outside [0, %d)", dev,
+              kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("ccq_moe_w4_forward_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int ccq_moe_w4_forward_noalloc(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
+                                          int mode, int64_t* ids_out, float* weights_out, void* y, int y_dtype,
+                                          const ccq_w4_experts* ex, void* stream) {
+  int rc = check_experts(ex, "ccq_moe_w4_forward_noalloc");
+  if (rc) return rc;
+  CCQ_REQUIRE(T >= 0 && k >= 1 && k <= 16 && k <= ex->num_experts,
+              "ccq_moe_w4_forward_noalloc: bad T=%lld / k=%lld", (long long)T, (long long)k);
+  CCQ_REQUIRE(T * k <= 65536 && T <= 65535, "ccq_moe_w4_forward_noalloc: T=%lld too large", (long long)T);
+  if (T == 0) return 0;
+  const size_t need = moe_layout(T, k, ex, 2).total;
+  CCQ_REQUIRE(need <= (size_t)CCQ_MOE_W4_NOALLOC_BYTES,
+              "ccq_moe_w4_forward_noalloc: T=%lld, k=%lld on this layer needs %zu bytes of scratch, the maximum "
+              "is %zu", (long long)T, (long long)k, need, (size_t)CCQ_MOE_W4_NOALLOC_BYTES);
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  return ccq_moe_w4_forward(x, x_dtype, logits, T, k, mode, ids_out, weights_out, y, y_dtype, ex, ws,
+                            (size_t)CCQ_MOE_W4_NOALLOC_BYTES, stream);
 }

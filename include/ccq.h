@@ -369,6 +369,23 @@ int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logits, int64_t 
                        const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/* Bytes of the per-GPU scratch array of ccq_moe_w4_forward_noalloc. */
+#define CCQ_MOE_W4_NOALLOC_BYTES (32u << 20)
+
+/* ccq_moe_w4_forward with no workspace argument: same arguments otherwise,
+ * same kernels, same results bit for bit.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * workspace is a static device array of CCQ_MOE_W4_NOALLOC_BYTES held by
+ * every GPU the library runs on until the process ends; a call whose
+ * ccq_moe_w4_workspace_size(T, k, ex) exceeds it fails with CCQ_EINVAL
+ * before any launch (at 64 experts, hidden 2048, inter 1408, top-6 that is
+ * T above about 500).  Nothing is allocated.  Calls that overlap in time on
+ * one GPU share the array and race: serialize them (one stream, or events). */
+int ccq_moe_w4_forward_noalloc(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
+                               int mode, int64_t* ids_out, float* weights_out, void* y, int y_dtype,
+                               const ccq_w4_experts* ex, void* stream);
+
 
 /* ------------------------------------------------------------------------
  * FP8 e4m3fn with 128x128 block weight scales (w [N, K] bytes, row = output
