@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_quantize_rows_fp8": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "ccq_kv_quant_fp8": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "ccq_kv_dequant_fp8": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "ccq_group_broadcast_scale": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "ccq_silu_mul": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "ccq_int4_dequant": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "ccq_int4_linear_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),

@@ -169,8 +169,29 @@ def silu_mul_fused(gate, up, out):
 
 
 def group_broadcast_scale(scale_groups, group_size: int, out):
-    """``out[i*G + j] = s[i]`` (reference ``kernels.py:258-268``); a layout
-    expansion, done with a device copy."""
-    s = _dev.to_device(scale_groups, torch.float32).reshape(-1)
-    res = s.repeat_interleave(int(group_size))
-    return _finish(res, scale_groups, out)
+    """``out[i*G + j] = s[i]`` for the ``groups * G`` leading elements of
+    ``out`` (reference ``kernels.py:258-268``: ``out`` is written in place,
+    elements past ``groups * G`` are left alone; ``ccq_group_broadcast_scale``).
+    Returns ``out``; with ``out=None`` a new ``[groups * G]`` array (numpy in
+    -> numpy out)."""
+    s = _dev.to_device(scale_groups, torch.float32).reshape(-1).contiguous()
+    G = int(group_size)
+    if G < 0:
+        raise ValueError(f"group_broadcast_scale: group_size={G} < 0")
+    n = s.numel() * G
+    if out is not None and int(np.prod(np.shape(out))) < n:
+        raise ValueError(f"group_broadcast_scale: out has {int(np.prod(np.shape(out)))} elements, {n} needed")
+    if isinstance(out, torch.Tensor) and out.is_cuda and out.is_contiguous() and out.dtype == torch.float32:
+        call("ccq_group_broadcast_scale", s.data_ptr(), s.numel(), G, out.data_ptr(), _dev.stream_ptr(out.device))
+        return out
+    dst = torch.empty(n, dtype=torch.float32, device=s.device)
+    call("ccq_group_broadcast_scale", s.data_ptr(), s.numel(), G, dst.data_ptr(), _dev.stream_ptr())
+    if out is None:
+        return _dev.to_host(dst) if _dev.is_host(scale_groups) else dst
+    if isinstance(out, torch.Tensor):
+        out.reshape(-1)[:n].copy_(dst.to(out.device, out.dtype))
+        return out
+    if not out.flags.c_contiguous:
+        raise ValueError("group_broadcast_scale: out must be C-contiguous (it is written in place)")
+    out.reshape(-1)[:n] = _dev.to_host(dst)
+    return out

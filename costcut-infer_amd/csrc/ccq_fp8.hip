@@ -116,10 +116,20 @@ __global__ void fp8_unpack_kernel(const uint8_t* __restrict__ tiled, uint8_t* __
 // Activation rows keep their 16-byte pieces swizzled by row (piece p of row
 // r at position p ^ f8_swz(r)), so the operand reads of 16 consecutive rows
 // hit 16 different bank groups.
+//
+// The MoE intermediate h = silu(g) * u is carried between the two stages as
+// two e4m3 parts with one scale per row and 128-column block,
+//     s = max(amax, 1e-12) / 448,  hi = RNE(h / s),  lo = RNE((h / s - hi) * 16),
+// so h = s * (hi + lo / 16) to about 2^-8 relative (a single e4m3 code
+// would keep 2^-4, which puts the layer output about 2% away from the float32
+// product).  The down stage (F8_ROWS with LO) multiplies both parts by the
+// same weight fragments: t = mfma(lo, w) / 16 + mfma(hi, w), one exact
+// power-of-two scaling between the two MFMA chains.
 enum { F8_STORE = 0, F8_ROWS = 1, F8_SILU_Q = 2 };
 
 struct Fp8GP {
   const uint8_t* a;            // activations e4m3fn [*, K]
+  const uint8_t* a_lo;         // LO kernels: their low parts [*, K] (same lda, scaled by 16)
   int64_t lda;
   const float* sa;             // their scales [*, K/128]
   int64_t ldsa;
@@ -136,7 +146,8 @@ struct Fp8GP {
   void* y;                     // F8_STORE: [M, N] y_dtype; F8_ROWS: [row id, N] y_dtype
   int64_t ldy;
   int y_dtype;
-  uint8_t* qy;                 // F8_SILU_Q: e4m3fn [row id, N] and scales [row id, N/128]
+  uint8_t* qy;                 // F8_SILU_Q: e4m3fn [row id, N] (high and low parts) and scales [row id, N/128]
+  uint8_t* qy_lo;
   float* sy;
   int64_t ldqy, ldsy;
   int M, N, K, KB;
@@ -144,14 +155,22 @@ struct Fp8GP {
 
 constexpr int F8_BM = 128;
 constexpr int F8_A_BYTES = F8_BM * 128;   // 128 rows x 128 e4m3 bytes
-constexpr int F8_B_BYTES = 16 * 2048;     // up to 16 weight tiles of 16 columns
-constexpr int F8_B_OFF = F8_A_BYTES;
-constexpr int F8_SA_OFF = F8_B_OFF + F8_B_BYTES;
-constexpr int F8_SW_OFF = F8_SA_OFF + F8_BM * 4;  // 2 x 64 copies of a block scale
-constexpr int F8_STAGE = F8_SW_OFF + 2 * 256;
 constexpr int F8_STAGES = 3;
 constexpr int F8_RID = F8_BM + 64;
-static_assert(F8_STAGES * F8_STAGE + 3 * F8_RID * 4 + 5 * F8_BM * 4 <= 160 * 1024, "LDS budget of one workgroup");
+
+// Stage layout: activation tile(s) (the low part after the high one), the
+// weight tiles, the rows' activation scales, 2 x 64 copies of block scales.
+template <bool LO, int NBT>
+struct F8Stage {
+  static constexpr int A = F8_A_BYTES * (LO ? 2 : 1);
+  static constexpr int B_OFF = A;
+  static constexpr int SA_OFF = B_OFF + NBT * 2048;
+  static constexpr int SW_OFF = SA_OFF + F8_BM * 4;
+  static constexpr int BYTES = SW_OFF + 2 * 256;
+};
+constexpr size_t f8_lds_bytes(int stage) { return (size_t)F8_STAGES * stage + 3 * F8_RID * 4 + 5 * F8_BM * 4; }
+static_assert(f8_lds_bytes(F8Stage<false, 16>::BYTES) <= 160 * 1024, "LDS budget of one workgroup");
+static_assert(f8_lds_bytes(F8Stage<true, 8>::BYTES) <= 160 * 1024, "LDS budget of one workgroup");
 
 __device__ __forceinline__ int f8_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
@@ -159,7 +178,7 @@ __device__ __forceinline__ f32x16 mfma_f8_32(const i32x8& a, const i32x8& b, f32
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-template <int EPI, int CTW>
+template <int EPI, int CTW, bool LO = false>
 __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   constexpr int NQ = EPI == F8_SILU_Q ? 2 : 1;
   constexpr int WGN = 64 * CTW;      // columns per matrix per item
@@ -170,6 +189,10 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   constexpr int CQ = C32 / NQ;
   constexpr int NSW = WGN == 256 || NQ == 2 ? 2 : 1;  // block scales per K block
   static_assert(NBT % 4 == 0 && NBT <= 16 && C32 >= 1 && C32 <= 2, "tile shape");
+  static_assert(!LO || EPI == F8_ROWS, "low activation parts feed the down stage only");
+  using SL = F8Stage<LO, NBT>;
+  constexpr int F8_STAGE = SL::BYTES, F8_B_OFF = SL::B_OFF, F8_SA_OFF = SL::SA_OFF, F8_SW_OFF = SL::SW_OFF;
+  constexpr int NA = LO ? 4 : 2;  // activation copies per wave and K block
   __shared__ __align__(16) char smem[F8_STAGES * F8_STAGE];
   __shared__ __align__(16) int Rid[3][F8_RID];
   __shared__ __align__(16) float part[4 * F8_BM];
@@ -225,7 +248,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   };
   const bool has_sa = wave == 4 || wave == 5;
   const bool has_sw = wave >= 6 && wave - 6 < NSW;
-  const int ncopy = 2 + BPW + (has_sa ? 1 : 0) + (has_sw ? 1 : 0);
+  const int ncopy = NA + BPW + (has_sa ? 1 : 0) + (has_sw ? 1 : 0);
   auto make_plan = [&](int j, Plan& P) {
     const int li = wx + j * nx;
     P.nb = li % nblk;
@@ -269,6 +292,11 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
     const uint8_t* ab = p.a + (int64_t)kb * 128;
 #pragma unroll
     for (int i = 0; i < 2; ++i) dma16(ab, P.aoff[i], st + (16 * wave + 8 * i) * 128);
+    if constexpr (LO) {
+      const uint8_t* al = p.a_lo + (int64_t)kb * 128;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) dma16(al, P.aoff[i], st + F8_A_BYTES + (16 * wave + 8 * i) * 128);
+    }
 #pragma unroll
     for (int b2 = 0; b2 < BPW; ++b2) {
       const int b = wave * BPW + b2;
@@ -314,25 +342,40 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) swv[q] = *reinterpret_cast<const float*>(S + F8_SW_OFF + q * 256);
     f32x16 t[2][C32];
+    // LO: the low parts first (part 0 at byte F8_A_BYTES), t /= 16, then the
+    // high parts accumulate onto t
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      i32x8 a[2], b[C32];
+    for (int part = LO ? 0 : 1; part < 2; ++part) {
+      const char* SA = S + (part == 0 ? F8_A_BYTES : 0);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(S + rt * 32 * 128 + adoff[s][0]);
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(S + rt * 32 * 128 + adoff[s][1]);
-        a[rt] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      for (int s = 0; s < 2; ++s) {
+        i32x8 a[2], b[C32];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(SA + rt * 32 * 128 + adoff[s][0]);
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(SA + rt * 32 * 128 + adoff[s][1]);
+          a[rt] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+#pragma unroll
+        for (int c = 0; c < C32; ++c) {
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(S + bdoff[c][s]);
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(S + bdoff[c][s] + 1024);
+          b[c] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+        const bool fresh = s == 0 && (LO ? part == 0 : true);
+#pragma unroll
+        for (int c = 0; c < C32; ++c)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) t[rt][c] = mfma_f8_32(a[rt], b[c], fresh ? f32x16{} : t[rt][c]);
       }
+      if (LO && part == 0) {
 #pragma unroll
-      for (int c = 0; c < C32; ++c) {
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(S + bdoff[c][s]);
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(S + bdoff[c][s] + 1024);
-        b[c] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+          for (int c = 0; c < C32; ++c)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t[rt][c][i] *= 0.0625f;
       }
-#pragma unroll
-      for (int c = 0; c < C32; ++c)
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) t[rt][c] = mfma_f8_32(a[rt], b[c], s == 0 ? f32x16{} : t[rt][c]);
     }
     // acc += (s_a[row] * s_w[block]) * t; register i of tile rt holds row
     // mw*64 + 32*rt + 8*(i/4) + 4*h + i%4
@@ -353,16 +396,15 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   auto epilogue = [&](int j, const Plan& P) {
     const int* R = Rid[j % 3];
     if constexpr (EPI == F8_SILU_Q) {
-      // h = silu(g) * u held in bf16, then e4m3 per row per 128-column block
-      // (this item's columns): scale = max(amax, 1e-12) / 448
+      // h = silu(g) * u in float32, then high and low e4m3 parts per row
+      // per 128-column block (this item's columns): scale = max(amax, 1e-12) / 448
       float hv[32], am[32];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const float g = acc[rt][0][i], u = acc[rt][1][i];
-          const float v = g * __frcp_rn(1.0f + __expf(-g)) * u;
-          hv[rt * 16 + i] = bf16_bits_to_f32(f32_to_bf16_bits(v));
+          hv[rt * 16 + i] = g * __frcp_rn(1.0f + __expf(-g)) * u;
           am[rt * 16 + i] = fabsf(hv[rt * 16 + i]);
         }
       const float wmax = half_wave_row_reduce<true>(am, c32);
@@ -382,7 +424,12 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
             const int row = row_of(rt, 4 * g + e);
             if (row < P.nvalid) {
               const float sc = fmaxf(amx[e], kAmaxFloor) / kFp8Max;
-              p.qy[(int64_t)R[row] * p.ldqy + col] = (uint8_t)f32_to_fp8_rne(hv[rt * 16 + 4 * g + e] / sc);
+              const float v = hv[rt * 16 + 4 * g + e] / sc;
+              const uint32_t qh = f32_to_fp8_rne(v);
+              // v - fp8(qh) is exact (qh is v's nearest e4m3 value), and so is * 16
+              const uint32_t ql = f32_to_fp8_rne((v - fp8_e4m3_to_f32(qh)) * 16.0f);
+              p.qy[(int64_t)R[row] * p.ldqy + col] = (uint8_t)qh;
+              p.qy_lo[(int64_t)R[row] * p.ldqy + col] = (uint8_t)ql;
             }
           }
         }
@@ -422,7 +469,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   int j = 0, kb = 0, slot = 0;
   for (int g = 0; g < total; ++g) {
     if (g + 1 < total)
-      wait_stage<7>(ncopy);
+      wait_stage<8>(ncopy);
     else
       wait_vmcnt<0>();
     lds_barrier();
@@ -463,9 +510,18 @@ static int f8_device_cus() {
 // actual number from meta when given).  K must hold at least 2 blocks.
 template <int EPI>
 static int launch_fp8_gemm(const Fp8GP& p, int64_t tiles, hipStream_t st) {
-  const int wgn = EPI == F8_SILU_Q ? 128 : (p.N % 256 == 0 ? 256 : 128);
+  const bool lo = p.a_lo != nullptr;
+  if (lo && EPI != F8_ROWS) return arg_error("fp8 gemm: low activation parts need the row epilogue");
+  // the high + low activation tiles take the LDS of half the weight tiles
+  const int wgn = EPI == F8_SILU_Q || lo ? 128 : (p.N % 256 == 0 ? 256 : 128);
   const int64_t items = tiles * (p.N / wgn), cus = f8_device_cus();
   const dim3 grid((unsigned)(items < cus ? items : cus)), block(512);
+  if constexpr (EPI == F8_ROWS) {
+    if (lo) {
+      hipLaunchKernelGGL((fp8_gemm_kernel<EPI, 2, true>), grid, block, 0, st, p);
+      return launch_status("fp8 gemm");
+    }
+  }
   if (wgn == 256)
     hipLaunchKernelGGL((fp8_gemm_kernel<EPI, (EPI == F8_SILU_Q ? 2 : 4)>), grid, block, 0, st, p);
   else
@@ -622,7 +678,8 @@ int check_fp8_experts(const ccq_fp8_experts* ex, const char* name) {
 struct F8MoeLayout {
   int64_t n, max_tiles;
   int bm;
-  size_t off_sorted, off_te, off_meta, off_counts, off_qx, off_sx, off_qh, off_sh, off_rows, off_align, total;
+  size_t off_sorted, off_te, off_meta, off_counts, off_qx, off_sx, off_qh, off_qh_lo, off_sh, off_rows, off_align,
+      total;
 };
 
 F8MoeLayout f8_moe_layout(int64_t T, int64_t k, const ccq_fp8_experts* ex) {
@@ -645,6 +702,8 @@ F8MoeLayout f8_moe_layout(int64_t T, int64_t k, const ccq_fp8_experts* ex) {
   L.off_sx = o;
   o += a256((size_t)T * (H / 128) * 4);
   L.off_qh = o;
+  o += a256((size_t)L.n * I);
+  L.off_qh_lo = o;
   o += a256((size_t)L.n * I);
   L.off_sh = o;
   o += a256((size_t)L.n * (I / 128) * 4);
@@ -712,6 +771,7 @@ static int moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const flo
   uint8_t* qx = (uint8_t*)(ws + L.off_qx);
   float* sx = (float*)(ws + L.off_sx);
   uint8_t* qh = (uint8_t*)(ws + L.off_qh);
+  uint8_t* qh_lo = (uint8_t*)(ws + L.off_qh_lo);
   float* sh = (float*)(ws + L.off_sh);
   void* rows = ws + L.off_rows;
 
@@ -737,6 +797,7 @@ static int moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const flo
   g.w_es = I * H;
   g.sw_es = (I / 128) * (H / 128);
   g.qy = qh;
+  g.qy_lo = qh_lo;
   g.sy = sh;
   g.ldqy = I;
   g.ldsy = I / 128;
@@ -748,6 +809,7 @@ static int moe_fp8_ffn(const void* x, int x_dtype, const int64_t* ids, const flo
 
   Fp8GP d = {};
   d.a = qh;
+  d.a_lo = qh_lo;
   d.lda = I;
   d.sa = sh;
   d.ldsa = I / 128;

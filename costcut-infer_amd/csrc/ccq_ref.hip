@@ -187,6 +187,13 @@ __global__ __launch_bounds__(256) void ref_linear_f32_kernel(const float* __rest
 }
 
 // out = g / (1 + exp(-g)) * u in float64, stored float32 (kernels.py:219-231)
+// out[i] = s[i / G] for i < groups * G.
+__global__ void group_broadcast_kernel(const float* __restrict__ s, float* __restrict__ out, int64_t n, int64_t G) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) out[i] = s[i / G];
+}
+
 __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ out,
                                 int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -510,6 +517,18 @@ extern "C" int ccq_f32_to_fp8(const float* x, uint8_t* out, int64_t n, void* str
   CCQ_REQUIRE(x && out, "ccq_f32_to_fp8: null pointer");
   hipLaunchKernelGGL(f32_to_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), x, out, n);
   return launch_status("ccq_f32_to_fp8");
+}
+
+extern "C" int ccq_group_broadcast_scale(const float* scale_groups, int64_t groups, int64_t group_size, float* out,
+                                         void* stream) {
+  CCQ_REQUIRE(groups >= 0 && group_size >= 0, "ccq_group_broadcast_scale: negative size");
+  CCQ_REQUIRE(group_size == 0 || groups <= INT64_MAX / group_size, "ccq_group_broadcast_scale: size overflows");
+  const int64_t n = groups * group_size;
+  if (n == 0) return 0;
+  CCQ_REQUIRE(scale_groups && out, "ccq_group_broadcast_scale: null pointer");
+  hipLaunchKernelGGL(group_broadcast_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), scale_groups,
+                     out, n, group_size);
+  return launch_status("ccq_group_broadcast_scale");
 }
 
 extern "C" int ccq_silu_mul(const float* gate, const float* up, float* out, int64_t n, void* stream) {

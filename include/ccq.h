@@ -78,6 +78,12 @@ int ccq_kv_dequant_fp8(const uint8_t* codes, const uint8_t* scales, float* out, 
 int ccq_fp8_dequant(const uint8_t* w, const float* scale, float* out,
                     int64_t rows, int64_t cols, void* stream);
 
+/* out[i * group_size + j] = scale_groups[i] for i < groups, j < group_size
+ * (float32; out holds at least groups * group_size elements, the rest is
+ * left as it is).  Replaces group_broadcast_scale (quant/kernels.py:258-268). */
+int ccq_group_broadcast_scale(const float* scale_groups, int64_t groups, int64_t group_size, float* out,
+                              void* stream);
+
 /* out = gate / (1 + exp(-gate)) * up, computed in float64, stored float32.
  * Replaces silu_mul_fused (quant/kernels.py:219-231). */
 int ccq_silu_mul(const float* gate, const float* up, float* out, int64_t n, void* stream);

@@ -55,12 +55,16 @@ def unpack(packed: np.ndarray) -> np.ndarray:
 
 
 def dequant(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray, group_size: int) -> np.ndarray:
-    """``W [K, N] f32 = (q - z) * s`` with the group index ``k // G``."""
-    q = unpack(qweight).astype(np.int64)
-    z = unpack(qzeros).astype(np.int64)
-    s = np.asarray(scales).astype(np.float64)
-    g = np.arange(q.shape[0]) // group_size
-    return ((q - z[g]).astype(np.float64) * s[g]).astype(np.float32)
+    """``W [K, N] f32 = (q - z) * s`` with the group index ``k // G``.  q - z
+    is an integer in [-15, 15] and s an fp16/bf16 value, so the float32
+    product is exact."""
+    q = unpack(qweight)
+    z = unpack(qzeros)
+    K, N = q.shape
+    G = int(group_size)
+    s = np.asarray(scales).astype(np.float32)
+    d = q.reshape(K // G, G, N).astype(np.float32) - z.astype(np.float32)[:, None, :]
+    return (d * s[:, None, :]).reshape(K, N)
 
 
 def linear(x: np.ndarray, qweight, qzeros, scales, group_size: int) -> np.ndarray:

@@ -13,7 +13,9 @@ restated here is the public DeepSeek-V3 style FP8 format:
 * activations ``x [T, K]``: ``amax = max|x|`` over each 128-channel block of a
   token, ``s_a = max(amax, 1e-12) / 448`` (float32), ``q = RNE(clip(x / s_a,
   -448, 448))`` to e4m3fn;
-* ``y = (fp8(q) * s_a) @ W.T`` in float32 (dequantize-then-matmul).
+* ``y = (fp8(q) * s_a) @ W.T`` in float32 (dequantize-then-matmul);
+* the MoE expert: ``expert_ffn`` of the reference on these dequantized
+  weights, the intermediate in float32.
 
 Parity against the reference is unpinned (the scheme is absent there).  RNE
 encoding is pinned against ``torch.Tensor.to(torch.float8_e4m3fn)``.
@@ -30,6 +32,19 @@ AMAX_FLOOR = np.float32(1e-12)
 FP8_MAX = np.float32(448.0)
 
 _POS = FP8_TABLE[:0x7F].astype(np.float64)  # codes 0x00..0x7E, increasing
+# two codes at once: entry b0 | b1 << 8 holds the float32 bits of
+# (FP8_TABLE[b0], FP8_TABLE[b1]) (a byte-pair lookup is much faster in numpy
+# than a per-byte one)
+_T32 = FP8_TABLE.astype(np.float32).view(np.uint32).astype(np.uint64)
+_PAIR = ((_T32[:, None] << np.uint64(32)) | _T32[None, :]).reshape(-1)
+
+
+def decode(w: np.ndarray) -> np.ndarray:
+    """e4m3fn bytes -> float32 values (``FP8_TABLE[w]``)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    if w.ndim == 0 or w.shape[-1] % 2:
+        return FP8_TABLE[w].astype(np.float32)
+    return _PAIR[w.view(np.uint16)].view(np.float32).reshape(w.shape)
 
 
 def float32_to_fp8_rne(x: np.ndarray) -> np.ndarray:
@@ -73,12 +88,17 @@ def act_dequant(q: np.ndarray, s: np.ndarray, block: int = BLOCK) -> np.ndarray:
 
 
 def block_dequant(w: np.ndarray, s_w: np.ndarray, block: int = BLOCK) -> np.ndarray:
-    """``W [N, K] f32 = fp8(w) * s_w[n//128, k//128]``."""
+    """``W [N, K] f32 = fp8(w) * s_w[n//128, k//128]``.  The decoded code has
+    at most 4 significant bits, so the float32 product is the correctly
+    rounded exact product (one rounding, as in float64 then a cast)."""
     w = np.asarray(w, dtype=np.uint8)
     N, K = w.shape
-    s = np.asarray(s_w, dtype=np.float64)
-    sf = np.repeat(np.repeat(s, block, axis=0)[:N], block, axis=1)[:, :K]
-    return (FP8_TABLE[w].astype(np.float64) * sf).astype(np.float32)
+    s = np.asarray(s_w, dtype=np.float32)
+    nb, kb = -(-N // block), -(-K // block)
+    dec = np.zeros((nb * block, kb * block), dtype=np.float32)
+    dec[:N, :K] = decode(w)
+    out = dec.reshape(nb, block, kb, block) * s[:nb, None, :kb, None]
+    return out.reshape(nb * block, kb * block)[:N, :K]
 
 
 def linear(x: np.ndarray, w: np.ndarray, s_w: np.ndarray) -> np.ndarray:
@@ -96,15 +116,17 @@ def to_bf16(x: np.ndarray) -> np.ndarray:
     return np.where(nan, np.float32(np.nan), out).astype(np.float32)
 
 
-def expert_ffn(x, wg, sg, wu, su, wd, sd, inter_bf16: bool = True) -> np.ndarray:
-    """One FP8-block expert: ``down(q(silu(q(x) Wg^T) * (q(x) Wu^T)))``.
+def expert_ffn(x, wg, sg, wu, su, wd, sd) -> np.ndarray:
+    """One FP8-block expert as the reference's ``expert_ffn`` computes it on
+    dequantized weights (``blocks/moe.py:122-141``): ``down(silu(x Wg^T) *
+    (x Wu^T))`` in float32, with x quantized per token per 128 (the block
+    scheme's dynamic activation quantization) before gate and up, and the
+    SiLU intermediate kept in float32 (no rounding or re-quantization
+    before the down projection).
 
-    ``wg, wu [I, H]``, ``wd [H, I]`` e4m3 bytes with block scales; the
-    intermediate is rounded to bf16 (``inter_bf16``) and re-quantized per token
-    per 128 before the down projection."""
+    ``wg, wu [I, H]``, ``wd [H, I]`` e4m3 bytes (row = output channel) with
+    block scales ``[N/128, K/128]``."""
     gate = linear(x, wg, sg)
     up = linear(x, wu, su)
     h = silu_mul_fused(gate, up)
-    if inter_bf16:
-        h = to_bf16(h)
-    return linear(h, wd, sd)
+    return h @ block_dequant(wd, sd).T

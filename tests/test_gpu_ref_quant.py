@@ -146,3 +146,26 @@ def test_fp8_linear_method_parity(gpu, batch):
     y = m.apply(w.tobytes(), {"l.fp8.weight_scale": s}, x)
     ref = rq.fp8_linear_apply(w.tobytes(), s, x)
     assert np.allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("groups,G", [(16, 128), (11, 128), (7, 3), (1, 1)])
+def test_group_broadcast_scale_bitexact(gpu, groups, G):
+    """ccq_group_broadcast_scale against the oracle, numpy and device forms;
+    an ``out`` longer than groups * G keeps its tail (the reference writes
+    only the leading elements)."""
+    from ccut.quant import kernels as qk
+    from oracle.ref_quant import group_broadcast_scale as ref_gbs
+
+    rng = np.random.default_rng(groups * G)
+    s = rng.standard_normal(groups).astype(np.float32)
+    ref = ref_gbs(s, G)
+    out = np.full(groups * G + 5, 7.0, dtype=np.float32)
+    got = qk.group_broadcast_scale(s, G, out)
+    assert got is out
+    assert np.array_equal(out[: groups * G].view(np.uint32), ref.view(np.uint32))
+    assert np.all(out[groups * G:] == 7.0)
+    dev = torch.full((groups * G + 3,), -1.0, device=gpu)
+    qk.group_broadcast_scale(torch.from_numpy(s).to(gpu), G, dev)
+    d = dev.cpu().numpy()
+    assert np.array_equal(d[: groups * G].view(np.uint32), ref.view(np.uint32)) and np.all(d[groups * G:] == -1.0)
+    assert np.array_equal(qk.group_broadcast_scale(s, G, None), ref)

@@ -161,3 +161,18 @@ def test_nf4_dequant_table_and_layout():
     t16 = np.linspace(-1, 1, 16).astype(np.float32)
     out16 = nf4_dequant_row(packed, scale, t16)
     assert out16[0, 9] == np.float32(t16[9] * scale[9])
+
+
+def test_group_broadcast_scale_loop():
+    """out[i*G + j] == s[i] element by element (a tile instead of a repeat,
+    or a wrong group size, fails), for G = 1, 3 and 128."""
+    from oracle.ref_quant import group_broadcast_scale
+
+    rng = np.random.default_rng(4)
+    for groups, G in ((5, 1), (7, 3), (16, 128)):
+        s = rng.standard_normal(groups).astype(np.float32)
+        out = group_broadcast_scale(s, G)
+        assert out.dtype == np.float32 and out.shape == (groups * G,)
+        for i in range(groups):
+            for j in range(G):
+                assert out[i * G + j] == s[i]
