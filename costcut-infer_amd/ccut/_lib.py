@@ -110,6 +110,7 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_fp8_act_quant": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "ccq_fp8_block_repack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ccq_fp8_block_unpack": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "ccq_fp8_block_dequant": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "ccq_fp8_block_linear_workspace_size": (_sz, [_i64, _i64]),
     "ccq_fp8_block_linear": (_int, [_vp, _int, _vp, _vp, _vp, _int, _i64, _i64, _i64, _vp, _sz, _vp]),
     "ccq_moe_fp8_workspace_size": (_sz, [_i64, _i64, ctypes.POINTER(ccq_fp8_experts)]),

@@ -12,11 +12,21 @@ and the metrics.  The expert weights come from ``reader`` in one of two ways:
   ``moe_ffn_fp8``); activations go to the int4 kernels as bfloat16.
 * otherwise ``reader.get(layer, eid, timeout)`` per routed expert returning
   float32 ``(w_gate [hidden, inter], w_up [hidden, inter], w_down [inter,
-  hidden])``, as the reference's reader does: ``expert_ffn`` per expert and
-  ``moe_combine`` (reference ``pipeline.py:155-179``).  An expert whose read
-  raises ``TimeoutError`` is left out of the step (its assignments
-  contribute nothing, the other weights are not renormalised), as in the
-  reference (``:159-163``).
+  hidden])``, the orientation ``expert_ffn`` takes: ``expert_ffn`` per
+  expert and ``moe_combine`` (reference ``pipeline.py:155-179``).  Weights
+  of any other shape raise ``ValueError`` (the reference's reader hands over
+  ``[out, in]`` slots here, ``pipeline.py:160-170``; this package's
+  ``ExpertReader`` returns ``[in, out]``).
+
+An expert whose read raises ``TimeoutError`` is handled by
+``on_expert_timeout``: ``"renormalize"`` (default) leaves it out and
+rescales each affected token's surviving routing weights so they keep the
+token's original weight sum -- the redistribution the reference's comment
+at ``pipeline.py:161`` describes, where its code only skips the expert;
+``"drop"`` leaves it out with the other weights unchanged (what the
+reference's code does); ``"raise"`` re-raises.  Timed-out experts and the
+assignments left out are counted in ``metrics.expert_timeouts`` /
+``metrics.dropped_assignments``.
 
 ``reader.prefetch(layer, ids)``, ``reader.stats()`` and ``reader.close()``
 are called when the reader has them.
@@ -51,6 +61,8 @@ class PipelineMetrics:
     ring_hits: int = 0
     ring_misses: int = 0
     ring_evicted: int = 0
+    expert_timeouts: int = 0
+    dropped_assignments: int = 0
 
     def overlap_ratio(self) -> float:
         return self.overlap_ns / self.compute_ns if self.compute_ns > 0 else 0.0
@@ -68,6 +80,8 @@ class PipelineMetrics:
             "spec_accept_rate": round(self.speculative_accept_rate(), 4),
             "ring_hits": self.ring_hits,
             "ring_misses": self.ring_misses,
+            "expert_timeouts": self.expert_timeouts,
+            "dropped_assignments": self.dropped_assignments,
         }
 
 
@@ -98,7 +112,10 @@ class ExpertPipeline:
     ``pipeline.py:87-208``)."""
 
     def __init__(self, reader, num_workers: int = 2, speculative_window: int = 4, prefetch_steps_ahead: int = 2,
-                 metrics_enabled: bool = True):
+                 metrics_enabled: bool = True, on_expert_timeout: str = "renormalize"):
+        if on_expert_timeout not in ("renormalize", "drop", "raise"):
+            raise ValueError(f"on_expert_timeout={on_expert_timeout!r}: expected 'renormalize', 'drop' or 'raise'")
+        self.on_expert_timeout = on_expert_timeout
         self.reader = reader
         self.num_workers = num_workers
         self.prefetch_steps_ahead = prefetch_steps_ahead
@@ -159,21 +176,7 @@ class ExpertPipeline:
             raise TypeError(f"reader.experts({layer}) returned {type(ex).__name__}, "
                             "expected W4Experts or Fp8Experts")
         else:
-            resolved: dict[int, tuple] = {}
-            for eid in sorted(set(e for e in flat_ids if e >= 0)):
-                try:
-                    resolved[eid] = self.reader.get(layer, int(eid), timeout=30.0)
-                except TimeoutError:
-                    continue  # left out of this step
-            ids_used = ids.clone()
-            for eid in set(e for e in flat_ids if e >= 0) - set(resolved):
-                ids_used[ids_used == eid] = -1
-            if resolved:
-                out = moe.moe_combine(xd, ids_used, weights, w_lookup=resolved.__getitem__, shared=s_out,
-                                      shared_gate=shared_gate)
-                shared_done = True
-            else:
-                out = torch.zeros_like(xd)
+            out, shared_done = self._per_expert(layer, xd, ids, weights, flat_ids, s_out, shared_gate)
         if s_out is not None and not shared_done:
             moe.shared_expert_add(out, s_out, shared_gate)
         torch.cuda.synchronize(xd.device)
@@ -192,6 +195,50 @@ class ExpertPipeline:
                 self.metrics.ring_hits = st.get("hits", 0)
                 self.metrics.ring_misses = st.get("misses", 0)
         return _dev.to_host(out) if _dev.is_host(x) else out
+
+    def _per_expert(self, layer: int, xd: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+                    flat_ids: list[int], s_out, shared_gate: float):
+        """The reference's per-expert path (``pipeline.py:155-179``): each
+        routed expert's float32 weights from ``reader.get``, ``expert_ffn`` +
+        ``moe_combine``; timeouts as ``on_expert_timeout`` says."""
+        H = xd.shape[1]
+        resolved: dict[int, tuple] = {}
+        for eid in sorted(set(e for e in flat_ids if e >= 0)):
+            try:
+                wg, wu, wd = self.reader.get(layer, int(eid), timeout=30.0)
+            except TimeoutError:
+                if self.on_expert_timeout == "raise":
+                    raise
+                if self.metrics is not None:
+                    self.metrics.expert_timeouts += 1
+                continue
+            I = wg.shape[1] if wg.ndim == 2 else -1
+            if tuple(wg.shape) != (H, I) or tuple(wu.shape) != (H, I) or tuple(wd.shape) != (I, H):
+                raise ValueError(f"reader.get({layer}, {eid}): expert weights gate {tuple(wg.shape)}, up "
+                                 f"{tuple(wu.shape)}, down {tuple(wd.shape)}; expected gate/up [hidden={H}, inter] "
+                                 f"and down [inter, hidden={H}]")
+            resolved[eid] = (wg, wu, wd)
+        missing = set(e for e in flat_ids if e >= 0) - set(resolved)
+        ids_used, w_used = ids, weights
+        if missing:
+            ids_used = ids.clone()
+            for eid in missing:
+                ids_used[ids_used == eid] = -1
+            kept = ids_used >= 0
+            if self.metrics is not None:
+                self.metrics.dropped_assignments += int((~kept & (ids >= 0)).sum().item())
+            if self.on_expert_timeout == "renormalize":
+                w_kept = torch.where(kept, weights, torch.zeros_like(weights))
+                total = torch.where(ids >= 0, weights, torch.zeros_like(weights)).sum(dim=1, keepdim=True)
+                left = w_kept.sum(dim=1, keepdim=True)
+                scale = torch.where(left != 0, total / torch.where(left != 0, left, torch.ones_like(left)),
+                                    torch.zeros_like(left))
+                w_used = (w_kept * scale).contiguous()
+        if resolved:
+            out = moe.moe_combine(xd, ids_used, w_used, w_lookup=resolved.__getitem__, shared=s_out,
+                                  shared_gate=shared_gate)
+            return out, True
+        return torch.zeros_like(xd), False
 
     def close(self) -> None:
         close = getattr(self.reader, "close", None)

@@ -7,18 +7,30 @@ A slot holds one expert's ``(gate, up, down)`` as float32 device tensors,
 dequantized on the GPU from the checkpoint segments:
 
 * ``F8_E4M3`` / ``F8_E5M2`` weight ``[out, in]`` with an optional per-row
-  ``weight_scale`` (``[out]`` or ``[out, 1]``, BF16 / F16 / F32):
-  ``fp8_dequant_mat`` (``ccq_fp8_dequant``); E5M2 is decoded by torch;
+  scale (``weight_scale`` / ``_scale``, ``[out]`` or ``[out, 1]``, BF16 /
+  F16 / F32): ``fp8_dequant_mat`` (``ccq_fp8_dequant``); E5M2 is decoded by
+  torch;
+* ``F8_E4M3`` weight ``[out, in]`` with 128x128 block scales
+  (``weight_scale_inv`` or ``weight_scale`` of shape ``[ceil(out/128),
+  ceil(in/128)]``, F32 / BF16): ``ccq_fp8_block_dequant``;
 * ``BF16`` / ``F16`` / ``F32`` weight: converted to float32;
 * AWQ ``qweight`` / ``qzeros`` / ``scales`` (int32 ``[K, N/8]``, int32
-  ``[K/G, N/8]``, F16/BF16 ``[K/G, N]``): ``ccq_awq_dequant`` to
-  ``[K, N]``.
+  ``[K/G, N/8]``, F16/BF16 ``[K/G, N]``), or the same packing under the
+  compressed-tensors group names ``weight`` (I32) / ``zero_points`` /
+  ``scales``: ``ccq_awq_dequant`` to ``[K, N]``.
 
-The slots keep the checkpoint's orientation, as the reference's do
-(``[out, in]`` for the FP8 / float layouts, ``[in, out]`` for AWQ).
+Every slot is in ``expert_ffn``'s orientation, ``[in, out]``: gate/up
+``[hidden, inter]``, down ``[inter, hidden]`` (reference
+``blocks/moe.py:122-141``).  FP8 and float checkpoints store ``[out, in]``
+and are transposed once when the slot is filled; AWQ is ``[in, out]``
+already.  (The reference's reader keeps the checkpoint's ``[out, in]`` and
+its pipeline hands those slots to ``expert_ffn`` untransposed,
+``experts/pipeline.py:170``: a shape error, or ``x @ W`` in place of
+``x @ W.T`` when hidden == inter.)
 
-``experts(layer)`` additionally packs a whole AWQ layer into the fused
-kernels' device format (``W4Experts``, built once per layer), which
+``experts(layer)`` additionally packs a whole AWQ layer (``W4Experts``) or
+block-FP8 layer (``Fp8Experts``, hidden and inter multiples of 128) into the
+fused kernels' device format, built once per layer, which
 ``ExpertPipeline`` uses instead of per-expert reads.
 """
 
@@ -135,15 +147,46 @@ class ExpertReader:
                     return base + suf
         return None
 
-    def _dequant(self, entry: ExpertEntry, proj: str) -> torch.Tensor:
-        segs = entry.segments
+    def _awq_keys(self, segs: dict, proj: str) -> tuple[str, str, str] | None:
+        """(weight, zeros, scales) segment keys of an AWQ-packed projection:
+        AutoAWQ names, or the compressed-tensors group names."""
         qkey = self._pick(segs, proj, (".qweight",))
-        if qkey is not None:  # AWQ
+        if qkey is not None:
+            base = qkey[: -len(".qweight")]
+            return qkey, base + ".qzeros", base + ".scales"
+        zkey = self._pick(segs, proj, (".zero_points",))
+        if zkey is not None:
+            base = zkey[: -len(".zero_points")]
+            wkey = base + ".weight" if base + ".weight" in segs else base
+            if wkey in segs and segs[wkey][3] in ("I32", "U32") and base + ".scales" in segs:
+                return wkey, zkey, base + ".scales"
+        return None
+
+    def _fp8_scale(self, entry: ExpertEntry, proj: str, rows: int, cols: int):
+        """("row", [rows] f32) or ("block", [ceil(rows/128), ceil(cols/128)]
+        f32) or ("row", ones) when the projection has no scale tensor."""
+        skey = self._pick(entry.segments, proj, (".weight_scale_inv", ".weight_scale", "_scale"))
+        if skey is None:
+            return "row", torch.ones(rows, dtype=torch.float32, device=self.device)
+        sc = self._device_tensor(entry, skey).float()
+        shape = tuple(sc.shape)
+        if sc.numel() == rows and (len(shape) <= 1 or shape[-1] == 1):
+            return "row", sc.reshape(-1)
+        blocks = (-(-rows // 128), -(-cols // 128))
+        if shape == blocks:
+            return "block", sc.contiguous()
+        raise ValueError(f"{proj}: scale {skey} of shape {shape} for a [{rows}, {cols}] weight (expected "
+                         f"[{rows}] / [{rows}, 1] per row or {list(blocks)} per 128x128 block)")
+
+    def _dequant(self, entry: ExpertEntry, proj: str) -> torch.Tensor:
+        """One projection as float32 ``[in, out]`` on the device."""
+        segs = entry.segments
+        keys = self._awq_keys(segs, proj)
+        if keys is not None:
             from ccut.quant import awq
 
-            base = qkey[: -len(".qweight")]
-            qw, qz, sc = (self._device_tensor(entry, base + s) for s in (".qweight", ".qzeros", ".scales"))
-            K, N = qw.shape[0], qw.shape[1] * 8
+            qw, qz, sc = (self._device_tensor(entry, k) for k in keys)
+            K = qw.shape[0]
             return awq.dequant(qw, qz, sc, K // sc.shape[0]).float()
         wkey = self._pick(segs, proj, (".weight", ""))
         if wkey is None:
@@ -151,21 +194,23 @@ class ExpertReader:
         raw, dtype, shape = self._read(entry, wkey)
         rows, cols = _shape_2d(int(entry.segments[wkey][2]), shape)
         if dtype in ("F8_E4M3", "F8_E5M2"):
-            skey = self._pick(segs, proj, (".weight_scale", "_scale", ".weight_scale_inv"))
-            scale = (torch.ones(rows, dtype=torch.float32, device=self.device) if skey is None
-                     else self._device_tensor(entry, skey).float().reshape(-1))
-            if scale.numel() != rows:
-                raise ValueError(f"{proj}: {scale.numel()} scales for {rows} rows (per-row scales expected)")
+            kind, scale = self._fp8_scale(entry, proj, rows, cols)
             w = torch.from_numpy(raw.copy()).to(self.device).reshape(rows, cols)
+            if kind == "block":
+                if dtype != "F8_E4M3":
+                    raise NotImplementedError(f"{proj}: block scales with {dtype} weights")
+                from ccut.quant import fp8_block
+
+                return fp8_block.dequant(w, scale).T.contiguous()
             if dtype == "F8_E4M3":
                 from ccut.quant import kernels as qk
 
                 out = torch.empty((rows, cols), dtype=torch.float32, device=self.device)
-                return qk.fp8_dequant_mat(w, scale, out)
-            return w.view(torch.float8_e5m2).float() * scale[:, None]
+                return qk.fp8_dequant_mat(w, scale, out).T.contiguous()
+            return (w.view(torch.float8_e5m2).float() * scale[:, None]).T.contiguous()
         if dtype in _FLOAT_DTYPES:
             t = torch.from_numpy(raw.copy()).view(_FLOAT_DTYPES[dtype]).reshape(rows, cols)
-            return t.to(self.device).float()
+            return t.to(self.device).float().T.contiguous()
         raise NotImplementedError(f"expert segment dtype {dtype} is not supported")
 
     def _device_tensor(self, entry: ExpertEntry, key: str) -> torch.Tensor:
@@ -243,8 +288,9 @@ class ExpertReader:
         return n
 
     def get(self, layer: int, expert_id: int, timeout: float = 30.0):
-        """``(gate, up, down)`` float32 device tensors of a ready expert,
-        waiting for its fill; ``TimeoutError`` when it is not ready in time."""
+        """``(gate [hidden, inter], up [hidden, inter], down [inter, hidden])``
+        float32 device tensors of a ready expert, waiting for its fill;
+        ``TimeoutError`` when it is not ready in time."""
         deadline = time.monotonic() + timeout
         with self._cv:
             ring = self.rings[layer]
@@ -271,28 +317,62 @@ class ExpertReader:
                 self._cv.wait(timeout=min(left, 0.5))
 
     def experts(self, layer: int):
-        """The whole layer as ``W4Experts`` when its experts are AWQ
-        segments (built once), else None (per-expert reads)."""
+        """The whole layer as ``W4Experts`` (AWQ segments) or ``Fp8Experts``
+        (e4m3 segments with 128x128 block scales, hidden and inter multiples
+        of 128), built once; None when the layer is in another format
+        (per-expert reads)."""
         if layer in self._layers:
             return self._layers[layer]
         e0 = self.index.get(layer, 0)
         ex = None
-        if e0 is not None and self._pick(e0.segments, "gate", (".qweight",)) is not None:
+        if e0 is not None and self._awq_keys(e0.segments, "gate") is not None:
             from ccut.blocks import moe
 
             def stack(proj):
                 parts = []
                 for eid in range(self.index.num_experts):
                     entry = self.index.entries[(layer, eid)]
-                    base = self._pick(entry.segments, proj, (".qweight",))[: -len(".qweight")]
-                    parts.append([self._device_tensor(entry, base + s) for s in (".qweight", ".qzeros", ".scales")])
+                    parts.append([self._device_tensor(entry, k) for k in self._awq_keys(entry.segments, proj)])
                 return tuple(torch.stack([p[i] for p in parts]) for i in range(3))
 
             gate, up, down = stack("gate"), stack("up"), stack("down")
             K = gate[0].shape[1]
             ex = moe.W4Experts.from_awq(gate, up, down, group_size=K // gate[2].shape[1])
+        elif e0 is not None and self._is_fp8_block(e0):
+            from ccut.blocks import moe
+
+            def stack_fp8(proj):
+                ws, ss = [], []
+                for eid in range(self.index.num_experts):
+                    entry = self.index.entries[(layer, eid)]
+                    wkey = self._pick(entry.segments, proj, (".weight", ""))
+                    raw, _, shape = self._read(entry, wkey)
+                    rows, cols = _shape_2d(int(entry.segments[wkey][2]), shape)
+                    kind, sc = self._fp8_scale(entry, proj, rows, cols)
+                    if kind != "block":
+                        raise ValueError(f"layer {layer} expert {eid} {proj}: per-row scales in a block-FP8 layer")
+                    ws.append(torch.from_numpy(raw.copy()).to(self.device).reshape(rows, cols))
+                    ss.append(sc)
+                return torch.stack(ws), torch.stack(ss)
+
+            ex = moe.Fp8Experts.from_block(stack_fp8("gate"), stack_fp8("up"), stack_fp8("down"))
         self._layers[layer] = ex
         return ex
+
+    def _is_fp8_block(self, entry: ExpertEntry) -> bool:
+        """e4m3 gate weight with 128x128 block scales, shapes the fused FP8
+        kernels take (both dimensions multiples of 128, at least 256)."""
+        wkey = self._pick(entry.segments, "gate", (".weight", ""))
+        if wkey is None or entry.segments[wkey][3] != "F8_E4M3":
+            return False
+        shape = tuple(entry.shapes.get(wkey, ()))
+        if len(shape) != 2 or shape[0] % 128 or shape[1] % 128 or min(shape) < 256:
+            return False
+        try:
+            kind, _ = self._fp8_scale(entry, "gate", shape[0], shape[1])
+        except ValueError:
+            return False
+        return kind == "block"
 
     def stats(self) -> dict:
         return dict(self._stats)

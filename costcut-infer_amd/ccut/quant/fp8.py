@@ -45,14 +45,16 @@ class Fp8LinearMethod(QuantizeMethodBase):
 
 class Fp8Config:
     """Bare ``quant_method="fp8"`` checkpoints (reference ``fp8.py:37-51``):
-    not parsed; the reference raises too."""
+    the 128x128 block form is parsed by ``ccut.quant.registry.Fp8BlockConfig``
+    (registered as "fp8"); any other form raises, as the reference's does."""
 
     name = "fp8"
 
     @classmethod
     def from_config(cls, quant_cfg: dict, model_dir=None):
-        raise NotImplementedError("bare fp8 checkpoints are not parsed; use compressed-tensors or the awq / "
-                                  "fp8-block configs in ccut.quant.registry")
+        from ccut.quant.registry import Fp8BlockConfig
+
+        return Fp8BlockConfig.from_config(quant_cfg, model_dir)
 
     def get_layer_spec(self, layer_name: str):
         raise NotImplementedError

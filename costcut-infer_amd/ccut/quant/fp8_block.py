@@ -25,7 +25,7 @@ from ccut._lib import call, lib
 
 BLOCK = 128
 
-__all__ = ["act_quant", "Fp8BlockWeights", "prepare", "unpack", "linear"]
+__all__ = ["act_quant", "Fp8BlockWeights", "prepare", "unpack", "dequant", "linear"]
 
 
 def act_quant(x) -> tuple[torch.Tensor, torch.Tensor]:
@@ -88,6 +88,22 @@ def unpack(w: Fp8BlockWeights) -> torch.Tensor:
     """Tiled bytes -> ``w [N, K]`` uint8 (inverse of the re-pack)."""
     out = torch.empty((w.N, w.K), dtype=torch.uint8, device=w.w_tiled.device)
     call("ccq_fp8_block_unpack", w.w_tiled.data_ptr(), out.data_ptr(), w.N, w.K, _dev.stream_ptr(out.device))
+    return out
+
+
+def dequant(w, s_w) -> torch.Tensor:
+    """``W [N, K] float32 = fp8(w) * s_w[n//128, k//128]`` on the device (any
+    N, K; ``s_w [ceil(N/128), ceil(K/128)]``), bit-exact."""
+    wd = w if isinstance(w, torch.Tensor) else _dev.to_device(np.ascontiguousarray(w).view(np.uint8))
+    wd = wd.to(_dev.require_gpu()).contiguous().view(torch.uint8)
+    if wd.dim() != 2:
+        raise ValueError(f"block FP8 weight must be [N, K], got {tuple(wd.shape)}")
+    N, K = wd.shape
+    s = _dev.to_device(s_w, torch.float32).contiguous()
+    if tuple(s.shape) != (-(-N // BLOCK), -(-K // BLOCK)):
+        raise ValueError(f"block scales of shape {tuple(s.shape)} do not match w [{N}, {K}]")
+    out = torch.empty((N, K), dtype=torch.float32, device=wd.device)
+    call("ccq_fp8_block_dequant", wd.data_ptr(), s.data_ptr(), out.data_ptr(), N, K, _dev.stream_ptr(wd.device))
     return out
 
 

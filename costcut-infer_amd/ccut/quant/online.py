@@ -1,15 +1,57 @@
-"""Load-time (online) FP8 quantization of BF16 weights (reference
-``python/ccut/quant/online.py:37-64``), on the GPU."""
+"""Online quantization: load-time FP8 quantization of BF16 weights
+(reference ``python/ccut/quant/online.py:37-64``) on the GPU, and the
+``OnlineQuantConfig`` a shorthand of ``resolve_checkpoint_quant`` selects
+(reference ``online.py:67-122``)."""
 
 from __future__ import annotations
+
+import re
+from pathlib import Path
 
 import numpy as np
 import torch
 
 from ccut import _dev
 from ccut._lib import call
+from ccut.quant.registry import QuantizationConfig
+from ccut.quant.spec import K_BF16, LayerQuantSpec, ScaleDesc, get_quant_key
 
-__all__ = ["quantize_buffer_inplace"]
+__all__ = ["quantize_buffer_inplace", "OnlineQuantConfig"]
+
+
+class OnlineQuantConfig(QuantizationConfig):
+    """Every layer quantized at load time with the shorthand's weight key,
+    except those matching an ignore regex (BF16 passthrough); the scales are
+    computed at load, so each spec names a placeholder scale tensor
+    ``<layer>.online_scale``."""
+
+    name = "online"
+
+    def __init__(self, shorthand: dict, weight_key_name: str, ignore_patterns: list[str]):
+        self.shorthand = shorthand
+        self.weight_key_name = weight_key_name
+        self.ignore_patterns = [re.compile(p) for p in (ignore_patterns or [])]
+        self._specs: dict[str, LayerQuantSpec] = {}
+
+    @classmethod
+    def from_config(cls, shorthand: dict, model_dir: str | Path | None = None,
+                    ignore_patterns: list[str] | None = None) -> "OnlineQuantConfig":
+        return cls(shorthand, shorthand["weight"], ignore_patterns or [])
+
+    def is_layer_skipped(self, layer_name: str) -> bool:
+        return any(rx.search(layer_name) for rx in self.ignore_patterns)
+
+    def get_layer_spec(self, layer_name: str) -> LayerQuantSpec:
+        spec = self._specs.get(layer_name)
+        if spec is None:
+            if self.is_layer_skipped(layer_name):
+                spec = LayerQuantSpec(layer_name, get_quant_key(K_BF16), skipped=True, quant_method=self.name)
+            else:
+                spec = LayerQuantSpec(layer_name, get_quant_key(self.weight_key_name),
+                                      scales=(ScaleDesc(f"{layer_name}.online_scale", "F32", ()),),
+                                      quant_method=self.name)
+            self._specs[layer_name] = spec
+        return spec
 
 
 def quantize_buffer_inplace(raw_bf16, scale, out, in_features: int | None = None) -> None:

@@ -130,9 +130,11 @@ class WeightOnlyMethod(QuantizeMethodBase):
             w = self.prepare(weight_bytes, scales)
             if isinstance(x, torch.Tensor) and x.is_cuda and x.dtype in (torch.float16, torch.bfloat16):
                 return awq.gemm(x, w)
-            # float32 / host activations: fp16 inputs to the MFMA, float32 out
+            # float32 / host activations: bfloat16 inputs to the MFMA (the
+            # range of float32, so no activation overflows as it would in
+            # float16 above 65504), float32 out
             xd = _dev.to_device(x, torch.float32)
-            y = awq.gemm(xd.to(torch.float16), w, out_dtype=torch.float32)
+            y = awq.gemm(xd.to(torch.bfloat16), w, out_dtype=torch.float32)
             return _return(y, x)
         if self.weight_dtype == QuantDType.INT4:
             scale = scales.get(self.scale_name) if self.scale_name else None

@@ -101,6 +101,18 @@ __global__ void fp8_unpack_kernel(const uint8_t* __restrict__ tiled, uint8_t* __
   }
 }
 
+// ------------------------------------------------------ block dequant --
+// out[n, k] = fp8(w[n, k]) * s_w[n / 128, k / 128] (float32, one rounding),
+// any N and K; s_w [ceil(N/128), ceil(K/128)].  Load-time / per-expert use.
+__global__ void fp8_block_dequant_kernel(const uint8_t* __restrict__ w, const float* __restrict__ s_w,
+                                         float* __restrict__ out, int64_t N, int64_t K) {
+  const int64_t n_el = N * K, KB = (K + 127) / 128;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_el; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / K, k = i - n * K;
+    out[i] = fp8_e4m3_to_f32(w[i]) * s_w[(n >> 7) * KB + (k >> 7)];
+  }
+}
+
 // ------------------------------------------------------ grouped GEMM --
 // Persistent grouped GEMM on v_mfma_f32_32x32x64_f8f6f4, the FP8 form of the
 // int4 kernel in ccq_w4.hip: one workgroup of 8 waves per compute unit walks
@@ -584,6 +596,17 @@ extern "C" int ccq_fp8_block_unpack(const uint8_t* tiled, uint8_t* w, int64_t N,
   hipLaunchKernelGGL(fp8_unpack_kernel, dim3(grid_of(N * K / 16, 256)), dim3(256), 0, as_stream(stream), tiled, w,
                      N, K);
   return launch_status("ccq_fp8_block_unpack");
+}
+
+extern "C" int ccq_fp8_block_dequant(const uint8_t* w, const float* s_w, float* out, int64_t N, int64_t K,
+                                     void* stream) {
+  CCQ_REQUIRE(N >= 0 && K >= 0, "ccq_fp8_block_dequant: negative shape");
+  CCQ_REQUIRE(N == 0 || K <= INT64_MAX / N, "ccq_fp8_block_dequant: N*K overflows");
+  if (N == 0 || K == 0) return 0;
+  CCQ_REQUIRE(w && s_w && out, "ccq_fp8_block_dequant: null pointer");
+  hipLaunchKernelGGL(fp8_block_dequant_kernel, dim3(grid_of(N * K, 256)), dim3(256), 0, as_stream(stream), w, s_w,
+                     out, N, K);
+  return launch_status("ccq_fp8_block_dequant");
 }
 
 namespace {

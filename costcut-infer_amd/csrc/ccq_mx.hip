@@ -99,8 +99,15 @@ __global__ __launch_bounds__(256) void mx_linear_f32_kernel(const float* __restr
 // all have a zero low byte), then v_cvt_f32_f16; FP8 through the hardware
 // e4m3fn converter (v_cvt_pk_f32_fp8).  The E8M0 scale (a power of two, 0
 // or NaN) multiplies each group's partial sum once; NVFP4's second scale
-// multiplies the row's sum.  Both are exact rescalings of the terms, so only
-// the order of the float32 additions differs from x @ W.T.
+// multiplies the row's sum.  This is not the reference's arithmetic, which
+// forms W = (lut * s) * scale2 per weight and then multiplies: a
+// power-of-two s rescales every term exactly only while products stay
+// normal (near e8m0 1 the subnormal roundings differ; at e8m0 254 the
+// reference's W can overflow to inf, and a zero activation times inf gives
+// NaN where the kernel gives 0), and scale2 is an arbitrary float32, so
+// applying it once to the sum rounds differently from applying it to each
+// weight.  Both differences are within float32 summation-order tolerance
+// for finite, normal-range scales.
 constexpr int kMxRPW = 4;
 
 typedef _Float16 mx_h2 __attribute__((ext_vector_type(2)));

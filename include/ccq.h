@@ -418,6 +418,14 @@ int ccq_fp8_block_repack(const uint8_t* w, uint8_t* tiled, int64_t N, int64_t K,
 int ccq_fp8_block_unpack(const uint8_t* tiled, uint8_t* w, int64_t N, int64_t K,
                          void* stream);
 
+/* out [N, K] f32 = fp8(w[n, k]) * s_w[n/128, k/128] (one float32
+ * rounding), any N, K; s_w [ceil(N/128), ceil(K/128)].  The per-expert
+ * weight-unpack stage of ExpertReader._fill / _dequant_seg
+ * (experts/reader.py:142-251) for block-scaled FP8 checkpoints
+ * (weight_scale_inv), whose per-row form is ccq_fp8_dequant. */
+int ccq_fp8_block_dequant(const uint8_t* w, const float* s_w, float* out, int64_t N, int64_t K,
+                          void* stream);
+
 /* Workspace of ccq_fp8_block_linear (the quantized activations). */
 size_t ccq_fp8_block_linear_workspace_size(int64_t M, int64_t K);
 

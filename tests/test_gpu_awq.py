@@ -133,7 +133,12 @@ def test_weight_only_method_awq(gpu):
     y = m.apply(qw, scales, x)
     assert isinstance(y, np.ndarray) and y.shape == (3, N) and y.dtype == np.float32
     ref = oawq.linear(x, qw, qz, s, G)
-    # x enters the MFMA as fp16 (one rounding of the float32 input)
+    # x enters the MFMA as bf16 (one rounding of the float32 input)
     assert np.abs(y - ref).max() <= TOL * np.abs(ref).max()
     y2 = m.apply(qw, scales, x)  # second call reuses the prepared weights
     assert np.array_equal(y, y2)
+    # activations past the float16 range stay finite (bf16 keeps float32's range)
+    xb = x * np.float32(1e6)
+    yb = m.apply(qw, scales, xb)
+    refb = oawq.linear(xb, qw, qz, s, G)
+    assert np.isfinite(yb).all() and np.abs(yb - refb).max() <= TOL * np.abs(refb).max()

@@ -1,7 +1,8 @@
 """ExpertReader (reference python/ccut/experts/reader.py:86-340) on the GPU:
-slots bit-identical to the oracle's dequant of the checkpoint segments,
-ring reuse, prefetch and timeouts; ExpertPipeline over a reader, per-expert
-(FP8 per-row) and fused (AWQ layer) paths, against the oracle."""
+slots bit-identical to the oracle's dequant of the checkpoint segments (in
+expert_ffn's [in, out] orientation), ring reuse, prefetch and timeouts;
+ExpertPipeline over a reader, per-expert (FP8 per-row) and fused (AWQ
+layer) paths, against the oracle."""
 
 from __future__ import annotations
 
@@ -31,10 +32,10 @@ def test_fp8_slots_bitexact_and_ring(gpu, tmp_path):
         for e in range(3):
             g, u, d = r.get(1, e, timeout=30.0)
             for proj, got in (("gate", g), ("up", u), ("down", d)):
-                codes, scale = ref[(1, e, proj)]
+                codes, scale = ref[(1, e, proj)]  # [out, in] as the checkpoint stores it
                 assert got.is_cuda and got.dtype == torch.float32
                 assert np.array_equal(got.cpu().numpy().view(np.uint32),
-                                      orq.fp8_dequant_mat(codes, scale).view(np.uint32))
+                                      orq.fp8_dequant_mat(codes, scale).T.view(np.uint32))
         # two slots: expert 0 of layer 1 was refilled away, 1 and 2 are ready
         assert r.rings[1].find(0) is None and r.rings[1].find(2) is not None
         st = r.stats()
@@ -58,22 +59,26 @@ def test_unreadable_segment_times_out(gpu, tmp_path):
         r.index.entries[(0, 1)] = type(e)(e.shard, segs, e.shapes)
         with pytest.raises(TimeoutError, match="not supported"):
             r.get(0, 1, timeout=1.0)
-        assert r.get(0, 0)[0].shape == (32, 64)
+        assert r.get(0, 0)[0].shape == (64, 32)  # gate [hidden, inter]
     finally:
         r.close()
 
 
-def test_pipeline_over_fp8_reader(gpu, tmp_path):
-    """The reference's per-expert path with the reader's [out, in] slots fed
-    to expert_ffn as it does (hidden = the slots' row count)."""
+@pytest.mark.parametrize("H,I", [(2048, 512), (64, 64)])
+def test_pipeline_over_fp8_reader(gpu, tmp_path, H, I):
+    """The per-expert path over an FP8 per-row checkpoint with the Ornith
+    shapes (hidden 2048, expert intermediate 512: gate/up stored [512, 2048],
+    down [2048, 512]) and with hidden == inter, where a missing transpose
+    would go unnoticed by the shapes: y = sum_e w * down(silu(x Wg^T) *
+    (x Wu^T)) with W as stored, i.e. x @ W.T."""
     from ccut.experts import ExpertPipeline
 
-    ref = write_fp8(tmp_path, L=1, E=4, H=64, I=64)
+    ref = write_fp8(tmp_path, L=1, E=4, H=H, I=I)
     r = _reader(tmp_path, 1, 4)
     pipe = ExpertPipeline(r)
     rng = np.random.default_rng(3)
-    x = (rng.standard_normal((6, 64)) * 0.05).astype(np.float32)
-    gate_w = (rng.standard_normal((4, 64)) * 0.2).astype(np.float32)
+    x = (rng.standard_normal((6, H)) * 0.05).astype(np.float32)
+    gate_w = (rng.standard_normal((4, H)) * 0.2).astype(np.float32)
     try:
         y = pipe.step(0, x, gate_w, top_k=2)
     finally:
@@ -81,7 +86,13 @@ def test_pipeline_over_fp8_reader(gpu, tmp_path):
     logits = (torch.from_numpy(x).to(gpu) @ torch.from_numpy(gate_w).to(gpu).T).cpu().numpy()
     w0, ids0 = omoe.topk_softmax(logits, 2)
     W = {e: tuple(orq.fp8_dequant_mat(*ref[(0, e, p)]) for p in ("gate", "up", "down")) for e in range(4)}
-    yr = omoe.moe_combine(x, ids0, w0, W.__getitem__)
+    yr = np.zeros_like(x)
+    for t in range(x.shape[0]):
+        for s_ in range(2):
+            wg, wu, wd = W[int(ids0[t, s_])]       # [out, in] as stored
+            g, u = x[t] @ wg.T, x[t] @ wu.T
+            yr[t] += w0[t, s_] * ((g / (1.0 + np.exp(-g.astype(np.float64))) * u).astype(np.float32) @ wd.T)
+    assert y.shape == (6, H)
     assert np.abs(y - yr).max() <= 1e-4 * np.abs(yr).max()
     assert pipe.metrics.steps == 1 and pipe.metrics.ring_misses >= 1
 

@@ -132,3 +132,29 @@ def test_mx_linear_one_hot_is_exact(gpu, fmt, G):
     call("ccq_mx_linear_f32", xd.data_ptr(), rd.data_ptr(), sd.data_ptr(), y.data_ptr(), K, K, N, fmt, G, s2,
          _dev.stream_ptr())
     assert np.array_equal(y.cpu().numpy(), w.T)
+
+
+def test_mx_linear_scale_edges_documented(gpu):
+    """The fused MX linear applies the E8M0 scale to each group's partial
+    sum and NVFP4's scale2 to the row sum, where the reference multiplies
+    every weight.  A non-power-of-two scale2 stays within float32
+    summation tolerance of the per-weight product.  At E8M0 byte 254 the
+    reference's per-weight W = lut * 2^127 is still finite (1.5 * 2^127 is
+    below the float32 maximum), so zero activations give 0 on both sides."""
+    from ccut.quant.mx import mx_linear
+
+    rng = np.random.default_rng(21)
+    rows, cols, G = 8, 256, 16
+    packed = rng.integers(0, 256, (rows, cols // 2)).astype(np.uint8)
+    sc = rng.integers(118, 136, rows * cols // G).astype(np.uint8)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    s2 = np.float32(0.7371)  # not a power of two
+    y = mx_linear(torch.from_numpy(packed).to(gpu), torch.from_numpy(sc).to(gpu), torch.from_numpy(x).to(gpu),
+                  "nvfp4", G, s2).cpu().numpy()
+    w = omx.dequant_mxfp4(packed, sc, G, s2).astype(np.float64)
+    ref = x.astype(np.float64) @ w.T
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    hi = np.full(rows * cols // G, 254, dtype=np.uint8)
+    yz = mx_linear(torch.from_numpy(packed).to(gpu), torch.from_numpy(hi).to(gpu),
+                   torch.zeros((2, cols), device=gpu), "mxfp4", G).cpu().numpy()
+    assert np.all(yz == 0.0)

@@ -86,18 +86,56 @@ def test_step_per_expert_reader_matches_oracle(gpu):
     assert len(r.prefetched) == 3 and set(r.prefetched[1]) == set(ids0[0].tolist())
 
 
-def test_step_timeout_leaves_expert_out(gpu):
+def test_step_timeout_policies(gpu):
+    """A timed-out expert: "renormalize" (default) rescales each affected
+    token's surviving weights to the token's original weight sum, "drop"
+    leaves them as they are (the reference's code), "raise" re-raises; the
+    metrics count the timeouts and the assignments left out."""
     from ccut.experts import ExpertPipeline
 
     x, gate_w, W = _case(2)
     w0, ids0 = omoe.topk_softmax(_logits(gpu, x, gate_w), 4)
     slow = int(ids0[0, 0])
-    pipe = ExpertPipeline(_Reader(W, slow=[slow]), metrics_enabled=False)
-    y = pipe.step(0, x, gate_w, top_k=4)
     zero = tuple(np.zeros_like(a) for a in W[slow])
-    ref = omoe.moe_combine(x, ids0, w0, lambda e: zero if e == slow else W[e])  # contributes nothing
+    lookup = lambda e: zero if e == slow else W[e]  # noqa: E731
+    hit = ids0 == slow
+    # drop: the slow expert contributes nothing, other weights unchanged
+    pipe = ExpertPipeline(_Reader(W, slow=[slow]), metrics_enabled=False, on_expert_timeout="drop")
+    y = pipe.step(0, x, gate_w, top_k=4)
+    ref = omoe.moe_combine(x, ids0, w0, lookup)
     assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
     assert pipe.metrics is None
+    # renormalize: surviving weights of affected tokens scaled by sum / kept sum
+    pipe = ExpertPipeline(_Reader(W, slow=[slow]))
+    y = pipe.step(0, x, gate_w, top_k=4)
+    kept = np.where(hit, 0.0, w0).astype(np.float32)
+    scale = (w0.sum(axis=1, keepdims=True) / kept.sum(axis=1, keepdims=True)).astype(np.float32)
+    ref = omoe.moe_combine(x, ids0, (kept * scale).astype(np.float32), lookup)
+    assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
+    assert pipe.metrics.expert_timeouts == 1 and pipe.metrics.dropped_assignments == int(hit.sum())
+    assert pipe.metrics.to_dict()["expert_timeouts"] == 1
+    # a token whose only routed expert timed out keeps zeros (one slot)
+    w1, ids1 = omoe.topk_softmax(_logits(gpu, x, gate_w), 1)
+    pipe = ExpertPipeline(_Reader(W, slow=[int(ids1[0, 0])]))
+    y1 = pipe.step(0, x, gate_w, top_k=1)
+    assert np.all(y1[ids1[:, 0] == ids1[0, 0]] == 0.0) and np.isfinite(y1).all()
+    # raise
+    pipe = ExpertPipeline(_Reader(W, slow=[slow]), on_expert_timeout="raise")
+    with pytest.raises(TimeoutError):
+        pipe.step(0, x, gate_w, top_k=4)
+    with pytest.raises(ValueError):
+        ExpertPipeline(_Reader(W), on_expert_timeout="ignore")
+
+
+def test_step_rejects_wrongly_oriented_weights(gpu):
+    """Weights handed over [out, in] (the reference reader's slot layout) are
+    refused rather than multiplied the wrong way round."""
+    from ccut.experts import ExpertPipeline
+
+    x, gate_w, W = _case(4)
+    Wt = {e: tuple(a.T.copy() for a in w) for e, w in W.items()}
+    with pytest.raises(ValueError, match="expected gate/up"):
+        ExpertPipeline(_Reader(Wt)).step(0, x, gate_w, top_k=2)
 
 
 def test_step_shared_expert_device_io(gpu):

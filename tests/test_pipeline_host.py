@@ -25,7 +25,7 @@ def test_metrics_ratios_and_dict():
     d = m.to_dict()
     assert d["overlap_ratio"] == 0.25 and d["spec_accept_rate"] == 0.75
     assert set(d) == {"compute_ns", "prefetch_ns", "overlap_ns", "overlap_ratio", "steps", "spec_accept_rate",
-                      "ring_hits", "ring_misses"}
+                      "ring_hits", "ring_misses", "expert_timeouts", "dropped_assignments"}
 
 
 def test_kv_mode_and_bytes(tmp_path):
