@@ -4,27 +4,31 @@
 Headline workload: int4 (AWQ, group 128) MoE expert FFN decode -- 64 experts,
 top-6 routing from softmax of N(0,1) router logits over [T, 64], hidden 2048,
 expert intermediate 1408, bf16 activations, T = 16 tokens.  One step is one
-MoE layer: top-k softmax -> expert schedule -> gate/up (+SiLU*up) -> down ->
-weighted combine, replayed from a HIP graph.  Steps rotate over 4 distinct
-layer weight sets (1.15 GB) so the 256 MiB Infinity Cache cannot serve
-repeated weights.  ``value`` is algorithmic bytes (weights of the experts
-actually routed + activations) per second of wall time for whole steps, with
-inputs resident in HBM.
+MoE layer from router logits (ccq_moe_w4_forward): the gate/up + SiLU kernel
+that routes the batch inside its workgroups, the down kernel, the weighted
+combine, replayed from a HIP graph.  Steps rotate over 4 distinct layer
+weight sets (1.15 GB) so the 256 MiB Infinity Cache cannot serve repeated
+weights.  ``value`` is algorithmic bytes (weights of the experts actually
+routed + activations) per second of wall time for whole steps, with inputs
+resident in HBM.
 
-``roofline`` is the dominant kernel of the step (the fused gate/up + SiLU
-dequant-GEMM): algorithmic bytes per launch / its average device time.
-Kernel device times come from :func:`device_time`: a spin kernel holds the
-stream while the host enqueues all launches, so they run back to back and
-the HIP events on that stream bracket device time only.
+``roofline`` is the dominant kernel of the step, that same routed gate/up
+launch (ccq_moe_w4_route_gate_up runs exactly it): algorithmic bytes per
+launch / its average device time.  Kernel device times come from
+:func:`device_time`: a spin kernel holds the stream while the host enqueues
+all launches, so they run back to back and the HIP events on that stream
+bracket device time only.
 
-Also reported (``extra``): the same layer at T=1, the AWQ skinny GEMM at
-K=4096 N=14336 M in {1,4,16} and the single AWQ GEMV K=2048 N=5632 (kernel
-GB/s); the prefill workloads as TFLOP/s against the matching dense MFMA
-peak: int4 MoE prefill (128 experts, skewed top-8, hidden 2048, inter 768,
-T = 512 and 4096, bf16 MFMA) and FP8 block MoE prefill (256 experts, top-8,
-T = 2048, hidden 7168, inter 2048, FP8 MFMA).  ``cpu_baseline`` times the reference's algorithm (the CPU oracle:
-per-call dequant to float32, BLAS matmuls, per-expert grouping) on a
-bounded sample.
+Also reported (``extra``): the same layer at T=1 (20 rotating layers, > 512
+MiB of routed weights), the AWQ skinny GEMM at K=4096 N=14336 M in {1,4,16}
+and the single AWQ GEMV K=2048 N=5632 (kernel GB/s); the prefill workloads
+as TFLOP/s against the matching dense MFMA peak: int4 MoE prefill (128
+experts, skewed top-8, hidden 2048, inter 768, T = 512 and 4096, bf16 MFMA,
+4 rotating weight sets) and FP8 block MoE prefill (256 experts, top-8,
+T = 2048, hidden 7168, inter 2048, FP8 MFMA).  ``cpu_baseline`` times the
+reference's algorithm (the CPU oracle: dequant to float32, BLAS matmuls,
+per-expert grouping) on the host, per workload, in two variants: dequant on
+every call, and matmuls on cached float32 weights.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -50,13 +54,16 @@ PEAK_FP8 = 5.0332e15       # dense fp8 MFMA FLOP/s
 PEAK_INT8 = 5.0332e15      # dense int8 MFMA OP/s
 
 E, TOPK, HID, INTER, GROUP = 64, 6, 2048, 1408, 128
-# HBM bytes / algorithmic bytes of one decode gate/up launch, from rocprofv3
-# FETCH_SIZE (x 2.000) + WRITE_SIZE (x 1.000) on the torch-free driver
-# (47 routed experts: 145.23 MB moved for 141.16 MB algorithmic), the factors
-# calibrated on a 64 MiB streaming read and write; counters cannot be taken
-# inside this process, so the bench scales its own algorithmic bytes by it
+# HBM bytes / algorithmic bytes of the routed decode gate/up launch, from
+# rocprofv3 FETCH_SIZE and WRITE_SIZE runs of the same kernel on the
+# torch-free driver (costcut-infer_amd/drivers/moe_driver.cpp, mode w4f,
+# T=16), each scaled by the counter's reading for a 64 MiB streaming copy
+# (profiles/moe_decode_int4_kernel_stats.md holds the table and commands);
+# counters cannot be taken inside this process, so the bench scales its own
+# algorithmic bytes by the measured ratio
 GATE_UP_TRAFFIC_RATIO = 1.029
 LAYERS = 4
+LAYERS_T1 = 20  # T=1 routes 6 experts (27 MB) per layer: 20 layers touch > 512 MiB
 METRIC = "int4 MoE decode GB/s (% HBM peak) + FP8/int4 prefill TFLOP/s (% MFMA peak)"
 
 
@@ -155,22 +162,23 @@ def moe_step_bytes(layer, x, T: int) -> tuple[int, int]:
     return uniq * layer.experts.bytes_per_expert + act, uniq
 
 
-def bench_moe(T: int, steps: int, warmup: int, dev):
-    """Whole MoE layer steps replayed from a HIP graph (wall time) plus the
-    device time of the gate/up kernel."""
+def bench_moe(T: int, steps: int, warmup: int, dev, n_layers: int = LAYERS):
+    """Whole MoE layer steps replayed from a HIP graph (wall time) over
+    ``n_layers`` distinct layers, plus the device time of the step's routed
+    gate/up kernel."""
     import torch
 
     from ccut import workloads as wl
     from ccut.blocks import moe
 
-    layers = [Layer(i, T, dev) for i in range(LAYERS)]
+    layers = [Layer(i, T, dev) for i in range(n_layers)]
     x = wl.activations(T, HID, seed=5, device=dev, dtype=torch.bfloat16)
-    ys = [torch.empty((T, HID), dtype=torch.bfloat16, device=dev) for _ in range(LAYERS)]
+    ys = [torch.empty((T, HID), dtype=torch.bfloat16, device=dev) for _ in range(n_layers)]
     per = [moe_step_bytes(l, x, T) for l in layers]
 
     def step(i):
-        l = layers[i % LAYERS]
-        moe.moe_forward_w4(x, l.logits, l.experts, TOPK, True, out=ys[i % LAYERS])
+        l = layers[i % n_layers]
+        moe.moe_forward_w4(x, l.logits, l.experts, TOPK, True, out=ys[i % n_layers])
 
     for i in range(warmup):
         step(i)
@@ -178,61 +186,64 @@ def bench_moe(T: int, steps: int, warmup: int, dev):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for i in range(LAYERS):
+        for i in range(n_layers):
             step(i)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for i in range(LAYERS):
+        for i in range(n_layers):
             step(i)
     graph.replay()
     torch.cuda.synchronize()
-    reps = max(1, steps // LAYERS)
-    n_steps = reps * LAYERS
+    reps = max(1, steps // n_layers)
+    n_steps = reps * n_layers
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):
         graph.replay()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    total_bytes = sum(per[i % LAYERS][0] for i in range(n_steps))
+    total_bytes = sum(per[i % n_layers][0] for i in range(n_steps))
     return {
-        "T": T, "steps": n_steps, "ms_per_step": dt / n_steps * 1e3, "GBps": total_bytes / dt / 1e9,
-        "unique_experts": [p[1] for p in per], "bytes_per_step": [p[0] for p in per],
+        "T": T, "steps": n_steps, "layers": n_layers, "ms_per_step": dt / n_steps * 1e3,
+        "GBps": total_bytes / dt / 1e9, "unique_experts": [p[1] for p in per],
+        "bytes_per_step": [p[0] for p in per], "distinct_bytes": sum(p[0] for p in per),
         "gate_up": time_gate_up(layers, x, T, dev),
     }
 
 
 def time_gate_up(layers, x, T: int, dev):
-    """Device time of the gate/up + SiLU kernel (ccq_moe_w4_gate_up), the
-    dominant kernel of the step, rotating over the layers.  Algorithmic bytes
-    per launch: gate and up weights (int4 + fp16 scales + int4 zeros) of the
-    routed experts, the activations read and the intermediate written."""
+    """Device time of the step's gate/up + SiLU kernel with the routing
+    inside its workgroups (ccq_moe_w4_route_gate_up: the first launch of
+    ccq_moe_w4_forward), rotating over the layers.  Algorithmic bytes per
+    launch: gate and up weights (int4 + fp16 scales + int4 zeros) of the
+    routed experts, the router logits and activations read, the routing and
+    the intermediate written."""
     import torch
 
-    from ccut import _lib
+    from ccut import _dev, _lib
     from ccut.blocks import moe
 
     lib = _lib.lib()
-    mt = lib.ccq_moe_align_max_tiles(T * TOPK, E, 16)
     stream = torch.cuda.current_stream().cuda_stream
     launches, gu_bytes, keep = [], [], []
     for l in layers:
         _, ids = moe.topk_softmax(l.logits, TOPK, True)
-        sch = moe.moe_align(ids, E, 16)
         desc = l.experts.descriptor()
-        inter = torch.empty((T * TOPK, INTER), dtype=torch.bfloat16, device=dev)
-        keep.append((sch, desc, inter))
+        nbytes = lib.ccq_moe_w4_workspace_size(T, TOPK, ctypes.byref(desc))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        keep.append((desc, ws))
         uniq = int(torch.unique(ids).numel())
-        gu_bytes.append(uniq * l.experts.gate_up_bytes_per_expert + x.numel() * 2 + T * TOPK * INTER * 2)
-        args = (ctypes.c_void_p(x.data_ptr()), 2, TOPK, ctypes.c_void_p(sch.sorted_ids.data_ptr()),
-                ctypes.c_void_p(sch.tile_expert.data_ptr()), ctypes.c_void_p(sch.meta.data_ptr()), mt,
-                ctypes.c_void_p(inter.data_ptr()), ctypes.byref(desc), ctypes.c_void_p(stream))
-        launches.append(lambda a=args: lib.ccq_moe_w4_gate_up(*a))
+        gu_bytes.append(uniq * l.experts.gate_up_bytes_per_expert + x.numel() * 2 + l.logits.numel() * 4
+                        + T * TOPK * (8 + 4) + T * TOPK * INTER * 2)
+        args = (ctypes.c_void_p(x.data_ptr()), _dev.DTYPE_CODE[x.dtype], ctypes.c_void_p(l.logits.data_ptr()), T,
+                TOPK, 1, None, None, ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), nbytes,
+                ctypes.c_void_p(stream))
+        launches.append(lambda a=args: lib.ccq_moe_w4_route_gate_up(*a))
     for f in launches:
-        _lib.check(f(), "ccq_moe_w4_gate_up")
+        _lib.check(f(), "ccq_moe_w4_route_gate_up")
     torch.cuda.synchronize()
-    avg = device_time(launches, reps=25)
+    avg = device_time(launches, reps=max(1, 100 // len(launches)))
     avg_bytes = sum(gu_bytes) / len(gu_bytes)
     return {"avg_us": avg * 1e6, "bytes": avg_bytes, "GBps": avg_bytes / avg / 1e9}
 
@@ -375,33 +386,41 @@ def bench_mx(fmt: str, M: int, K: int, N: int, dev, copies: int = 6):
     return {"avg_us": avg * 1e6, "bytes": nb, "GBps": nb / avg / 1e9, "frac_hbm": nb / avg / PEAK_HBM}
 
 
-def bench_int4_prefill(T: int, dev):
+def bench_int4_prefill(T: int, dev, sets: int = 4):
     """int4 (AWQ g128) MoE prefill layer: 128 experts, top-8 of a skewed
     router (logits N(0,1) + per-expert bias N(0,2)), hidden 2048, inter 768,
     bf16 activations; device time of whole ccq_moe_w4_ffn calls (align,
-    grouped gate/up + SiLU, grouped down, combine) after routing."""
+    grouped gate/up + SiLU, grouped down, combine) after routing, rotating
+    over ``sets`` distinct weight sets (each routed set is 157-189 MB, so 4
+    sets exceed the 256 MiB Infinity Cache)."""
     import torch
 
     from ccut import workloads as wl
     from ccut.blocks import moe
 
     Ep, Hp, Ip, k = 128, 2048, 768, 8
-    ex = moe.W4Experts.from_awq(wl.awq_experts(Ep, Hp, Ip, GROUP, seed=71, device=dev),
-                                wl.awq_experts(Ep, Hp, Ip, GROUP, seed=72, device=dev),
-                                wl.awq_experts(Ep, Ip, Hp, GROUP, seed=73, device=dev), GROUP)
+    exs = [moe.W4Experts.from_awq(wl.awq_experts(Ep, Hp, Ip, GROUP, seed=71 + 10 * i, device=dev),
+                                  wl.awq_experts(Ep, Hp, Ip, GROUP, seed=72 + 10 * i, device=dev),
+                                  wl.awq_experts(Ep, Ip, Hp, GROUP, seed=73 + 10 * i, device=dev), GROUP)
+           for i in range(sets)]
     x = wl.activations(T, Hp, seed=74, device=dev)
     lg = wl.router_logits(T, Ep, seed=75, device=dev, skew_std=2.0)
     w, ids = moe.topk_softmax(lg, k, True)
-    moe.moe_ffn_w4(x, ids, w, ex)
+    for ex in exs:
+        moe.moe_ffn_w4(x, ids, w, ex)
     torch.cuda.synchronize()
-    t = device_time([lambda: moe.moe_ffn_w4(x, ids, w, ex)], reps=10)
+    t = device_time([lambda ex=ex: moe.moe_ffn_w4(x, ids, w, ex) for ex in exs], reps=max(1, 12 // sets))
     uniq = int(torch.unique(ids).numel())
     flops = 2.0 * T * k * 3 * Hp * Ip
-    nbytes = uniq * ex.bytes_per_expert + T * Hp * 2 * 2
+    nbytes = uniq * exs[0].bytes_per_expert + T * Hp * 2 * 2
     counts = torch.bincount(ids.reshape(-1), minlength=Ep)
-    return {"T": T, "us": t * 1e6, "TFLOPs": flops / t / 1e12, "frac_bf16_peak": flops / t / PEAK_BF16,
-            "GBps": nbytes / t / 1e9, "frac_hbm": nbytes / t / PEAK_HBM, "experts_routed": uniq,
-            "max_expert_rows": int(counts.max()), "min_expert_rows": int(counts.min())}
+    res = {"T": T, "us": t * 1e6, "TFLOPs": flops / t / 1e12, "frac_bf16_peak": flops / t / PEAK_BF16,
+           "GBps": nbytes / t / 1e9, "frac_hbm": nbytes / t / PEAK_HBM, "experts_routed": uniq,
+           "max_expert_rows": int(counts.max()), "min_expert_rows": int(counts.min()), "weight_sets": sets,
+           "distinct_routed_bytes": sets * uniq * exs[0].bytes_per_expert}
+    del exs
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_fp8_prefill(dev, T: int = 2048):
@@ -438,48 +457,177 @@ def bench_fp8_prefill(dev, T: int = 2048):
     return res
 
 
-def cpu_baseline(T: int, budget_s: float = 20.0):
-    """The reference algorithm on the host: per-call dequant of each routed
-    expert to float32 + BLAS matmuls + per-expert grouping (oracle)."""
+# ---------------------------------------------------------- CPU baseline --
+def _median_s(fn, runs: int = 5) -> float:
+    """Median wall seconds of ``runs`` calls after one warmup call."""
+    import statistics
+
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _combine_subset(omoe, x, ids, w, lookup):
+    """moe_combine over the assignments with an expert id >= 0 (the oracle's
+    grouping and float32 weighted sum; -1 marks an assignment left out)."""
     import numpy as np
 
+    out = np.zeros_like(x)
+    for eid, toks in omoe.expert_order(ids).items():
+        if eid < 0:
+            continue
+        wg, wu, wd = lookup(eid)
+        y = omoe.expert_ffn(x[np.array(toks, dtype=np.int64)], wg, wu, wd)
+        for i, t in enumerate(toks):
+            out[t] += w[t, list(ids[t]).index(eid)] * y[i]
+    return out
+
+
+def cpu_baselines(runs: int = 5) -> dict:
+    """The reference's algorithm on the host for every workload, in two
+    variants: (i) ``dequant`` -- every call dequantizes the weights it uses to
+    float32 and multiplies (WeightOnlyMethod.apply / expert_ffn on freshly
+    dequantized experts, quant/weight_only.py:37-54, blocks/moe.py:122-174);
+    (ii) ``cached`` -- float32 weights dequantized once, matmuls only (the
+    LinearProj cache, models/generic.py:137-161).  The oracle's numpy
+    restatement (kind "port"), BLAS and the per-expert dequants on all
+    threads of this process's CPU affinity; median of ``runs`` after one
+    warmup.  Expert weights come from a small pool of distinct experts reused
+    by id (the work per call does not depend on which expert it is).  The
+    FP8 layer is timed on its first 4 routed experts and extrapolated by
+    assignment count (labelled), so is the int4 layer at T=4096 (its first
+    8192 assignments)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
     from oracle import awq as oawq
+    from oracle import fp8_block as ofb
     from oracle import moe as omoe
+    from oracle.ref_quant import silu_mul_fused
 
+    cores = len(os.sched_getaffinity(0))
+    os.environ["OMP_NUM_THREADS"] = str(cores)
+    torch.set_num_threads(cores)
     rng = np.random.default_rng(3)
+    out = {}
+    pool = ThreadPoolExecutor(max_workers=cores)
 
-    def mk(K, N):
+    def awq_mat(K, N):
         q = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
         z = rng.integers(0, 16, size=(K // GROUP, N), dtype=np.uint8)
         s = (np.abs(rng.standard_normal((K // GROUP, N))) * 0.01 + 1e-3).astype(np.float16)
         return oawq.pack(q), oawq.pack(z), s
 
-    # a bounded pool of distinct experts reused across ids (the dequant work per
-    # call is what the reference does; which expert it is does not matter)
-    pool = [(mk(HID, INTER), mk(HID, INTER), mk(INTER, HID)) for _ in range(8)]
+    def entry(name, nbytes, flops, t_dequant, t_cached, sample, extrapolated=False):
+        out[name] = {"dequant": {"s": t_dequant, "GBps": nbytes / t_dequant / 1e9, "TFLOPs": flops / t_dequant / 1e12},
+                     "cached": {"s": t_cached, "GBps": nbytes / t_cached / 1e9, "TFLOPs": flops / t_cached / 1e12},
+                     "bytes": nbytes, "flops": flops, "cores": cores, "kind": "port", "sample": sample,
+                     "extrapolated": extrapolated}
 
-    def lookup(e):
-        g, u, d = pool[e % len(pool)]
-        return (oawq.dequant(*g, GROUP), oawq.dequant(*u, GROUP), oawq.dequant(*d, GROUP))
+    with threadpool_limits(cores):
+        # single AWQ linears: GEMV K=2048 N=5632 and the skinny GEMM K=4096 N=14336
+        for (M, K, N, name) in ((1, 2048, 5632, "awq_gemv_k2048_n5632"), (1, 4096, 14336, "awq_gemm_k4096_n14336_m1"),
+                                (4, 4096, 14336, "awq_gemm_k4096_n14336_m4"),
+                                (16, 4096, 14336, "awq_gemm_k4096_n14336_m16")):
+            qw, qz, s = awq_mat(K, N)
+            x = rng.standard_normal((M, K)).astype(np.float32)
+            W = oawq.dequant(qw, qz, s, GROUP)
+            chunks = [(r, min(K, r + 8 * GROUP)) for r in range(0, K, 8 * GROUP)]
 
-    x = rng.standard_normal((T, HID)).astype(np.float32)
-    steps, t0, nbytes = 0, time.perf_counter(), 0
-    per_expert = 3 * (HID * INTER // 2 + (HID // GROUP) * INTER * 2 + (HID // GROUP) * INTER // 2)
-    while True:
-        lg = rng.standard_normal((T, E)).astype(np.float32)
-        w, ids = omoe.topk_softmax(lg, TOPK)
-        omoe.moe_combine(x, ids, w, lookup)
-        nbytes += len(np.unique(ids)) * per_expert + x.nbytes
-        steps += 1
-        if time.perf_counter() - t0 > budget_s or steps >= 64:
-            break
-    dt = time.perf_counter() - t0
-    cores = len(os.sched_getaffinity(0))
-    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{steps} MoE decode steps at T={T} (64 experts, top-6, H=2048, I=1408, AWQ g128): "
-                      f"numpy oracle, per-call dequant to float32 + BLAS, {dt:.1f} s; BLAS may use all {cores} "
-                      f"cores, dequant is single-threaded",
-            "ms_per_step": dt / steps * 1e3}
+            def dequant_par():  # row blocks of 8 groups on the worker threads
+                parts = pool.map(lambda rc: oawq.dequant(qw[rc[0]:rc[1]], qz[rc[0] // GROUP:rc[1] // GROUP],
+                                                         s[rc[0] // GROUP:rc[1] // GROUP], GROUP), chunks)
+                return np.concatenate(list(parts), axis=0)
+
+            td = _median_s(lambda: x @ dequant_par(), runs)
+            tc = _median_s(lambda: x @ W, runs)
+            nb = K * N // 2 + (K // GROUP) * N * 2 + (K // GROUP) * N // 2 + M * (K + N) * 2
+            entry(name, nb, 2.0 * M * K * N, td, tc, f"x [{M}, {K}] @ W [{K}, {N}], one full call")
+        # int4 MoE layers (decode T=1, 16; prefill T=512, 4096): the routed
+        # experts in first-appearance order, up to max_a assignments of them
+        # (the rest extrapolated by assignment count)
+        for (T, Ep, Hp, Ip, k, skew, max_a, name) in ((16, E, HID, INTER, TOPK, 0.0, None, "moe_decode_T16"),
+                                                      (1, E, HID, INTER, TOPK, 0.0, None, "moe_decode_T1"),
+                                                      (512, 128, 2048, 768, 8, 2.0, None, "int4_moe_prefill_T512"),
+                                                      (4096, 128, 2048, 768, 8, 2.0, 8192,
+                                                       "int4_moe_prefill_T4096")):
+            P = 4
+            experts = [(awq_mat(Hp, Ip), awq_mat(Hp, Ip), awq_mat(Ip, Hp)) for _ in range(P)]
+            cached = {e: tuple(oawq.dequant(*m, GROUP) for m in experts[e]) for e in range(P)}
+            x = rng.standard_normal((T, Hp)).astype(np.float32)
+            lg = rng.standard_normal((T, Ep)).astype(np.float32)
+            if skew:
+                lg = lg + rng.standard_normal((1, Ep)).astype(np.float32) * skew
+            w, ids = omoe.topk_softmax(lg, k)
+            order = omoe.expert_order(ids)
+            routed, n_sub = [], 0
+            for e, toks in order.items():
+                if max_a is not None and n_sub >= max_a:
+                    break
+                routed.append(e)
+                n_sub += len(toks)
+            keep = np.isin(ids, routed)
+            ids_s = np.where(keep, ids, -1)  # assignments outside the subset: no expert (contribute nothing)
+
+            def lookup_of(mats):
+                return lambda e: mats[e]
+
+            def per_call():
+                mats = dict(zip(routed, pool.map(lambda e: tuple(oawq.dequant(*m, GROUP) for m in experts[e % P]),
+                                                 routed)))
+                return _combine_subset(omoe, x, ids_s, w, lookup_of(mats))
+
+            td = _median_s(per_call, runs)
+            tc = _median_s(lambda: _combine_subset(omoe, x, ids_s, w, lambda e: cached[e % P]), runs)
+            scale = T * k / n_sub
+            per_expert = 2 * (Hp * Ip // 2 + (Hp // GROUP) * Ip * 2 + (Hp // GROUP) * Ip // 2) + \
+                (Ip * Hp // 2 + (Ip // GROUP) * Hp * 2 + (Ip // GROUP) * Hp // 2)
+            nb = len(order) * per_expert + T * Hp * 2 * 2
+            sample = f"top-{k} of {Ep} experts, {len(order)} routed, T={T}, H={Hp}, I={Ip}: "
+            sample += "the whole layer" if scale == 1 else \
+                f"{len(routed)} experts ({n_sub} of {T * k} assignments) timed, x {scale:.2f} by assignment count"
+            entry(name, nb, 2.0 * T * k * 3 * Hp * Ip, td * scale, tc * scale, sample, extrapolated=scale != 1)
+        # FP8 block MoE prefill: 4 routed experts timed, extrapolated by assignments
+        Ep, Hp, Ip, T, k = 256, 7168, 2048, 2048, 8
+        lg = rng.standard_normal((T, Ep)).astype(np.float32)
+        w, ids = omoe.topk_softmax(lg, k)
+        order = omoe.expert_order(ids)
+        sub = list(order)[:4]
+        n_sub = sum(len(order[e]) for e in sub)
+        x = rng.standard_normal((T, Hp)).astype(np.float32)
+        P = 4
+
+        def fp8_mat(N, K):
+            return (rng.integers(0, 0x7E, size=(N, K), dtype=np.uint8),
+                    (np.abs(rng.standard_normal((N // 128, K // 128))) * 0.01 + 1e-3).astype(np.float32))
+
+        fexp = [(fp8_mat(Ip, Hp), fp8_mat(Ip, Hp), fp8_mat(Hp, Ip)) for _ in range(P)]
+        fcached = {e: tuple(ofb.block_dequant(*m) for m in fexp[e]) for e in range(P)}
+
+        def fp8_layer(deq):
+            mats = dict(zip(sub, pool.map(lambda e: deq(e % P), sub)))
+            for e in sub:
+                rows = np.asarray(order[e])
+                xq = ofb.act_dequant(*ofb.act_quant(x[rows]))
+                g, u, d = mats[e]
+                silu_mul_fused(xq @ g.T, xq @ u.T) @ d.T
+
+        td = _median_s(lambda: fp8_layer(lambda i: tuple(ofb.block_dequant(*m) for m in fexp[i])), runs)
+        tc = _median_s(lambda: fp8_layer(lambda i: fcached[i]), runs)
+        scale = T * k / n_sub
+        nb = len(order) * (3 * Hp * Ip + 3 * (Hp // 128) * (Ip // 128) * 4) + T * Hp * 2 * 2
+        entry("fp8_moe_prefill_T2048", nb, 2.0 * T * k * 3 * Hp * Ip, td * scale, tc * scale,
+              f"4 of {len(order)} routed experts ({n_sub} of {T * k} assignments) timed, x {scale:.1f} by "
+              "assignment count", extrapolated=True)
+    pool.shutdown()
+    return out
 
 
 def main():
@@ -501,7 +649,7 @@ def main():
         f"gate/up kernel {gu['avg_us']:.2f} us = {gu['GBps']:.1f} GB/s")
     extra = {}
     if not args.no_extra:
-        t1 = bench_moe(1, args.steps, args.warmup, dev)
+        t1 = bench_moe(1, args.steps, args.warmup, dev, n_layers=LAYERS_T1)
         extra["moe_decode_T1"] = t1
         log(f"moe decode T=1: {t1['GBps']:.1f} GB/s, {t1['ms_per_step'] * 1e3:.1f} us/step; gate/up kernel "
             f"{t1['gate_up']['avg_us']:.2f} us = {t1['gate_up']['GBps']:.1f} GB/s")
@@ -534,7 +682,20 @@ def main():
         extra["fp8_moe_prefill_T2048"] = r
         log(f"fp8 block MoE prefill T=2048: {r['us']:.1f} us, {r['TFLOPs']:.1f} TFLOP/s ({r['frac_fp8_peak']:.3f} "
             f"of fp8 peak, {r['frac_roofline']:.3f} of its HBM roofline), {r['GBps']:.0f} GB/s")
-    cpu = None if args.no_cpu else cpu_baseline(args.tokens)
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baselines (the reference algorithm on the host)")
+        cpus = cpu_baselines()
+        extra["cpu_baselines"] = cpus
+        hd = cpus[f"moe_decode_T{args.tokens}"] if f"moe_decode_T{args.tokens}" in cpus else cpus["moe_decode_T16"]
+        cpu = {"value": round(hd["dequant"]["GBps"], 4), "unit": "GB/s", "cores": hd["cores"], "kind": "port",
+               "sample": "the MoE decode layer (64 experts, top-6, H=2048, I=1408, AWQ g128, T=16): numpy oracle, "
+                         "per-call dequant of every routed expert to float32 (parallel over experts) + BLAS "
+                         f"matmuls + per-expert grouping, median of 5 after a warmup, {hd['cores']} threads",
+               "cached_fp32_value": round(hd["cached"]["GBps"], 4)}
+        for name, r in cpus.items():
+            log(f"cpu {name}: dequant {r['dequant']['s'] * 1e3:.1f} ms, cached {r['cached']['s'] * 1e3:.1f} ms"
+                + (" (extrapolated)" if r["extrapolated"] else ""))
     out = {
         "metric": METRIC,
         "value": round(head["GBps"], 2),
@@ -553,7 +714,8 @@ def main():
                    "tokens": args.tokens, "experts": E, "top_k": TOPK, "hidden": HID, "inter": INTER,
                    "group": GROUP, "hip_graph": True},
         "frac_hbm_peak": round(head["GBps"] * 1e9 / PEAK_HBM, 4),
-        "roofline": {"bound": "hbm", "kernel": "w4_stream_kernel<bf16,f16,SiLU,MT=2,NQ=2> (MoE gate/up)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "w4_stream_kernel<bf16,f16,SiLU,MT=2,NQ=2,ROUTE=1> (MoE gate/up, routed in-kernel)",
                      "achieved": round(gu["GBps"], 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": round(gu["GBps"] * 1e9 / PEAK_HBM, 4), "avg_us": round(gu["avg_us"], 3),
                      "algorithmic_bytes": round(gu["bytes"]),

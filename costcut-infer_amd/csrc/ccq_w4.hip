@@ -2049,45 +2049,39 @@ static bool fused_route(const MoeLayout& L, const ccq_w4_experts* ex, int64_t k)
          L.max_tiles <= RT_MAXTILES;
 }
 
-extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k, int mode,
-                                  int64_t* ids_out, float* weights_out, void* y, int y_dtype,
-                                  const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_experts(ex, "ccq_moe_w4_forward");
+// Argument checks shared by ccq_moe_w4_forward and its routed gate/up stage
+// (y is not used by the stage).
+static int check_forward_args(const char* name, const void* x, int x_dtype, const float* logits, int64_t T,
+                              int64_t k, int mode, const void* y, int y_dtype, const ccq_w4_experts* ex,
+                              void* workspace, size_t workspace_bytes, bool need_y) {
+  int rc = check_experts(ex, name);
   if (rc) return rc;
-  CCQ_REQUIRE(T >= 0 && k >= 1 && k <= 16 && k <= ex->num_experts, "ccq_moe_w4_forward: bad T=%lld / k=%lld",
-              (long long)T, (long long)k);
-  CCQ_REQUIRE(mode >= 0 && mode <= 4, "ccq_moe_w4_forward: mode=%d not in {0,1,2,3,4}", mode);
-  CCQ_REQUIRE(T * k <= 65536 && T <= 65535, "ccq_moe_w4_forward: T=%lld too large", (long long)T);
-  CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "ccq_moe_w4_forward: x_dtype must be f16|bf16");
-  CCQ_REQUIRE(y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "ccq_moe_w4_forward: bad y_dtype");
+  CCQ_REQUIRE(T >= 0 && k >= 1 && k <= 16 && k <= ex->num_experts, "%s: bad T=%lld / k=%lld", name, (long long)T,
+              (long long)k);
+  CCQ_REQUIRE(mode >= 0 && mode <= 4, "%s: mode=%d not in {0,1,2,3,4}", name, mode);
+  CCQ_REQUIRE(T * k <= 65536 && T <= 65535, "%s: T=%lld too large", name, (long long)T);
+  CCQ_REQUIRE(x_dtype == CCQ_F16 || x_dtype == CCQ_BF16, "%s: x_dtype must be f16|bf16", name);
+  CCQ_REQUIRE(!need_y || y_dtype == CCQ_F16 || y_dtype == CCQ_BF16 || y_dtype == CCQ_F32, "%s: bad y_dtype", name);
   if (T == 0) return 0;
-  CCQ_REQUIRE(x && logits && y, "ccq_moe_w4_forward: null pointer");
-  rc = check_expert_ptrs(ex, true, "ccq_moe_w4_forward");
+  CCQ_REQUIRE(x && logits && (y || !need_y), "%s: null pointer", name);
+  rc = check_expert_ptrs(ex, true, name);
   if (rc) return rc;
-  rc = check_expert_ptrs(ex, false, "ccq_moe_w4_forward");
+  rc = check_expert_ptrs(ex, false, name);
   if (rc) return rc;
-  CCQ_REQUIRE(aligned(x, 16), "ccq_moe_w4_forward: x must be 16-byte aligned");
+  CCQ_REQUIRE(aligned(x, 16), "%s: x must be 16-byte aligned", name);
   const MoeLayout L = moe_layout(T, k, ex, 2);
   CCQ_REQUIRE(workspace && workspace_bytes >= L.total && aligned(workspace, 256),
-              "ccq_moe_w4_forward: workspace of %zu bytes (256-byte aligned) needed, %zu given", L.total,
-              workspace_bytes);
-  hipStream_t st = as_stream(stream);
-  char* ws = (char*)workspace;
-  int64_t* ids = ids_out != nullptr ? ids_out : (int64_t*)(ws + L.off_ids);
-  float* wts = weights_out != nullptr ? weights_out : (float*)(ws + L.off_wts);
-  if (!fused_route(L, ex, k)) {  // separate routing kernel, then the FFN
-    rc = ccq_topk_softmax(logits, wts, ids, T, ex->num_experts, k, mode, stream);
-    if (rc) return rc;
-    return ccq_moe_w4_ffn(x, x_dtype, ids, wts, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream);
-  }
+              "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", name, L.total, workspace_bytes);
+  return 0;
+}
+
+// The routed gate/up launch of a decode batch: routing in every workgroup,
+// the schedule, ids and weights written by workgroup 0, the SiLU(gate)*up
+// intermediate into the workspace.
+static int launch_route_gate_up(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k, int mode,
+                                int64_t* ids, float* wts, const ccq_w4_experts* ex, char* ws, const MoeLayout& L,
+                                hipStream_t st) {
   const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
-  int32_t* sorted = (int32_t*)(ws + L.off_sorted);
-  int32_t* tile_expert = (int32_t*)(ws + L.off_tile_expert);
-  int32_t* meta = (int32_t*)(ws + L.off_meta);
-  int32_t* counts = (int32_t*)(ws + L.off_counts);
-  void* inter = ws + L.off_inter;
-  float* rows = (float*)(ws + L.off_rows);
-  // gate/up + SiLU with the routing done inside its workgroups
   W4SP w = {};
   w.x = x;
   w.ldx = H;
@@ -2099,7 +2093,7 @@ extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logit
   w.szw = (int)sz_words_per_column(H, G);
   w.w_es = H * I / 8;
   w.sz_es = I * w.szw;
-  w.y = inter;
+  w.y = ws + L.off_inter;
   w.ldy = I;
   w.y_dtype = x_dtype;
   w.N = (int)I;
@@ -2113,11 +2107,55 @@ extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logit
   w.rmode = mode;
   w.ids_out = ids;
   w.wts_out = wts;
-  w.sched_rows = sorted;
-  w.sched_tile_expert = tile_expert;
-  w.sched_meta = meta;
-  w.sched_counts = counts;
-  rc = launch_stream<EPI_SILU>(w, 2, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.max_tiles, st);
+  w.sched_rows = (int32_t*)(ws + L.off_sorted);
+  w.sched_tile_expert = (int32_t*)(ws + L.off_tile_expert);
+  w.sched_meta = (int32_t*)(ws + L.off_meta);
+  w.sched_counts = (int32_t*)(ws + L.off_counts);
+  return launch_stream<EPI_SILU>(w, 2, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.max_tiles, st);
+}
+
+extern "C" int ccq_moe_w4_route_gate_up(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
+                                        int mode, int64_t* ids_out, float* weights_out, const ccq_w4_experts* ex,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_forward_args("ccq_moe_w4_route_gate_up", x, x_dtype, logits, T, k, mode, nullptr, CCQ_F32, ex,
+                              workspace, workspace_bytes, false);
+  if (rc || T == 0) return rc;
+  const MoeLayout L = moe_layout(T, k, ex, 2);
+  if (!fused_route(L, ex, k)) {
+    set_error("ccq_moe_w4_route_gate_up: T=%lld, k=%lld is not a decode batch routed in the gate/up kernel",
+              (long long)T, (long long)k);
+    return CCQ_EUNSUPPORTED;
+  }
+  char* ws = (char*)workspace;
+  int64_t* ids = ids_out != nullptr ? ids_out : (int64_t*)(ws + L.off_ids);
+  float* wts = weights_out != nullptr ? weights_out : (float*)(ws + L.off_wts);
+  return launch_route_gate_up(x, x_dtype, logits, T, k, mode, ids, wts, ex, ws, L, as_stream(stream));
+}
+
+extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k, int mode,
+                                  int64_t* ids_out, float* weights_out, void* y, int y_dtype,
+                                  const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_forward_args("ccq_moe_w4_forward", x, x_dtype, logits, T, k, mode, y, y_dtype, ex, workspace,
+                              workspace_bytes, true);
+  if (rc || T == 0) return rc;
+  const MoeLayout L = moe_layout(T, k, ex, 2);
+  hipStream_t st = as_stream(stream);
+  char* ws = (char*)workspace;
+  int64_t* ids = ids_out != nullptr ? ids_out : (int64_t*)(ws + L.off_ids);
+  float* wts = weights_out != nullptr ? weights_out : (float*)(ws + L.off_wts);
+  if (!fused_route(L, ex, k)) {  // separate routing kernel, then the FFN
+    rc = ccq_topk_softmax(logits, wts, ids, T, ex->num_experts, k, mode, stream);
+    if (rc) return rc;
+    return ccq_moe_w4_ffn(x, x_dtype, ids, wts, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream);
+  }
+  const int64_t H = ex->hidden;
+  int32_t* sorted = (int32_t*)(ws + L.off_sorted);
+  int32_t* tile_expert = (int32_t*)(ws + L.off_tile_expert);
+  int32_t* meta = (int32_t*)(ws + L.off_meta);
+  void* inter = ws + L.off_inter;
+  float* rows = (float*)(ws + L.off_rows);
+  // gate/up + SiLU with the routing done inside its workgroups
+  rc = launch_route_gate_up(x, x_dtype, logits, T, k, mode, ids, wts, ex, ws, L, st);
   if (rc) return rc;
   rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
   if (rc) return rc;

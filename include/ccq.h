@@ -375,6 +375,18 @@ int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logits, int64_t 
                        const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/* The first of ccq_moe_w4_forward's three launches for a decode batch: the
+ * gate/up + SiLU kernel that routes the batch inside its workgroups, leaving
+ * the routing (ids_out / weights_out, or the workspace), the expert schedule
+ * and the intermediate in the workspace exactly as ccq_moe_w4_forward does
+ * before its down and combine launches.  Arguments as ccq_moe_w4_forward
+ * (no output); CCQ_EUNSUPPORTED for batches that ccq_moe_w4_forward routes
+ * with the separate routing kernel.  The stage the forward's routing and
+ * gate/up share with ccq_moe_w4_gate_up (experts/pipeline.py:145-170). */
+int ccq_moe_w4_route_gate_up(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
+                             int mode, int64_t* ids_out, float* weights_out, const ccq_w4_experts* ex,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of the per-GPU scratch array of ccq_moe_w4_forward_noalloc. */
 #define CCQ_MOE_W4_NOALLOC_BYTES (32u << 20)
 

@@ -291,3 +291,54 @@ def test_moe_combine_api_with_expert_fn(gpu):
     ref = omoe.moe_combine(x, ids, w, W.__getitem__)
     assert isinstance(y, np.ndarray)
     assert np.allclose(y, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_route_gate_up_stage_matches_forward(gpu):
+    """ccq_moe_w4_route_gate_up is the forward's first launch: the routing
+    and the expert schedule it leaves (ids, weights, the head of the
+    workspace) are bit-identical to those of ccq_moe_w4_forward; a batch the
+    forward routes with the separate routing kernel is refused."""
+    import ctypes
+
+    from ccut import _lib
+    from ccut._lib import CCQ_BF16, CCQ_EUNSUPPORTED, CCQ_F32
+    from ccut.blocks import moe
+
+    E, H, I, T, k = 64, 2048, 1408, 16, 6
+    gate, up, down = _experts(E, H, I, 128, seed=77)
+    dev = lambda t: tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(dev(gate), dev(up), dev(down), group_size=128)
+    desc = ex.descriptor()
+    lib = _lib.lib()
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16).to(gpu)
+    lg = torch.randn((T, E), generator=g).to(gpu)
+    nbytes = lib.ccq_moe_w4_workspace_size(T, k, ctypes.byref(desc))
+    outs = []
+    for stage in (True, False):
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+        ids = torch.full((T, k), -5, dtype=torch.int64, device=gpu)
+        w = torch.zeros((T, k), dtype=torch.float32, device=gpu)
+        st = torch.cuda.current_stream().cuda_stream
+        if stage:
+            rc = lib.ccq_moe_w4_route_gate_up(x.data_ptr(), CCQ_BF16, lg.data_ptr(), T, k, 1, ids.data_ptr(),
+                                              w.data_ptr(), ctypes.byref(desc), ws.data_ptr(), nbytes, st)
+        else:
+            y = torch.empty((T, H), dtype=torch.float32, device=gpu)
+            rc = lib.ccq_moe_w4_forward(x.data_ptr(), CCQ_BF16, lg.data_ptr(), T, k, 1, ids.data_ptr(), w.data_ptr(),
+                                        y.data_ptr(), CCQ_F32, ctypes.byref(desc), ws.data_ptr(), nbytes, st)
+        assert rc == 0, _lib.last_error()
+        outs.append((ids, w, ws))
+    torch.cuda.synchronize()
+    (ia, wa, sa), (ib, wb, sb) = outs
+    assert torch.equal(ia, ib) and torch.equal(wa.view(torch.int32), wb.view(torch.int32))
+    n_sched = lib.ccq_moe_align_max_tiles(T * k, E, 16) * 16 * 4  # sorted ids: the head of the workspace
+    assert torch.equal(sa[:n_sched], sb[:n_sched])
+    Tb = 200
+    nb = lib.ccq_moe_w4_workspace_size(Tb, k, ctypes.byref(desc))
+    wsb = torch.empty(nb, dtype=torch.uint8, device=gpu)
+    xb = torch.zeros((Tb, H), dtype=torch.bfloat16, device=gpu)
+    lgb = torch.zeros((Tb, E), device=gpu)
+    rc = lib.ccq_moe_w4_route_gate_up(xb.data_ptr(), CCQ_BF16, lgb.data_ptr(), Tb, k, 1, None, None,
+                                      ctypes.byref(desc), wsb.data_ptr(), nb, None)
+    assert rc == CCQ_EUNSUPPORTED and "decode batch" in _lib.last_error()
