@@ -41,6 +41,7 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
 
@@ -141,6 +142,36 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
+}
+
+// Global -> VGPR 16-byte load of p + OFF issued as inline assembly, so that
+// the compiler adds no wait of its own for it (it counts only the loads it
+// issues itself): the caller waits with wait_vmcnt_tied, whose "+v"
+// operands keep every use of the registers after that wait.  The address is
+// a VGPR pair; VMEM reads of VGPRs written by VALU need no wait states.
+// The load is marked non-temporal (nt): for data read once, such as weight
+// streams.
+template <int OFF>
+__device__ __forceinline__ void gload16_nt(u32x4& dst, const void* p) {
+  static_assert(OFF >= 0 && OFF < 4096, "13-bit signed immediate offset");
+  asm volatile("global_load_dwordx4 %0, %1, off offset:%2 nt" : "=v"(dst) : "v"(p), "n"(OFF));
+}
+
+// Lane id computed where it is used: the compiler cannot hoist inline
+// assembly out of a loop, so values derived from it are not kept live (in
+// registers or spilled) across the loop.
+__device__ __forceinline__ int lane_id_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// s_waitcnt vmcnt(N) that the compiler sees as producing the four register
+// quads of one gload16 batch.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_tied(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
 }
 
 // Wait until at most N vector-memory operations of this wave are in flight.

@@ -22,6 +22,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace ccq {
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
@@ -75,16 +77,30 @@ __global__ __launch_bounds__(256) void fp8_act_quant_kernel(const void* __restri
 }
 
 // ----------------------------------------------------------- re-pack --
-// One thread per 16-byte piece of the tiled layout (a contiguous 16 bytes of
-// one row of w).
+// Tiled layout: 2 KiB chunks, one per (16-column tile nt, K block kb), in
+// the order [nt / 8][kb][nt % 8]: the 8 tiles of a 128-column block are
+// contiguous at each K block (16 KiB), so a workgroup streaming a column
+// block reads one contiguous range per K block.  Inside a chunk, piece
+// 64 h + l (16 bytes) holds row nt*16 + (l & 15), k = kb*128 + 32 (l >> 4)
+// + 16 h.  One thread per piece.
+__device__ __forceinline__ void fp8_tiled_piece(int64_t i, int64_t KB, int64_t& n, int64_t& k) {
+  const int l = (int)(i & 63), h = (int)((i >> 6) & 1);
+  const int64_t chunk = i >> 7, t8 = chunk & 7, rest = chunk >> 3, kb = rest % KB, nt = (rest / KB) * 8 + t8;
+  n = nt * 16 + (l & 15);
+  k = kb * 128 + 32 * (l >> 4) + 16 * h;
+}
+// byte offset of chunk (nt, kb) in the tiled layout
+__host__ __device__ __forceinline__ int64_t fp8_chunk_off(int64_t nt, int64_t kb, int64_t KB) {
+  return (((nt >> 3) * KB + kb) * 8 + (nt & 7)) * 2048;
+}
+
 __global__ void fp8_repack_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ tiled, int64_t N,
                                   int64_t K) {
   const int64_t KB = K / 128, pieces = N * K / 16;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int l = (int)(i & 63), h = (int)((i >> 6) & 1);
-    const int64_t tile = i >> 7, kb = tile % KB, nt = tile / KB;
-    const int64_t n = nt * 16 + (l & 15), k = kb * 128 + 32 * (l >> 4) + 16 * h;
+    int64_t n, k;
+    fp8_tiled_piece(i, KB, n, k);
     *reinterpret_cast<u32x4*>(tiled + i * 16) = *reinterpret_cast<const u32x4*>(w + n * K + k);
   }
 }
@@ -94,9 +110,8 @@ __global__ void fp8_unpack_kernel(const uint8_t* __restrict__ tiled, uint8_t* __
   const int64_t KB = K / 128, pieces = N * K / 16;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pieces;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int l = (int)(i & 63), h = (int)((i >> 6) & 1);
-    const int64_t tile = i >> 7, kb = tile % KB, nt = tile / KB;
-    const int64_t n = nt * 16 + (l & 15), k = kb * 128 + 32 * (l >> 4) + 16 * h;
+    int64_t n, k;
+    fp8_tiled_piece(i, KB, n, k);
     *reinterpret_cast<u32x4*>(w + n * K + k) = *reinterpret_cast<const u32x4*>(tiled + i * 16);
   }
 }
@@ -188,6 +203,11 @@ __device__ __forceinline__ int f8_swz(int r) { return ((r >> 1) & 7) ^ ((r & 1) 
 
 __device__ __forceinline__ f32x16 mfma_f8_32(const i32x8& a, const i32x8& b, f32x16 c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// The same product with B scaled by 2^-4 inside the MFMA: E8M0 block scales
+// 127 (1.0) for A and 123 (2^-4) for B.
+__device__ __forceinline__ f32x16 mfma_f8_32_b16th(const i32x8& a, const i32x8& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 123);
 }
 
 template <int EPI, int CTW, bool LO = false>
@@ -281,7 +301,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
 #pragma unroll
     for (int b2 = 0; b2 < BPW; ++b2) {
       const int b = wave * BPW + b2, t = b >> 1, q = t / TPM, nt = P.nb * TPM + (t - q * TPM);
-      P.bsrc[b2] = (q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + (int64_t)nt * KB * 2048 + (b & 1) * 1024;
+      P.bsrc[b2] = (q == 0 ? p.w0 : p.w1) + (int64_t)ex * p.w_es + fp8_chunk_off(nt, 0, KB) + (b & 1) * 1024;
     }
     P.soff = 0;
     if (has_sa) {
@@ -312,7 +332,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
 #pragma unroll
     for (int b2 = 0; b2 < BPW; ++b2) {
       const int b = wave * BPW + b2;
-      dma16(P.bsrc[b2] + (int64_t)kb * 2048, lane * 16, st + F8_B_OFF + (b >> 1) * 2048 + (b & 1) * 1024);
+      dma16(P.bsrc[b2] + (int64_t)kb * 16384, lane * 16, st + F8_B_OFF + (b >> 1) * 2048 + (b & 1) * 1024);
     }
     if (has_sa) dma4(p.sa + kb, P.soff, st + F8_SA_OFF + (wave - 4) * 256);
     if (has_sw) dma4(P.swsrc + kb, 0u, st + F8_SW_OFF + (wave - 6) * 256);
@@ -504,6 +524,462 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   }
 }
 
+// ------------------------------------------ MoE stages, weights in VGPRs --
+// The MoE stages (F8_SILU_Q gate/up, F8_ROWS down with the high and low
+// intermediate parts) on the same persistent schedule, with the weights
+// streamed straight into registers.  A workgroup is RB_NW waves; wave w
+// owns RB_CG 32-column MFMA groups of every 128-row tile -- for gate/up,
+// gate columns nb*128 + 16(RB_CG w + cg) + c and the same up columns
+// (c = lane & 15, the up half in lanes 16..31); for down, columns
+// nb*256 + 32(RB_CG w + cg) + (lane & 31) -- and loads their 16-byte
+// weight slices itself, RB_D K blocks ahead (64 B per lane and K block:
+// 96 KiB of weights in flight per compute unit at RB_D = 3).  Only the activation tiles and their scales go through LDS, in a
+// ring of SA K blocks filled by LDS DMA; one barrier per K block.  Both the
+// copies and the weight loads are inline assembly sharing the wave's
+// in-order vmcnt (a compiler-issued load would be waited for by a count
+// that ignores the copies issued after it, draining the pipeline), and the
+// weight registers are handed to the compiler by a wait whose "+v" operands
+// are those registers.  Every wave issues the same number of memory
+// operations per K block (waves without a scale to copy copy one into a
+// pad), so all waits are fixed vmcnt values; the first steps wait for
+// more, and the steps past the end re-issue the last K block's loads so
+// that the counts stay exact.  All four row tiles of an item are computed
+// whatever its number of valid rows: MFMA time stays under the weight
+// stream's time at 128 rows.
+constexpr int RB_NW = 8;  // waves per workgroup
+constexpr int RB_CG = 1;  // 32-column MFMA groups per wave
+constexpr int RB_D = 3;   // K blocks of weight loads issued ahead per wave
+static_assert(RB_NW * RB_CG == 8, "256 columns (down) / 2 x 128 (gate/up) per item");
+static_assert(RB_CG == 1, "one register set of weight quads per K block and wait");
+
+template <bool LO>
+struct RbStage {
+  static constexpr int NA = LO ? 2 : 1;                  // activation parts
+  static constexpr int SA = LO ? 4 : 6;                  // activation ring stages
+  static constexpr int RPW = F8_BM / RB_NW;              // activation rows copied per wave (8 per copy)
+  static constexpr int A = F8_A_BYTES * NA;
+  static constexpr int SA_OFF = A;                       // s_a of the 128 rows
+  static constexpr int SW_OFF = SA_OFF + F8_BM * 4;      // 2 x 64 copies of a block scale
+  static constexpr int PAD_OFF = SW_OFF + 2 * 256;       // the copies of waves 4.. (count padding)
+  static constexpr int BYTES = PAD_OFF + (RB_NW > 4 ? (RB_NW - 4) * 256 : 0);
+  static constexpr int NB = 4 * RB_CG;                   // weight loads per wave and K block
+  static constexpr int A_OPS = NA * RPW / 8 + 1;        // activation + scale copies per wave and K block
+  static constexpr int N_OPS = A_OPS + NB;               // memory operations per wave and K block
+  // vmcnt allowed in steady state while waiting for the activation stage of
+  // step g (copied at step g - SA + 1, followed by that step's weight loads
+  // and SA - 2 whole steps)
+  static constexpr int WAIT_A = NB + (SA - 2) * N_OPS;
+  // vmcnt allowed while waiting for the weights of step g (loaded at step
+  // g - RB_D, followed by RB_D - 1 whole steps and step g's copies; the
+  // prologue follows each of its weight loads by A_OPS pad copies, so the
+  // count holds from step 0)
+  static constexpr int WAIT_B = (RB_D - 1) * N_OPS + A_OPS;
+  static_assert(WAIT_A < 64 && WAIT_B < 64, "vmcnt is 6 bits");
+};
+template <bool LO>
+constexpr size_t rb_lds_bytes() {
+  return (size_t)RbStage<LO>::SA * RbStage<LO>::BYTES + 3 * F8_RID * 4 + (RB_NW + 1) * F8_BM * 4;
+}
+static_assert(rb_lds_bytes<true>() <= 160 * 1024 && rb_lds_bytes<false>() <= 160 * 1024, "LDS budget");
+
+template <int EPI, bool LO>
+__global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
+  static_assert(EPI == F8_SILU_Q || EPI == F8_ROWS, "MoE stages");
+  static_assert(!LO || EPI == F8_ROWS, "the low parts feed the down stage");
+  using SL = RbStage<LO>;
+  constexpr int NA = SL::NA, SA = SL::SA, D = RB_D, NW = RB_NW, CG = RB_CG, RPW = SL::RPW;
+  constexpr int WGN = EPI == F8_SILU_Q ? 128 : 256;  // columns of each matrix per item
+  __shared__ __align__(16) char smem[SA * SL::BYTES];
+  __shared__ __align__(16) int Rid[3][F8_RID];
+  __shared__ __align__(16) float part[NW * F8_BM];
+  __shared__ __align__(16) float amax_s[F8_BM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31, h = lane >> 5;
+  const int nblk = p.N / WGN;
+  const int ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
+  const int xcd = blockIdx.x & 7, wx = blockIdx.x >> 3;
+  const int nx = ((int)gridDim.x - xcd + 7) >> 3;
+  const int items_x = (ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0) * nblk;
+  if (wx >= items_x) return;
+  const int nmine = (items_x - wx + nx - 1) / nx;
+  const int KB = p.KB;
+
+  auto tile_of = [&](int j) { return xcd + 8 * ((wx + j * nx) / nblk); };
+  auto fetch_rows = [&](int j) {  // row ids of item j (+ its expert) into Rid[j % 3], by DMA
+    if (j >= nmine) return;
+    const int tile = tile_of(j);
+    const uint32_t dst = lds_addr(&Rid[j % 3][0]);
+    if (wave >= NW - 2) {
+      // (lane offsets recomputed here, not kept live across the K loop)
+      const uint32_t loff = (uint32_t)lane_id_here() * 4;
+      dma4(p.rows + (int64_t)tile * F8_BM + (wave - (NW - 2)) * 64, loff, dst + (wave - (NW - 2)) * 256);
+    }
+    if (wave == NW - 3) dma4(p.tile_expert + tile, 0u, dst + F8_BM * 4);
+  };
+  for (int j = 0; j < 2 && j < nmine; ++j) {
+    const int tile = tile_of(j);
+    if (tid < F8_BM) Rid[j][tid] = p.rows[(int64_t)tile * F8_BM + tid];
+    if (tid == F8_BM) Rid[j][F8_BM] = p.tile_expert[tile];
+  }
+  __syncthreads();
+
+  // ---- per-item plan of this wave ----
+  struct Plan {
+    uint32_t aoff[RPW / 8];  // the activation rows this wave copies (8 per copy)
+    uint32_t soff;           // waves 0, 1: their s_a rows
+    const uint8_t* b;        // this lane's weight slices of MFMA group 0, K block 0
+    const float* scsrc;      // waves 2, 3: the block scale copied
+    int nvalid, nb;
+  };
+  auto make_plan = [&](int j, Plan& P) {
+    // (lane values recomputed here, not kept live across the K loop)
+    const int lane = lane_id_here(), c32 = lane & 31, h = lane >> 5;
+    const int li = wx + j * nx;
+    P.nb = li % nblk;
+    const int* R = Rid[j % 3];
+    const int ex = __builtin_amdgcn_readfirstlane(R[F8_BM]);
+    P.nvalid = (int)(__popcll(__ballot(R[lane] >= 0)) + __popcll(__ballot(R[64 + lane] >= 0)));
+    const int rid0 = R[0];
+#pragma unroll
+    for (int i = 0; i < RPW / 8; ++i) {
+      const int row = RPW * wave + 8 * i + (lane >> 3);
+      const int rid = R[row] >= 0 ? R[row] : rid0;
+      const int arow = EPI == F8_SILU_Q ? rid / p.row_div : rid;  // the down stage's rows are assignments
+      P.aoff[i] = (uint32_t)((int64_t)arow * p.lda + ((lane & 7) ^ f8_swz(row)) * 16);
+    }
+    P.soff = 0;
+    if (wave < 2) {
+      const int row = 64 * wave + lane;
+      const int rid = R[row] >= 0 ? R[row] : rid0;
+      P.soff = (uint32_t)((int64_t)(EPI == F8_SILU_Q ? rid / p.row_div : rid) * p.ldsa * 4);
+    }
+    int64_t nt;  // the lane's 16-column weight tile
+    const uint8_t* base = p.w0;
+    if constexpr (EPI == F8_SILU_Q) {
+      nt = (int64_t)P.nb * 8 + CG * wave;
+      if (c32 >= 16) base = p.w1;
+    } else {
+      nt = (int64_t)P.nb * 16 + 2 * CG * wave + (c32 >> 4);
+    }
+    P.b = base + (int64_t)ex * p.w_es + fp8_chunk_off(nt, 0, KB) + (16 * h + (c32 & 15)) * 16;
+    P.scsrc = nullptr;
+    if (wave == 2 || wave == 3) {
+      const int q = wave - 2;
+      if constexpr (EPI == F8_SILU_Q)
+        P.scsrc = (q == 0 ? p.sw0 : p.sw1) + (int64_t)ex * p.sw_es + (int64_t)P.nb * KB;
+      else
+        P.scsrc = p.sw0 + (int64_t)ex * p.sw_es + (int64_t)(2 * P.nb + q) * KB;
+    }
+  };
+  Plan cur, nxt;
+  const uint32_t lds0 = lds_addr(smem);
+  // activation copies of K block kb of a plan into ring slot `slot`: NA x
+  // RPW / 8 row copies + 1 scale copy per wave
+  // (the plan is chosen by select, not by branch: every copy and load is
+  // issued on one path, so no register of an in-flight load is merged
+  // between branches)
+  auto issue_a = [&](bool next, int kb, int slot) {
+    const uint32_t st = lds0 + slot * SL::BYTES;
+    const uint8_t* ab = p.a + (int64_t)kb * 128;
+    uint32_t aoff[RPW / 8];
+#pragma unroll
+    for (int i = 0; i < RPW / 8; ++i) aoff[i] = next ? nxt.aoff[i] : cur.aoff[i];
+#pragma unroll
+    for (int i = 0; i < RPW / 8; ++i) dma16(ab, aoff[i], st + (RPW * wave + 8 * i) * 128);
+    if constexpr (LO) {
+      const uint8_t* al = p.a_lo + (int64_t)kb * 128;
+#pragma unroll
+      for (int i = 0; i < RPW / 8; ++i) dma16(al, aoff[i], st + F8_A_BYTES + (RPW * wave + 8 * i) * 128);
+    }
+    // one scale copy per wave, chosen by wave-uniform selects: the s_a rows
+    // (waves 0, 1), a block scale (waves 2, 3) or a pad copy
+    const float* src = wave >= 2 && wave < 4 ? (next ? nxt.scsrc : cur.scsrc) : p.sa;
+    const uint32_t voff = wave < 2 ? (next ? nxt.soff : cur.soff) : 0u;
+    const uint32_t dst = wave < 2 ? SL::SA_OFF + wave * 256
+                                  : (wave < 4 ? SL::SW_OFF + (wave - 2) * 256 : SL::PAD_OFF + (wave - 4) * 256);
+    dma4(src + kb, voff, st + dst);
+  };
+  // this lane's weight slices of K block kb: the B operands [k-step][half]
+  // (bytes 0..15 and 16..31 of the lane's 32 are the two 1 KiB halves),
+  // loaded by inline assembly and waited for with wait_vmcnt_tied
+  auto issue_b = [&](bool next, int kb, u32x4 (&bq)[2][2]) {
+    const uint8_t* b = (next ? nxt.b : cur.b) + (int64_t)kb * 16384;
+    gload16_nt<0>(bq[0][0], b);
+    gload16_nt<1024>(bq[0][1], b);
+    gload16_nt<512>(bq[1][0], b);
+    gload16_nt<1536>(bq[1][1], b);
+  };
+
+  // ---- MFMA side.  The weights are the A operand (MFMA rows = the wave's
+  // 32 weight columns: gate/up, 16 gate columns then the same 16 up
+  // columns) and the activations the B operand (MFMA columns = the 32 rows
+  // of a row tile; lane (c32, h) holds row c32, pieces 4s + 2h, 4s + 2h + 1
+  // of k-step s).  Register i of row tile rt then holds row 32 rt + c32 and
+  // weight column 8 (i / 4) + 4 h + i % 4 of the wave's group: for gate/up,
+  // i < 8 a gate column and i + 8 the same up column. ----
+  const int fsw = f8_swz(c32);
+  uint32_t adoff[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) adoff[s][e] = c32 * 128 + (((4 * s + 2 * h + e) ^ fsw) * 16);
+  // down: which of the two copied block scales (the 128-column block of the wave's columns)
+  const int swq = (CG * wave) / 4;
+
+  f32x16 acc[4][CG];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) acc[rt][cg] = f32x16{};
+
+  // One K block over the row tiles holding valid rows (nrt = 1..4,
+  // wave-uniform), software-pipelined: the MFMAs of row tile rt + 1 are
+  // issued before the scaling of row tile rt, which then runs under them.
+  auto compute = [&](int slot, int nrt, const i32x8 (&bq)[CG][2]) {
+    const char* S = smem + slot * SL::BYTES;
+    // block scales of the wave's columns: gate (copy 0) and up (copy 1), or
+    // the one block of the down columns
+    const float sw0 = *reinterpret_cast<const float*>(S + SL::SW_OFF + (EPI == F8_SILU_Q ? 0 : swq * 256));
+    const float sw1 = EPI == F8_SILU_Q ? *reinterpret_cast<const float*>(S + SL::SW_OFF + 256) : sw0;
+    auto mma = [&](int rt) {
+      f32x16 t;
+      // LO: the low parts first, scaled by 1/16 inside the MFMA, then the
+      // high parts accumulate onto them
+#pragma unroll
+      for (int part = LO ? 0 : 1; part < 2; ++part) {
+        const char* ar = S + (part == 0 ? F8_A_BYTES : 0) + rt * 32 * 128;
+        i32x8 a[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(ar + adoff[st][0]);
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(ar + adoff[st][1]);
+          a[st] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const bool fresh = st == 0 && (LO ? part == 0 : true);
+          if (LO && part == 0)
+            t = mfma_f8_32_b16th(bq[0][st], a[st], fresh ? f32x16{} : t);
+          else
+            t = mfma_f8_32(bq[0][st], a[st], fresh ? f32x16{} : t);
+        }
+      }
+      return t;
+    };
+    // acc += (s_a[row] * s_w[column]) * t; the lane's row has one s_a
+    auto scale = [&](int rt, const f32x16& t) {
+      const float sa = *reinterpret_cast<const float*>(S + SL::SA_OFF + (32 * rt + c32) * 4);
+      const float f0 = sa * sw0, f1 = sa * sw1;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[rt][0][i] = fmaf(i < 8 ? f0 : f1, t[i], acc[rt][0][i]);
+    };
+    f32x16 t = mma(0);
+#pragma unroll
+    for (int rt = 1; rt < 4; ++rt) {
+      if (rt < nrt) {
+        const f32x16 tn = mma(rt);
+        scale(rt - 1, t);
+        t = tn;
+      } else if (rt == nrt) {
+        scale(rt - 1, t);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (nrt == 4) scale(3, t);
+  };
+
+  auto epilogue = [&](int j, const Plan& P) {
+    const int* R = Rid[j % 3];
+    if constexpr (EPI == F8_SILU_Q) {
+      // h = silu(gate) * up in float32 in the lane (registers i, i + 8).  Row
+      // amax over the item's 128 columns: the lane's 8, the lane holding the
+      // row's other 8 columns of the wave (h ^ 1), then the waves via LDS.
+      float hq[4][8];
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float g = acc[rt][0][i], u = acc[rt][0][i + 8];
+          const float hv = g * __frcp_rn(1.0f + __expf(-g)) * u;
+          hq[rt][i] = hv;
+          am = fmaxf(am, fabsf(hv));
+        }
+        am = fmaxf(am, __shfl_xor(am, 32, 64));
+        if (h == 0) part[wave * F8_BM + 32 * rt + c32] = am;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      lds_barrier();
+      if (tid < F8_BM) {
+        float mx = part[tid];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) mx = fmaxf(mx, part[w * F8_BM + tid]);
+        amax_s[tid] = mx;
+      }
+      lds_barrier();
+      // columns 8q + 4h .. + 3 of the wave's 16: four bytes per store
+      const int64_t col0 = (int64_t)P.nb * WGN + 16 * (CG * wave) + 4 * h;
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        const int row = 32 * rt + c32;
+        if (row < P.nvalid) {
+          const float sc = fmaxf(amax_s[row], kAmaxFloor) / kFp8Max;
+          const int64_t o = (int64_t)R[row] * p.ldqy + col0;
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            uint32_t wh = 0, wl = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = hq[rt][4 * q + e] / sc;
+              const uint32_t qh = f32_to_fp8_rne(v);
+              // v - fp8(qh) is exact (qh is v's nearest e4m3 value), and so is * 16
+              const uint32_t ql = f32_to_fp8_rne((v - fp8_e4m3_to_f32(qh)) * 16.0f);
+              wh |= qh << (8 * e);
+              wl |= ql << (8 * e);
+            }
+            *reinterpret_cast<uint32_t*>(p.qy + o + 8 * q) = wh;
+            *reinterpret_cast<uint32_t*>(p.qy_lo + o + 8 * q) = wl;
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (tid < P.nvalid) p.sy[(int64_t)R[tid] * p.ldsy + P.nb] = fmaxf(amax_s[tid], kAmaxFloor) / kFp8Max;
+    } else {
+      // columns 8q + 4h .. + 3 of the wave's 32: four values per store
+      const int64_t col0 = (int64_t)P.nb * WGN + 32 * (CG * wave) + 4 * h;
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        const int row = 32 * rt + c32;
+        if (row < P.nvalid) {
+          const int64_t o = (int64_t)R[row] * p.ldy + col0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16& v = acc[rt][0];
+            if (p.y_dtype == CCQ_F32) {
+              *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.y) + o + 8 * q) =
+                  f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            } else {
+              const bool bf = p.y_dtype == CCQ_BF16;
+              uint32_t w2[2];
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const float x0 = v[4 * q + 2 * e], x1 = v[4 * q + 2 * e + 1];
+                w2[e] = bf ? (f32_to_bf16_bits(x0) | (f32_to_bf16_bits(x1) << 16))
+                           : (f32_to_f16_bits(x0) | (f32_to_f16_bits(x1) << 16));
+              }
+              *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.y) + o + 8 * q) = u32x2{w2[0], w2[1]};
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) acc[rt][cg] = f32x16{};
+  };
+
+  // ---- the pipeline over all K blocks of all items of this workgroup.  Step
+  // g: wait for its activation stage, barrier, copy the activations of step
+  // g + SA - 1 into the slot step g - 1 used, wait for its weights, compute,
+  // load the weights of step g + D into the registers just used.  Steps past
+  // the end re-issue the last step's loads (same counts).  `cur` is the
+  // plan of the current item, `nxt` that of the next one. ----
+  make_plan(0, cur);
+  nxt = cur;
+  if (nmine > 1) make_plan(1, nxt);
+  // (next item?, kb) of the step `ahead` steps after (j, kb), ahead < KB,
+  // clamped to the last step
+  auto ahead_of = [&](int j, int kb, int ahead, bool& next, int& pk) {
+    int k2 = kb + ahead, j2 = j;
+    if (k2 >= KB) {
+      k2 -= KB;
+      ++j2;
+    }
+    if (j2 >= nmine) {
+      j2 = nmine - 1;
+      k2 = KB - 1;
+    }
+    next = j2 != j;
+    pk = k2;
+  };
+#pragma unroll
+  for (int g = 0; g < SA - 1; ++g) {
+    bool nx_;
+    int pk;
+    ahead_of(0, 0, g, nx_, pk);
+    issue_a(nx_, pk, g);
+  }
+  u32x4 bq[D][2][2];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    bool nx_;
+    int pk;
+    ahead_of(0, 0, d, nx_, pk);
+    issue_b(nx_, pk, bq[d]);
+#pragma unroll
+    for (int i = 0; i < SL::A_OPS; ++i) dma4(p.sa, 0u, lds0 + SL::PAD_OFF + (wave & 3) * 256);
+  }
+  const int total = nmine * KB;
+  int slot = 0, j = 0, kb = 0;
+  for (int g0 = 0; g0 < total; g0 += D) {  // step g uses register set g % D
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int g = g0 + d;
+      if (g >= total) break;
+      if (g >= SA - 1)
+        wait_vmcnt<SL::WAIT_A>();
+      else
+        wait_vmcnt<0>();
+      lds_barrier();
+      if (kb == 0) {
+        if (j + 2 < nmine) fetch_rows(j + 2);
+        if (j > 0 && j + 1 < nmine) make_plan(j + 1, nxt);
+      }
+      {
+        bool nx_;
+        int pk;
+        ahead_of(j, kb, SA - 1, nx_, pk);
+        issue_a(nx_, pk, slot == 0 ? SA - 1 : slot - 1);
+      }
+      wait_vmcnt_tied<SL::WAIT_B>(bq[d][0][0], bq[d][0][1], bq[d][1][0], bq[d][1][1]);
+      {
+        i32x8 bw[CG][2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const u32x4 lo = bq[d][st][0], hi = bq[d][st][1];
+          bw[0][st] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+        compute(slot, (cur.nvalid + 31) >> 5, bw);
+      }
+      {
+        bool nx_;
+        int pk;
+        ahead_of(j, kb, D, nx_, pk);
+        issue_b(nx_, pk, bq[d]);
+      }
+      slot = slot + 1 == SA ? 0 : slot + 1;
+      __builtin_amdgcn_sched_barrier(0);  // one step at a time
+      if (kb + 1 == KB) {
+        epilogue(j, cur);
+        cur = nxt;
+        ++j;
+        kb = 0;
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        ++kb;
+      }
+    }
+  }
+  // no copy into LDS outlives the workgroup, and the registers of the last
+  // (unused) weight loads stay reserved until they have landed
+#pragma unroll
+  for (int d = 0; d < D; ++d) wait_vmcnt_tied<0>(bq[d][0][0], bq[d][0][1], bq[d][1][0], bq[d][1][1]);
+}
+
 // Compute units of the current device (one persistent workgroup each; at
 // least 8 so that every XCD gets one).
 static int f8_device_cus() {
@@ -520,9 +996,36 @@ static int f8_device_cus() {
 
 // tiles = 128-row schedule tiles the grid is sized for (the kernel reads the
 // actual number from meta when given).  K must hold at least 2 blocks.
+// The MoE stages with the weights in registers need K blocks of lookahead
+// inside one item plus the next (KB >= 6), a schedule (rows, experts) and
+// outputs aligned for their vector stores (4 columns per store).
+static bool use_rb(const Fp8GP& p, bool silu) {
+  if (p.KB < 6 || p.rows == nullptr || p.tile_expert == nullptr) return false;
+  if (silu)
+    return p.ldqy % 4 == 0 && ((uintptr_t)p.qy & 3) == 0 && ((uintptr_t)p.qy_lo & 3) == 0;
+  const uintptr_t al = p.y_dtype == CCQ_F32 ? 15 : 7;
+  return p.ldy % 4 == 0 && ((uintptr_t)p.y & al) == 0;
+}
+
 template <int EPI>
 static int launch_fp8_gemm(const Fp8GP& p, int64_t tiles, hipStream_t st) {
   const bool lo = p.a_lo != nullptr;
+  if constexpr (EPI != F8_STORE) {
+    if (use_rb(p, EPI == F8_SILU_Q)) {
+      const int wgn = EPI == F8_SILU_Q ? 128 : 256;
+      if (p.N % wgn == 0) {
+        const int64_t items = tiles * (p.N / wgn), cus = f8_device_cus();
+        const dim3 grid((unsigned)(items < cus ? items : cus)), block(RB_NW * 64);
+        if constexpr (EPI == F8_SILU_Q)
+          hipLaunchKernelGGL((fp8_moe_rb_kernel<F8_SILU_Q, false>), grid, block, 0, st, p);
+        else if (lo)
+          hipLaunchKernelGGL((fp8_moe_rb_kernel<F8_ROWS, true>), grid, block, 0, st, p);
+        else
+          hipLaunchKernelGGL((fp8_moe_rb_kernel<F8_ROWS, false>), grid, block, 0, st, p);
+        return launch_status("fp8 moe gemm");
+      }
+    }
+  }
   if (lo && EPI != F8_ROWS) return arg_error("fp8 gemm: low activation parts need the row epilogue");
   // the high + low activation tiles take the LDS of half the weight tiles
   const int wgn = EPI == F8_SILU_Q || lo ? 128 : (p.N % 256 == 0 ? 256 : 128);
@@ -576,7 +1079,7 @@ extern "C" int ccq_fp8_act_quant(const void* x, int x_dtype, int64_t rows, int64
 
 extern "C" int ccq_fp8_block_repack(const uint8_t* w, uint8_t* tiled, int64_t N, int64_t K, void* stream) {
   CCQ_REQUIRE(N >= 0 && K >= 0, "ccq_fp8_block_repack: negative shape");
-  CCQ_REQUIRE(N % 16 == 0 && K % 128 == 0, "ccq_fp8_block_repack: need N %% 16 == 0 and K %% 128 == 0");
+  CCQ_REQUIRE(N % 128 == 0 && K % 128 == 0, "ccq_fp8_block_repack: need N %% 128 == 0 and K %% 128 == 0");
   if (N == 0 || K == 0) return 0;
   CCQ_REQUIRE(w && tiled, "ccq_fp8_block_repack: null pointer");
   CCQ_REQUIRE(w != tiled, "ccq_fp8_block_repack: in-place is not supported");
@@ -588,7 +1091,7 @@ extern "C" int ccq_fp8_block_repack(const uint8_t* w, uint8_t* tiled, int64_t N,
 
 extern "C" int ccq_fp8_block_unpack(const uint8_t* tiled, uint8_t* w, int64_t N, int64_t K, void* stream) {
   CCQ_REQUIRE(N >= 0 && K >= 0, "ccq_fp8_block_unpack: negative shape");
-  CCQ_REQUIRE(N % 16 == 0 && K % 128 == 0, "ccq_fp8_block_unpack: need N %% 16 == 0 and K %% 128 == 0");
+  CCQ_REQUIRE(N % 128 == 0 && K % 128 == 0, "ccq_fp8_block_unpack: need N %% 128 == 0 and K %% 128 == 0");
   if (N == 0 || K == 0) return 0;
   CCQ_REQUIRE(w && tiled, "ccq_fp8_block_unpack: null pointer");
   CCQ_REQUIRE(w != tiled, "ccq_fp8_block_unpack: in-place is not supported");

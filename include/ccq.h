@@ -421,8 +421,10 @@ int ccq_moe_w4_forward_noalloc(const void* x, int x_dtype, const float* logits, 
 int ccq_fp8_act_quant(const void* x, int x_dtype, int64_t rows, int64_t K,
                       uint8_t* q, float* s, void* stream);
 
-/* Re-pack w [N, K] e4m3fn into the gfx950 MFMA tile layout (same bytes);
- * N % 16 == 0, K % 128 == 0, 16-byte aligned, not in place.  Load-time step
+/* Re-pack w [N, K] e4m3fn into the gfx950 MFMA tile layout (same bytes):
+ * 2 KiB chunks per (16-column tile, 128-wide K block), the 8 tiles of each
+ * 128-column block contiguous at each K block; N % 128 == 0, K % 128 == 0,
+ * 16-byte aligned, not in place.  Load-time step
  * (QuantizeMethodBase.process_weights_after_loading, quant/method.py:60-62). */
 int ccq_fp8_block_repack(const uint8_t* w, uint8_t* tiled, int64_t N, int64_t K,
                          void* stream);

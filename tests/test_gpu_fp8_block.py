@@ -115,7 +115,11 @@ def _moe_ref(x, ids, wts, wg, sg, wu, su, wd, sd):
     return y
 
 
-@pytest.mark.parametrize("T,k,E,H,I", [(1, 2, 8, 256, 256), (20, 2, 8, 256, 384), (70, 4, 6, 384, 256)])
+# the last three run the stages with the weights streamed into registers
+# (K blocks >= 6 and a multiple of 4): 150 rows per expert (a full and a
+# ragged tile), a few rows per expert with empty experts, and gate/up only
+@pytest.mark.parametrize("T,k,E,H,I", [(1, 2, 8, 256, 256), (20, 2, 8, 256, 384), (70, 4, 6, 384, 256),
+                                       (300, 4, 8, 1024, 1024), (40, 2, 24, 1536, 1024), (96, 2, 4, 2048, 512)])
 def test_moe_fp8_parity(gpu, T, k, E, H, I):
     from ccut.blocks import moe
 

@@ -142,7 +142,8 @@ def test_fp8_block_rejects_bad_args(lib):
     assert lib.ccq_fp8_act_quant(p, 9, 4, 128, p, p, None) == CCQ_EINVAL and "x_dtype" in last_error()
     assert lib.ccq_fp8_act_quant(p, CCQ_BF16, 0, 128, p, p, None) == 0
     assert lib.ccq_fp8_block_repack(p, p, 24, 128, None) == CCQ_EINVAL
-    assert lib.ccq_fp8_block_repack(p, p, 32, 128, None) == CCQ_EINVAL and "in-place" in last_error()
+    assert lib.ccq_fp8_block_repack(p, p, 64, 128, None) == CCQ_EINVAL and "N % 128" in last_error()
+    assert lib.ccq_fp8_block_repack(p, p, 128, 128, None) == CCQ_EINVAL and "in-place" in last_error()
     assert lib.ccq_fp8_block_linear_workspace_size(4, 100) == 0
     need = lib.ccq_fp8_block_linear_workspace_size(4, 256)
     assert need > 0 and need % 256 == 0
