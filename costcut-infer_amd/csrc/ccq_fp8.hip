@@ -796,51 +796,59 @@ __global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
       // h = silu(gate) * up in float32 in the lane (registers i, i + 8).  Row
       // amax over the item's 128 columns: the lane's 8, the lane holding the
       // row's other 8 columns of the wave (h ^ 1), then the waves via LDS.
+      // Row tiles without valid rows are skipped (wave-uniform).
+      const int nrt = (P.nvalid + 31) >> 5;
       float hq[4][8];
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
-        float am = 0.f;
+        if (rt < nrt) {
+          float am = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float g = acc[rt][0][i], u = acc[rt][0][i + 8];
-          const float hv = g * __frcp_rn(1.0f + __expf(-g)) * u;
-          hq[rt][i] = hv;
-          am = fmaxf(am, fabsf(hv));
+          for (int i = 0; i < 8; ++i) {
+            const float g = acc[rt][0][i], u = acc[rt][0][i + 8];
+            const float hv = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+            hq[rt][i] = hv;
+            am = fmaxf(am, fabsf(hv));
+          }
+          am = fmaxf(am, __shfl_xor(am, 32, 64));
+          if (h == 0) part[wave * F8_BM + 32 * rt + c32] = am;
         }
-        am = fmaxf(am, __shfl_xor(am, 32, 64));
-        if (h == 0) part[wave * F8_BM + 32 * rt + c32] = am;
         __builtin_amdgcn_sched_barrier(0);
       }
       lds_barrier();
-      if (tid < F8_BM) {
+      if (tid < 32 * nrt) {
         float mx = part[tid];
 #pragma unroll
         for (int w = 1; w < NW; ++w) mx = fmaxf(mx, part[w * F8_BM + tid]);
         amax_s[tid] = mx;
       }
       lds_barrier();
-      // columns 8q + 4h .. + 3 of the wave's 16: four bytes per store
+      // columns 8q + 4h .. + 3 of the wave's 16: four bytes per store.  The
+      // e4m3 conversions are the hardware's (v_cvt_pk_fp8_f32, round to
+      // nearest even; equal to the software encoder for every |v| <= 460,
+      // and |v| <= 448 (1 + 2^-22) here).
       const int64_t col0 = (int64_t)P.nb * WGN + 16 * (CG * wave) + 4 * h;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
         const int row = 32 * rt + c32;
-        if (row < P.nvalid) {
-          const float sc = fmaxf(amax_s[row], kAmaxFloor) / kFp8Max;
+        if (rt < nrt && row < P.nvalid) {
+          const float am = fmaxf(amax_s[row], kAmaxFloor);
+          const float inv = kFp8Max / am;  // v = h / (am / 448) up to an ulp
           const int64_t o = (int64_t)R[row] * p.ldqy + col0;
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            uint32_t wh = 0, wl = 0;
+            float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float v = hq[rt][4 * q + e] / sc;
-              const uint32_t qh = f32_to_fp8_rne(v);
-              // v - fp8(qh) is exact (qh is v's nearest e4m3 value), and so is * 16
-              const uint32_t ql = f32_to_fp8_rne((v - fp8_e4m3_to_f32(qh)) * 16.0f);
-              wh |= qh << (8 * e);
-              wl |= ql << (8 * e);
-            }
-            *reinterpret_cast<uint32_t*>(p.qy + o + 8 * q) = wh;
-            *reinterpret_cast<uint32_t*>(p.qy_lo + o + 8 * q) = wl;
+            for (int e = 0; e < 4; ++e) v[e] = hq[rt][4 * q + e] * inv;
+            int wh = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+            wh = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], wh, true);
+            // v - fp8(hi) is exact (hi is v's nearest e4m3 value), and so is * 16
+            const auto b01 = __builtin_amdgcn_cvt_pk_f32_fp8(wh, false);
+            const auto b23 = __builtin_amdgcn_cvt_pk_f32_fp8(wh, true);
+            int wl = __builtin_amdgcn_cvt_pk_fp8_f32((v[0] - b01[0]) * 16.0f, (v[1] - b01[1]) * 16.0f, 0, false);
+            wl = __builtin_amdgcn_cvt_pk_fp8_f32((v[2] - b23[0]) * 16.0f, (v[3] - b23[1]) * 16.0f, wl, true);
+            *reinterpret_cast<uint32_t*>(p.qy + o + 8 * q) = (uint32_t)wh;
+            *reinterpret_cast<uint32_t*>(p.qy_lo + o + 8 * q) = (uint32_t)wl;
           }
         }
         __builtin_amdgcn_sched_barrier(0);
