@@ -1250,19 +1250,23 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
   uint32_t magic_v = Act<AT>::kMagic2;
   asm volatile("v_mov_b32 %0, %0" : "+v"(magic_v));  // keep the magic in a VGPR (far from any MFMA)
 
-  auto fold = [&](const float (&s)[C32]) {
+  // two = the wave's second 32-row tile holds valid rows (wave-uniform;
+  // without, its MFMAs, fold and correction are skipped)
+  auto fold = [&](const float (&s)[C32], bool two) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < 2; ++rt) {
+      if (rt == 1 && !two) break;
 #pragma unroll
       for (int c = 0; c < C32; ++c)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[rt][c][i] = fmaf(s[c], t[rt][c][i], acc[rt][c][i]);
+    }
   };
 
-  auto compute = [&](int slot, int kt) {
+  auto compute = [&](int slot, int kt, bool two) {
     const char* S = smem + slot * GG_STAGE;
     const bool mine = h == (kt & 1);
-    if (late && (kt & 1)) fold(scp);  // products of the even k-tile before
+    if (late && (kt & 1)) fold(scp, two);  // products of the even k-tile before
     u32x4 bq[C32][2];
 #pragma unroll
     for (int c = 0; c < C32; ++c) {
@@ -1286,20 +1290,22 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
 #pragma unroll
       for (int c = 0; c < C32; ++c) {
         const V b = dq_b3<AT>(bq[c][s & 1][s >> 1], mask_s, magic_v);
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) t[rt][c] = mfma32(a[rt], b, s == 0 ? f32x16{} : t[rt][c]);
+        t[0][c] = mfma32(a[0], b, s == 0 ? f32x16{} : t[0][c]);
+        if (two) t[1][c] = mfma32(a[1], b, s == 0 ? f32x16{} : t[1][c]);
       }
     }
-    if (!late) fold(sc);
+    if (!late) fold(sc, two);
 #pragma unroll
     for (int c = 0; c < C32; ++c) scp[c] = sc[c];
     if ((kt & 1) == 1 || kt + 1 == KT) {
-      if (late) fold(scp);  // the window's products go in before its correction
+      if (late) fold(scp, two);  // the window's products go in before its correction
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < 2; ++rt) {
+        if (rt == 1 && !two) break;
 #pragma unroll
         for (int c = 0; c < C32; ++c)
           acc[rt][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(za[rt], zb[c], acc[rt][c], 0, 0, 0);
+      }
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) za[rt] = 0.f;
 #pragma unroll
@@ -1378,7 +1384,7 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
     const bool last = kt + 1 == KT;
     const int slot2 = slot == 0 ? 2 : slot - 1;  // (slot + 2) % 3
     if (!last && g + 2 < total) issue(kt + 2 < KT ? cur : nxt, kt + 2 < KT ? kt + 2 : kt + 2 - KT, slot2);
-    if (mw * 64 < cur.nvalid) compute(slot, kt);
+    if (mw * 64 < cur.nvalid) compute(slot, kt, mw * 64 + 32 < cur.nvalid);
     if (last) {
       epilogue(j, cur);
       // the next item's second k-step is issued after the stores, so the
