@@ -1319,22 +1319,42 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
   auto epilogue = [&](int j, const Plan& P) {
     const int* R = Rid[j % 3];
     if constexpr (EPI == EPI_SILU) {
+      // h = silu(g) * u, rounded to the output type (hardware conversions,
+      // round to nearest even).  Stores: lanes c32 and c32 ^ 1 swap one value
+      // per row pair (DPP), so the even lane writes columns (c, c + 1) of the
+      // even row and the odd lane those of the odd row, one 4-byte store each.
       float rs[32];
-      const int64_t col = P.nb * WGN + nw * CTW * 16 + c32;
+      const int64_t col2 = P.nb * WGN + nw * CTW * 16 + (c32 & ~1);
+      const bool odd = (c32 & 1) != 0, bf = p.y_dtype == CCQ_BF16;
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int row = row_of(rt, i);
-          float sum = 0.f;
-          if (row < P.nvalid) {
-            const float g = acc[rt][0][i], u = acc[rt][1][i];
-            const float hv = g * __frcp_rn(1.0f + __expf(-g)) * u;
-            const uint32_t hb = p.y_dtype == CCQ_BF16 ? f32_to_bf16_bits(hv) : f32_to_f16_bits(hv);
-            reinterpret_cast<uint16_t*>(p.y)[(int64_t)R[row] * p.ldy + col] = (uint16_t)hb;
-            sum = p.y_dtype == CCQ_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+        for (int m = 0; m < 8; ++m) {
+          float hv[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float g = acc[rt][0][2 * m + e], u = acc[rt][1][2 * m + e];
+            hv[e] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
           }
-          rs[rt * 16 + i] = sum;
+          // own rounded values (rows 2m, 2m + 1 of this column) for the group sums
+          uint32_t own;
+          if (bf) {
+            own = bf16x2_bits(hv[0], hv[1]);
+            rs[rt * 16 + 2 * m] = __uint_as_float(own << 16);
+            rs[rt * 16 + 2 * m + 1] = __uint_as_float(own & 0xFFFF0000u);
+          } else {
+            own = f32_to_f16_bits(hv[0]) | (f32_to_f16_bits(hv[1]) << 16);
+            rs[rt * 16 + 2 * m] = f16_bits_to_f32(own & 0xFFFFu);
+            rs[rt * 16 + 2 * m + 1] = f16_bits_to_f32(own >> 16);
+          }
+          // the even lane sends row 2m + 1, the odd lane row 2m
+          const uint32_t send = odd ? (own & 0xFFFFu) : (own >> 16);
+          const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+          const uint32_t word = odd ? (recv | (own & 0xFFFF0000u)) : ((own & 0xFFFFu) | (recv << 16));
+          const int row = row_of(rt, 2 * m + (odd ? 1 : 0));
+          if (row < P.nvalid) *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)R[row] * p.ldy + col2) = word;
+          if (row_of(rt, 2 * m) >= P.nvalid) rs[rt * 16 + 2 * m] = 0.f;
+          if (row_of(rt, 2 * m + 1) >= P.nvalid) rs[rt * 16 + 2 * m + 1] = 0.f;
         }
       if (p.sxo != nullptr) {
         // group sums of the stored rows over this item's 128 columns: 32 per
@@ -1347,15 +1367,32 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
               ((part[tid] + part[GG_BM + tid]) + part[2 * GG_BM + tid]) + part[3 * GG_BM + tid];
       }
     } else {
+      // rows of columns (c, c + 1) per store, as above: the even lane writes
+      // the even row of a row pair, the odd lane the odd row
+      const bool odd = (c32 & 1) != 0;
+      const int64_t col2 = P.nb * WGN + nw * CTW * 16 + (c32 & ~1);
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int row = row_of(rt, i);
-          if (row >= P.nvalid) continue;
-          const int64_t o = (int64_t)R[row] * p.ldy + P.nb * WGN + nw * CTW * 16 + c32;
+        for (int m = 0; m < 8; ++m) {
+          const int row = row_of(rt, 2 * m + (odd ? 1 : 0));
 #pragma unroll
-          for (int c = 0; c < C32; ++c) store_val(p.y, o + c * 32, acc[rt][c][i], p.y_dtype);
+          for (int c = 0; c < C32; ++c) {
+            const float v0 = acc[rt][c][2 * m], v1 = acc[rt][c][2 * m + 1];
+            const float fs = odd ? v0 : v1;
+            const float fr = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(fs), 0xB1, 0xF, 0xF, false));
+            const float lo = odd ? fr : v0, hi = odd ? v1 : fr;  // columns (c & ~1), (c | 1) of the row
+            if (row < P.nvalid) {
+              const int64_t o = (int64_t)R[row] * p.ldy + col2 + c * 32;
+              if (p.y_dtype == CCQ_F32)
+                *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(p.y) + o) = f32x2{lo, hi};
+              else if (p.y_dtype == CCQ_BF16)
+                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.y) + o) = bf16x2_bits(lo, hi);
+              else
+                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.y) + o) =
+                    f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+            }
+          }
         }
     }
 #pragma unroll

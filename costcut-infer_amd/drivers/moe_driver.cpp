@@ -9,6 +9,9 @@
 //                           ccq_moe_w4_forward (prints the distinct experts)
 //   moe_driver fp8 T reps   FP8 block prefill: 256 experts top-8, hidden
 //                           7168, inter 2048, ccq_moe_fp8_ffn
+//   moe_driver gemm M K N reps copies
+//                           AWQ g128 linear y [M, N] = x [M, K] @ W,
+//                           ccq_w4_gemm over `copies` rotating weight sets
 // Build: hipcc -O2 -Iinclude costcut-infer_amd/drivers/moe_driver.cpp
 //        -Lcostcut-infer_amd/ccut/_lib -lccq_hip -Wl,-rpath,<that dir> -o <binary>
 #include <hip/hip_runtime.h>
@@ -28,7 +31,36 @@ static void fill_rand_u32(void* d, size_t words, uint32_t seed, uint32_t mask, u
   for (auto& v : h) v = (g() & mask) | orv;
   CK(hipMemcpy(d, h.data(), words * 4, hipMemcpyHostToDevice));
 }
+static int run_gemm(int argc, char** argv) {
+  const int64_t M = argc > 2 ? atoll(argv[2]) : 1, K = argc > 3 ? atoll(argv[3]) : 2048,
+                N = argc > 4 ? atoll(argv[4]) : 5632;
+  const int reps = argc > 5 ? atoi(argv[5]) : 20, copies = argc > 6 ? atoi(argv[6]) : 16;
+  const int64_t szw = ccq_awq_sz_words(K, 128);
+  std::vector<void*> w(copies), z(copies);
+  for (int c = 0; c < copies; ++c) {
+    w[c] = dalloc(K * N / 2);
+    fill_rand_u32(w[c], K * N / 8, 11 + c, ~0u, 0);
+    z[c] = dalloc(N * szw * 4);
+    fill_rand_u32(z[c], N * szw, 101 + c, 0x000F007Fu, 0x3C00u);
+  }
+  void* x = dalloc(M * K * 2);
+  fill_rand_u32(x, M * K / 2, 7, 0x807F807Fu, 0x3F003F00u);
+  void* y = dalloc(M * N * 2);
+  const size_t wsb = ccq_w4_gemm_workspace_size(M, K, N, 128);
+  void* ws = wsb ? dalloc(wsb) : nullptr;
+  for (int r = 0; r < reps; ++r) {
+    const int c = r % copies;
+    const int rc = ccq_w4_gemm(x, CCQ_F16, (const int32_t*)w[c], (const uint32_t*)z[c], CCQ_F16, y, CCQ_F16, M, K, N,
+                               128, ws, wsb, nullptr);
+    if (rc) { printf("rc=%d %s\n", rc, ccq_last_error()); return 4; }
+  }
+  CK(hipDeviceSynchronize());
+  printf("gemm M=%lld K=%lld N=%lld reps %d copies %d done\n", (long long)M, (long long)K, (long long)N, reps, copies);
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  if (argc > 1 && !strcmp(argv[1], "gemm")) return run_gemm(argc, argv);
   const bool fp8 = argc > 1 && !strcmp(argv[1], "fp8");
   const bool fwd = argc > 1 && !strcmp(argv[1], "w4f");  // decode shape through ccq_moe_w4_forward (logits)
   const bool dec = fwd || (argc > 1 && !strcmp(argv[1], "w4d"));  // int4 MoE decode shape
