@@ -149,6 +149,11 @@ __device__ __forceinline__ const void* uniform_ptr(const void* p) {
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }
+// The same copy marked non-temporal (nt), for data read once (weight
+// streams), so it does not push reused data (activation tiles) out of L2.
+__device__ __forceinline__ void dma16_nt(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
+}
 __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(lds) : "memory");
 }

@@ -1197,7 +1197,7 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
     for (int i = 0; i < 4; ++i) dma16(xb, P.aoff[i], st + (16 * wave + 4 * i) * 256);
 #pragma unroll
     for (int b2 = 0; b2 < BPW; ++b2)
-      dma16(P.bsrc[b2] + (int64_t)kt * 1024, lane * 16, st + GG_B_OFF + (wave * BPW + b2) * 1024);
+      dma16_nt(P.bsrc[b2] + (int64_t)kt * 1024, lane * 16, st + GG_B_OFF + (wave * BPW + b2) * 1024);
     if (has_sz) dma4(P.zsrc + kt * 4, P.zoff, st + GG_SZ_OFF + wave * 256);
     if (has_sx) dma4(p.sx + kt, P.soff, st + GG_SX_OFF + (wave - 4) * 256);
   };
