@@ -783,6 +783,24 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   RouteSmem& rs = *reinterpret_cast<RouteSmem*>(&part[0][0][0][0][0]);
   static_assert(!ROUTE || (EPI == EPI_SILU && sizeof(RouteSmem) <= sizeof(part)), "routing in gate/up only");
   constexpr bool routed = ROUTE;  // p.logits is set exactly for this instance
+  const int r16 = lane & 15, kq = lane >> 4;
+  // activation fragments, lane r16 holding MFMA row r16.  A routed batch
+  // (T <= 16 tokens) multiplies every expert's weights by all its tokens:
+  // the MFMA rows are the tokens, the same for every job, so their
+  // fragments are loaded once, before the routing, and each job stores
+  // only the rows of the tokens routed to its expert.  k-tiles past K
+  // repeat the last one (those k-tiles get a zero scale)
+  V a[MT][4], b[MT][4];
+  auto load_frags = [&](V (&f)[MT][4], int xrow) {
+    const AT* xr = reinterpret_cast<const AT*>(p.x) + (int64_t)xrow * p.ldx + 8 * kq;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int kt = min(wave + 8 * m, KT - 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f[m][j] = *reinterpret_cast<const V*>(xr + kt * 128 + 32 * j);
+    }
+  };
+  if constexpr (routed) load_frags(a, r16 < p.rT ? r16 : 0);
   int ntiles;
   if constexpr (routed) {
     route_decode(p, rs);
@@ -791,10 +809,11 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
   }
   // jobs of the workgroup: a contiguous range on a schedule (one or two
-  // tiles, one set of activation fragments each); for dense rows (one
-  // tile) every gridDim-th job, so that the workgroups together sweep the
-  // weights in address order (measured 7% faster than contiguous ranges on
-  // a load-only copy of the stream)
+  // tiles); for dense rows (one tile) every gridDim-th job, so that the
+  // workgroups together sweep the weights in address order (measured 7%
+  // faster than contiguous ranges on a load-only copy of the stream; for
+  // the routed stage, whose consecutive jobs then change experts, 12%
+  // slower)
   constexpr bool IL = EPI == EPI_STORE;
   const int J = ntiles * NJ;
   const int lo = IL ? (int)blockIdx.x : (int)((int64_t)blockIdx.x * J / gridDim.x);
@@ -807,14 +826,22 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
 
   // ---- experts and row ids of the range's tiles: scalar loads, issued
   // together; lane r16 keeps row r16 ----
-  const int r16 = lane & 15, kq = lane >> 4;
-  int exA = 0, exB = 0, rid[2];
+  int exA = 0, exB = 0, rid[2] = {-1, -1};
+  // routed: each tile's expert and, per token, its assignment in the tile
+  // (-1: not routed there), copied out of the routing scratch into the
+  // second-tile fragment area (unused with token rows)
+  int* const ste = reinterpret_cast<int*>(&xb[0]);
+  int* const tok2a = ste + RT_MAXTILES;
+  static_assert(!ROUTE || (MT == 2 && (RT_MAXTILES * 17) * 4 <= XB * 16), "routed tables fit the fragment area");
   if constexpr (routed) {  // the schedule routed above, in LDS
-    exA = __builtin_amdgcn_readfirstlane(rs.tile_expert[tA]);
-    exB = __builtin_amdgcn_readfirstlane(rs.tile_expert[tB]);
-    rid[0] = rs.sorted[tA * 16 + r16];
-    rid[1] = rs.sorted[tB * 16 + r16];
-    lds_barrier();  // every wave has read it before the first job reuses the space
+    for (int i = tid; i < ntiles * 16; i += blockDim.x) tok2a[i] = -1;
+    for (int t = tid; t < ntiles; t += blockDim.x) ste[t] = rs.tile_expert[t];
+    __syncthreads();
+    for (int i = tid; i < ntiles * 16; i += blockDim.x) {
+      const int asg = rs.sorted[i];
+      if (asg >= 0) tok2a[(i & ~15) + asg / p.row_div] = asg;
+    }
+    __syncthreads();  // every wave has read the routing scratch before the first job reuses the space
   } else if (p.rows != nullptr) {  // expert schedule (rows and tile_expert both set)
     const int32_t* ra = p.rows + (int64_t)tA * 16;
     const int32_t* rb = p.rows + (int64_t)tB * 16;
@@ -833,29 +860,18 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     rid[0] = tA * 16 + r16 < p.M ? tA * 16 + r16 : -1;
     rid[1] = tB * 16 + r16 < p.M ? tB * 16 + r16 : -1;
   }
-  if (wave == 0 && lane < 32) Rid[kq][r16] = kq == 0 ? rid[0] : rid[1];  // read after the first barrier
+  if (!routed && wave == 0 && lane < 32) Rid[kq][r16] = kq == 0 ? rid[0] : rid[1];  // read after the first barrier
   const int nvalid0 = (int)__popcll(__ballot(lane < 16 && rid[0] >= 0));
   const int nvalid1 = (int)__popcll(__ballot(lane < 16 && rid[1] >= 0));
 
-  // ---- activation fragments (issued before the weights, so that waiting
+  // ---- tile-row fragments (issued before the weights, so that waiting
   // for them does not wait for the weight stream): a padding row reads the
-  // tile's first row, and k-tiles past K repeat the last one (padding rows
-  // are never stored, and those k-tiles get a zero scale) ----
-  V a[MT][4], b[MT][4];
-  {
+  // tile's first row (padding rows are never stored) ----
+  if constexpr (!routed) {
     const int rA = rid[0] >= 0 ? rid[0] : __shfl(rid[0], 0, 64);
     const int rB = rid[1] >= 0 ? rid[1] : __shfl(rid[1], 0, 64);
-    const AT* xa = reinterpret_cast<const AT*>(p.x) + (int64_t)(rA / p.row_div) * p.ldx + 8 * kq;
-    const AT* xbp = reinterpret_cast<const AT*>(p.x) + (int64_t)(rB / p.row_div) * p.ldx + 8 * kq;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const int kt = min(wave + 8 * m, KT - 1);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        a[m][j] = *reinterpret_cast<const V*>(xa + kt * 128 + 32 * j);
-        if constexpr (MT == 2) b[m][j] = *reinterpret_cast<const V*>(xbp + kt * 128 + 32 * j);
-      }
-    }
+    load_frags(a, rA / p.row_div);
+    if constexpr (MT == 2) load_frags(b, rB / p.row_div);
   }
 
   // ---- the weight stream: a wave's share of one job is MT x NQ tiles (16 B
@@ -871,7 +887,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   auto load = [&](int i, u32x4 (&w)[MT][NQ], uint32_t& z) {
     const bool real = i < n;
     const int job = job_of(real ? i : 0);
-    const int tl = job / NJ, nj = job - tl * NJ, e_x = tl == tA ? exA : exB;
+    const int tl = job / NJ, nj = job - tl * NJ;
+    const int e_x = routed ? __builtin_amdgcn_readfirstlane(ste[tl]) : (tl == tA ? exA : exB);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const int kt = min(wave + 8 * m, KT - 1);
@@ -904,7 +921,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
 
   // park the second tile's fragments in LDS, group sums of the first
   if constexpr (MT == 2) {
-    if (ntl > 1) {
+    if (!routed && ntl > 1) {
 #pragma unroll
       for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -977,7 +994,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   auto reduce = [&](int job, int pp, int jj) {
     const int tl = job / NJ, nj = job - tl * NJ, ts = tl == tA ? 0 : 1;
     const int u = tid & 255, l = u >> 2, i4 = u & 3, row = 4 * (l >> 4) + i4;
-    if (row >= (ts == 0 ? nvalid0 : nvalid1)) return;
+    const int orow = routed ? tok2a[tl * 16 + row] : (row < (ts == 0 ? nvalid0 : nvalid1) ? Rid[ts][row] : -1);
+    if (orow < 0) return;
     float pv[NQ][8];
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
@@ -991,7 +1009,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
       for (int w = 1; w < 8; ++w) s += pv[q][w];
       v[q] = s;
     }
-    const int64_t o = (int64_t)Rid[ts][row] * p.ldy + (l & 15);
+    const int64_t o = (int64_t)orow * p.ldy + (l & 15);
     if constexpr (EPI == EPI_SILU) {
       const float g = v[0], up = v[1];
       store_val(p.y, o + nj * 16, g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * up, p.y_dtype);
@@ -1006,7 +1024,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // blocks of D jobs first (loads without conditions), then the rest ----
   const int iB = ntl > 1 ? (tA + 1) * NJ - lo : n;  // first job of the second tile
   auto enter = [&](int i) {
-    if constexpr (MT == 2) {
+    if constexpr (MT == 2 && !routed) {  // (token rows: the same fragments for every tile)
       if (i == iB) {  // the range moves on to its second tile
 #pragma unroll
         for (int m = 0; m < MT; ++m)
@@ -2105,10 +2123,11 @@ static int moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const floa
 }
 
 // Whether a decode batch routes inside the gate/up kernel: the streaming
-// kernels take both stages and the batch fits the in-workgroup router.
+// kernels take both stages, the batch fits the in-workgroup router and has
+// at most 16 tokens (the gate/up kernel's MFMA rows are the tokens).
 static bool fused_route(const MoeLayout& L, const ccq_w4_experts* ex, int64_t k) {
   const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
-  return !L.grouped && L.n <= RT_MAXN && ex->num_experts <= RT_MAXE && k <= 16 &&
+  return !L.grouped && L.n <= RT_MAXN && L.n / k <= 16 && ex->num_experts <= RT_MAXE && k <= 16 &&
          L.n / k * ex->num_experts <= RT_MAXLG &&
          stream_nq(EPI_SILU, I, H, G) > 0 && stream_nq(EPI_ROWS, H, I, G) > 0 && L.max_tiles <= device_cus() &&
          L.max_tiles <= RT_MAXTILES;

@@ -365,8 +365,8 @@ int ccq_moe_w4_ffn_shared(const void* x, int x_dtype, const int64_t* ids, const 
  * there) + ccq_moe_w4_ffn in one call.  logits [T, E] f32 with
  * E = ex->num_experts; ids_out [T, k] int64 and weights_out [T, k] f32
  * receive the routing (either may be null: the workspace keeps it);
- * workspace as ccq_moe_w4_ffn.  Decode batches (T*k <= 256, E <= 256, T*E <= 4096,
- * k <= 16) route inside the gate/up kernel's workgroups (three launches in
+ * workspace as ccq_moe_w4_ffn.  Decode batches (T <= 16, T*k <= 256, E <= 256,
+ * T*E <= 4096, k <= 16) route inside the gate/up kernel's workgroups (three launches in
  * all); larger ones run the routing kernel and ccq_moe_w4_ffn.  Same results
  * either way.  Replaces moe_forward (models/generic.py:348-378): topk_softmax
  * + expert grouping + expert_ffn + combine. */

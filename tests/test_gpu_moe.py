@@ -226,8 +226,8 @@ def test_moe_w4_large_batch_schedule_matches_align(gpu):
     assert np.abs(y.cpu().numpy() - r).max() <= TOL * np.abs(r).max()
 
 
-@pytest.mark.parametrize("E,T,k,skew", [(64, 16, 6, 0.0), (64, 42, 6, 5.0), (128, 32, 8, 3.0), (256, 16, 8, 2.0),
-                                         (8, 1, 2, 0.0), (5, 7, 5, 0.0)])
+@pytest.mark.parametrize("E,T,k,skew", [(64, 16, 6, 0.0), (64, 16, 16, 5.0), (128, 16, 12, 3.0), (256, 16, 8, 2.0),
+                                         (64, 42, 6, 5.0), (128, 32, 8, 3.0), (8, 1, 2, 0.0), (5, 7, 5, 0.0)])
 def test_moe_w4_routed_schedule_matches_align(gpu, E, T, k, skew):
     """Decode batches routed inside the gate/up kernel: the routing equals
     the oracle's topk_softmax, and the expert schedule the layer leaves at
