@@ -203,13 +203,14 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
       __builtin_amdgcn_wave_barrier();
     }
   }
-  // padding and tile -> expert map
-  for (int i = tid; i < nactive; i += 1024) {
+  // padding and tile -> expert map: a wave per expert, its lanes over the
+  // expert's padding slots and tiles
+  for (int i = w; i < nactive; i += kAlignWaves) {
     const int e = sm.inv[i];
     const int b = sm.base[e], c = sm.cnt[e];
     const int p = (int)cdiv(c, tile_m) * tile_m;
-    for (int j = c; j < p; ++j) sorted_ids[b + j] = -1;
-    for (int t = b / tile_m; t < (b + p) / tile_m; ++t) tile_expert[t] = e;
+    for (int j = c + lane; j < p; j += 64) sorted_ids[b + j] = -1;
+    for (int t = b / tile_m + lane; t < (b + p) / tile_m; t += 64) tile_expert[t] = e;
   }
 }
 
