@@ -570,10 +570,10 @@ struct RbStage {
   // and SA - 2 whole steps)
   static constexpr int WAIT_A = NB + (SA - 2) * N_OPS;
   // vmcnt allowed while waiting for the weights of step g (loaded at step
-  // g - RB_D, followed by RB_D - 1 whole steps and step g's copies; the
-  // prologue follows each of its weight loads by A_OPS pad copies, so the
-  // count holds from step 0)
-  static constexpr int WAIT_B = (RB_D - 1) * N_OPS + A_OPS;
+  // g - RB_D, followed by RB_D - 1 whole steps; step g's copies are issued
+  // after this wait; the prologue follows each of its weight loads by A_OPS
+  // pad copies, so the count also holds, with room, from step 0)
+  static constexpr int WAIT_B = (RB_D - 1) * N_OPS;
   static_assert(WAIT_A < 64 && WAIT_B < 64, "vmcnt is 6 bits");
 };
 template <bool LO>
@@ -737,7 +737,9 @@ __global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
   // One K block over the row tiles holding valid rows (nrt = 1..4,
   // wave-uniform), software-pipelined: the MFMAs of row tile rt + 1 are
   // issued before the scaling of row tile rt, which then runs under them.
-  auto compute = [&](int slot, int nrt, const i32x8 (&bq)[CG][2]) {
+  // mid (the activation copies of a later step) runs after the first row
+  // tile's MFMAs are issued, so that its scalar work overlaps them
+  auto compute = [&](int slot, int nrt, const i32x8 (&bq)[CG][2], auto&& mid) {
     const char* S = smem + slot * SL::BYTES;
     // block scales of the wave's columns: gate (copy 0) and up (copy 1), or
     // the one block of the down columns
@@ -776,6 +778,7 @@ __global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
       for (int i = 0; i < 16; ++i) acc[rt][0][i] = fmaf(i < 8 ? f0 : f1, t[i], acc[rt][0][i]);
     };
     f32x16 t = mma(0);
+    mid();
 #pragma unroll
     for (int rt = 1; rt < 4; ++rt) {
       if (rt < nrt) {
@@ -947,12 +950,16 @@ __global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
         if (j + 2 < nmine) fetch_rows(j + 2);
         if (j > 0 && j + 1 < nmine) make_plan(j + 1, nxt);
       }
-      {
+      // the activation copies of step g + SA - 1 go into the slot step g - 1
+      // used (free after the barrier), issued inside the compute after this
+      // step's weight wait; every step issues them, so the per-step order of
+      // memory operations (copies, then weight loads) is unchanged
+      auto copy_ahead = [&]() {
         bool nx_;
         int pk;
         ahead_of(j, kb, SA - 1, nx_, pk);
         issue_a(nx_, pk, slot == 0 ? SA - 1 : slot - 1);
-      }
+      };
       wait_vmcnt_tied<SL::WAIT_B>(bq[d][0][0], bq[d][0][1], bq[d][1][0], bq[d][1][1]);
       {
         i32x8 bw[CG][2];
@@ -961,7 +968,7 @@ __global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
           const u32x4 lo = bq[d][st][0], hi = bq[d][st][1];
           bw[0][st] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         }
-        compute(slot, (cur.nvalid + 31) >> 5, bw);
+        compute(slot, (cur.nvalid + 31) >> 5, bw, copy_ahead);
       }
       {
         bool nx_;
