@@ -186,6 +186,150 @@ __global__ __launch_bounds__(256) void ref_linear_f32_kernel(const float* __rest
     for (int b = 0; b < nb; ++b) y[(b0 + b) * out_f + r] = acc[b];
 }
 
+// The same Linear for the byte formats (fp8 e4m3, int8; one scale per output
+// row) and int4 (one scale per input column), streaming W in 16-byte pieces.
+// A workgroup is 4 waves x RT output rows; lane l of a wave takes bytes
+// 16 l + 1024 i of each of its rows (all RT rows at once, so every lane
+// reads its piece of x once per RT rows), BB batch rows per pass from x
+// staged in LDS (int4: x[c] * s[c] staged, the column scale taken out of
+// the sum; fp8/int8: the row scale applied to the row's sum).  fp8 codes
+// decode with the hardware converter (v_cvt_pk_f32_fp8: e4m3fn, exact,
+// NaN for 0x7F / 0xFF as fp8_e4m3_to_f32 above).  Sums are float32 FMAs,
+// in a different order from ref_linear_f32_kernel.
+// rows per wave: 8 for passes of 2+ batch rows (halves the x reads per
+// weight; measured 46 -> 26 us at 4 x 4096 x 14336), 4 for single rows (more
+// waves for small N)
+template <int BB>
+constexpr int rv_rows() { return BB == 1 ? 4 : 8; }
+constexpr int RV_LDS = 64 * 1024;     // staged x bytes per workgroup at most
+
+// Sums over the wave of V values per lane (V a power of two <= 64): halving
+// exchanges (V - 1 shuffles), then whole-value ones; lane l ends with the
+// sum of value l & (V - 1), in a fixed order.
+template <int V>
+__device__ __forceinline__ float wave_reduce_scatter(float (&v)[V], int lane) {
+#pragma unroll
+  for (int m = 1, n = V; m < V; m <<= 1, n >>= 1) {
+    const bool up = (lane & m) != 0;
+#pragma unroll
+    for (int j = 0; j < n / 2; ++j) {
+      const float keep = up ? v[2 * j + 1] : v[2 * j];
+      const float send = up ? v[2 * j] : v[2 * j + 1];
+      v[j] = keep + __shfl_xor(send, m, 64);
+    }
+  }
+  float t = v[0];
+#pragma unroll
+  for (int m = V; m < 64; m <<= 1) t += __shfl_xor(t, m, 64);
+  return t;
+}
+
+template <int kFmt, int BB>
+__global__ __launch_bounds__(256) void ref_linear_vec_kernel(const float* __restrict__ x,
+                                                             const uint8_t* __restrict__ w,
+                                                             const float* __restrict__ scale,
+                                                             float* __restrict__ y, int64_t batch,
+                                                             int64_t in_f, int64_t out_f) {
+  extern __shared__ __align__(16) float xs[];  // [BB][in_f]
+  constexpr bool kNib = kFmt == 0;
+  constexpr int RV_RT = rv_rows<BB>();
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b0 = (int64_t)blockIdx.y * BB;
+  const int nb = (int)min<int64_t>(BB, batch - b0);
+  // x rows of this pass (rows past the batch: zeros), int4 with the column
+  // scale; 16 bytes per thread and copy, 8 copies in flight per thread
+  const int q4 = (int)(in_f / 4), nq = BB * q4;  // 16-byte pieces per row, per pass
+  for (int i0 = 0; i0 < nq; i0 += 8 * 256) {
+    f32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 256 + tid, b = i / q4, c4 = i - b * q4;
+      v[u] = i < nq && b < nb ? *reinterpret_cast<const f32x4*>(x + (b0 + b) * in_f + 4 * c4)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+      if (kNib && i < nq) {
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(scale + 4 * c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] *= sc[e];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 256 + tid;
+      if (i < nq) *reinterpret_cast<f32x4*>(&xs[4 * i]) = v[u];
+    }
+  }
+  __syncthreads();
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * RV_RT;
+  if (row0 >= out_f) return;
+  const int64_t row_bytes = kNib ? in_f / 2 : in_f;  // a multiple of 16
+  const uint8_t* wr[RV_RT];
+#pragma unroll
+  for (int r = 0; r < RV_RT; ++r) wr[r] = w + min(row0 + r, out_f - 1) * row_bytes;  // past the end: the last row, not stored
+  float acc[RV_RT][BB];
+#pragma unroll
+  for (int r = 0; r < RV_RT; ++r)
+#pragma unroll
+    for (int b = 0; b < BB; ++b) acc[r][b] = 0.f;
+  for (int64_t off = (int64_t)lane * 16; off < row_bytes; off += 1024) {
+    u32x4 q[RV_RT];
+#pragma unroll
+    for (int r = 0; r < RV_RT; ++r) q[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr[r] + off));
+    constexpr int NE = kNib ? 32 : 16;  // elements per 16-byte piece
+    const int64_t c0 = kNib ? 2 * off : off;
+#pragma unroll
+    for (int h = 0; h < NE / 8; ++h) {  // 8 elements (32 x bytes per batch row) at a time
+      float xv[BB][8];
+#pragma unroll
+      for (int b = 0; b < BB; ++b) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(&xs[b * in_f + c0 + 8 * h]);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(&xs[b * in_f + c0 + 8 * h + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xv[b][e] = lo[e];
+          xv[b][4 + e] = hi[e];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RV_RT; ++r) {
+        float wv[8];
+        if constexpr (kFmt == 1) {  // fp8: bytes 8h .. 8h + 7 of the piece
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const uint32_t word = q[r][2 * h + d];
+            const auto p0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+            const auto p1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
+            wv[4 * d] = p0[0];
+            wv[4 * d + 1] = p0[1];
+            wv[4 * d + 2] = p1[0];
+            wv[4 * d + 3] = p1[1];
+          }
+        } else if constexpr (kFmt == 2) {  // int8
+#pragma unroll
+          for (int e = 0; e < 8; ++e) wv[e] = (float)((int)(q[r][(8 * h + e) >> 2] << (24 - 8 * (e & 3))) >> 24);
+        } else {  // int4: nibbles 8h .. 8h + 7 = word h, low nibble first (column 2j, 2j + 1 of byte j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) wv[e] = (float)((int)(q[r][h] << (28 - 4 * e)) >> 28);  // signed nibble
+        }
+#pragma unroll
+        for (int b = 0; b < BB; ++b)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r][b] = fmaf(xv[b][e], wv[e], acc[r][b]);
+      }
+    }
+  }
+  float flat[RV_RT * BB];
+#pragma unroll
+  for (int r = 0; r < RV_RT; ++r)
+#pragma unroll
+    for (int b = 0; b < BB; ++b) flat[r * BB + b] = acc[r][b];
+  const float v = wave_reduce_scatter<RV_RT * BB>(flat, lane);
+  if (lane < RV_RT * BB) {  // lane l: row l / BB, batch row l % BB
+    const int r = lane / BB, b = lane % BB;
+    const int64_t row = row0 + r;
+    if (row < out_f && b < nb) y[(b0 + b) * out_f + row] = kNib ? v : v * scale[row];
+  }
+}
+
 // out = g / (1 + exp(-g)) * u in float64, stored float32 (kernels.py:219-231)
 // out[i] = s[i / G] for i < groups * G.
 __global__ void group_broadcast_kernel(const float* __restrict__ s, float* __restrict__ out, int64_t n, int64_t G) {
@@ -573,6 +717,39 @@ static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* sc
   if (in_f == 0) {  // empty sum; a fill kernel rather than a memset node
     hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_for(batch * out_f, 256)), dim3(256), 0, as_stream(stream), y,
                        batch * out_f);
+    return launch_status(name);
+  }
+  // the streaming kernel: fp8 / int8 / int4 rows of whole 16-byte pieces,
+  // 16-byte aligned, x rows that fit the staging area
+  const int64_t rbytes = fmt == 0 ? in_f / 2 : in_f;
+  if (fmt != 3 && rbytes % 16 == 0 && aligned(w, 16) && aligned(x, 16) && (fmt != 0 || aligned(scale, 16)) &&
+      in_f * 4 <= RV_LDS) {
+    // batch rows per pass: as many as the batch and the staging area allow
+    int bb = 1;
+    while (bb < 8 && bb * 2 <= batch && in_f * 4 * bb * 2 <= RV_LDS) bb *= 2;
+    const dim3 g((unsigned)cdiv(out_f, 4 * (bb == 1 ? rv_rows<1>() : rv_rows<2>())), (unsigned)cdiv(batch, bb));
+    CCQ_REQUIRE(cdiv(batch, bb) <= 65535, "%s: batch too large", name);
+    const size_t lds = (size_t)bb * in_f * 4;
+#define CCQ_RV(F, B) hipLaunchKernelGGL((ref_linear_vec_kernel<F, B>), g, dim3(256), lds, as_stream(stream), x, w, scale, y, batch, in_f, out_f)
+#define CCQ_RV_B(F)   \
+  do {                \
+    if (bb == 8)      \
+      CCQ_RV(F, 8);   \
+    else if (bb == 4) \
+      CCQ_RV(F, 4);   \
+    else if (bb == 2) \
+      CCQ_RV(F, 2);   \
+    else              \
+      CCQ_RV(F, 1);   \
+  } while (0)
+    if (fmt == 1)
+      CCQ_RV_B(1);
+    else if (fmt == 2)
+      CCQ_RV_B(2);
+    else
+      CCQ_RV_B(0);
+#undef CCQ_RV_B
+#undef CCQ_RV
     return launch_status(name);
   }
   if (fmt == 1)

@@ -169,3 +169,79 @@ def test_group_broadcast_scale_bitexact(gpu, groups, G):
     d = dev.cpu().numpy()
     assert np.array_equal(d[: groups * G].view(np.uint32), ref.view(np.uint32)) and np.all(d[groups * G:] == -1.0)
     assert np.array_equal(qk.group_broadcast_scale(s, G, None), ref)
+
+
+# ---- the streaming float32 Linear (16-byte weight pieces, x staged in LDS):
+# rows whose bytes are whole 16-byte pieces; batches 1..17 cover the 1-, 2-
+# and 4-row passes and their remainders, out_features not a multiple of the
+# 16 rows of a workgroup.  The bound is the float32 summation error scale
+# |x| @ |W|.T (the order of the sum differs from the oracle's); a wrong
+# element, row or scale is off by the size of y itself.
+def _err_ok(y, ref, x, w_f32):
+    bound = np.abs(x).astype(np.float64) @ np.abs(w_f32).astype(np.float64).T
+    return bool(np.all(np.abs(y.astype(np.float64) - ref.astype(np.float64)) <= 1e-5 * bound + 1e-30))
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 9, 17])
+@pytest.mark.parametrize("out_f,in_f", [(37, 512), (300, 2048)])
+def test_fp8_linear_f32_streaming(gpu, batch, out_f, in_f):
+    from ccut.quant.method import fp8_linear_f32
+
+    rng = np.random.default_rng(1000 * batch + out_f)
+    w = rng.integers(0, 0x7F, size=(out_f, in_f), dtype=np.uint8)  # no NaN codes
+    w[rng.random(w.shape) < 0.5] |= 0x80
+    s = (rng.random(out_f) * 0.1 + 1e-3).astype(np.float32)
+    x = rng.standard_normal((batch, in_f)).astype(np.float32)
+    y = fp8_linear_f32(w.tobytes(), s, x)
+    ref = rq.fp8_linear_apply(w.tobytes(), s, x)
+    assert y.shape == ref.shape
+    assert _err_ok(y, ref, x, rq.fp8_dequant_mat(w, s))
+
+
+def test_fp8_linear_f32_streaming_all_codes_exact(gpu):
+    """One-hot x: y[0, r] = fp8(code r) * s[r] with one rounding, as the
+    reference forms W; every code, NaN codes included (rows of zeros
+    elsewhere, so 0 * NaN never enters a sum)."""
+    from ccut.quant.method import fp8_linear_f32
+
+    in_f, c0 = 64, 37
+    w = np.zeros((256, in_f), dtype=np.uint8)
+    w[:, c0] = np.arange(256, dtype=np.uint8)
+    s = np.linspace(0.5, 3.0, 256).astype(np.float32)
+    x = np.zeros((1, in_f), dtype=np.float32)
+    x[0, c0] = 1.0
+    y = fp8_linear_f32(w.tobytes(), s, x)[0] + np.float32(0)  # -0 -> +0, as the sum over the row gives
+    want = rq.fp8_dequant_mat(w, s)[:, c0] + np.float32(0)
+    nan = np.isnan(want)
+    assert nan.sum() == 2 and np.array_equal(np.isnan(y), nan)
+    assert np.array_equal(y[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("batch", [1, 4, 6])
+@pytest.mark.parametrize("out_f,in_f", [(19, 256), (130, 4096)])
+def test_int8_linear_f32_streaming(gpu, batch, out_f, in_f):
+    from ccut.quant.int8 import w8a16_linear
+    from oracle import int8 as oi8
+
+    rng = np.random.default_rng(7 * batch + in_f)
+    w = rng.integers(-128, 128, size=(out_f, in_f), dtype=np.int8)
+    s = (rng.random(out_f) * 0.02 + 1e-3).astype(np.float32)
+    x = rng.standard_normal((batch, in_f)).astype(np.float32)
+    y = w8a16_linear(w.tobytes(), s, x)
+    y = y.cpu().numpy() if isinstance(y, torch.Tensor) else y
+    ref = oi8.w8a16(w, s, x)
+    assert _err_ok(y, ref, x, oi8.dequant_row(w, s))
+
+
+@pytest.mark.parametrize("batch", [1, 2, 8])
+@pytest.mark.parametrize("out_f,in_f", [(21, 64), (260, 2048)])
+def test_int4_linear_f32_streaming(gpu, batch, out_f, in_f):
+    from ccut.quant.weight_only import int4_linear_f32
+
+    rng = np.random.default_rng(3 * batch + out_f)
+    p = rng.integers(0, 256, size=(out_f, in_f // 2), dtype=np.uint8)
+    s = (rng.random(in_f) + 0.1).astype(np.float32)
+    x = rng.standard_normal((batch, in_f)).astype(np.float32)
+    y = int4_linear_f32(p.tobytes(), s, x)
+    ref = rq.weight_only_apply(p.tobytes(), s, x)
+    assert _err_ok(y, ref, x, rq.int4_dequant_row(p, s))
