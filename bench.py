@@ -364,6 +364,38 @@ def bench_int8(M: int, K: int, N: int, dev, copies: int = 1):
             "TOPs": ops / avg / 1e12, "frac_int8_peak": ops / avg / PEAK_INT8, "workspace_bytes": nws}
 
 
+def bench_ref_fp8_linear(M: int, K: int, N: int, dev, copies: int = 12):
+    """The reference's own FP8 format (e4m3fn ``[N, K]``, one float32 scale
+    per output row, the checkpoints' per-channel FP8) through
+    ``ccq_fp8_linear_f32``: y = x @ (fp8(W) * s).T in float32 for float32 x
+    [M, K]; device time per call over ``copies`` distinct weight matrices.
+    Algorithmic bytes: N*K + 4*N + 4*M*K + 4*M*N."""
+    import torch
+
+    from ccut import _lib
+
+    lib = _lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = ctypes.c_void_p
+    g = torch.Generator(device=dev).manual_seed(17)
+    ws = [torch.randint(0, 0x7F, (N, K), generator=g, device=dev, dtype=torch.uint8) for _ in range(copies)]
+    sc = torch.rand(N, generator=g, device=dev) * 0.01
+    x = torch.randn((M, K), generator=g, device=dev)
+    y = torch.empty((M, N), device=dev)
+
+    def call(w):
+        _lib.check(lib.ccq_fp8_linear_f32(vp(x.data_ptr()), vp(w.data_ptr()), vp(sc.data_ptr()), vp(y.data_ptr()),
+                                          M, K, N, stream), "ccq_fp8_linear_f32")
+
+    launches = [lambda w=w: call(w) for w in ws]
+    launches[0]()
+    torch.cuda.synchronize()
+    avg = device_time(launches, reps=max(1, 24 // copies))
+    nb = N * K + 4 * N + 4 * M * K + 4 * M * N
+    return {"avg_us": avg * 1e6, "bytes": nb, "GBps": nb / avg / 1e9, "frac_hbm": nb / avg / PEAK_HBM,
+            "weight_sets": copies}
+
+
 def bench_mx(fmt: str, M: int, K: int, N: int, dev, copies: int = 6):
     """MX linear y = x @ W.T through ``ccut.quant.mx.mx_linear`` (the fused
     dequant-linear up to 8 batch rows, dequant + float32 library GEMM above),
@@ -673,6 +705,11 @@ def main():
             extra[f"int8_w8a8_k4096_n14336_m{M}"] = r
             log(f"int8 w8a8 K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "
                 f"({r['frac_hbm']:.3f} of HBM peak), {r['TOPs']:.1f} TOP/s ({r['frac_int8_peak']:.3f} of int8 peak)")
+        for M in (1, 4, 16):
+            r = bench_ref_fp8_linear(M, 4096, 14336, dev)
+            extra[f"ref_fp8_rowscale_linear_k4096_n14336_m{M}"] = r
+            log(f"reference FP8 per-row linear K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "
+                f"({r['frac_hbm']:.3f} of HBM peak)")
         for fmt, M in (("mxfp4", 1), ("mxfp8", 1), ("mxfp4", 16)):
             r = bench_mx(fmt, M, 4096, 14336, dev)
             extra[f"{fmt}_linear_k4096_n14336_m{M}"] = r
