@@ -397,8 +397,8 @@ def bench_ref_fp8_linear(M: int, K: int, N: int, dev, copies: int = 12):
 
 
 def bench_mx(fmt: str, M: int, K: int, N: int, dev, copies: int = 6):
-    """MX linear y = x @ W.T through ``ccut.quant.mx.mx_linear`` (the fused
-    dequant-linear up to 8 batch rows, dequant + float32 library GEMM above),
+    """MX linear y = x @ W.T through ``ccut.quant.mx.mx_linear`` (the
+    decoded-weight MFMA kernel, W formed in registers, bf16 hi/lo products),
     ``copies`` distinct weights.  Algorithmic bytes: weight codes + E8M0
     scales (one per 32 columns) + 4*M*K (x) + 4*M*N (y)."""
     import torch
@@ -710,7 +710,7 @@ def main():
             extra[f"ref_fp8_rowscale_linear_k4096_n14336_m{M}"] = r
             log(f"reference FP8 per-row linear K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "
                 f"({r['frac_hbm']:.3f} of HBM peak)")
-        for fmt, M in (("mxfp4", 1), ("mxfp8", 1), ("mxfp4", 16)):
+        for fmt, M in (("mxfp4", 1), ("mxfp8", 1), ("mxfp4", 16), ("mxfp8", 16), ("mxfp4", 64)):
             r = bench_mx(fmt, M, 4096, 14336, dev)
             extra[f"{fmt}_linear_k4096_n14336_m{M}"] = r
             log(f"{fmt} linear K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "

@@ -86,6 +86,7 @@ SIGNATURES: dict[str, tuple] = {
                                       ctypes.POINTER(ccq_fp8_experts), _vp, _sz, _vp]),
     "ccq_mx_dequant": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, ctypes.c_float, _vp]),
     "ccq_mx_linear_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp]),
+    "ccq_wq_mfma_linear_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, ctypes.c_float, _vp]),
     "ccq_awq_dequant": (_int, [_vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
     "ccq_awq_repack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ccq_awq_unpack_tiled": (_int, [_vp, _vp, _i64, _i64, _vp]),

@@ -68,12 +68,6 @@ def _args(weight_bytes, scale, rows_hint: int | None, cols: int, fmt: int, group
     return raw, sc, rows
 
 
-# Batches up to this size run the fused kernel (W formed in registers, the
-# weight bytes read once); larger ones dequantize W to float32 once and run
-# a plain float32 library GEMM, the reference's own dequant-then-matmul.
-FUSED_MAX_BATCH = 8
-
-
 def mx_linear(weight_bytes, scale, x, weight_dtype: str, group_size: int = 32, scale2: float | None = None):
     """``x @ W.T`` (float32) for MX weights; numpy in -> numpy out."""
     fmt = _fmt(weight_dtype)
@@ -83,15 +77,11 @@ def mx_linear(weight_bytes, scale, x, weight_dtype: str, group_size: int = 32, s
     batch, in_f = xd.shape
     raw, sc, rows = _args(weight_bytes, scale, None, in_f, fmt, group_size)
     s2 = float(1.0 if scale2 is None else np.float32(scale2))
-    if batch > FUSED_MAX_BATCH:
-        w = torch.empty((rows, in_f), dtype=torch.float32, device=xd.device)
-        call("ccq_mx_dequant", raw.data_ptr(), sc.data_ptr() if sc is not None else None, w.data_ptr(), rows, in_f,
-             fmt, group_size, s2, _dev.stream_ptr())
-        y = xd @ w.T
-    else:
-        y = torch.empty((batch, rows), dtype=torch.float32, device=xd.device)
-        call("ccq_mx_linear_f32", xd.data_ptr(), raw.data_ptr(), sc.data_ptr() if sc is not None else None,
-             y.data_ptr(), batch, in_f, rows, fmt, group_size, s2, _dev.stream_ptr())
+    # one call for every batch size: W formed in registers; from 8 rows on,
+    # in_features % 256 == 0, the products run on the matrix cores
+    y = torch.empty((batch, rows), dtype=torch.float32, device=xd.device)
+    call("ccq_mx_linear_f32", xd.contiguous().data_ptr(), raw.data_ptr(), sc.data_ptr() if sc is not None else None,
+         y.data_ptr(), batch, in_f, rows, fmt, group_size, s2, _dev.stream_ptr())
     return _dev.to_host(y) if _dev.is_host(x) else y
 
 

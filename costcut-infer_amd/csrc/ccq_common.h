@@ -117,6 +117,47 @@ __device__ __forceinline__ uint32_t f32_to_fp8_rne(float v) {
   return sign | code;
 }
 
+// ---------------------------------------------------------- MX decoders --
+// E8M0 scale byte -> float: 2^(e-127); e = 0 -> 0 and e = 255 -> NaN, as
+// the reference's mx_e8m0_to_float (quant/kernels.py:240-256).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  return e == 0u ? 0.f : (e == 255u ? __int_as_float(0x7fc00000) : __int_as_float((int)(e << 23)));
+}
+
+typedef _Float16 mx_h2 __attribute__((ext_vector_type(2)));
+
+// Columns 8w..8w+7 of one 32-bit word of the reference's 4-bit codes (low
+// nibble = even column; table 0, .5, 1, 1.5, -0, -.5, -1, -1.5 on code & 7,
+// quant/mx.py:80), as float32: one v_perm_b32 per 4 codes picks the f16
+// high bytes of the table's values (their low bytes are all zero), then
+// v_cvt_f32_f16.
+__device__ __forceinline__ void mx4_word(uint32_t w, float (&v)[8]) {
+  constexpr uint32_t kLutLo = 0x3E3C3800u;  // f16 high bytes of 0, .5, 1, 1.5
+  constexpr uint32_t kLutHi = 0xBEBCB880u;  // and of -0, -.5, -1, -1.5
+  const uint32_t e = __builtin_amdgcn_perm(kLutHi, kLutLo, w & 0x07070707u);         // even columns
+  const uint32_t o = __builtin_amdgcn_perm(kLutHi, kLutLo, (w >> 4) & 0x07070707u);  // odd columns
+  const uint32_t sel[4] = {0x040C000Cu, 0x050C010Cu, 0x060C020Cu, 0x070C030Cu};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const mx_h2 hv = __builtin_bit_cast(mx_h2, __builtin_amdgcn_perm(o, e, sel[b]));
+    v[2 * b] = (float)hv.x;
+    v[2 * b + 1] = (float)hv.y;
+  }
+}
+
+// ------------------------------------- decoded-weight MFMA linear (host) --
+// y[M, N] = x[M, K] @ W[N, K]^T on bf16 MFMA with the weights decoded in
+// registers (ccq_wmfma.hip).  fmt: WQ_FP8_ROW e4m3 codes with a float32
+// scale per output row; WQ_INT8_ROW int8 codes, float32 row scale;
+// WQ_MXFP8 e4m3 codes with E8M0 group scales [N, K / G]; WQ_MXFP4 the
+// reference's 4-bit codes (two per byte) with optional E8M0 group scales and
+// the factor scale2 on each sum.  Returns 0 or a launch status, or -1 when
+// the shape or alignment is not one the kernel takes (the caller then runs
+// its own kernel); nothing is launched in that case.
+enum WqFmt { WQ_FP8_ROW = 0, WQ_INT8_ROW = 1, WQ_MXFP8 = 2, WQ_MXFP4 = 3 };
+int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale, int group_size, float scale2,
+                   float* y, int64_t M, int64_t K, int64_t N, hipStream_t stream, const char* name);
+
 // --------------------------------------------------------- wave helpers --
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 

@@ -1,0 +1,272 @@
+// Decoded-weight MFMA linear: y[M, N] = x[M, K] @ W[N, K]^T, float32 in and
+// out, for the byte-coded weight formats whose reference layers dequantize W
+// to float32 and multiply (Fp8LinearMethod.apply / LinearMethod.apply for
+// fp8 and int8 keys, quant/fp8.py:35-42, quant/method.py:100-140; the MX
+// formats of MxLinearMethod.apply, quant/mx.py:37-94).  For batches past a
+// few rows the streaming kernels re-read W once per pass of batch rows; this
+// kernel reads W once for up to 64 rows and runs the products on the
+// matrix cores.
+//
+// Arithmetic.  Each weight is decoded in registers to its exact value in
+// bf16: e4m3 codes (4 significant bits) times a power-of-two E8M0 scale,
+// int8 codes (8 bits), the reference's 4-bit table values times the E8M0
+// scale -- all exact in bf16 while the scaled value stays a normal float.
+// Activations are split x = hi + lo with hi = bf16(x), lo = bf16(x - hi)
+// (|x - hi - lo| <= 2^-17 |x|), and every k-step runs two MFMAs,
+// v_mfma_f32_16x16x32_bf16(hi, W) and (lo, W): products of bf16 values are
+// exact in the float32 accumulator, so y carries float32 summation error
+// only, in an order of its own.  Row scales (FP8 / INT8 per row) and NVFP4's
+// second scale multiply the finished sum, as the streaming kernels do.
+//
+// Tiling.  A workgroup of 8 waves owns 64 output columns and up to 64 batch
+// rows (MT tiles of 16; more rows -> more workgroups along y, each reading W
+// again).  K runs in chunks of 256: waves 0-3 take the first 128 k of a
+// chunk, waves 4-7 the second, each wave 16 columns, and the two halves'
+// partial sums are added at the end through LDS in a fixed order.  Lane l
+// of a wave holds column l & 15 and the 32 consecutive k of quarter q =
+// l >> 4 of its half; MFMA i of the chunk takes each lane's values
+// 8i..8i+7, so its 32 k are a fixed permutation of the chunk's -- the same
+// permutation on the activation side, read from LDS.  The activation chunk
+// (hi and lo bf16, [16 MT][256]) is staged in LDS, double-buffered, one
+// barrier per chunk.  Weights (non-temporal loads), scale bytes and the
+// activation chunk are loaded PD chunks ahead into a register ring, so the
+// wait for chunk c leaves chunks c+1..c+PD-1 in flight.
+#include "ccq_common.h"
+
+namespace ccq {
+
+constexpr int WQ_KC = 256;                 // k per chunk
+constexpr int WQ_CG = 4;                   // 16-column groups per workgroup
+constexpr int WQ_THREADS = 512;            // 8 waves: 4 column groups x 2 k halves
+constexpr int WQ_RS = WQ_KC + 8;           // LDS row stride in bf16 (rows 4 banks apart)
+constexpr int WQ_COLS = 16 * WQ_CG;        // output columns per workgroup
+
+struct WqP {
+  const float* x;
+  const uint8_t* w;
+  const void* scale;  // float [N] (row formats), E8M0 bytes [N, K / G] (MX), or null (MXFP4 only)
+  float* y;
+  int64_t M, K, N;
+  int G;
+  float s2;
+};
+
+template <int FMT>
+struct WqTraits {
+  static constexpr int WB = FMT == WQ_MXFP4 ? 1 : 2;      // 16-byte weight pieces per lane and chunk
+  static constexpr int KDIV = FMT == WQ_MXFP4 ? 2 : 1;    // k per weight byte
+  static constexpr bool MX = FMT == WQ_MXFP8 || FMT == WQ_MXFP4;
+};
+
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float (&v)[8]) {
+  u32x4 r;
+  r[0] = bf16x2_bits(v[0], v[1]);
+  r[1] = bf16x2_bits(v[2], v[3]);
+  r[2] = bf16x2_bits(v[4], v[5]);
+  r[3] = bf16x2_bits(v[6], v[7]);
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// The lane's weight values 8i..8i+7 of the chunk (times the group scale s
+// for the MX formats) as the MFMA's B fragment.
+template <int FMT>
+__device__ __forceinline__ bf16x8 wq_decode(const u32x4 (&wr)[WqTraits<FMT>::WB], int i, float s) {
+  float v[8];
+  if constexpr (FMT == WQ_MXFP4) {
+    mx4_word(wr[0][i], v);
+  } else {
+    const uint32_t w0 = wr[i >> 1][(i & 1) * 2], w1 = wr[i >> 1][(i & 1) * 2 + 1];
+    if constexpr (FMT == WQ_INT8_ROW) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = (float)(int8_t)(w0 >> (8 * j));
+        v[4 + j] = (float)(int8_t)(w1 >> (8 * j));
+      }
+    } else {
+      const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w0, false);
+      const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w0, true);
+      const auto c = __builtin_amdgcn_cvt_pk_f32_fp8((int)w1, false);
+      const auto d = __builtin_amdgcn_cvt_pk_f32_fp8((int)w1, true);
+      v[0] = a[0], v[1] = a[1], v[2] = b[0], v[3] = b[1];
+      v[4] = c[0], v[5] = c[1], v[6] = d[0], v[7] = d[1];
+    }
+  }
+  if constexpr (WqTraits<FMT>::MX) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= s;
+  }
+  return pack_bf16x8(v);
+}
+
+template <int FMT, int MT, int PD>
+__global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
+  using Tr = WqTraits<FMT>;
+  constexpr int XR = 2 * MT;  // activation float4s per thread and chunk
+  __shared__ __align__(16) uint16_t Xh[2][16 * MT][WQ_RS];
+  __shared__ __align__(16) uint16_t Xl[2][16 * MT][WQ_RS];
+  __shared__ __align__(16) f32x4 red[WQ_CG][MT][64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = wave & 3, kh = wave >> 2;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int64_t M = p.M, K = p.K, N = p.N;
+  const int64_t n = (int64_t)blockIdx.x * WQ_COLS + 16 * cg + c16;
+  const int64_t m0 = (int64_t)blockIdx.y * 16 * MT;
+  const int nch = (int)(K / WQ_KC);
+  const int64_t row_bytes = K / Tr::KDIV;
+  const uint8_t* wrow = p.w + imin64(n, N - 1) * row_bytes;  // columns past N read row N-1, never stored
+  const int lane_k = kh * (WQ_KC / 2) + q * 32;             // first k of the lane's 32 in a chunk
+  const int64_t gpr = Tr::MX ? K / p.G : 0;
+  const uint8_t* srow = Tr::MX && p.scale ? reinterpret_cast<const uint8_t*>(p.scale) + imin64(n, N - 1) * gpr : nullptr;
+
+  u32x4 wr[PD][Tr::WB];
+  uint32_t sr[PD];
+  float4 xr[PD][XR];
+
+  auto load_chunk = [&](int s, int c) {
+    const int64_t kb = (int64_t)c * WQ_KC;
+    const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + (kb + lane_k) / Tr::KDIV);
+#pragma unroll
+    for (int j = 0; j < Tr::WB; ++j) wr[s][j] = __builtin_nontemporal_load(wp + j);
+    if constexpr (Tr::MX) {
+      sr[s] = 127u;  // scale 1 for MXFP4 without scales
+      if (srow) {
+        const int64_t g0 = (kb + lane_k) / p.G;
+        sr[s] = p.G == 32 ? (uint32_t)srow[g0] : (uint32_t)*reinterpret_cast<const uint16_t*>(srow + g0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+      const int idx = tid + WQ_THREADS * j, row = idx >> 6, col4 = idx & 63;
+      const int64_t gr = m0 + row;
+      xr[s][j] = gr < M ? *reinterpret_cast<const float4*>(p.x + gr * K + kb + 4 * col4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stage_x = [&](int s, int buf) {
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+      const int idx = tid + WQ_THREADS * j, row = idx >> 6, col4 = idx & 63;
+      const float4 v = xr[s][j];
+      const uint32_t h01 = bf16x2_bits(v.x, v.y), h23 = bf16x2_bits(v.z, v.w);
+      const uint32_t l01 = bf16x2_bits(v.x - __uint_as_float(h01 << 16), v.y - __uint_as_float(h01 & 0xffff0000u));
+      const uint32_t l23 = bf16x2_bits(v.z - __uint_as_float(h23 << 16), v.w - __uint_as_float(h23 & 0xffff0000u));
+      *reinterpret_cast<u32x2*>(&Xh[buf][row][4 * col4]) = u32x2{h01, h23};
+      *reinterpret_cast<u32x2*>(&Xl[buf][row][4 * col4]) = u32x2{l01, l23};
+    }
+  };
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < PD; ++s)
+    if (s < nch) load_chunk(s, s);
+
+  for (int c0 = 0; c0 < nch; c0 += PD) {
+#pragma unroll
+    for (int s = 0; s < PD; ++s) {
+      const int c = c0 + s;
+      if (c < nch) {
+        const int buf = c & 1;
+        stage_x(s, buf);
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float sc = 1.f;
+          if constexpr (Tr::MX) sc = e8m0_to_f32(p.G == 32 ? (sr[s] & 255u) : ((sr[s] >> (8 * (i >> 1))) & 255u));
+          const bf16x8 b = wq_decode<FMT>(wr[s], i, sc);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&Xh[buf][16 * t + c16][lane_k + 8 * i]);
+            const bf16x8 al = *reinterpret_cast<const bf16x8*>(&Xl[buf][16 * t + c16][lane_k + 8 * i]);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, acc[t], 0, 0, 0);
+          }
+        }
+        if (c + PD < nch) load_chunk(s, c + PD);
+      }
+    }
+  }
+
+  // second k half -> LDS; the first adds it (fixed order) and stores
+  if (kh == 1)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[cg][t][lane] = acc[t];
+  __syncthreads();
+  if (kh == 0 && n < N) {
+    float f = 1.f;
+    if constexpr (FMT == WQ_FP8_ROW || FMT == WQ_INT8_ROW) f = reinterpret_cast<const float*>(p.scale)[n];
+    if constexpr (FMT == WQ_MXFP4) f = p.s2;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const f32x4 o = red[cg][t][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t r = m0 + 16 * t + 4 * q + i;
+        if (r < M) {
+          const float v = acc[t][i] + o[i];
+          p.y[r * N + n] = (FMT == WQ_MXFP8) ? v : v * f;
+        }
+      }
+    }
+  }
+}
+
+template <int FMT>
+static void wq_launch(int mt, const WqP& p, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(p.N, WQ_COLS), (unsigned)cdiv(p.M, 16 * mt));
+  if (mt == 1)
+    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 1, 4>), grid, dim3(WQ_THREADS), 0, st, p);
+  else if (mt == 2)
+    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 2, 3>), grid, dim3(WQ_THREADS), 0, st, p);
+  else
+    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 4, 2>), grid, dim3(WQ_THREADS), 0, st, p);
+}
+
+int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale, int group_size, float scale2,
+                   float* y, int64_t M, int64_t K, int64_t N, hipStream_t stream, const char* name) {
+  const bool mx = fmt == WQ_MXFP8 || fmt == WQ_MXFP4;
+  if (fmt < WQ_FP8_ROW || fmt > WQ_MXFP4) return -1;
+  if (M <= 0 || N <= 0 || K <= 0 || K % WQ_KC != 0) return -1;
+  if (!x || !w || !y || !aligned(x, 16) || !aligned(w, 16)) return -1;
+  if (!mx && !scale) return -1;
+  if (fmt == WQ_MXFP8 && !scale) return -1;
+  if (mx && scale && group_size != 16 && group_size != 32) return -1;
+  if (mx && scale && group_size == 16 && !aligned(scale, 2)) return -1;
+  if (cdiv(M, 64) > 65535 || cdiv(N, WQ_COLS) > 0x7fffffff) return -1;
+  const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const WqP p{x, w, scale, y, M, K, N, mx && scale ? group_size : 32, scale2};
+  switch (fmt) {
+    case WQ_FP8_ROW: wq_launch<WQ_FP8_ROW>(mt, p, stream); break;
+    case WQ_INT8_ROW: wq_launch<WQ_INT8_ROW>(mt, p, stream); break;
+    case WQ_MXFP8: wq_launch<WQ_MXFP8>(mt, p, stream); break;
+    default: wq_launch<WQ_MXFP4>(mt, p, stream); break;
+  }
+  return launch_status(name);
+}
+
+}  // namespace ccq
+
+using namespace ccq;
+
+extern "C" int ccq_wq_mfma_linear_f32(const float* x, const uint8_t* w, const void* scale, float* y, int64_t batch,
+                                      int64_t in_features, int64_t out_features, int fmt, int group_size,
+                                      float scale2, void* stream) {
+  CCQ_REQUIRE(fmt >= WQ_FP8_ROW && fmt <= WQ_MXFP4, "ccq_wq_mfma_linear_f32: fmt=%d (0 fp8 row, 1 int8 row, 2 MXFP8, 3 MXFP4)", fmt);
+  CCQ_REQUIRE(batch >= 0 && in_features >= 0 && out_features >= 0, "ccq_wq_mfma_linear_f32: negative shape");
+  if (batch == 0 || out_features == 0) return 0;
+  CCQ_REQUIRE(x && w && y, "ccq_wq_mfma_linear_f32: null pointer");
+  CCQ_REQUIRE(in_features > 0 && in_features % WQ_KC == 0, "ccq_wq_mfma_linear_f32: in_features=%lld must be a positive multiple of %d",
+              (long long)in_features, WQ_KC);
+  CCQ_REQUIRE(aligned(x, 16) && aligned(w, 16), "ccq_wq_mfma_linear_f32: x and w must be 16-byte aligned");
+  CCQ_REQUIRE(fmt == WQ_MXFP4 || scale, "ccq_wq_mfma_linear_f32: fmt %d needs its scales", fmt);
+  CCQ_REQUIRE(fmt < WQ_MXFP8 || !scale || group_size == 16 || group_size == 32,
+              "ccq_wq_mfma_linear_f32: group_size=%d (16 or 32)", group_size);
+  CCQ_REQUIRE(fmt < WQ_MXFP8 || !scale || group_size == 32 || aligned(scale, 2),
+              "ccq_wq_mfma_linear_f32: group-16 scales must be 2-byte aligned");
+  CCQ_REQUIRE(cdiv(batch, 64) <= 65535, "ccq_wq_mfma_linear_f32: batch too large");
+  return wq_mfma_linear(fmt, x, w, scale, group_size, scale2, y, batch, in_features, out_features,
+                        as_stream(stream), "ccq_wq_mfma_linear_f32");
+}

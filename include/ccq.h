@@ -183,6 +183,23 @@ int ccq_mx_linear_f32(const float* x, const uint8_t* w, const uint8_t* scale_e8m
                       int64_t out_features, int fmt, int group_size,
                       float scale2, void* stream);
 
+/* y[b, r] = sum_c x[b,c] * W[r,c] in float32 on the matrix cores: each
+ * weight decoded in registers to its exact bf16 value, x split into bf16
+ * hi + lo (float32-grade products), W read once per 64 batch rows.
+ * fmt 0: e4m3fn codes [out, in] with a float32 scale per row (scale float*);
+ * 1: int8 codes, float32 row scale; 2: MXFP8 (E8M0 scales [out, in/G],
+ * G 16 or 32); 3: MXFP4 / NVFP4 codes as ccq_mx_dequant (scales optional,
+ * scale2 on each sum).  in_features a positive multiple of 256; x and w
+ * 16-byte aligned.  The batched form of Fp8LinearMethod.apply
+ * (quant/fp8.py:35-42), LinearMethod.apply for fp8 / int8 keys
+ * (quant/method.py:100-140) and MxLinearMethod.apply (quant/mx.py:37-58):
+ * ccq_mx_linear_f32 calls it for every batch, ccq_fp8_linear_f32 from 2
+ * rows and ccq_int8_linear_f32 from 8 rows on (where it measured faster). */
+int ccq_wq_mfma_linear_f32(const float* x, const uint8_t* w, const void* scale,
+                           float* y, int64_t batch, int64_t in_features,
+                           int64_t out_features, int fmt, int group_size,
+                           float scale2, void* stream);
+
 /* Bytes of workspace ccq_int8_linear needs for this shape (0: none). */
 size_t ccq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t N);
 

@@ -203,3 +203,17 @@ def test_mx_rejects_bad_args(lib):
     assert lib.ccq_mx_linear_f32(p, p, p, p, 1, 64, 8, 0, 0, 1.0, None) == CCQ_EINVAL and "group_size" in last_error()
     assert lib.ccq_mx_linear_f32(p, p, None, p, 0, 64, 8, 1, 32, 1.0, None) == 0  # empty batch, no scales: ok
     assert lib.ccq_e8m0_to_f32(p, p, -1, None) == CCQ_EINVAL
+
+
+def test_wq_mfma_rejects_bad_args(lib):
+    from ccut._lib import CCQ_EINVAL, last_error
+
+    p = ctypes.c_void_p(256)
+    f = lib.ccq_wq_mfma_linear_f32
+    assert f(p, p, p, p, 4, 256, 8, 4, 32, 1.0, None) == CCQ_EINVAL and "fmt" in last_error()
+    assert f(p, p, p, p, 4, 320, 8, 0, 0, 1.0, None) == CCQ_EINVAL and "multiple of 256" in last_error()
+    assert f(p, p, p, p, -1, 256, 8, 0, 0, 1.0, None) == CCQ_EINVAL and "negative" in last_error()
+    assert f(p, p, None, p, 4, 256, 8, 0, 0, 1.0, None) == CCQ_EINVAL and "scales" in last_error()
+    assert f(p, p, p, p, 4, 256, 8, 2, 8, 1.0, None) == CCQ_EINVAL and "group_size" in last_error()
+    assert f(ctypes.c_void_p(260), p, p, p, 4, 256, 8, 0, 0, 1.0, None) == CCQ_EINVAL and "aligned" in last_error()
+    assert f(p, p, None, p, 0, 256, 8, 3, 32, 1.0, None) == 0  # empty batch: nothing to do
