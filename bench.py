@@ -212,6 +212,44 @@ def bench_moe(T: int, steps: int, warmup: int, dev, n_layers: int = LAYERS):
     }
 
 
+def bench_moe_shared(T: int, dev, n_layers: int = LAYERS):
+    """The decode layer with a shared expert in the same kernels
+    (``ccq_moe_w4_forward_shared``: 64 routed experts + the shared one last,
+    top-6, every token's seventh slot the shared expert with gate 0.5);
+    device time per layer over ``n_layers`` distinct weight sets.
+    Algorithmic bytes: the routed experts' and the shared expert's weights
+    once, activations, logits, routing."""
+    import dataclasses
+
+    import torch
+
+    from ccut import workloads as wl
+    from ccut.blocks import moe
+
+    layers = []
+    for i in range(n_layers):
+        ex = moe.W4Experts.from_awq(
+            wl.awq_experts(E + 1, HID, INTER, GROUP, seed=2000 + 3 * i, device=dev),
+            wl.awq_experts(E + 1, HID, INTER, GROUP, seed=2001 + 3 * i, device=dev),
+            wl.awq_experts(E + 1, INTER, HID, GROUP, seed=2002 + 3 * i, device=dev), GROUP)
+        layers.append((dataclasses.replace(ex, shared_expert=True), wl.router_logits(T, E, seed=90 + i, device=dev)))
+    x = wl.activations(T, HID, seed=5, device=dev, dtype=torch.bfloat16)
+    y = torch.empty((T, HID), dtype=torch.bfloat16, device=dev)
+    nb = []
+    for ex, lg in layers:
+        _, ids = moe.topk_softmax(lg, TOPK, True)
+        uniq = int(torch.unique(ids).numel()) + 1
+        nb.append(uniq * ex.bytes_per_expert + x.numel() * 2 * 2 + lg.numel() * 4 + T * (TOPK + 1) * 12)
+    launches = [lambda ex=ex, lg=lg: moe.moe_forward_w4(x, lg, ex, TOPK, True, out=y, shared_gate=0.5)
+                for ex, lg in layers]
+    launches[0]()
+    torch.cuda.synchronize()
+    avg = device_time(launches, reps=8)
+    b = sum(nb) / len(nb)
+    return {"T": T, "avg_us": avg * 1e6, "bytes": b, "GBps": b / avg / 1e9, "frac_hbm": b / avg / PEAK_HBM,
+            "layers": n_layers}
+
+
 def time_gate_up(layers, x, T: int, dev):
     """Device time of the step's gate/up + SiLU kernel with the routing
     inside its workgroups (ccq_moe_w4_route_gate_up: the first launch of
@@ -689,6 +727,10 @@ def main():
             r = bench_gemm(M, 4096, 14336, dev=dev, copies=24)
             extra[f"awq_gemm_k4096_n14336_m{M}"] = r
             log(f"awq gemm K=4096 N=14336 M={M}: {r['GBps']:.1f} GB/s ({r['avg_us']:.2f} us)")
+        r = bench_moe_shared(16, dev)
+        extra["moe_decode_T16_shared_expert"] = r
+        log(f"MoE decode T=16 + shared expert in-kernel: {r['avg_us']:.2f} us, {r['GBps']:.1f} GB/s "
+            f"({r['frac_hbm']:.3f} of HBM peak)")
         r = bench_gemm(1, 2048, 5632, dev=dev, copies=96)
         extra["awq_gemv_k2048_n5632"] = r
         log(f"awq gemv K=2048 N=5632: {r['GBps']:.1f} GB/s ({r['avg_us']:.2f} us)")

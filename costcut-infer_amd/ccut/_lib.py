@@ -108,6 +108,8 @@ SIGNATURES: dict[str, tuple] = {
                                   ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
     "ccq_moe_w4_route_gate_up": (_int, [_vp, _int, _vp, _i64, _i64, _int, _vp, _vp,
                                         ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
+    "ccq_moe_w4_forward_shared": (_int, [_vp, _int, _vp, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _vp, _int,
+                                         ctypes.POINTER(ccq_w4_experts), _vp, _sz, _vp]),
     "ccq_moe_w4_forward_noalloc": (_int, [_vp, _int, _vp, _i64, _i64, _int, _vp, _vp, _vp, _int,
                                           ctypes.POINTER(ccq_w4_experts), _vp]),
     "ccq_fp8_act_quant": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),

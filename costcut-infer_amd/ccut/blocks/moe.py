@@ -225,11 +225,26 @@ class W4Experts:
     hidden: int
     inter: int
     group_size: int = 128
+    # the last expert of the stack is the layer's shared expert (every token
+    # takes it with the shared gate as weight); num_experts counts it
+    shared_expert: bool = False
+
+    @property
+    def routed_experts(self) -> int:
+        return self.num_experts - (1 if self.shared_expert else 0)
 
     @staticmethod
-    def from_awq(gate: tuple, up: tuple, down: tuple, group_size: int = 128) -> "W4Experts":
+    def from_awq(gate: tuple, up: tuple, down: tuple, group_size: int = 128, shared: tuple | None = None
+                 ) -> "W4Experts":
         """Each of ``gate``/``up``/``down`` is ``(qweight [E, K, N/8],
-        qzeros [E, K/G, N/8], scales [E, K/G, N])`` in AWQ layout."""
+        qzeros [E, K/G, N/8], scales [E, K/G, N])`` in AWQ layout.
+        ``shared``: the shared expert as ``(gate, up, down)``, each
+        ``(qweight [K, N/8], qzeros [K/G, N/8], scales [K/G, N])``, stored
+        after the routed experts."""
+        if shared is not None:
+            def cat(t, one):
+                return tuple(torch.cat([_dev.to_device(a), _dev.to_device(b).unsqueeze(0)]) for a, b in zip(t, one))
+            gate, up, down = cat(gate, shared[0]), cat(up, shared[1]), cat(down, shared[2])
         def stack(t, K, N):
             qw, qz, sc = (_dev.to_device(a) for a in t)
             E = qw.shape[0]
@@ -260,7 +275,7 @@ class W4Experts:
         if not (g[2] == u[2] == d[2]):
             raise ValueError("gate, up and down scales must share one dtype")
         return W4Experts(g[0], g[1], u[0], u[1], d[0], d[1], g[2], num_experts=E, hidden=hidden, inter=inter,
-                         group_size=group_size)
+                         group_size=group_size, shared_expert=shared is not None)
 
     def descriptor(self) -> ccq_w4_experts:
         code = 1 if self.scale_dtype == torch.float16 else 2
@@ -289,21 +304,30 @@ def moe_ffn_w4(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, expert
     """Expert FFN + weighted combine for already-routed tokens (one call of
     ``ccq_moe_w4_ffn``: align, gate/up + SiLU, down, combine).  ``shared``
     ([T, H] float32, the shared expert's output): ``shared_gate * shared``
-    is added in the combine's epilogue (``ccq_moe_w4_ffn_shared``)."""
+    is added in the combine's epilogue (``ccq_moe_w4_ffn_shared``).  When
+    the stack holds the shared expert (``experts.shared_expert``), every
+    token takes it as one more slot with weight ``shared_gate``: its FFN
+    runs in the same kernels and is added after the routed sum."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"activations must be float16 or bfloat16, got {x.dtype}")
     x = x.contiguous()
     T, H = x.shape
     if H != experts.hidden:
         raise ValueError(f"x has {H} features, experts expect {experts.hidden}")
-    k = ids.shape[1]
     out_dtype = out_dtype or x.dtype
     y = torch.empty((T, H), dtype=out_dtype, device=x.device)
+    ids = _dev.to_device(ids).to(torch.int64)
+    weights = _dev.to_device(weights).to(torch.float32)
+    if experts.shared_expert:
+        if shared is not None:
+            raise ValueError("the stack holds the shared expert: pass shared_gate only")
+        ids = torch.cat([ids, torch.full((T, 1), experts.routed_experts, dtype=torch.int64, device=ids.device)], 1)
+        weights = torch.cat([weights, torch.full((T, 1), float(np.float32(shared_gate)), device=weights.device)], 1)
+    ids, weights = ids.contiguous(), weights.contiguous()
+    k = ids.shape[1]
     desc = experts.descriptor()
     nbytes = lib().ccq_moe_w4_workspace_size(T, k, desc)
     ws = _dev.workspace("moe_w4", nbytes, x.device)
-    ids = ids.to(torch.int64).contiguous()
-    weights = weights.to(torch.float32).contiguous()
     if shared is not None:
         sd = _shared_rows(shared, T, H, x.device)
         call("ccq_moe_w4_ffn_shared", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], ids.data_ptr(), weights.data_ptr(),
@@ -317,14 +341,18 @@ def moe_ffn_w4(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, expert
 
 def moe_forward_w4(x: torch.Tensor, router_logits: torch.Tensor, experts: W4Experts, top_k: int,
                    norm_topk_prob: bool = True, out_dtype: torch.dtype | None = None,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None, shared_gate: float = 1.0) -> torch.Tensor:
     """Routed MoE layer on AWQ experts: ``topk_softmax`` routing, expert
     grouping, gate/up + SiLU, down and the weighted combine in one call of
     ``ccq_moe_w4_forward`` (the compute of ``ExpertPipeline.step``, reference
     ``experts/pipeline.py:145-179``, and ``moe_forward``,
     ``models/generic.py:361-378``).  Decode batches are routed inside the
     gate/up kernel.  ``out``: optional [T, H] tensor to write (its dtype
-    wins over ``out_dtype``)."""
+    wins over ``out_dtype``).  A stack with the shared expert
+    (``experts.shared_expert``) runs ``ccq_moe_w4_forward_shared``: logits
+    over the routed experts, the shared expert's FFN in the same kernels,
+    ``shared_gate * shared(x)`` added after the routed sum (reference
+    ``pipeline.py:181-190``, ``blocks/moe.py:177-179``)."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"activations must be float16 or bfloat16, got {x.dtype}")
     x = x.contiguous()
@@ -332,16 +360,24 @@ def moe_forward_w4(x: torch.Tensor, router_logits: torch.Tensor, experts: W4Expe
     if H != experts.hidden:
         raise ValueError(f"x has {H} features, experts expect {experts.hidden}")
     lg = _dev.to_device(router_logits, torch.float32).contiguous()
-    if lg.dim() != 2 or lg.shape[0] != T or lg.shape[1] != experts.num_experts:
-        raise ValueError(f"router logits must be [{T}, {experts.num_experts}], got {tuple(lg.shape)}")
+    E = experts.routed_experts
+    if lg.dim() != 2 or lg.shape[0] != T or lg.shape[1] != E:
+        raise ValueError(f"router logits must be [{T}, {E}], got {tuple(lg.shape)}")
     if out is None:
         out = torch.empty((T, H), dtype=out_dtype or x.dtype, device=x.device)
     elif out.shape != (T, H) or not out.is_contiguous() or out.device != x.device:
         raise ValueError(f"out must be a contiguous [{T}, {H}] tensor on {x.device}")
     desc = experts.descriptor()
+    mode = _MODE_TOPK_THEN_SOFTMAX if norm_topk_prob else _MODE_SOFTMAX_ALL
+    if experts.shared_expert:
+        nbytes = lib().ccq_moe_w4_workspace_size(T, top_k + 1, desc)
+        ws = _dev.workspace("moe_w4", nbytes, x.device)
+        call("ccq_moe_w4_forward_shared", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], lg.data_ptr(), T, top_k, mode,
+             float(np.float32(shared_gate)), None, None, out.data_ptr(), _dev.DTYPE_CODE[out.dtype], desc,
+             ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
+        return out
     nbytes = lib().ccq_moe_w4_workspace_size(T, top_k, desc)
     ws = _dev.workspace("moe_w4", nbytes, x.device)
-    mode = _MODE_TOPK_THEN_SOFTMAX if norm_topk_prob else _MODE_SOFTMAX_ALL
     call("ccq_moe_w4_forward", x.data_ptr(), _dev.DTYPE_CODE[x.dtype], lg.data_ptr(), T, top_k, mode, None, None,
          out.data_ptr(), _dev.DTYPE_CODE[out.dtype], desc, ws.data_ptr(), nbytes, _dev.stream_ptr(x.device))
     return out

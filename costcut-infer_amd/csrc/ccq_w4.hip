@@ -579,8 +579,12 @@ struct W4SP {
   // and workgroup 0 writes the routing and the schedule for the next kernels
   const float* logits;
   int rT, rE, rk, rmode;
-  int64_t* ids_out;            // [rT, rk]
-  float* wts_out;              // [rT, rk]
+  // 1: the stack holds one more expert (index rE, the shared expert) that
+  // every token takes as assignment slot rk with weight rshared_w
+  int rshared;
+  float rshared_w;
+  int64_t* ids_out;            // [rT, rk + rshared]
+  float* wts_out;              // [rT, rk + rshared]
   int32_t* sched_rows;         // [tiles * 16], as ccq_moe_align's sorted_ids
   int32_t* sched_tile_expert;  // [tiles]
   int32_t* sched_meta;         // [2]
@@ -635,19 +639,28 @@ __device__ __forceinline__ int wave_incl_sum(int v) {
 // barrier.
 __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int T = p.rT, E = p.rE, k = p.rk, n = T * k;
-  const int nslots = n + 15 * min(n, E);  // the padded schedule is at most this long
-  for (int e = tid; e < E; e += blockDim.x) rs.cnt[e] = 0;
+  // E logits per token, Es experts in the schedule (E + the shared one),
+  // ks assignment slots per token (the shared one last)
+  const int T = p.rT, E = p.rE, k = p.rk, ks = k + p.rshared, Es = E + p.rshared, n = T * ks;
+  const int nslots = n + 15 * min(n, Es);  // the padded schedule is at most this long
+  for (int e = tid; e < Es; e += blockDim.x) rs.cnt[e] = 0;
   for (int i = tid; i < nslots; i += blockDim.x) rs.sorted[i] = -1;
   for (int i = tid; i < T * E; i += blockDim.x) rs.lg[i] = p.logits[i];
   __syncthreads();
   auto keep = [&](int t, float w, int id) {
     if (lane < k) {
-      const int a = t * k + lane;
+      const int a = t * ks + lane;
       rs.sid[a] = id >= 0 && id < E ? id : -1;
       if (blockIdx.x == 0) {
         p.ids_out[a] = id;
         p.wts_out[a] = w;
+      }
+    } else if (lane == k && p.rshared) {
+      const int a = t * ks + k;
+      rs.sid[a] = E;
+      if (blockIdx.x == 0) {
+        p.ids_out[a] = E;
+        p.wts_out[a] = p.rshared_w;
       }
     }
   };
@@ -675,7 +688,7 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
   __syncthreads();
   if (wave == 0) {
     int nbits = 1;
-    while ((1 << nbits) < E) ++nbits;  // <= 8
+    while ((1 << nbits) < Es) ++nbits;  // <= 8
     const int nch = (n + 63) / 64;     // <= RT_CHUNKS
     const uint64_t lt = (1ull << lane) - 1ull;
     int key[RT_CHUNKS], rank[RT_CHUNKS], cnt[RT_CHUNKS];
@@ -741,7 +754,7 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
     const int nt = rs.ntiles;
     for (int i = tid; i < nt * 16; i += blockDim.x) p.sched_rows[i] = rs.sorted[i];
     for (int i = tid; i < nt; i += blockDim.x) p.sched_tile_expert[i] = rs.tile_expert[i];
-    for (int x = tid; x < E; x += blockDim.x) p.sched_counts[x] = rs.cnt[x];
+    for (int x = tid; x < Es; x += blockDim.x) p.sched_counts[x] = rs.cnt[x];
     if (tid == 0) {
       p.sched_meta[0] = nt;
       p.sched_meta[1] = rs.nactive;
@@ -2173,12 +2186,12 @@ static int check_forward_args(const char* name, const void* x, int x_dtype, cons
 // intermediate into the workspace.
 static int launch_route_gate_up(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k, int mode,
                                 int64_t* ids, float* wts, const ccq_w4_experts* ex, char* ws, const MoeLayout& L,
-                                hipStream_t st) {
+                                hipStream_t st, int shared = 0, float shared_w = 0.f) {
   const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
   W4SP w = {};
   w.x = x;
   w.ldx = H;
-  w.row_div = (int)k;
+  w.row_div = (int)(k + shared);
   w.w0 = (const uint32_t*)ex->w_gate;
   w.sz0 = ex->sz_gate;
   w.w1 = (const uint32_t*)ex->w_up;
@@ -2195,9 +2208,11 @@ static int launch_route_gate_up(const void* x, int x_dtype, const float* logits,
   w.nib_mask = 0x000F000Fu;
   w.logits = logits;
   w.rT = (int)T;
-  w.rE = (int)ex->num_experts;
+  w.rE = (int)(ex->num_experts - shared);
   w.rk = (int)k;
   w.rmode = mode;
+  w.rshared = shared;
+  w.rshared_w = shared_w;
   w.ids_out = ids;
   w.wts_out = wts;
   w.sched_rows = (int32_t*)(ws + L.off_sorted);
@@ -2253,6 +2268,66 @@ extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logit
   rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
   if (rc) return rc;
   return launch_combine(rows, CCQ_F32, wts, ids, ex->num_experts, y, y_dtype, T, k, H, st);
+}
+
+// ids / weights [T, k] -> [T, k + 1], the shared expert's slot (expert E,
+// weight g) last
+__global__ void append_shared_slot_kernel(const int64_t* __restrict__ ids, const float* __restrict__ wts,
+                                          int64_t* __restrict__ ids2, float* __restrict__ wts2, int64_t T, int64_t k,
+                                          int64_t E, float g) {
+  const int64_t ks = k + 1;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < T * ks; i += stride) {
+    const int64_t t = i / ks, j = i - t * ks;
+    ids2[i] = j < k ? ids[t * k + j] : E;
+    wts2[i] = j < k ? wts[t * k + j] : g;
+  }
+}
+
+extern "C" int ccq_moe_w4_forward_shared(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
+                                         int mode, float shared_gate, int64_t* ids_out, float* weights_out, void* y,
+                                         int y_dtype, const ccq_w4_experts* ex, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  const char* name = "ccq_moe_w4_forward_shared";
+  int rc = check_experts(ex, name);
+  if (rc) return rc;
+  CCQ_REQUIRE(ex->num_experts >= 2, "%s: the stack holds the routed experts and the shared expert last", name);
+  CCQ_REQUIRE(k >= 1 && k <= 15 && k < ex->num_experts, "%s: bad k=%lld for %lld routed experts", name,
+              (long long)k, (long long)(ex->num_experts - 1));
+  const int64_t ks = k + 1, Er = ex->num_experts - 1;
+  CCQ_REQUIRE(T >= 0 && T * ks <= 65536 && T <= 65535, "%s: bad T=%lld", name, (long long)T);
+  // the checks of ccq_moe_w4_forward with k + 1 slots (workspace included)
+  rc = check_forward_args(name, x, x_dtype, logits, T, ks, mode, y, y_dtype, ex, workspace, workspace_bytes, true);
+  if (rc || T == 0) return rc;
+  const MoeLayout L = moe_layout(T, ks, ex, 2);
+  hipStream_t st = as_stream(stream);
+  char* ws = (char*)workspace;
+  int64_t* ids = ids_out != nullptr ? ids_out : (int64_t*)(ws + L.off_ids);
+  float* wts = weights_out != nullptr ? weights_out : (float*)(ws + L.off_wts);
+  if (!fused_route(L, ex, ks)) {
+    // routing over the Er logits into the (not yet used) down-row area,
+    // then the shared slot appended, then the FFN with k + 1 slots
+    int64_t* tids = (int64_t*)(ws + L.off_rows);
+    float* twts = (float*)(ws + L.off_rows + align256((size_t)(T * k) * 8));
+    rc = ccq_topk_softmax(logits, twts, tids, T, Er, k, mode, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(append_shared_slot_kernel, dim3(grid_for(T * ks, 256)), dim3(256), 0, st, tids, twts, ids,
+                       wts, T, k, Er, shared_gate);
+    rc = launch_status(name);
+    if (rc) return rc;
+    return ccq_moe_w4_ffn(x, x_dtype, ids, wts, y, y_dtype, T, ks, ex, workspace, workspace_bytes, stream);
+  }
+  int32_t* sorted = (int32_t*)(ws + L.off_sorted);
+  int32_t* tile_expert = (int32_t*)(ws + L.off_tile_expert);
+  int32_t* meta = (int32_t*)(ws + L.off_meta);
+  void* inter = ws + L.off_inter;
+  float* rows = (float*)(ws + L.off_rows);
+  rc = launch_route_gate_up(x, x_dtype, logits, T, k, mode, ids, wts, ex, ws, L, st, 1, shared_gate);
+  if (rc) return rc;
+  rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
+  if (rc) return rc;
+  return launch_combine(rows, CCQ_F32, wts, ids, ex->num_experts, y, y_dtype, T, ks, ex->hidden, st);
 }
 
 // ---------------------------------------------------------------------------

@@ -404,6 +404,21 @@ int ccq_moe_w4_route_gate_up(const void* x, int x_dtype, const float* logits, in
                              int mode, int64_t* ids_out, float* weights_out, const ccq_w4_experts* ex,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* The MoE layer with its shared expert's FFN in the same kernels: ex holds
+ * E = num_experts - 1 routed experts and the shared expert last (index E);
+ * logits are [T, E].  Every token takes the shared expert as one more
+ * assignment slot (slot k, weight shared_gate), so its gate/up + SiLU and
+ * down run inside the routed experts' launches and the combine adds
+ * shared_gate * shared(x) after the routed sum, in the reference's order:
+ * y = sum_j w_j * expert_ffn(x, e_j) + shared_gate * shared_ffn(x)
+ * (experts/pipeline.py:145-190, blocks/moe.py:177-179).  k <= 15;
+ * ids_out / weights_out, when given, are [T, k + 1] (the shared slot
+ * last); the workspace is ccq_moe_w4_workspace_size(T, k + 1, ex). */
+int ccq_moe_w4_forward_shared(const void* x, int x_dtype, const float* logits, int64_t T,
+                              int64_t k, int mode, float shared_gate, int64_t* ids_out,
+                              float* weights_out, void* y, int y_dtype, const ccq_w4_experts* ex,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of the per-GPU scratch array of ccq_moe_w4_forward_noalloc. */
 #define CCQ_MOE_W4_NOALLOC_BYTES (32u << 20)
 

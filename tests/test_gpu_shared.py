@@ -95,3 +95,48 @@ def test_moe_ffn_fp8_shared_epilogue(gpu):
     moe.shared_expert_add(y0, sh, 0.8)
     y1 = moe.moe_ffn_fp8(x, ids, w, ex, out_dtype=torch.float32, shared=sh, shared_gate=0.8)
     assert np.array_equal(y1.cpu().numpy(), y0.cpu().numpy())
+
+
+def _awq_stack(rng, E, K, N, G):
+    from oracle import awq as oawq
+
+    q = rng.integers(0, 16, size=(E, K, N), dtype=np.uint8)
+    z = rng.integers(0, 16, size=(E, K // G, N), dtype=np.uint8)
+    s = (np.abs(rng.standard_normal((E, K // G, N))) * 0.01 + 1e-3).astype(np.float16)
+    return (np.stack([oawq.pack(a) for a in q]), np.stack([oawq.pack(a) for a in z]), s)
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 2, 8), (5, 3, 8), (16, 6, 64), (40, 2, 8)])
+def test_shared_expert_ffn_in_the_layer(gpu, T, k, E):
+    """The shared expert's FFN as the stack's last expert (every token's slot
+    k, weight shared_gate) through ccq_moe_w4_forward_shared: in-kernel
+    routing for decode batches (T <= 16), the routing kernel above; the
+    routed sum then shared_gate * shared_ffn(x), against the oracle's
+    expert_ffn on dequantized weights (reference pipeline.py:145-190)."""
+    from ccut.blocks import moe
+    from oracle import awq as oawq
+    from oracle import moe as omoe
+
+    H, I, G = 256, 384, 128
+    rng = np.random.default_rng(T * 100 + k * 10 + E)
+    gate, up, down = _awq_stack(rng, E + 1, H, I, G), _awq_stack(rng, E + 1, H, I, G), _awq_stack(rng, E + 1, I, H, G)
+    routed = [tuple(a[:E] for a in t) for t in (gate, up, down)]
+    shared = tuple(tuple(a[E] for a in t) for t in (gate, up, down))
+    to = lambda t: tuple(torch.from_numpy(np.ascontiguousarray(a)).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(to(routed[0]), to(routed[1]), to(routed[2]), G,
+                                shared=tuple(to(s) for s in shared))
+    assert ex.shared_expert and ex.num_experts == E + 1 and ex.routed_experts == E
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    g = 0.625
+    y = moe.moe_forward_w4(x.to(gpu), torch.from_numpy(lg).to(gpu), ex, top_k=k, out_dtype=torch.float32,
+                           shared_gate=g).cpu().numpy()
+    lut = {e: tuple(oawq.dequant(t[0][e], t[1][e], t[2][e], G) for t in (gate, up, down)) for e in range(E + 1)}
+    w0, ids0 = omoe.topk_softmax(lg, k)
+    xf = x.float().numpy()
+    ref = omoe.moe_combine(xf, ids0, w0, lut.__getitem__) + np.float32(g) * omoe.expert_ffn(xf, *lut[E])
+    assert np.max(np.abs(y - ref)) <= 2e-2 * np.max(np.abs(ref))
+    # the ids-given form appends the same slot: the same kernels, the same result
+    yi = moe.moe_ffn_w4(x.to(gpu), torch.from_numpy(ids0.astype(np.int64)).to(gpu), torch.from_numpy(w0).to(gpu), ex,
+                        out_dtype=torch.float32, shared_gate=g).cpu().numpy()
+    assert np.max(np.abs(yi - ref)) <= 2e-2 * np.max(np.abs(ref))
