@@ -706,10 +706,10 @@ extern "C" int ccq_int4_dequant(const uint8_t* packed, const float* scale, float
 
 // Batch sizes from which the fp8 / int8 row-scale linears run on the MFMA
 // kernel instead of the streaming one (measured at K=4096 N=14336: fp8
-// 18.7 vs 20.4 us at 2 rows, the streaming kernel faster at 1; int8 even
-// at 8 rows, the streaming kernel faster below).
+// 18.2 vs 20.4 us at 2 rows, the streaming kernel faster at 1; int8 18.2
+// vs 26.1 us at 4 rows, the streaming kernel faster below).
 constexpr int64_t kWqMinBatchFp8 = 2;
-constexpr int64_t kWqMinBatchInt8 = 8;
+constexpr int64_t kWqMinBatchInt8 = 4;
 
 static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* scale, float* y, int64_t batch,
                       int64_t in_f, int64_t out_f, void* stream, const char* name, const float* table = nullptr,

@@ -29,8 +29,8 @@
 // permutation on the activation side, read from LDS.  The activation chunk
 // (hi and lo bf16, [16 MT][256]) is staged in LDS, double-buffered, one
 // barrier per chunk.  Weights (non-temporal loads), scale bytes and the
-// activation chunk are loaded PD chunks ahead into a register ring, so the
-// wait for chunk c leaves chunks c+1..c+PD-1 in flight.
+// activation chunk are loaded PD chunks ahead into a register ring (PD 2-6,
+// wq_depth), so the wait for chunk c leaves chunks c+1..c+PD-1 in flight.
 #include "ccq_common.h"
 
 namespace ccq {
@@ -98,10 +98,39 @@ __device__ __forceinline__ bf16x8 wq_decode(const u32x4 (&wr)[WqTraits<FMT>::WB]
   return pack_bf16x8(v);
 }
 
-template <int FMT, int MT, int PD>
+// Scale bytes of MXFP4 layers without scales: E8M0 127 (scale 1), read at
+// offset 0, so that every chunk issues the same loads.
+__device__ const uint8_t wq_unit_scale[4] = {127, 127, 127, 127};
+
+// Ring loads as inline assembly, so that the compiler adds no waits of its
+// own for them (its waits drain every load at the loop head); wq_wait then
+// waits for one chunk's loads and wq_tie hands each register of the slot to
+// the compiler after that wait.  check_inflight.py verifies on the register
+// allocator's output that no instruction reads, copies or spills a ring
+// register while its load is in flight.
+__device__ __forceinline__ void wq_load16(u32x4& dst, const void* p) {
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst) : "v"(p));
+}
+__device__ __forceinline__ void wq_load_u8(uint32_t& dst, const void* p) {
+  asm volatile("global_load_ubyte %0, %1, off" : "=v"(dst) : "v"(p));
+}
+template <int N>
+__device__ __forceinline__ void wq_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <typename T>
+__device__ __forceinline__ void wq_tie(T& r) {
+  asm volatile("" : "+v"(r));
+}
+
+template <int FMT, int MT, int PD, bool G16>
 __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
   using Tr = WqTraits<FMT>;
-  constexpr int XR = 2 * MT;  // activation float4s per thread and chunk
+  constexpr int XR = 2 * MT;                        // activation 16-byte pieces per thread and chunk
+  constexpr int NSC = Tr::MX ? (G16 ? 2 : 1) : 0;   // scale bytes per lane and chunk
+  constexpr int LPC = Tr::WB + NSC + XR;            // loads per lane and chunk
+  static_assert((PD - 1) * LPC < 64, "loads in flight fit vmcnt");
   __shared__ __align__(16) uint16_t Xh[2][16 * MT][WQ_RS];
   __shared__ __align__(16) uint16_t Xl[2][16 * MT][WQ_RS];
   __shared__ __align__(16) f32x4 red[WQ_CG][MT][64];
@@ -117,37 +146,51 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
   const int64_t row_bytes = K / Tr::KDIV;
   const uint8_t* wrow = p.w + imin64(n, N - 1) * row_bytes;  // columns past N read row N-1, never stored
   const int lane_k = kh * (WQ_KC / 2) + q * 32;             // first k of the lane's 32 in a chunk
-  const int64_t gpr = Tr::MX ? K / p.G : 0;
-  const uint8_t* srow = Tr::MX && p.scale ? reinterpret_cast<const uint8_t*>(p.scale) + imin64(n, N - 1) * gpr : nullptr;
+  const bool has_sc = Tr::MX && p.scale != nullptr;
+  const int G = G16 ? 16 : 32;
+  const uint8_t* srow = has_sc ? reinterpret_cast<const uint8_t*>(p.scale) + imin64(n, N - 1) * (K / G) : wq_unit_scale;
 
   u32x4 wr[PD][Tr::WB];
-  uint32_t sr[PD];
-  float4 xr[PD][XR];
+  uint32_t sr[PD][NSC > 0 ? NSC : 1];
+  u32x4 xr[PD][XR];
 
-  auto load_chunk = [&](int s, int c) {
+  // every lane issues LPC loads per chunk (x rows past M read row M-1 and
+  // are zeroed when staged), so the wait counts are exact
+  auto issue = [&](int s, int c) {
     const int64_t kb = (int64_t)c * WQ_KC;
-    const u32x4* wp = reinterpret_cast<const u32x4*>(wrow + (kb + lane_k) / Tr::KDIV);
-#pragma unroll
-    for (int j = 0; j < Tr::WB; ++j) wr[s][j] = __builtin_nontemporal_load(wp + j);
-    if constexpr (Tr::MX) {
-      sr[s] = 127u;  // scale 1 for MXFP4 without scales
-      if (srow) {
-        const int64_t g0 = (kb + lane_k) / p.G;
-        sr[s] = p.G == 32 ? (uint32_t)srow[g0] : (uint32_t)*reinterpret_cast<const uint16_t*>(srow + g0);
-      }
+    const uint8_t* wp = wrow + (kb + lane_k) / Tr::KDIV;
+    gload16_nt<0>(wr[s][0], wp);
+    if constexpr (Tr::WB == 2) gload16_nt<16>(wr[s][1], wp);
+    if constexpr (NSC > 0) {
+      const uint8_t* sp = srow + (has_sc ? (kb + lane_k) / G : 0);
+      wq_load_u8(sr[s][0], sp);
+      if constexpr (NSC == 2) wq_load_u8(sr[s][1], sp + (has_sc ? 1 : 0));
     }
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
       const int idx = tid + WQ_THREADS * j, row = idx >> 6, col4 = idx & 63;
-      const int64_t gr = m0 + row;
-      xr[s][j] = gr < M ? *reinterpret_cast<const float4*>(p.x + gr * K + kb + 4 * col4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int64_t gr = imin64(m0 + row, M - 1);
+      wq_load16(xr[s][j], p.x + gr * K + kb + 4 * col4);
     }
+  };
+  auto wait_slot = [&](int s, bool steady) {
+    if (steady)
+      wq_wait<(PD - 1) * LPC>();
+    else
+      wq_wait<0>();
+#pragma unroll
+    for (int j = 0; j < Tr::WB; ++j) wq_tie(wr[s][j]);
+#pragma unroll
+    for (int j = 0; j < NSC; ++j) wq_tie(sr[s][j]);
+#pragma unroll
+    for (int j = 0; j < XR; ++j) wq_tie(xr[s][j]);
   };
   auto stage_x = [&](int s, int buf) {
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
       const int idx = tid + WQ_THREADS * j, row = idx >> 6, col4 = idx & 63;
-      const float4 v = xr[s][j];
+      float4 v = __builtin_bit_cast(float4, xr[s][j]);
+      if (m0 + row >= M) v = make_float4(0.f, 0.f, 0.f, 0.f);
       const uint32_t h01 = bf16x2_bits(v.x, v.y), h23 = bf16x2_bits(v.z, v.w);
       const uint32_t l01 = bf16x2_bits(v.x - __uint_as_float(h01 << 16), v.y - __uint_as_float(h01 & 0xffff0000u));
       const uint32_t l23 = bf16x2_bits(v.z - __uint_as_float(h23 << 16), v.w - __uint_as_float(h23 & 0xffff0000u));
@@ -162,7 +205,7 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
 
 #pragma unroll
   for (int s = 0; s < PD; ++s)
-    if (s < nch) load_chunk(s, s);
+    if (s < nch) issue(s, s);
 
   for (int c0 = 0; c0 < nch; c0 += PD) {
 #pragma unroll
@@ -170,12 +213,13 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
       const int c = c0 + s;
       if (c < nch) {
         const int buf = c & 1;
+        wait_slot(s, c + PD - 1 < nch);  // steady: chunks c+1..c+PD-1 were issued after chunk c
         stage_x(s, buf);
         lds_barrier();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float sc = 1.f;
-          if constexpr (Tr::MX) sc = e8m0_to_f32(p.G == 32 ? (sr[s] & 255u) : ((sr[s] >> (8 * (i >> 1))) & 255u));
+          if constexpr (Tr::MX) sc = e8m0_to_f32(sr[s][NSC == 2 ? (i >> 1) : 0] & 255u);
           const bf16x8 b = wq_decode<FMT>(wr[s], i, sc);
 #pragma unroll
           for (int t = 0; t < MT; ++t) {
@@ -185,7 +229,7 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, acc[t], 0, 0, 0);
           }
         }
-        if (c + PD < nch) load_chunk(s, c + PD);
+        if (c + PD < nch) issue(s, c + PD);
       }
     }
   }
@@ -214,15 +258,22 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
   }
 }
 
-template <int FMT>
+// Ring depth (chunks loaded ahead) per row-tile count: as deep as the
+// registers allow without spills (INT8's decode needs more registers).
+template <int FMT, int MT>
+constexpr int wq_depth() {
+  return FMT == WQ_INT8_ROW ? (MT == 1 ? 4 : (MT == 2 ? 3 : 2)) : (MT == 1 ? 6 : (MT == 2 ? 4 : 3));
+}
+
+template <int FMT, bool G16>
 static void wq_launch(int mt, const WqP& p, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(p.N, WQ_COLS), (unsigned)cdiv(p.M, 16 * mt));
   if (mt == 1)
-    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 1, 4>), grid, dim3(WQ_THREADS), 0, st, p);
+    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 1, wq_depth<FMT, 1>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
   else if (mt == 2)
-    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 2, 3>), grid, dim3(WQ_THREADS), 0, st, p);
+    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 2, wq_depth<FMT, 2>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 4, 2>), grid, dim3(WQ_THREADS), 0, st, p);
+    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 4, wq_depth<FMT, 4>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
 }
 
 int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale, int group_size, float scale2,
@@ -234,15 +285,25 @@ int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale,
   if (!mx && !scale) return -1;
   if (fmt == WQ_MXFP8 && !scale) return -1;
   if (mx && scale && group_size != 16 && group_size != 32) return -1;
-  if (mx && scale && group_size == 16 && !aligned(scale, 2)) return -1;
   if (cdiv(M, 64) > 65535 || cdiv(N, WQ_COLS) > 0x7fffffff) return -1;
   const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const WqP p{x, w, scale, y, M, K, N, mx && scale ? group_size : 32, scale2};
+  const bool g16 = mx && scale && group_size == 16;
   switch (fmt) {
-    case WQ_FP8_ROW: wq_launch<WQ_FP8_ROW>(mt, p, stream); break;
-    case WQ_INT8_ROW: wq_launch<WQ_INT8_ROW>(mt, p, stream); break;
-    case WQ_MXFP8: wq_launch<WQ_MXFP8>(mt, p, stream); break;
-    default: wq_launch<WQ_MXFP4>(mt, p, stream); break;
+    case WQ_FP8_ROW: wq_launch<WQ_FP8_ROW, false>(mt, p, stream); break;
+    case WQ_INT8_ROW: wq_launch<WQ_INT8_ROW, false>(mt, p, stream); break;
+    case WQ_MXFP8:
+      if (g16)
+        wq_launch<WQ_MXFP8, true>(mt, p, stream);
+      else
+        wq_launch<WQ_MXFP8, false>(mt, p, stream);
+      break;
+    default:
+      if (g16)
+        wq_launch<WQ_MXFP4, true>(mt, p, stream);
+      else
+        wq_launch<WQ_MXFP4, false>(mt, p, stream);
+      break;
   }
   return launch_status(name);
 }
@@ -264,8 +325,6 @@ extern "C" int ccq_wq_mfma_linear_f32(const float* x, const uint8_t* w, const vo
   CCQ_REQUIRE(fmt == WQ_MXFP4 || scale, "ccq_wq_mfma_linear_f32: fmt %d needs its scales", fmt);
   CCQ_REQUIRE(fmt < WQ_MXFP8 || !scale || group_size == 16 || group_size == 32,
               "ccq_wq_mfma_linear_f32: group_size=%d (16 or 32)", group_size);
-  CCQ_REQUIRE(fmt < WQ_MXFP8 || !scale || group_size == 32 || aligned(scale, 2),
-              "ccq_wq_mfma_linear_f32: group-16 scales must be 2-byte aligned");
   CCQ_REQUIRE(cdiv(batch, 64) <= 65535, "ccq_wq_mfma_linear_f32: batch too large");
   return wq_mfma_linear(fmt, x, w, scale, group_size, scale2, y, batch, in_features, out_features,
                         as_stream(stream), "ccq_wq_mfma_linear_f32");

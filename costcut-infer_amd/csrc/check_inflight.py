@@ -1,16 +1,19 @@
-"""Build-time check of the register-streamed FP8 MoE kernels
-(``fp8_moe_rb_kernel`` in ccq_fp8.hip).
+"""Build-time check of the kernels that stream data into registers with
+inline-assembly loads: the register-streamed FP8 MoE kernels
+(``fp8_moe_rb_kernel`` in ccq_fp8.hip) and the decoded-weight MFMA linear
+(``wq_mfma_kernel`` in ccq_wmfma.hip).
 
-Their weight loads are inline-assembly ``global_load_dwordx4`` whose
-destination registers are handed to the compiler only by a later
-``s_waitcnt`` with ``"+v"`` operands.  Between the load and that wait the
-data has not arrived, so the compiler must neither read, copy nor spill
-those registers.  This script compiles ccq_fp8.hip for gfx950, dumps each
-kernel's machine code after greedy register allocation (virtual registers,
-with every copy and spill the allocator inserted), and runs a dataflow over
-the control-flow graph: a (virtual register, sub-register) defined by such a
-load is in flight until an ``s_waitcnt`` inline assembly takes it as a tied
-operand; any other instruction that names it while in flight is reported.
+Their loads are inline-assembly ``global_load_*`` whose destination
+registers are handed to the compiler only by a later inline assembly that
+takes them as tied (``"+v"``) operands, after an ``s_waitcnt``.  Between the
+load and that hand-over the data has not arrived, so the compiler must
+neither read, copy nor spill those registers.  This script compiles each
+source for gfx950, dumps each kernel's machine code after greedy register
+allocation (virtual registers, with every copy and spill the allocator
+inserted), and runs a dataflow over the control-flow graph: a (virtual
+register, sub-register) defined by such a load is in flight until an inline
+assembly takes it as a tied operand; any other instruction that names it
+while in flight is reported.
 
     python costcut-infer_amd/csrc/check_inflight.py      # exit 1 on a finding
 
@@ -30,9 +33,9 @@ INCLUDE = CSRC.parent.parent / "include"
 HIPCC = "/opt/rocm/bin/hipcc"
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
          "-packed-fp32-ops", f"-I{INCLUDE}", "--cuda-device-only"]
-KERNELS = ["_ZN3ccq17fp8_moe_rb_kernelILi1ELb0EEEvNS_5Fp8GPE",
-           "_ZN3ccq17fp8_moe_rb_kernelILi1ELb1EEEvNS_5Fp8GPE",
-           "_ZN3ccq17fp8_moe_rb_kernelILi2ELb0EEEvNS_5Fp8GPE"]
+# source -> pattern of the kernels to check (every instance in the build)
+TARGETS = {"ccq_fp8.hip": r"_ZN3ccq17fp8_moe_rb_kernel\w+",
+           "ccq_wmfma.hip": r"_ZN3ccq14wq_mfma_kernel\w+"}
 
 
 def _overlap(a, b):
@@ -70,13 +73,16 @@ def check_mir(text: str) -> list[str]:
         b = work.pop()
         live = set(state[b])
         for ins in blocks[b]["ins"]:
-            if "INLINEASM" in ins and "global_load_dwordx4" in ins:
-                d = re.search(r"def (?:undef )?%(\d+)(?:\.(\w+))?", ins)
+            if "INLINEASM" in ins and "global_load" in ins and "global_load_lds" not in ins:  # (LDS DMA: no register)
+                d = re.search(r"def (?:undef |dead |early-clobber )*%(\d+)(?:\.(\w+))?", ins)
+                if d is None:  # a load whose destination is not a virtual register
+                    found.setdefault("unparsed load: " + ins[:160], b)
+                    continue
                 key = (d.group(1), d.group(2) or "")
                 live = {x for x in live if not _overlap(x, key)}
                 live.add(key)
                 continue
-            if "INLINEASM" in ins and "s_waitcnt" in ins:
+            if "INLINEASM" in ins and "tiedto" in ins:
                 for v, sub in re.findall(r"reguse tiedto:\$\d+\], %(\d+)(?:\.(\w+))?", ins):
                     live = {x for x in live if not _overlap(x, (v, sub))}
                 continue
@@ -95,26 +101,31 @@ def check_mir(text: str) -> list[str]:
 
 
 def main() -> int:
-    src = CSRC / "ccq_fp8.hip"
     bad = 0
     with tempfile.TemporaryDirectory() as td:
-        asm = Path(td) / "ccq_fp8.s"
-        subprocess.run([HIPCC, *FLAGS, "-S", str(src), "-o", str(asm)], check=True, capture_output=True)
-        text = asm.read_text()
-        for k in KERNELS:
-            m = re.search(r"\.name:\s+" + re.escape(k) + r"\b(.*?)\.vgpr_count:\s+(\d+)", text, re.S)
-            sp = re.search(r"\.vgpr_spill_count:\s+(\d+)", text[m.end():m.end() + 400]) if m else None
-            vg, spills = (m.group(2) if m else "?"), (sp.group(1) if sp else "?")
-            r = subprocess.run([HIPCC, *FLAGS, "-S", str(src), "-o", "/dev/null", "-mllvm", "-print-after=greedy",
-                                "-mllvm", f"-filter-print-funcs={k}"], capture_output=True, text=True)
-            dump = r.stdout + r.stderr
-            first = dump.split("# *** IR Dump After")
-            mir = next((f for f in first if "# Machine code for function " + k in f), "")
-            issues = check_mir(mir)
-            print(f"{k}: {vg} VGPRs, {spills} spills, {len(issues)} in-flight register uses")
-            for line in issues[:10]:
-                print("   ", line)
-            bad += len(issues) + (0 if spills == "0" else 1)
+        for name, pattern in TARGETS.items():
+            src = CSRC / name
+            asm = Path(td) / (src.stem + ".s")
+            subprocess.run([HIPCC, *FLAGS, "-S", str(src), "-o", str(asm)], check=True, capture_output=True)
+            text = asm.read_text()
+            kernels = sorted(set(re.findall(r"\.name:\s+(" + pattern + r")\b", text)))
+            if not kernels:
+                print(f"{name}: no kernel matches {pattern}")
+                bad += 1
+            for k in kernels:
+                m = re.search(r"\.name:\s+" + re.escape(k) + r"\b(.*?)\.vgpr_count:\s+(\d+)", text, re.S)
+                sp = re.search(r"\.vgpr_spill_count:\s+(\d+)", text[m.end():m.end() + 400]) if m else None
+                vg, spills = (m.group(2) if m else "?"), (sp.group(1) if sp else "?")
+                r = subprocess.run([HIPCC, *FLAGS, "-S", str(src), "-o", "/dev/null", "-mllvm", "-print-after=greedy",
+                                    "-mllvm", f"-filter-print-funcs={k}"], capture_output=True, text=True)
+                dump = r.stdout + r.stderr
+                first = dump.split("# *** IR Dump After")
+                mir = next((f for f in first if "# Machine code for function " + k in f), "")
+                issues = check_mir(mir)
+                print(f"{k}: {vg} VGPRs, {spills} spills, {len(issues)} in-flight register uses")
+                for line in issues[:10]:
+                    print("   ", line)
+                bad += len(issues) + (0 if spills == "0" else 1)
     return 1 if bad else 0
 
 

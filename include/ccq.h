@@ -194,7 +194,7 @@ int ccq_mx_linear_f32(const float* x, const uint8_t* w, const uint8_t* scale_e8m
  * (quant/fp8.py:35-42), LinearMethod.apply for fp8 / int8 keys
  * (quant/method.py:100-140) and MxLinearMethod.apply (quant/mx.py:37-58):
  * ccq_mx_linear_f32 calls it for every batch, ccq_fp8_linear_f32 from 2
- * rows and ccq_int8_linear_f32 from 8 rows on (where it measured faster). */
+ * rows and ccq_int8_linear_f32 from 4 rows on (where it measured faster). */
 int ccq_wq_mfma_linear_f32(const float* x, const uint8_t* w, const void* scale,
                            float* y, int64_t batch, int64_t in_features,
                            int64_t out_features, int fmt, int group_size,
