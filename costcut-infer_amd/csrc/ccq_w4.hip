@@ -1766,7 +1766,10 @@ extern "C" int ccq_w4_gemm(const void* x, int x_dtype, const int32_t* w_tiled, c
     return launch_group_gemm<EPI_STORE>(g, x_dtype == CCQ_BF16, scale_dtype == CCQ_BF16, g.tiles, st);
   }
   const int64_t szw_d = sz_words_per_column(K, group_size);
-  const int nq = stream_nq(EPI_STORE, N, K, group_size);
+  // 16-column jobs (one quad) when 32-column jobs would leave CUs idle
+  // (K=2048 N=5632: 176 jobs of 32 columns, 352 of 16)
+  int nq = stream_nq(EPI_STORE, N, K, group_size);
+  if (nq == 2 && N / 32 < device_cus() && K <= 4096) nq = 1;
   if (M <= 16 && nq > 0) {
     // decode: one 16-row tile, weights streamed once
     W4SP w = {};
