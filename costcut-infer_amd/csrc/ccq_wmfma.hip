@@ -38,7 +38,10 @@ namespace ccq {
 constexpr int WQ_KC = 256;                 // k per chunk
 constexpr int WQ_CG = 4;                   // 16-column groups per workgroup
 constexpr int WQ_THREADS = 512;            // 8 waves: 4 column groups x 2 k halves
-constexpr int WQ_RS = WQ_KC + 8;           // LDS row stride in bf16 (rows 4 banks apart)
+// LDS row stride in bf16: rows 4 banks apart (padding 0 measured 3.5x the
+// bank-conflict cycles and 91 against 53 us at 64 rows; 16 or 24 the same
+// as 8)
+constexpr int WQ_RS = WQ_KC + 8;
 constexpr int WQ_COLS = 16 * WQ_CG;        // output columns per workgroup
 
 struct WqP {
@@ -119,6 +122,17 @@ __device__ __forceinline__ void wq_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// vmcnt(PD - 1 chunks of B + nx loads) for a wave-uniform nx in [0, NX]
+template <int PD, int B, int NX>
+__device__ __forceinline__ void wq_wait_nx(int nx) {
+  if (nx == NX) {
+    wq_wait<(PD - 1) * (B + NX)>();
+  } else if constexpr (NX > 0) {
+    wq_wait_nx<PD, B, NX - 1>(nx);
+  } else {
+    wq_wait<0>();
+  }
+}
 template <typename T>
 __device__ __forceinline__ void wq_tie(T& r) {
   asm volatile("" : "+v"(r));
@@ -154,8 +168,12 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
   uint32_t sr[PD][NSC > 0 ? NSC : 1];
   u32x4 xr[PD][XR];
 
-  // every lane issues LPC loads per chunk (x rows past M read row M-1 and
-  // are zeroed when staged), so the wait counts are exact
+  // activation piece j of a thread is row wave + 8j of the tile (wave-
+  // uniform): pieces of rows past M are not loaded (zeroed when staged), so
+  // a wave issues LPC - XR + nx loads per chunk, nx its valid pieces
+  int nx = 0;
+#pragma unroll
+  for (int j = 0; j < XR; ++j) nx += m0 + wave + 8 * j < M ? 1 : 0;
   auto issue = [&](int s, int c) {
     const int64_t kb = (int64_t)c * WQ_KC;
     const uint8_t* wp = wrow + (kb + lane_k) / Tr::KDIV;
@@ -168,14 +186,13 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_mfma_kernel(const WqP p) {
     }
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
-      const int idx = tid + WQ_THREADS * j, row = idx >> 6, col4 = idx & 63;
-      const int64_t gr = imin64(m0 + row, M - 1);
-      wq_load16(xr[s][j], p.x + gr * K + kb + 4 * col4);
+      const int row = wave + 8 * j, col4 = tid & 63;
+      if (j < nx) wq_load16(xr[s][j], p.x + (m0 + row) * K + kb + 4 * col4);
     }
   };
   auto wait_slot = [&](int s, bool steady) {
     if (steady)
-      wq_wait<(PD - 1) * LPC>();
+      wq_wait_nx<PD, LPC - XR, XR>(nx);
     else
       wq_wait<0>();
 #pragma unroll

@@ -12,6 +12,11 @@
 //   moe_driver gemm M K N reps copies
 //                           AWQ g128 linear y [M, N] = x [M, K] @ W,
 //                           ccq_w4_gemm over `copies` rotating weight sets
+//   moe_driver wq fmt M K N reps copies
+//                           decoded-weight MFMA linear (float32 x and y),
+//                           ccq_wq_mfma_linear_f32: fmt 0 FP8 row scale,
+//                           1 INT8 row scale, 2 MXFP8, 3 MXFP4 (E8M0 scales
+//                           per 32 columns)
 // Build: hipcc -O2 -Iinclude costcut-infer_amd/drivers/moe_driver.cpp
 //        -Lcostcut-infer_amd/ccut/_lib -lccq_hip -Wl,-rpath,<that dir> -o <binary>
 #include <hip/hip_runtime.h>
@@ -59,8 +64,41 @@ static int run_gemm(int argc, char** argv) {
   return 0;
 }
 
+static int run_wq(int argc, char** argv) {
+  const int fmt = argc > 2 ? atoi(argv[2]) : 3;
+  const int64_t M = argc > 3 ? atoll(argv[3]) : 16, K = argc > 4 ? atoll(argv[4]) : 4096,
+                N = argc > 5 ? atoll(argv[5]) : 14336;
+  const int reps = argc > 6 ? atoi(argv[6]) : 24, copies = argc > 7 ? atoi(argv[7]) : 12;
+  const int64_t wbytes = fmt == 3 ? N * K / 2 : N * K;
+  const bool mx = fmt >= 2;
+  std::vector<void*> w(copies);
+  for (int c = 0; c < copies; ++c) {
+    w[c] = dalloc(wbytes);
+    fill_rand_u32(w[c], wbytes / 4, 11 + c, 0x77777777u, 0);  // finite e4m3 / int8 / 4-bit codes
+  }
+  void* sc = mx ? dalloc(N * K / 32) : dalloc(N * 4);
+  if (mx)
+    fill_rand_u32(sc, N * K / 128, 5, 0x03030303u, 0x7C7C7C7Cu);  // E8M0 124..127
+  else
+    fill_rand_u32(sc, N, 5, 0x007FFFFFu, 0x3C000000u);  // float scales in [2^-7, 2^-6)
+  void* x = dalloc(M * K * 4);
+  fill_rand_u32(x, M * K, 7, 0x807FFFFFu, 0x3F000000u);  // floats of magnitude [0.5, 1)
+  void* y = dalloc(M * N * 4);
+  for (int r = 0; r < reps; ++r) {
+    const int c = r % copies;
+    const int rc = ccq_wq_mfma_linear_f32((const float*)x, (const uint8_t*)w[c], sc, (float*)y, M, K, N, fmt, 32,
+                                          1.0f, nullptr);
+    if (rc) { printf("rc=%d %s\n", rc, ccq_last_error()); return 4; }
+  }
+  CK(hipDeviceSynchronize());
+  printf("wq fmt=%d M=%lld K=%lld N=%lld reps %d copies %d done\n", fmt, (long long)M, (long long)K, (long long)N, reps,
+         copies);
+  return 0;
+}
+
 int main(int argc, char** argv) {
   if (argc > 1 && !strcmp(argv[1], "gemm")) return run_gemm(argc, argv);
+  if (argc > 1 && !strcmp(argv[1], "wq")) return run_wq(argc, argv);
   const bool fp8 = argc > 1 && !strcmp(argv[1], "fp8");
   const bool fwd = argc > 1 && !strcmp(argv[1], "w4f");  // decode shape through ccq_moe_w4_forward (logits)
   const bool dec = fwd || (argc > 1 && !strcmp(argv[1], "w4d"));  // int4 MoE decode shape
