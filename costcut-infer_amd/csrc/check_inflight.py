@@ -22,6 +22,7 @@ It also reports each kernel's VGPR and spill counts (from the assembly).
 
 from __future__ import annotations
 
+import concurrent.futures as cf
 import re
 import subprocess
 import sys
@@ -100,9 +101,23 @@ def check_mir(text: str) -> list[str]:
     return [f"bb.{b}: {ins}" for ins, b in found.items()]
 
 
-def main() -> int:
+def _check_kernel(src: Path, text: str, k: str) -> tuple[str, int]:
+    m = re.search(r"\.name:\s+" + re.escape(k) + r"\b(.*?)\.vgpr_count:\s+(\d+)", text, re.S)
+    sp = re.search(r"\.vgpr_spill_count:\s+(\d+)", text[m.end():m.end() + 400]) if m else None
+    vg, spills = (m.group(2) if m else "?"), (sp.group(1) if sp else "?")
+    r = subprocess.run([HIPCC, *FLAGS, "-S", str(src), "-o", "/dev/null", "-mllvm", "-print-after=greedy",
+                        "-mllvm", f"-filter-print-funcs={k}"], capture_output=True, text=True)
+    dump = r.stdout + r.stderr
+    mir = next((f for f in dump.split("# *** IR Dump After") if "# Machine code for function " + k in f), "")
+    issues = check_mir(mir)
+    lines = [f"{k}: {vg} VGPRs, {spills} spills, {len(issues)} in-flight register uses"]
+    lines += ["    " + line for line in issues[:10]]
+    return "\n".join(lines), len(issues) + (0 if spills == "0" else 1)
+
+
+def main(jobs: int = 8) -> int:
     bad = 0
-    with tempfile.TemporaryDirectory() as td:
+    with tempfile.TemporaryDirectory() as td, cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for name, pattern in TARGETS.items():
             src = CSRC / name
             asm = Path(td) / (src.stem + ".s")
@@ -112,20 +127,9 @@ def main() -> int:
             if not kernels:
                 print(f"{name}: no kernel matches {pattern}")
                 bad += 1
-            for k in kernels:
-                m = re.search(r"\.name:\s+" + re.escape(k) + r"\b(.*?)\.vgpr_count:\s+(\d+)", text, re.S)
-                sp = re.search(r"\.vgpr_spill_count:\s+(\d+)", text[m.end():m.end() + 400]) if m else None
-                vg, spills = (m.group(2) if m else "?"), (sp.group(1) if sp else "?")
-                r = subprocess.run([HIPCC, *FLAGS, "-S", str(src), "-o", "/dev/null", "-mllvm", "-print-after=greedy",
-                                    "-mllvm", f"-filter-print-funcs={k}"], capture_output=True, text=True)
-                dump = r.stdout + r.stderr
-                first = dump.split("# *** IR Dump After")
-                mir = next((f for f in first if "# Machine code for function " + k in f), "")
-                issues = check_mir(mir)
-                print(f"{k}: {vg} VGPRs, {spills} spills, {len(issues)} in-flight register uses")
-                for line in issues[:10]:
-                    print("   ", line)
-                bad += len(issues) + (0 if spills == "0" else 1)
+            for report, n in ex.map(lambda k: _check_kernel(src, text, k), kernels):
+                print(report)
+                bad += n
     return 1 if bad else 0
 
 
