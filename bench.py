@@ -20,8 +20,11 @@ all launches, so they run back to back and the HIP events on that stream
 bracket device time only.
 
 Also reported (``extra``): the same layer at T=1 (20 rotating layers, > 512
-MiB of routed weights), the AWQ skinny GEMM at K=4096 N=14336 M in {1,4,16}
-and the single AWQ GEMV K=2048 N=5632 (kernel GB/s); the prefill workloads
+MiB of routed weights), the T=16 layer with a shared expert run in the same
+kernels (65 experts), the AWQ skinny GEMM at K=4096 N=14336 M in {1,4,16}
+and the single AWQ GEMV K=2048 N=5632 (kernel GB/s); the reference-format
+FP8 per-row and the MX linears (MXFP4 / MXFP8, up to 64 rows on the
+decoded-weight MFMA kernel), INT8 W8A8, the FP8 quantizers; the prefill workloads
 as TFLOP/s against the matching dense MFMA peak: int4 MoE prefill (128
 experts, skewed top-8, hidden 2048, inter 768, T = 512 and 4096, bf16 MFMA,
 4 rotating weight sets) and FP8 block MoE prefill (256 experts, top-8,
