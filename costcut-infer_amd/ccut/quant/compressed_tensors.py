@@ -4,11 +4,19 @@ the ``ignore`` regexes of ``quantization_config`` -> one ``LayerQuantSpec``
 per layer.
 
 Weight strategies: ``channel`` / ``tensor`` (FP8 or INT8, as the
-reference), ``group`` (FP8 as the reference; **int4** -> ``K_AWQ_W4A16``
-with the group size along the input dimension, the AWQ GEMM packing under
-the group tensor names ``<layer>.weight`` / ``.scales`` / ``.zero_points``)
-and ``block`` (FP8 with ``block_structure [128, 128]`` -> ``K_FP8_BLOCK128``,
-scales ``<layer>.weight_scale`` [out/128, in/128]).  Activation strategies:
+reference; int4 raises), ``group`` (FP8 as the reference; **int4** ->
+``K_AWQ_W4A16`` with the group size along the input dimension) and
+``block`` (FP8 with ``block_structure [128, 128]`` -> ``K_FP8_BLOCK128``,
+scales ``<layer>.weight_scale`` [out/128, in/128]).
+
+The int4 group layout read here is this package's own: the AWQ GEMM packing
+(``qweight`` [in, out/8] int32, 4-bit zero points packed the same way, fp16
+scales [in/G, out]) stored under ``<layer>.weight`` / ``.zero_points`` /
+``.scales``.  It is not the compressed-tensors ``pack-quantized`` layout
+(``weight_packed`` [out, in/8], ``weight_scale``, ``weight_zero_point``,
+symmetric by default); a config whose ``format`` names that layout raises
+``NotImplementedError`` for its int4 groups, as the reference raises for
+every integer group.  Activation strategies:
 ``token`` / ``tensor`` / ``channel`` / ``dynamic`` / ``row`` as the
 reference, and ``group`` (per token per group, the activation side of block
 FP8).
@@ -73,6 +81,9 @@ def _weight_key(w_cfg: dict) -> QuantKey:
     strategy = str(w_cfg.get("strategy", "tensor")).casefold()
     dt = _elem_type(w_cfg)
     fp8 = "fp8" in dt or "float" in dt
+    if dt == "int4" and strategy != "group":
+        raise ValueError(f"compressed-tensors int4 weights with strategy {strategy!r}: only group-wise int4 "
+                         "(strategy 'group') is supported")
     if strategy == "channel":
         return _with_scale(get_quant_key(K_FP8_STATIC_CHANNEL_SYM if fp8 else K_INT8_STATIC_CHANNEL_SYM),
                            ScaleStrategy.PER_CHANNEL)
@@ -202,6 +213,11 @@ class CompressedTensorsConfig(QuantizationConfig):
             w_cfg = group["weights"]
             a_cfg = group.get("input_activations") or {}
             w_key = _weight_key(w_cfg)
+            fmt = str(group.get("format") or self.quant_cfg.get("format") or "").casefold()
+            if w_key.is_awq() and fmt == "pack-quantized":
+                raise NotImplementedError(
+                    f"{layer_name}: compressed-tensors pack-quantized int4 (weight_packed [out, in/8]) is not "
+                    "read; int4 groups must be stored in the AWQ GEMM packing under .weight/.zero_points/.scales")
             a_key = _act_key(a_cfg) if a_cfg else None
             strategy = str(w_cfg.get("strategy", "tensor")).casefold()
             if strategy == "group":

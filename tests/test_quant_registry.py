@@ -118,6 +118,32 @@ def test_compressed_tensors_int4_group_is_awq(tmp_path):
         resolve_checkpoint_quant(_write(tmp_path, _ct(sym))).get_layer_spec(name)
 
 
+@pytest.mark.parametrize("strategy", ["channel", "tensor"])
+def test_compressed_tensors_int4_not_group_raises(tmp_path, strategy):
+    """int4 weights with a per-channel or per-tensor scale have no kernel
+    here: they must raise, not resolve to the INT8 keys (whose kernels would
+    read packed nibbles as int8 codes)."""
+    w = {"num_bits": 4, "type": "int", "strategy": strategy, "symmetric": True}
+    cfg = resolve_checkpoint_quant(_write(tmp_path, _ct(w)))
+    with pytest.raises(ValueError, match="int4"):
+        cfg.get_layer_spec("model.layers.0.mlp.experts.0.up_proj")
+
+
+def test_compressed_tensors_pack_quantized_int4_raises(tmp_path):
+    """The compressed-tensors pack-quantized layout (weight_packed [out, in/8])
+    is not the AWQ-packed layout the int4 kernels read: such a config raises
+    instead of loading nibbles in the wrong order."""
+    w = {"num_bits": 4, "type": "int", "strategy": "group", "group_size": 128, "symmetric": False}
+    qc = dict(_ct(w), format="pack-quantized")
+    cfg = resolve_checkpoint_quant(_write(tmp_path, qc))
+    with pytest.raises(NotImplementedError, match="pack-quantized"):
+        cfg.get_layer_spec("model.layers.0.mlp.experts.0.up_proj")
+    # FP8 channel groups under the same format key still resolve
+    qf = dict(_ct(FP8_CHANNEL, FP8_TOKEN), format="pack-quantized")
+    spec = resolve_checkpoint_quant(_write(tmp_path, qf)).get_layer_spec("model.layers.0.mlp.experts.0.up_proj")
+    assert spec.weight_key.weight_dtype == QuantDType.FP8_E4M3
+
+
 def test_compressed_tensors_fp8_block(tmp_path):
     """FP8 strategy=block [128, 128] with per-token-group activations ->
     K_FP8_BLOCK128, dispatched to the block FP8 method."""
