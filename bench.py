@@ -14,10 +14,14 @@ resident in HBM.
 
 ``roofline`` is the dominant kernel of the step, that same routed gate/up
 launch (ccq_moe_w4_route_gate_up runs exactly it): algorithmic bytes per
-launch / its average device time.  Kernel device times come from
-:func:`device_time`: a spin kernel holds the stream while the host enqueues
-all launches, so they run back to back and the HIP events on that stream
-bracket device time only.
+launch / its average duration.  That duration comes from :func:`kernel_time`:
+HIP events that each launch's own dispatch records at the kernel's start and
+end (ccq_launch_timer), the interval rocprofv3's kernel trace reports; the
+average over back-to-back launches bracketed by one pair of events (which
+adds the gap between launches) is reported beside it.  Other device times
+come from :func:`device_time`: a spin kernel holds the stream while the host
+enqueues all launches, so they run back to back and the HIP events on that
+stream bracket device time only.
 
 Also reported (``extra``): the same layer at T=1 (20 rotating layers, > 512
 MiB of routed weights), the T=16 layer with a shared expert run in the same
@@ -132,6 +136,40 @@ def device_time(launches, reps: int = 1) -> float:
             return a.elapsed_time(b) * 1e-3 / n
         hold_ms = 2.0 * host_ms + 5.0
     raise RuntimeError("device_time: host enqueue never finished inside the stream hold")
+
+
+def kernel_time(launches, reps: int = 1) -> float:
+    """Average duration in seconds of the one kernel each of ``launches``
+    enqueues (a ccq entry point that launches exactly one kernel), from a
+    pair of HIP events per launch that the kernel's own dispatch records
+    (``ccq_launch_timer`` -> hipExtLaunchKernel): the interval from the
+    kernel's start to its end, which is what rocprofv3's kernel trace
+    reports, without the gap between back-to-back launches that events
+    bracketing the whole run include.  The launches run back to back behind
+    a stream hold as in :func:`device_time`."""
+    import torch
+
+    from ccut import _lib
+
+    lib = _lib.lib()
+    n = len(launches) * reps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for a, b in evs:  # creates the HIP events, so that cuda_event is a handle
+        a.record()
+        b.record()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(_sleep_calibration() * (5.0 + 0.05 * n)))
+    i = 0
+    for _r in range(reps):
+        for f in launches:
+            a, b = evs[i]
+            _lib.check(lib.ccq_launch_timer(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b.cuda_event)),
+                       "ccq_launch_timer")
+            f()
+            lib.ccq_launch_timer(None, None)  # a call that launched nothing leaves no armed timer behind
+            i += 1
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) * 1e-3 / n
 
 
 # -------------------------------------------------------------- workloads --
@@ -284,9 +322,12 @@ def time_gate_up(layers, x, T: int, dev):
     for f in launches:
         _lib.check(f(), "ccq_moe_w4_route_gate_up")
     torch.cuda.synchronize()
-    avg = device_time(launches, reps=max(1, 100 // len(launches)))
+    reps = max(1, 100 // len(launches))
+    avg = kernel_time(launches, reps=reps)
+    b2b = device_time(launches, reps=reps)
     avg_bytes = sum(gu_bytes) / len(gu_bytes)
-    return {"avg_us": avg * 1e6, "bytes": avg_bytes, "GBps": avg_bytes / avg / 1e9}
+    return {"avg_us": avg * 1e6, "bytes": avg_bytes, "GBps": avg_bytes / avg / 1e9,
+            "back_to_back_us": b2b * 1e6}
 
 
 def bench_gemm(M: int, K: int, N: int, dev, copies: int):
@@ -719,7 +760,8 @@ def main():
     head = bench_moe(args.tokens, args.steps, args.warmup, dev)
     gu = head["gate_up"]
     log(f"moe decode T={args.tokens}: {head['GBps']:.1f} GB/s, {head['ms_per_step'] * 1e3:.1f} us/step; "
-        f"gate/up kernel {gu['avg_us']:.2f} us = {gu['GBps']:.1f} GB/s")
+        f"gate/up kernel {gu['avg_us']:.2f} us = {gu['GBps']:.1f} GB/s ({gu['back_to_back_us']:.2f} us per "
+        "launch back to back)")
     extra = {}
     if not args.no_extra:
         t1 = bench_moe(1, args.steps, args.warmup, dev, n_layers=LAYERS_T1)

@@ -56,6 +56,7 @@ class ccq_fp8_experts(ctypes.Structure):
 SIGNATURES: dict[str, tuple] = {
     "ccq_version": (_int, []),
     "ccq_last_error": (ctypes.c_char_p, []),
+    "ccq_launch_timer": (_int, [_vp, _vp]),
     "ccq_fp8_to_f32": (_int, [_vp, _vp, _i64, _vp]),
     "ccq_f32_to_fp8": (_int, [_vp, _vp, _i64, _vp]),
     "ccq_fp8_dequant": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),

@@ -8,6 +8,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -20,6 +21,25 @@ namespace ccq {
 void set_error(const char* fmt, ...);
 int arg_error(const char* fmt, ...);           // sets message, returns CCQ_EINVAL
 int launch_status(const char* what);           // hipGetLastError -> code
+
+// Events for the next kernel launched through launch() on this thread
+// (ccq_launch_timer): hipExtLaunchKernel records them when that kernel
+// starts and ends executing, so their elapsed time is the kernel's own
+// duration.  take_launch_timer returns the pair and clears it.
+struct LaunchTimer {
+  hipEvent_t start, stop;
+};
+LaunchTimer take_launch_timer();
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes, hipStream_t st,
+                   Args... args) {
+  const LaunchTimer t = take_launch_timer();
+  if (t.start != nullptr)
+    hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, st, t.start, t.stop, 0u, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds_bytes, st, args...);
+}
 
 #define CCQ_REQUIRE(cond, ...)                                  \
   do {                                                          \

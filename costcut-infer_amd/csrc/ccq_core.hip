@@ -22,6 +22,14 @@ int arg_error(const char* fmt, ...) {
   return CCQ_EINVAL;
 }
 
+static thread_local LaunchTimer g_timer = {nullptr, nullptr};
+
+LaunchTimer take_launch_timer() {
+  const LaunchTimer t = g_timer;
+  g_timer = LaunchTimer{nullptr, nullptr};
+  return t;
+}
+
 int launch_status(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -36,3 +44,10 @@ int launch_status(const char* what) {
 extern "C" int ccq_version(void) { return 100; }
 
 extern "C" const char* ccq_last_error(void) { return ccq::g_err; }
+
+extern "C" int ccq_launch_timer(void* start_event, void* stop_event) {
+  CCQ_REQUIRE((start_event == nullptr) == (stop_event == nullptr),
+              "ccq_launch_timer: give both events or neither");
+  ccq::g_timer = ccq::LaunchTimer{reinterpret_cast<hipEvent_t>(start_event), reinterpret_cast<hipEvent_t>(stop_event)};
+  return 0;
+}

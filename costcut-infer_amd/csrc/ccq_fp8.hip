@@ -1032,11 +1032,11 @@ static int launch_fp8_gemm(const Fp8GP& p, int64_t tiles, hipStream_t st) {
         const int64_t items = tiles * (p.N / wgn), cus = f8_device_cus();
         const dim3 grid((unsigned)(items < cus ? items : cus)), block(RB_NW * 64);
         if constexpr (EPI == F8_SILU_Q)
-          hipLaunchKernelGGL((fp8_moe_rb_kernel<F8_SILU_Q, false>), grid, block, 0, st, p);
+          launch((fp8_moe_rb_kernel<F8_SILU_Q, false>), grid, block, 0, st, p);
         else if (lo)
-          hipLaunchKernelGGL((fp8_moe_rb_kernel<F8_ROWS, true>), grid, block, 0, st, p);
+          launch((fp8_moe_rb_kernel<F8_ROWS, true>), grid, block, 0, st, p);
         else
-          hipLaunchKernelGGL((fp8_moe_rb_kernel<F8_ROWS, false>), grid, block, 0, st, p);
+          launch((fp8_moe_rb_kernel<F8_ROWS, false>), grid, block, 0, st, p);
         return launch_status("fp8 moe gemm");
       }
     }
@@ -1048,14 +1048,14 @@ static int launch_fp8_gemm(const Fp8GP& p, int64_t tiles, hipStream_t st) {
   const dim3 grid((unsigned)(items < cus ? items : cus)), block(512);
   if constexpr (EPI == F8_ROWS) {
     if (lo) {
-      hipLaunchKernelGGL((fp8_gemm_kernel<EPI, 2, true>), grid, block, 0, st, p);
+      launch((fp8_gemm_kernel<EPI, 2, true>), grid, block, 0, st, p);
       return launch_status("fp8 gemm");
     }
   }
   if (wgn == 256)
-    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, (EPI == F8_SILU_Q ? 2 : 4)>), grid, block, 0, st, p);
+    launch((fp8_gemm_kernel<EPI, (EPI == F8_SILU_Q ? 2 : 4)>), grid, block, 0, st, p);
   else
-    hipLaunchKernelGGL((fp8_gemm_kernel<EPI, 2>), grid, block, 0, st, p);
+    launch((fp8_gemm_kernel<EPI, 2>), grid, block, 0, st, p);
   return launch_status("fp8 gemm");
 }
 
@@ -1069,11 +1069,11 @@ int launch_act_quant(const void* x, int x_dtype, int64_t ldx, int64_t rows, int6
   const int64_t KB = K / 128;
   const dim3 grid(grid_of(rows * KB * 16, 256));
   if (x_dtype == CCQ_BF16)
-    hipLaunchKernelGGL(fp8_act_quant_kernel<CCQ_BF16>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
+    launch(fp8_act_quant_kernel<CCQ_BF16>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
   else if (x_dtype == CCQ_F16)
-    hipLaunchKernelGGL(fp8_act_quant_kernel<CCQ_F16>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
+    launch(fp8_act_quant_kernel<CCQ_F16>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
   else
-    hipLaunchKernelGGL(fp8_act_quant_kernel<CCQ_F32>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
+    launch(fp8_act_quant_kernel<CCQ_F32>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
   return launch_status("fp8 act quant");
 }
 
@@ -1099,7 +1099,7 @@ extern "C" int ccq_fp8_block_repack(const uint8_t* w, uint8_t* tiled, int64_t N,
   CCQ_REQUIRE(w && tiled, "ccq_fp8_block_repack: null pointer");
   CCQ_REQUIRE(w != tiled, "ccq_fp8_block_repack: in-place is not supported");
   CCQ_REQUIRE(aligned(w, 16) && aligned(tiled, 16), "ccq_fp8_block_repack: pointers must be 16-byte aligned");
-  hipLaunchKernelGGL(fp8_repack_kernel, dim3(grid_of(N * K / 16, 256)), dim3(256), 0, as_stream(stream), w, tiled,
+  launch(fp8_repack_kernel, dim3(grid_of(N * K / 16, 256)), dim3(256), 0, as_stream(stream), w, tiled,
                      N, K);
   return launch_status("ccq_fp8_block_repack");
 }
@@ -1111,7 +1111,7 @@ extern "C" int ccq_fp8_block_unpack(const uint8_t* tiled, uint8_t* w, int64_t N,
   CCQ_REQUIRE(w && tiled, "ccq_fp8_block_unpack: null pointer");
   CCQ_REQUIRE(w != tiled, "ccq_fp8_block_unpack: in-place is not supported");
   CCQ_REQUIRE(aligned(w, 16) && aligned(tiled, 16), "ccq_fp8_block_unpack: pointers must be 16-byte aligned");
-  hipLaunchKernelGGL(fp8_unpack_kernel, dim3(grid_of(N * K / 16, 256)), dim3(256), 0, as_stream(stream), tiled, w,
+  launch(fp8_unpack_kernel, dim3(grid_of(N * K / 16, 256)), dim3(256), 0, as_stream(stream), tiled, w,
                      N, K);
   return launch_status("ccq_fp8_block_unpack");
 }
@@ -1122,7 +1122,7 @@ extern "C" int ccq_fp8_block_dequant(const uint8_t* w, const float* s_w, float* 
   CCQ_REQUIRE(N == 0 || K <= INT64_MAX / N, "ccq_fp8_block_dequant: N*K overflows");
   if (N == 0 || K == 0) return 0;
   CCQ_REQUIRE(w && s_w && out, "ccq_fp8_block_dequant: null pointer");
-  hipLaunchKernelGGL(fp8_block_dequant_kernel, dim3(grid_of(N * K, 256)), dim3(256), 0, as_stream(stream), w, s_w,
+  launch(fp8_block_dequant_kernel, dim3(grid_of(N * K, 256)), dim3(256), 0, as_stream(stream), w, s_w,
                      out, N, K);
   return launch_status("ccq_fp8_block_dequant");
 }

@@ -513,19 +513,19 @@ extern "C" int ccq_int8_act_quant(const float* x, int8_t* xq, float* x_scale, in
   if (K % 4 == 0 && K > 0 && aligned(x, 16) && aligned(xq, 4)) {
     const int64_t n4 = K / 4;
     if (n4 <= 256)
-      hipLaunchKernelGGL(int8_act_quant_vec_kernel<1>, grid, block, 0, st, x, xq, x_scale, K);
+      launch(int8_act_quant_vec_kernel<1>, grid, block, 0, st, x, xq, x_scale, K);
     else if (n4 <= 512)
-      hipLaunchKernelGGL(int8_act_quant_vec_kernel<2>, grid, block, 0, st, x, xq, x_scale, K);
+      launch(int8_act_quant_vec_kernel<2>, grid, block, 0, st, x, xq, x_scale, K);
     else if (n4 <= 1024)
-      hipLaunchKernelGGL(int8_act_quant_vec_kernel<4>, grid, block, 0, st, x, xq, x_scale, K);
+      launch(int8_act_quant_vec_kernel<4>, grid, block, 0, st, x, xq, x_scale, K);
     else if (n4 <= 2048)
-      hipLaunchKernelGGL(int8_act_quant_vec_kernel<8>, grid, block, 0, st, x, xq, x_scale, K);
+      launch(int8_act_quant_vec_kernel<8>, grid, block, 0, st, x, xq, x_scale, K);
     else if (n4 <= 4096)
-      hipLaunchKernelGGL(int8_act_quant_vec_kernel<16>, grid, block, 0, st, x, xq, x_scale, K);
+      launch(int8_act_quant_vec_kernel<16>, grid, block, 0, st, x, xq, x_scale, K);
     else
-      hipLaunchKernelGGL(int8_act_quant_kernel, grid, block, 0, st, x, xq, x_scale, K);
+      launch(int8_act_quant_kernel, grid, block, 0, st, x, xq, x_scale, K);
   } else {
-    hipLaunchKernelGGL(int8_act_quant_kernel, grid, block, 0, st, x, xq, x_scale, K);
+    launch(int8_act_quant_kernel, grid, block, 0, st, x, xq, x_scale, K);
   }
   return launch_status("ccq_int8_act_quant");
 }
@@ -547,7 +547,7 @@ extern "C" int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int
   hipStream_t st = as_stream(stream);
   if (K == 0 || K % 16 != 0 || !aligned(xq, 16) || !aligned(w, 16)) {  // exact per-output sums
     const int64_t n = M * N;
-    hipLaunchKernelGGL(int8_gemm_scalar_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, xq, x_scale, w,
+    launch(int8_gemm_scalar_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, xq, x_scale, w,
                        w_scale, y, (int)M, (int)N, K);
     return launch_status("ccq_int8_linear");
   }
@@ -561,7 +561,7 @@ extern "C" int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int
     const int64_t kper = cdiv(cdiv(K, s), 16) * 16;
     nsplit = (int)cdiv(K, kper);
     CCQ_REQUIRE(cdiv(N, 32) <= 0x7fffffff, "ccq_int8_linear: N too large");
-    hipLaunchKernelGGL(int8_gemm_skinny_kernel<false>, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0,
+    launch(int8_gemm_skinny_kernel<false>, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0,
                        st, xq, (const float*)nullptr, (float*)nullptr, x_scale, w, w_scale, y, (int32_t*)workspace,
                        (int)M, (int)N, K, kper);
   } else if (int8_big(M, K, N)) {
@@ -569,17 +569,17 @@ extern "C" int ccq_int8_linear(const int8_t* xq, const float* x_scale, const int
     const dim3 grid((unsigned)cdiv(N, BG_T), (unsigned)cdiv(M, BG_T), (unsigned)cdiv(K, kper));
     CCQ_REQUIRE(grid.y <= 65535, "ccq_int8_linear: M=%lld too large", (long long)M);
     nsplit = (int)grid.z;
-    hipLaunchKernelGGL(int8_gemm_big_kernel, grid, dim3(256), 0, st, xq, x_scale, w, w_scale, y,
+    launch(int8_gemm_big_kernel, grid, dim3(256), 0, st, xq, x_scale, w, w_scale, y,
                        (int32_t*)workspace, (int)M, (int)N, K, kper);
   } else {
     const int64_t kper = cdiv(cdiv(K, s), I8_KC) * I8_KC;
     const dim3 grid((unsigned)cdiv(N, I8_BT), (unsigned)cdiv(M, I8_BT), (unsigned)cdiv(K, kper));
     nsplit = (int)grid.z;
-    hipLaunchKernelGGL(int8_gemm_kernel, grid, dim3(256), 0, st, xq, x_scale, w, w_scale, y, (int32_t*)workspace,
+    launch(int8_gemm_kernel, grid, dim3(256), 0, st, xq, x_scale, w, w_scale, y, (int32_t*)workspace,
                        (int)M, (int)N, K, kper);
   }
   if (nsplit > 1)
-    hipLaunchKernelGGL(int8_splitk_epilogue_kernel, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
+    launch(int8_splitk_epilogue_kernel, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
                        (const int32_t*)workspace, x_scale, w_scale, y, (int)M, (int)N, nsplit);
   return launch_status("ccq_int8_linear");
 }
@@ -616,11 +616,11 @@ extern "C" int ccq_int8_w8a8_linear(const float* x, float* x_scale, const int8_t
     const int s = int8_splits(M, K, N);
     const int64_t kper = cdiv(cdiv(K, s), 16) * 16;
     const int nsplit = (int)cdiv(K, kper);
-    hipLaunchKernelGGL(int8_gemm_skinny_kernel<true>, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0,
+    launch(int8_gemm_skinny_kernel<true>, dim3((unsigned)cdiv(N, 32), (unsigned)nsplit), dim3(256), 0,
                        st, (const int8_t*)nullptr, x, x_scale, (const float*)x_scale, w, w_scale, y,
                        (int32_t*)workspace, (int)M, (int)N, K, kper);
     if (nsplit > 1)
-      hipLaunchKernelGGL(int8_splitk_epilogue_kernel, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
+      launch(int8_splitk_epilogue_kernel, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
                          (const int32_t*)workspace, x_scale, w_scale, y, (int)M, (int)N, nsplit);
     return launch_status("ccq_int8_w8a8_linear");
   }
@@ -637,7 +637,7 @@ extern "C" int ccq_int8_dequant(const int8_t* w, const float* scale, float* out,
   CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_int8_dequant: negative shape");
   if (rows == 0 || cols == 0) return 0;
   CCQ_REQUIRE(w && scale && out, "ccq_int8_dequant: null pointer");
-  hipLaunchKernelGGL(int8_dequant_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream), w,
+  launch(int8_dequant_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream), w,
                      scale, out, rows, cols);
   return launch_status("ccq_int8_dequant");
 }

@@ -250,7 +250,7 @@ extern "C" int ccq_e8m0_to_f32(const uint8_t* e8m0, float* out, int64_t n, void*
   CCQ_REQUIRE(n >= 0, "ccq_e8m0_to_f32: negative size");
   if (n == 0) return 0;
   CCQ_REQUIRE(e8m0 && out, "ccq_e8m0_to_f32: null pointer");
-  hipLaunchKernelGGL(e8m0_to_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), e8m0, out, n);
+  launch(e8m0_to_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), e8m0, out, n);
   return launch_status("ccq_e8m0_to_f32");
 }
 
@@ -264,23 +264,23 @@ extern "C" int ccq_mx_dequant(const uint8_t* w, const uint8_t* scale_e8m0, float
     const dim3 g(grid_for(units, 256));
     hipStream_t st = as_stream(stream);
     if (fmt == 1 && group_size == 32)
-      hipLaunchKernelGGL((mx_dequant_vec_kernel<true, 32>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols, scale2);
+      launch((mx_dequant_vec_kernel<true, 32>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols, scale2);
     else if (fmt == 1)
-      hipLaunchKernelGGL((mx_dequant_vec_kernel<true, 16>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols, scale2);
+      launch((mx_dequant_vec_kernel<true, 16>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols, scale2);
     else if (group_size == 32)
-      hipLaunchKernelGGL((mx_dequant_vec_kernel<false, 32>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols,
+      launch((mx_dequant_vec_kernel<false, 32>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols,
                          scale2);
     else
-      hipLaunchKernelGGL((mx_dequant_vec_kernel<false, 16>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols,
+      launch((mx_dequant_vec_kernel<false, 16>), g, dim3(256), 0, st, w, scale_e8m0, out, rows, cols,
                          scale2);
     return launch_status("ccq_mx_dequant");
   }
   const dim3 grid(grid_for(rows * cols, 256));
   if (fmt == 1)
-    hipLaunchKernelGGL(mx_dequant_kernel<true>, grid, dim3(256), 0, as_stream(stream), w, scale_e8m0, out, rows,
+    launch(mx_dequant_kernel<true>, grid, dim3(256), 0, as_stream(stream), w, scale_e8m0, out, rows,
                        cols, group_size, scale2);
   else
-    hipLaunchKernelGGL(mx_dequant_kernel<false>, grid, dim3(256), 0, as_stream(stream), w, scale_e8m0, out, rows,
+    launch(mx_dequant_kernel<false>, grid, dim3(256), 0, as_stream(stream), w, scale_e8m0, out, rows,
                        cols, group_size, scale2);
   return launch_status("ccq_mx_dequant");
 }
@@ -303,25 +303,25 @@ extern "C" int ccq_mx_linear_f32(const float* x, const uint8_t* w, const uint8_t
     const dim3 grid((unsigned)cdiv(out_features, 4 * kMxRPW), (unsigned)cdiv(batch, kMxBB));
     hipStream_t st = as_stream(stream);
     if (fmt == 1 && group_size == 32)
-      hipLaunchKernelGGL((mx_linear_f32_vec_kernel<true, 32>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
+      launch((mx_linear_f32_vec_kernel<true, 32>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
                          in_features, out_features, scale2);
     else if (fmt == 1)
-      hipLaunchKernelGGL((mx_linear_f32_vec_kernel<true, 16>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
+      launch((mx_linear_f32_vec_kernel<true, 16>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
                          in_features, out_features, scale2);
     else if (group_size == 32)
-      hipLaunchKernelGGL((mx_linear_f32_vec_kernel<false, 32>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
+      launch((mx_linear_f32_vec_kernel<false, 32>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
                          in_features, out_features, scale2);
     else
-      hipLaunchKernelGGL((mx_linear_f32_vec_kernel<false, 16>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
+      launch((mx_linear_f32_vec_kernel<false, 16>), grid, dim3(256), 0, st, x, w, scale_e8m0, y, batch,
                          in_features, out_features, scale2);
     return launch_status("ccq_mx_linear_f32");
   }
   const dim3 grid((unsigned)cdiv(out_features, 4), (unsigned)cdiv(batch, kMxBB));
   if (fmt == 1)
-    hipLaunchKernelGGL(mx_linear_f32_kernel<true>, grid, dim3(256), 0, as_stream(stream), x, w, scale_e8m0, y,
+    launch(mx_linear_f32_kernel<true>, grid, dim3(256), 0, as_stream(stream), x, w, scale_e8m0, y,
                        batch, in_features, out_features, group_size, scale2);
   else
-    hipLaunchKernelGGL(mx_linear_f32_kernel<false>, grid, dim3(256), 0, as_stream(stream), x, w, scale_e8m0, y,
+    launch(mx_linear_f32_kernel<false>, grid, dim3(256), 0, as_stream(stream), x, w, scale_e8m0, y,
                        batch, in_features, out_features, group_size, scale2);
   return launch_status("ccq_mx_linear_f32");
 }

@@ -582,15 +582,15 @@ extern "C" int ccq_quantize_rows_fp8(const uint16_t* w_bf16, const float* scale,
   if (cols % 8 == 0 && nv <= 2048 && aligned(w_bf16, 16) && aligned(out, 8)) {
     const dim3 g((unsigned)rows), b(256);
     if (nv <= 256)
-      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<1>, g, b, 0, st, w_bf16, scale, out, cols);
+      launch(quant_rows_fp8_vec_kernel<1>, g, b, 0, st, w_bf16, scale, out, cols);
     else if (nv <= 512)
-      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<2>, g, b, 0, st, w_bf16, scale, out, cols);
+      launch(quant_rows_fp8_vec_kernel<2>, g, b, 0, st, w_bf16, scale, out, cols);
     else if (nv <= 1024)
-      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<4>, g, b, 0, st, w_bf16, scale, out, cols);
+      launch(quant_rows_fp8_vec_kernel<4>, g, b, 0, st, w_bf16, scale, out, cols);
     else
-      hipLaunchKernelGGL(quant_rows_fp8_vec_kernel<8>, g, b, 0, st, w_bf16, scale, out, cols);
+      launch(quant_rows_fp8_vec_kernel<8>, g, b, 0, st, w_bf16, scale, out, cols);
   } else {
-    hipLaunchKernelGGL(quant_rows_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, st, w_bf16, scale, out, cols);
+    launch(quant_rows_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, st, w_bf16, scale, out, cols);
   }
   return launch_status("ccq_quantize_rows_fp8");
 }
@@ -604,7 +604,7 @@ extern "C" int ccq_kv_quant_fp8(const float* kv, uint8_t* out, uint8_t* scales, 
   hipStream_t st = as_stream(stream);
   const int tpr = kv_tpr(dim, kv, out);
 #define CCQ_KVQ(T)                                                                                            \
-  hipLaunchKernelGGL(kv_quant_fp8_vec_kernel<T>, dim3((unsigned)cdiv(rows, 256 / T)), dim3(256), 0, st, kv, out, \
+  launch(kv_quant_fp8_vec_kernel<T>, dim3((unsigned)cdiv(rows, 256 / T)), dim3(256), 0, st, kv, out, \
                      scales, rows, dim)
   switch (tpr) {
     case 1: CCQ_KVQ(1); break;
@@ -614,7 +614,7 @@ extern "C" int ccq_kv_quant_fp8(const float* kv, uint8_t* out, uint8_t* scales, 
     case 16: CCQ_KVQ(16); break;
     case 32: CCQ_KVQ(32); break;
     case 64: CCQ_KVQ(64); break;
-    default: hipLaunchKernelGGL(kv_quant_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, st, kv, out, scales, dim);
+    default: launch(kv_quant_fp8_kernel, dim3((unsigned)rows), dim3(256), 0, st, kv, out, scales, dim);
   }
 #undef CCQ_KVQ
   return launch_status("ccq_kv_quant_fp8");
@@ -630,7 +630,7 @@ extern "C" int ccq_kv_dequant_fp8(const uint8_t* codes, const uint8_t* scales, f
   hipStream_t st = as_stream(stream);
   const int tpr = kv_tpr(dim, out, codes);
 #define CCQ_KVD(T)                                                                                          \
-  hipLaunchKernelGGL(kv_dequant_fp8_vec_kernel<T>, dim3((unsigned)cdiv(rows, 256 / T)), dim3(256), 0, st, codes, \
+  launch(kv_dequant_fp8_vec_kernel<T>, dim3((unsigned)cdiv(rows, 256 / T)), dim3(256), 0, st, codes, \
                      scales, out, rows, dim)
   switch (tpr) {
     case 1: CCQ_KVD(1); break;
@@ -641,7 +641,7 @@ extern "C" int ccq_kv_dequant_fp8(const uint8_t* codes, const uint8_t* scales, f
     case 32: CCQ_KVD(32); break;
     case 64: CCQ_KVD(64); break;
     default:
-      hipLaunchKernelGGL(kv_dequant_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, codes, scales, out, n, dim);
+      launch(kv_dequant_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, codes, scales, out, n, dim);
   }
 #undef CCQ_KVD
   return launch_status("ccq_kv_dequant_fp8");
@@ -651,7 +651,7 @@ extern "C" int ccq_fp8_to_f32(const uint8_t* code, float* out, int64_t n, void* 
   CCQ_REQUIRE(n >= 0, "ccq_fp8_to_f32: n < 0");
   if (n == 0) return 0;
   CCQ_REQUIRE(code && out, "ccq_fp8_to_f32: null pointer");
-  hipLaunchKernelGGL(fp8_to_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), code, out, n);
+  launch(fp8_to_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), code, out, n);
   return launch_status("ccq_fp8_to_f32");
 }
 
@@ -659,7 +659,7 @@ extern "C" int ccq_f32_to_fp8(const float* x, uint8_t* out, int64_t n, void* str
   CCQ_REQUIRE(n >= 0, "ccq_f32_to_fp8: n < 0");
   if (n == 0) return 0;
   CCQ_REQUIRE(x && out, "ccq_f32_to_fp8: null pointer");
-  hipLaunchKernelGGL(f32_to_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), x, out, n);
+  launch(f32_to_fp8_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), x, out, n);
   return launch_status("ccq_f32_to_fp8");
 }
 
@@ -670,7 +670,7 @@ extern "C" int ccq_group_broadcast_scale(const float* scale_groups, int64_t grou
   const int64_t n = groups * group_size;
   if (n == 0) return 0;
   CCQ_REQUIRE(scale_groups && out, "ccq_group_broadcast_scale: null pointer");
-  hipLaunchKernelGGL(group_broadcast_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), scale_groups,
+  launch(group_broadcast_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), scale_groups,
                      out, n, group_size);
   return launch_status("ccq_group_broadcast_scale");
 }
@@ -679,7 +679,7 @@ extern "C" int ccq_silu_mul(const float* gate, const float* up, float* out, int6
   CCQ_REQUIRE(n >= 0, "ccq_silu_mul: n < 0");
   if (n == 0) return 0;
   CCQ_REQUIRE(gate && up && out, "ccq_silu_mul: null pointer");
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), gate, up, out, n);
+  launch(silu_mul_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), gate, up, out, n);
   return launch_status("ccq_silu_mul");
 }
 
@@ -688,7 +688,7 @@ extern "C" int ccq_fp8_dequant(const uint8_t* w, const float* scale, float* out,
   CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_fp8_dequant: negative shape");
   if (rows == 0 || cols == 0) return 0;
   CCQ_REQUIRE(w && scale && out, "ccq_fp8_dequant: null pointer");
-  hipLaunchKernelGGL(fp8_dequant_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream), w,
+  launch(fp8_dequant_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream), w,
                      scale, out, rows, cols);
   return launch_status("ccq_fp8_dequant");
 }
@@ -699,7 +699,7 @@ extern "C" int ccq_int4_dequant(const uint8_t* packed, const float* scale, float
   CCQ_REQUIRE(cols % 2 == 0, "ccq_int4_dequant: cols=%lld must be even (2 nibbles per byte)", (long long)cols);
   if (rows == 0 || cols == 0) return 0;
   CCQ_REQUIRE(packed && scale && out, "ccq_int4_dequant: null pointer");
-  hipLaunchKernelGGL(int4_dequant_kernel, dim3(grid_for(rows * cols / 2, 256)), dim3(256), 0, as_stream(stream),
+  launch(int4_dequant_kernel, dim3(grid_for(rows * cols / 2, 256)), dim3(256), 0, as_stream(stream),
                      packed, scale, out, rows, cols);
   return launch_status("ccq_int4_dequant");
 }
@@ -722,7 +722,7 @@ static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* sc
   dim3 grid((unsigned)cdiv(out_f, 4), (unsigned)cdiv(batch, kLinBB));
   CCQ_REQUIRE(grid.x <= 0x7fffffffu, "%s: out_features too large", name);
   if (in_f == 0) {  // empty sum; a fill kernel rather than a memset node
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_for(batch * out_f, 256)), dim3(256), 0, as_stream(stream), y,
+    launch(zero_f32_kernel, dim3(grid_for(batch * out_f, 256)), dim3(256), 0, as_stream(stream), y,
                        batch * out_f);
     return launch_status(name);
   }
@@ -744,7 +744,7 @@ static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* sc
     const dim3 g((unsigned)cdiv(out_f, 4 * (bb == 1 ? rv_rows<1>() : rv_rows<2>())), (unsigned)cdiv(batch, bb));
     CCQ_REQUIRE(cdiv(batch, bb) <= 65535, "%s: batch too large", name);
     const size_t lds = (size_t)bb * in_f * 4;
-#define CCQ_RV(F, B) hipLaunchKernelGGL((ref_linear_vec_kernel<F, B>), g, dim3(256), lds, as_stream(stream), x, w, scale, y, batch, in_f, out_f)
+#define CCQ_RV(F, B) launch((ref_linear_vec_kernel<F, B>), g, dim3(256), lds, as_stream(stream), x, w, scale, y, batch, in_f, out_f)
 #define CCQ_RV_B(F)   \
   do {                \
     if (bb == 8)      \
@@ -767,16 +767,16 @@ static int ref_linear(int fmt, const float* x, const uint8_t* w, const float* sc
     return launch_status(name);
   }
   if (fmt == 1)
-    hipLaunchKernelGGL(ref_linear_f32_kernel<1>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+    launch(ref_linear_f32_kernel<1>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
                        in_f, out_f, table, table_len);
   else if (fmt == 2)
-    hipLaunchKernelGGL(ref_linear_f32_kernel<2>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+    launch(ref_linear_f32_kernel<2>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
                        in_f, out_f, table, table_len);
   else if (fmt == 3)
-    hipLaunchKernelGGL(ref_linear_f32_kernel<3>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+    launch(ref_linear_f32_kernel<3>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
                        in_f, out_f, table, table_len);
   else
-    hipLaunchKernelGGL(ref_linear_f32_kernel<0>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
+    launch(ref_linear_f32_kernel<0>, grid, dim3(256), 0, as_stream(stream), x, w, scale, y, batch,
                        in_f, out_f, table, table_len);
   return launch_status(name);
 }
@@ -807,7 +807,7 @@ extern "C" int ccq_nf4_dequant(const uint8_t* packed, const float* scale, const 
   CCQ_REQUIRE(table_len >= 0 && table_len <= 16, "ccq_nf4_dequant: table_len=%d outside [0, 16]", table_len);
   if (rows == 0 || cols == 0) return 0;
   CCQ_REQUIRE(packed && scale && out && (table || table_len == 0), "ccq_nf4_dequant: null pointer");
-  hipLaunchKernelGGL(nf4_dequant_kernel, dim3(grid_for(rows * cols / 2, 256)), dim3(256), 0, as_stream(stream),
+  launch(nf4_dequant_kernel, dim3(grid_for(rows * cols / 2, 256)), dim3(256), 0, as_stream(stream),
                      packed, scale, table, table_len, out, rows, cols);
   return launch_status("ccq_nf4_dequant");
 }
@@ -817,7 +817,7 @@ extern "C" int ccq_int8_quantize_cols(const float* x, const float* amax, int8_t*
   CCQ_REQUIRE(rows >= 0 && cols >= 0, "ccq_int8_quantize_cols: negative shape");
   if (rows == 0 || cols == 0) return 0;
   CCQ_REQUIRE(x && amax && out, "ccq_int8_quantize_cols: null pointer");
-  hipLaunchKernelGGL(int8_quantize_cols_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream),
+  launch(int8_quantize_cols_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, as_stream(stream),
                      x, amax, out, rows, cols);
   return launch_status("ccq_int8_quantize_cols");
 }

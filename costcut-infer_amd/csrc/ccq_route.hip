@@ -305,13 +305,13 @@ static void launch_combine_v(const void* rows, const float* wts, const int64_t* 
   const int64_t cols = VEC ? H / (RT == CCQ_F32 ? 4 : 8) : H;
   dim3 grid((unsigned)cdiv(cols, 256), (unsigned)T);
   if (y_dtype == CCQ_F32)
-    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F32, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+    launch((moe_combine_kernel<CCQ_F32, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
                        (int)k, H, shared, sg);
   else if (y_dtype == CCQ_BF16)
-    hipLaunchKernelGGL((moe_combine_kernel<CCQ_BF16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+    launch((moe_combine_kernel<CCQ_BF16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
                        (int)k, H, shared, sg);
   else
-    hipLaunchKernelGGL((moe_combine_kernel<CCQ_F16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+    launch((moe_combine_kernel<CCQ_F16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
                        (int)k, H, shared, sg);
 }
 
@@ -527,17 +527,17 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
   const int64_t nchunks = cdiv(n, kChunk);
   // below ~6K assignments one workgroup is faster than three launches
   if (scratch == nullptr || n <= 6 * kChunk || scratch_bytes < align_scratch_bytes(n, E)) {
-    hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
+    launch(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
                        tile_expert, meta, counts);
     return launch_status("moe_align");
   }
   int32_t* ccnt = (int32_t*)scratch;
   int32_t* cfirst = ccnt + nchunks * E;
-  hipLaunchKernelGGL(align_chunk_count_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
+  launch(align_chunk_count_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
                      cfirst);
-  hipLaunchKernelGGL(align_plan_kernel, dim3(1), dim3(1024), 0, st, (int)E, (int)nchunks, (int)tile_m, ccnt, cfirst,
+  launch(align_plan_kernel, dim3(1), dim3(1024), 0, st, (int)E, (int)nchunks, (int)tile_m, ccnt, cfirst,
                      sorted_ids, tile_expert, meta, counts);
-  hipLaunchKernelGGL(align_chunk_scatter_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
+  launch(align_chunk_scatter_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
                      cfirst, sorted_ids);
   return launch_status("moe_align (chunked)");
 }
@@ -559,13 +559,13 @@ extern "C" int ccq_topk_softmax(const float* logits, float* weights, int64_t* id
   const dim3 grid((unsigned)cdiv(T, 4));
   hipStream_t st = as_stream(stream);
   if (E <= 64)
-    hipLaunchKernelGGL(topk_softmax_kernel<1>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
+    launch(topk_softmax_kernel<1>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
   else if (E <= 128)
-    hipLaunchKernelGGL(topk_softmax_kernel<2>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
+    launch(topk_softmax_kernel<2>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
   else if (E <= 256)
-    hipLaunchKernelGGL(topk_softmax_kernel<4>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
+    launch(topk_softmax_kernel<4>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k, mode);
   else
-    hipLaunchKernelGGL(topk_softmax_kernel<16>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k,
+    launch(topk_softmax_kernel<16>, grid, dim3(256), 0, st, logits, weights, ids, T, (int)E, (int)k,
                        mode);
   return launch_status("ccq_topk_softmax");
 }
@@ -628,7 +628,7 @@ extern "C" int ccq_shared_expert_add(float* y, const float* shared, float shared
   if (n == 0) return 0;
   CCQ_REQUIRE(y && shared, "ccq_shared_expert_add: null pointer");
   const int64_t g = cdiv(n, 256);
-  hipLaunchKernelGGL(shared_add_kernel, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(256), 0, as_stream(stream), y,
+  launch(shared_add_kernel, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(256), 0, as_stream(stream), y,
                      shared, shared_gate, n);
   return launch_status("ccq_shared_expert_add");
 }

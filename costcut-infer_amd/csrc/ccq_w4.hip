@@ -492,11 +492,11 @@ template <typename AT, typename ST, int NB, int EPI>
 static void launch_skinny_gs(const SkinnyP& p, dim3 grid, int waves, size_t lds, hipStream_t st, int G) {
   const dim3 block(64 * waves);
   if (G == 128)
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, ST, NB, 4, EPI>), grid, block, lds, st, p);
+    launch((w4_skinny_kernel<AT, ST, NB, 4, EPI>), grid, block, lds, st, p);
   else if (G == 64)
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, ST, NB, 2, EPI>), grid, block, lds, st, p);
+    launch((w4_skinny_kernel<AT, ST, NB, 2, EPI>), grid, block, lds, st, p);
   else if constexpr (NB <= 2)  // plan_skinny never pairs 4 column tiles with G = 32
-    hipLaunchKernelGGL((w4_skinny_kernel<AT, ST, NB, 1, EPI>), grid, block, lds, st, p);
+    launch((w4_skinny_kernel<AT, ST, NB, 1, EPI>), grid, block, lds, st, p);
 }
 
 template <typename AT, typename ST, int EPI>
@@ -1530,10 +1530,10 @@ static int launch_row_group_sums(const void* x, int x_bf16, int64_t ldx, int64_t
   const int64_t KT = K / 128, threads = M * KT * 16 > nrows_out ? M * KT * 16 : nrows_out;
   const int64_t blocks = cdiv(threads, 256);
   if (x_bf16)
-    hipLaunchKernelGGL(row_group_sums_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
+    launch(row_group_sums_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const __bf16*)x, ldx, M, KT, out, ldo, rows_out, nrows_out);
   else
-    hipLaunchKernelGGL(row_group_sums_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st,
+    launch(row_group_sums_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st,
                        (const _Float16*)x, ldx, M, KT, out, ldo, rows_out, nrows_out);
   return launch_status("row group sums");
 }
@@ -1560,16 +1560,16 @@ static void launch_stream_t(const W4SP& p, int nq, dim3 grid, hipStream_t st) {
   const bool mt4 = p.KT > 16;
   if constexpr (EPI == EPI_SILU) {
     if (p.logits != nullptr)  // routing inside the workgroups
-      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 2, true>), grid, block, 0, st, p);
+      launch((w4_stream_kernel<AT, ST, EPI, 2, 2, true>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
+      launch((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
   } else if (nq == 2)  // two quads: K <= 2048, two k-tiles per wave
-    hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
+    launch((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
   else if constexpr (EPI != EPI_SILU) {
     if (mt4)
-      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 4, 1>), grid, block, 0, st, p);
+      launch((w4_stream_kernel<AT, ST, EPI, 4, 1>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((w4_stream_kernel<AT, ST, EPI, 2, 1>), grid, block, 0, st, p);
+      launch((w4_stream_kernel<AT, ST, EPI, 2, 1>), grid, block, 0, st, p);
   }
 }
 
@@ -1602,10 +1602,10 @@ static int launch_group_gemm(const W4GP& p, int x_bf16, int s_bf16, int64_t tile
 #define CCQ_LAUNCH_GG(AT, ST)                                                                  \
   do {                                                                                         \
     if (wgn == 256)                                                                            \
-      hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, (EPI == EPI_SILU ? 2 : 4)>), grid, \
+      launch((w4_group_gemm_kernel<AT, ST, EPI, (EPI == EPI_SILU ? 2 : 4)>), grid, \
                          block, 0, st, p);                                                     \
     else                                                                                       \
-      hipLaunchKernelGGL((w4_group_gemm_kernel<AT, ST, EPI, 2>), grid, block, 0, st, p);      \
+      launch((w4_group_gemm_kernel<AT, ST, EPI, 2>), grid, block, 0, st, p);      \
   } while (0)
   if (x_bf16) {
     if (s_bf16)
@@ -1649,7 +1649,7 @@ extern "C" int ccq_awq_dequant(const int32_t* qweight, const int32_t* qzeros, co
   CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_awq_dequant: scale_dtype must be f16|bf16");
   if (K == 0 || N == 0) return 0;
   CCQ_REQUIRE(qweight && qzeros && scales && out, "ccq_awq_dequant: null pointer");
-  hipLaunchKernelGGL(awq_dequant_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
+  launch(awq_dequant_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
                      (const uint32_t*)qweight, (const uint32_t*)qzeros, (const uint16_t*)scales,
                      scale_dtype == CCQ_BF16 ? 1 : 0, out, K, N, group_size);
   return launch_status("ccq_awq_dequant");
@@ -1662,7 +1662,7 @@ extern "C" int ccq_awq_repack(const int32_t* qweight, int32_t* tiled, int64_t K,
   if (K == 0 || N == 0) return 0;
   CCQ_REQUIRE(qweight && tiled, "ccq_awq_repack: null pointer");
   CCQ_REQUIRE((const void*)qweight != (const void*)tiled, "ccq_awq_repack: in-place repack is not supported");
-  hipLaunchKernelGGL(awq_repack_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
+  launch(awq_repack_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
                      (const uint32_t*)qweight, (uint32_t*)tiled, K, N);
   return launch_status("ccq_awq_repack");
 }
@@ -1673,7 +1673,7 @@ extern "C" int ccq_awq_unpack_tiled(const int32_t* tiled, int32_t* qweight, int6
   if (K == 0 || N == 0) return 0;
   CCQ_REQUIRE(qweight && tiled, "ccq_awq_unpack_tiled: null pointer");
   CCQ_REQUIRE((const void*)qweight != (const void*)tiled, "ccq_awq_unpack_tiled: in-place is not supported");
-  hipLaunchKernelGGL(awq_unpack_tiled_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
+  launch(awq_unpack_tiled_kernel, dim3(grid1d(K * N / 8)), dim3(256), 0, as_stream(stream),
                      (const uint32_t*)tiled, (uint32_t*)qweight, K, N);
   return launch_status("ccq_awq_unpack_tiled");
 }
@@ -1692,7 +1692,7 @@ extern "C" int ccq_awq_pack_sz(const int32_t* qzeros, const void* scales, int sc
   CCQ_REQUIRE(scale_dtype == CCQ_F16 || scale_dtype == CCQ_BF16, "ccq_awq_pack_sz: scale_dtype must be f16|bf16");
   if (K == 0 || N == 0) return 0;
   CCQ_REQUIRE(qzeros && scales && sz, "ccq_awq_pack_sz: null pointer");
-  hipLaunchKernelGGL(awq_pack_sz_kernel, dim3(grid1d(N * sz_words_per_column(K, group_size))), dim3(256), 0,
+  launch(awq_pack_sz_kernel, dim3(grid1d(N * sz_words_per_column(K, group_size))), dim3(256), 0,
                      as_stream(stream), (const uint32_t*)qzeros, (const uint16_t*)scales, sz, K, N, group_size);
   return launch_status("ccq_awq_pack_sz");
 }
@@ -2315,7 +2315,7 @@ extern "C" int ccq_moe_w4_forward_shared(const void* x, int x_dtype, const float
     float* twts = (float*)(ws + L.off_rows + align256((size_t)(T * k) * 8));
     rc = ccq_topk_softmax(logits, twts, tids, T, Er, k, mode, stream);
     if (rc) return rc;
-    hipLaunchKernelGGL(append_shared_slot_kernel, dim3(grid_for(T * ks, 256)), dim3(256), 0, st, tids, twts, ids,
+    launch(append_shared_slot_kernel, dim3(grid_for(T * ks, 256)), dim3(256), 0, st, tids, twts, ids,
                        wts, T, k, Er, shared_gate);
     rc = launch_status(name);
     if (rc) return rc;

@@ -286,11 +286,11 @@ template <int FMT, bool G16>
 static void wq_launch(int mt, const WqP& p, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(p.N, WQ_COLS), (unsigned)cdiv(p.M, 16 * mt));
   if (mt == 1)
-    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 1, wq_depth<FMT, 1>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
+    launch((wq_mfma_kernel<FMT, 1, wq_depth<FMT, 1>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
   else if (mt == 2)
-    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 2, wq_depth<FMT, 2>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
+    launch((wq_mfma_kernel<FMT, 2, wq_depth<FMT, 2>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((wq_mfma_kernel<FMT, 4, wq_depth<FMT, 4>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
+    launch((wq_mfma_kernel<FMT, 4, wq_depth<FMT, 4>(), G16>), grid, dim3(WQ_THREADS), 0, st, p);
 }
 
 int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale, int group_size, float scale2,

@@ -40,6 +40,16 @@ int ccq_version(void);
 /* message of the last failed call on this thread ("" if none) */
 const char* ccq_last_error(void);
 
+/* Kernel-exact timing, for benchmarks: the next kernel that a ccq entry
+ * point launches on this thread records start_event when it begins
+ * executing and stop_event when it ends (hipExtLaunchKernel), so
+ * hipEventElapsedTime(start, stop) is that kernel's own duration -- the
+ * interval rocprofv3's kernel trace reports -- without the gap between
+ * back-to-back launches.  Applies to one launch, then clears; both events
+ * (hipEvent_t, created with timing) or neither (clears).  No counterpart in
+ * the reference: its kernels are host code. */
+int ccq_launch_timer(void* start_event, void* stop_event);
+
 /* ------------------------------------------------------------------------
  * Reference formats (exact reference semantics, float32 I/O)
  * ---------------------------------------------------------------------- */
@@ -53,8 +63,6 @@ int ccq_fp8_to_f32(const uint8_t* code, float* out, int64_t n, void* stream);
  * Replaces float32_to_fp8_e4m3 (quant/kernels.py:77-123). */
 int ccq_f32_to_fp8(const float* x, uint8_t* out, int64_t n, void* stream);
 
-/* out[r,c] = fp8(w[r,c]) * scale[r]   (w [rows,cols] e4m3fn, scale [rows]).
- * Replaces fp8_dequant_mat / fp8_dequant_row (quant/kernels.py:126-171). */
 /* Load-time FP8 quantization of a BF16 weight [rows, cols] (row-major
  * bf16 bits) to e4m3 codes [rows, cols], per output row: scale[r] when
  * scale is non-null, else amax(|row|)/448 (0 -> 1); scales <= 0 or NaN
@@ -75,6 +83,8 @@ int ccq_kv_quant_fp8(const float* kv, uint8_t* out, uint8_t* scales, int64_t row
 int ccq_kv_dequant_fp8(const uint8_t* codes, const uint8_t* scales, float* out, int64_t rows, int64_t dim,
                        void* stream);
 
+/* out[r,c] = fp8(w[r,c]) * scale[r]   (w [rows,cols] e4m3fn, scale [rows]).
+ * Replaces fp8_dequant_mat / fp8_dequant_row (quant/kernels.py:126-171). */
 int ccq_fp8_dequant(const uint8_t* w, const float* scale, float* out,
                     int64_t rows, int64_t cols, void* stream);
 
