@@ -52,6 +52,15 @@ class ccq_fp8_experts(ctypes.Structure):
     ]
 
 
+class ccq_fp8row_experts(ctypes.Structure):
+    _fields_ = [
+        ("w_gate", _vp), ("s_gate", _vp),
+        ("w_up", _vp), ("s_up", _vp),
+        ("w_down", _vp), ("s_down", _vp),
+        ("num_experts", _i64), ("hidden", _i64), ("inter", _i64),
+    ]
+
+
 # name -> (restype, argtypes); the order follows include/ccq.h
 SIGNATURES: dict[str, tuple] = {
     "ccq_version": (_int, []),
@@ -122,6 +131,11 @@ SIGNATURES: dict[str, tuple] = {
     "ccq_moe_fp8_workspace_size": (_sz, [_i64, _i64, ctypes.POINTER(ccq_fp8_experts)]),
     "ccq_moe_fp8_ffn": (_int, [_vp, _int, _vp, _vp, _vp, _int, _i64, _i64,
                                ctypes.POINTER(ccq_fp8_experts), _vp, _sz, _vp]),
+    "ccq_moe_fp8row_workspace_size": (_sz, [_i64, _i64, ctypes.POINTER(ccq_fp8row_experts)]),
+    "ccq_moe_fp8row_ffn": (_int, [_vp, _vp, _vp, _vp, _int, _i64, _i64, ctypes.POINTER(ccq_fp8row_experts), _vp,
+                                  _sz, _vp]),
+    "ccq_moe_fp8row_ffn_shared": (_int, [_vp, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _i64, _i64,
+                                         ctypes.POINTER(ccq_fp8row_experts), _vp, _sz, _vp]),
 }
 
 _lock = threading.Lock()

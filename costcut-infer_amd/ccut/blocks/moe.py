@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from ccut import _dev
-from ccut._lib import call, ccq_fp8_experts, ccq_w4_experts, lib
+from ccut._lib import call, ccq_fp8_experts, ccq_fp8row_experts, ccq_w4_experts, lib
 from ccut.quant import awq
 
 __all__ = [
@@ -37,6 +37,8 @@ __all__ = [
     "moe_forward_w4",
     "Fp8Experts",
     "moe_forward_fp8",
+    "Fp8RowExperts",
+    "moe_ffn_fp8row",
 ]
 
 _MODE_SOFTMAX_ALL, _MODE_TOPK_THEN_SOFTMAX, _MODE_RAW_EXP, _MODE_PLAIN, _MODE_ROUTE_NORM = 0, 1, 2, 3, 4
@@ -480,3 +482,107 @@ def moe_forward_fp8(x: torch.Tensor, router_logits: torch.Tensor, experts: Fp8Ex
     ``models/generic.py:361-378``, with the block-scaled FP8 format)."""
     w, ids = topk_softmax(router_logits, top_k, norm_topk_prob)
     return moe_ffn_fp8(x, ids, w, experts, out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# experts in the reference checkpoint's FP8 format (e4m3 [out, in], one scale
+# per output row)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Fp8RowExperts:
+    """All experts of one MoE layer as the reference's checkpoints store them
+    and its ``ExpertReader`` reads them (``experts/reader.py:142-251``):
+    e4m3 codes ``[out, in]`` with one scale per output row, used in place by
+    ``ccq_moe_fp8row_ffn`` (no re-pack).  gate/up ``w [E, I, H]`` with
+    ``s [E, I]``; down ``w [E, H, I]`` with ``s [E, H]``; scales float32."""
+
+    w_gate: torch.Tensor
+    s_gate: torch.Tensor
+    w_up: torch.Tensor
+    s_up: torch.Tensor
+    w_down: torch.Tensor
+    s_down: torch.Tensor
+    num_experts: int
+    hidden: int
+    inter: int
+
+    @staticmethod
+    def from_rows(gate: tuple, up: tuple, down: tuple) -> "Fp8RowExperts":
+        """Each of ``gate``/``up``/``down`` is ``(w [E, N, K] e4m3fn bytes
+        (uint8 or float8_e4m3fn), s [E, N] or [E, N, 1] (BF16 / F16 / F32,
+        widened to float32 exactly as the reference's ``_read_scale``))``."""
+        def one(t):
+            w = t[0]
+            if isinstance(w, torch.Tensor):
+                w = w.view(torch.uint8) if w.dtype != torch.uint8 else w
+                w = _dev.to_device(w.contiguous())
+            else:
+                w = _dev.to_device(np.ascontiguousarray(w).view(np.uint8))
+            sc = _dev.to_device(t[1], torch.float32)
+            if w.dim() != 3:
+                raise ValueError(f"FP8 expert weights must be [E, N, K], got {tuple(w.shape)}")
+            E, N, K = w.shape
+            if sc.dim() == 3 and sc.shape[-1] == 1:
+                sc = sc.reshape(E, N)
+            if tuple(sc.shape) != (E, N):
+                raise ValueError(f"per-row scales of a [E, N, K] = {tuple(w.shape)} weight must be [E, N] or "
+                                 f"[E, N, 1], got {tuple(sc.shape)}")
+            return w, sc.contiguous(), E, N, K
+
+        wg, sg, E, I, H = one(gate)
+        wu, su, E2, I2, H2 = one(up)
+        wd, sd, E3, H3, I3 = one(down)
+        if not (E == E2 == E3 and I == I2 == I3 and H == H2 == H3):
+            raise ValueError("gate/up [E, I, H] and down [E, H, I] shapes disagree")
+        if H % 256 or I % 256:
+            raise ValueError(f"hidden={H} and inter={I} must be multiples of 256 for the fused FP8 kernels")
+        return Fp8RowExperts(wg, sg, wu, su, wd, sd, num_experts=E, hidden=H, inter=I)
+
+    def descriptor(self) -> ccq_fp8row_experts:
+        return ccq_fp8row_experts(self.w_gate.data_ptr(), self.s_gate.data_ptr(), self.w_up.data_ptr(),
+                                  self.s_up.data_ptr(), self.w_down.data_ptr(), self.s_down.data_ptr(),
+                                  self.num_experts, self.hidden, self.inter)
+
+    @property
+    def bytes_per_expert(self) -> int:
+        """Bytes of one expert in its checkpoint form (e4m3 weights + BF16
+        row scales of gate, up and down): the algorithmic traffic of reading
+        it once."""
+        H, I = self.hidden, self.inter
+        return 3 * H * I + (2 * I + H) * 2
+
+
+def moe_ffn_fp8row(x, ids, weights, experts: Fp8RowExperts, out_dtype: torch.dtype = torch.float32, *,
+                   shared=None, shared_gate: float = 1.0) -> torch.Tensor:
+    """Expert FFN + weighted combine for already-routed float32 tokens on
+    per-row FP8 experts, one call of ``ccq_moe_fp8row_ffn`` -- what the
+    reference's ``ExpertPipeline.step`` computes per expert with
+    ``reader.get`` + ``expert_ffn`` + the weighted add
+    (``experts/pipeline.py:155-179``).  ``shared`` [T, H] float32 is added
+    as ``shared_gate * shared`` in the combine (``ccq_moe_fp8row_ffn_shared``)."""
+    xd = _dev.to_device(x, torch.float32).contiguous()
+    if xd.dim() != 2:
+        raise ValueError(f"x must be [T, hidden], got {tuple(xd.shape)}")
+    T, H = xd.shape
+    if H != experts.hidden:
+        raise ValueError(f"x has {H} features, experts expect {experts.hidden}")
+    ids = _dev.to_device(ids, torch.int64).contiguous()
+    wts = _dev.to_device(weights, torch.float32).contiguous()
+    if ids.dim() != 2 or ids.shape[0] != T or tuple(wts.shape) != tuple(ids.shape):
+        raise ValueError(f"ids {tuple(ids.shape)} and weights {tuple(wts.shape)} must both be [T={T}, k]")
+    k = ids.shape[1]
+    y = torch.empty((T, H), dtype=out_dtype, device=xd.device)
+    desc = experts.descriptor()
+    nbytes = lib().ccq_moe_fp8row_workspace_size(T, k, desc)
+    ws = _dev.workspace("moe_fp8row", nbytes, xd.device)
+    if shared is not None:
+        sd = _shared_rows(shared, T, H, xd.device)
+        call("ccq_moe_fp8row_ffn_shared", xd.data_ptr(), ids.data_ptr(), wts.data_ptr(), sd.data_ptr(),
+             float(np.float32(shared_gate)), y.data_ptr(), _dev.DTYPE_CODE[out_dtype], T, k, desc, ws.data_ptr(),
+             nbytes, _dev.stream_ptr(xd.device))
+    else:
+        call("ccq_moe_fp8row_ffn", xd.data_ptr(), ids.data_ptr(), wts.data_ptr(), y.data_ptr(),
+             _dev.DTYPE_CODE[out_dtype], T, k, desc, ws.data_ptr(), nbytes, _dev.stream_ptr(xd.device))
+    return y

@@ -8,8 +8,10 @@ routed experts, the experts' FFN with the weighted combine, the shared expert
 and the metrics.  The expert weights come from ``reader`` in one of two ways:
 
 * ``reader.experts(layer)`` returning a whole layer in device format
-  (``W4Experts`` or ``Fp8Experts``): one fused call (``moe_ffn_w4`` /
-  ``moe_ffn_fp8``); activations go to the int4 kernels as bfloat16.
+  (``W4Experts``, ``Fp8Experts`` or ``Fp8RowExperts``): one fused call
+  (``moe_ffn_w4`` / ``moe_ffn_fp8`` / ``moe_ffn_fp8row``); activations go
+  to the int4 kernels as bfloat16, to the per-row FP8 kernels (the
+  reference checkpoint's own format) as float32.
 * otherwise ``reader.get(layer, eid, timeout)`` per routed expert returning
   float32 ``(w_gate [hidden, inter], w_up [hidden, inter], w_down [inter,
   hidden])``, the orientation ``expert_ffn`` takes: ``expert_ffn`` per
@@ -126,6 +128,16 @@ class ExpertPipeline:
         fn = getattr(self.reader, "prefetch", None)
         return fn(layer, ids) if fn is not None else 0
 
+    @staticmethod
+    def router_logits(x, gate_w) -> torch.Tensor:
+        """The router ``x @ gate_w.T`` in float32 (reference
+        ``pipeline.py:145``) as a device tensor [T, E]."""
+        xd = _dev.to_device(x, torch.float32)
+        gw = _dev.to_device(gate_w, torch.float32)
+        if xd.dim() != 2 or gw.dim() != 2 or xd.shape[1] != gw.shape[1]:
+            raise ValueError(f"router: x {tuple(xd.shape)} and gate_w {tuple(gw.shape)} must be [T, H] and [E, H]")
+        return xd @ gw.T
+
     def step(self, layer: int, x, gate_w, top_k: int = 8, norm_topk_prob: bool = True,
              shared_projs: dict | None = None, shared_gate: float = 1.0):
         """``y [T, hidden]`` float32 for ``x [T, hidden]``: numpy in, numpy
@@ -140,8 +152,7 @@ class ExpertPipeline:
         xd = _dev.to_device(x, torch.float32)
         if xd.dim() != 2:
             raise ValueError(f"x must be [T, hidden], got {tuple(xd.shape)}")
-        gw = _dev.to_device(gate_w, torch.float32)
-        logits = xd @ gw.T
+        logits = self.router_logits(xd, gate_w)
         weights, ids = moe.topk_softmax(logits, top_k, norm_topk_prob)
         ids_h = ids.cpu().numpy()
         self.history.record(ids_h[0])  # the first token's experts, as the reference records
@@ -172,9 +183,13 @@ class ExpertPipeline:
             out = moe.moe_ffn_fp8(xd, ids, weights, ex, out_dtype=torch.float32, shared=s_out,
                                   shared_gate=shared_gate)
             shared_done = True
+        elif isinstance(ex, moe.Fp8RowExperts):
+            out = moe.moe_ffn_fp8row(xd, ids, weights, ex, out_dtype=torch.float32, shared=s_out,
+                                     shared_gate=shared_gate)
+            shared_done = True
         elif ex is not None:
             raise TypeError(f"reader.experts({layer}) returned {type(ex).__name__}, "
-                            "expected W4Experts or Fp8Experts")
+                            "expected W4Experts, Fp8Experts or Fp8RowExperts")
         else:
             out, shared_done = self._per_expert(layer, xd, ids, weights, flat_ids, s_out, shared_gate)
         if s_out is not None and not shared_done:

@@ -28,10 +28,13 @@ its pipeline hands those slots to ``expert_ffn`` untransposed,
 ``experts/pipeline.py:170``: a shape error, or ``x @ W`` in place of
 ``x @ W.T`` when hidden == inter.)
 
-``experts(layer)`` additionally packs a whole AWQ layer (``W4Experts``) or
-block-FP8 layer (``Fp8Experts``, hidden and inter multiples of 128) into the
-fused kernels' device format, built once per layer, which
-``ExpertPipeline`` uses instead of per-expert reads.
+``experts(layer)`` additionally hands over a whole layer in a fused
+kernels' device format, built once per layer, which ``ExpertPipeline``
+uses instead of per-expert reads: an AWQ layer as ``W4Experts``, a
+block-FP8 layer as ``Fp8Experts`` (hidden and inter multiples of 128), and
+the reference checkpoint's own format -- e4m3 ``[out, in]`` with per-row
+scales, hidden and inter multiples of 256 -- as ``Fp8RowExperts`` (the
+codes in place, scales widened to float32).
 """
 
 from __future__ import annotations
@@ -317,9 +320,10 @@ class ExpertReader:
                 self._cv.wait(timeout=min(left, 0.5))
 
     def experts(self, layer: int):
-        """The whole layer as ``W4Experts`` (AWQ segments) or ``Fp8Experts``
+        """The whole layer as ``W4Experts`` (AWQ segments), ``Fp8Experts``
         (e4m3 segments with 128x128 block scales, hidden and inter multiples
-        of 128), built once; None when the layer is in another format
+        of 128) or ``Fp8RowExperts`` (e4m3 with per-row scales, multiples of
+        256), built once; None when the layer is in another format
         (per-expert reads)."""
         if layer in self._layers:
             return self._layers[layer]
@@ -356,8 +360,47 @@ class ExpertReader:
                 return torch.stack(ws), torch.stack(ss)
 
             ex = moe.Fp8Experts.from_block(stack_fp8("gate"), stack_fp8("up"), stack_fp8("down"))
+        elif e0 is not None and self._is_fp8_row(e0):
+            from ccut.blocks import moe
+
+            def stack_rows(proj):
+                ws, ss = [], []
+                for eid in range(self.index.num_experts):
+                    entry = self.index.entries[(layer, eid)]
+                    wkey = self._pick(entry.segments, proj, (".weight", ""))
+                    raw, dtype, shape = self._read(entry, wkey)
+                    if dtype != "F8_E4M3":
+                        raise ValueError(f"layer {layer} expert {eid} {proj}: {dtype} weight in an F8_E4M3 layer")
+                    rows, cols = _shape_2d(int(entry.segments[wkey][2]), shape)
+                    kind, sc = self._fp8_scale(entry, proj, rows, cols)
+                    if kind != "row":
+                        raise ValueError(f"layer {layer} expert {eid} {proj}: block scales in a per-row FP8 layer")
+                    ws.append(torch.from_numpy(raw.copy()).to(self.device).reshape(rows, cols))
+                    ss.append(sc)
+                return torch.stack(ws), torch.stack(ss)
+
+            ex = moe.Fp8RowExperts.from_rows(stack_rows("gate"), stack_rows("up"), stack_rows("down"))
         self._layers[layer] = ex
         return ex
+
+    def _is_fp8_row(self, entry: ExpertEntry) -> bool:
+        """e4m3 gate/up/down weights with one scale per output row (or none),
+        in shapes the fused per-row kernels take (hidden and inter multiples
+        of 256): the reference checkpoint's own expert format."""
+        for proj in ("gate", "up", "down"):
+            wkey = self._pick(entry.segments, proj, (".weight", ""))
+            if wkey is None or entry.segments[wkey][3] != "F8_E4M3":
+                return False
+            shape = tuple(entry.shapes.get(wkey, ()))
+            if len(shape) != 2 or shape[0] % 256 or shape[1] % 256:
+                return False
+            try:
+                kind, _ = self._fp8_scale(entry, proj, shape[0], shape[1])
+            except ValueError:
+                return False
+            if kind != "row":
+                return False
+        return True
 
     def _is_fp8_block(self, entry: ExpertEntry) -> bool:
         """e4m3 gate weight with 128x128 block scales, shapes the fused FP8

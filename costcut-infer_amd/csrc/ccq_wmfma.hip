@@ -35,6 +35,14 @@
 
 namespace ccq {
 
+int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
+                 size_t scratch_bytes);
+size_t align_scratch_bytes(int64_t n, int64_t E);
+int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
+                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared,
+                   float shared_gate);
+
 constexpr int WQ_KC = 256;                 // k per chunk
 constexpr int WQ_CG = 4;                   // 16-column groups per workgroup
 constexpr int WQ_THREADS = 512;            // 8 waves: 4 column groups x 2 k halves
@@ -325,6 +333,351 @@ int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale,
   return launch_status(name);
 }
 
+
+// ---------------------------------------------------------------------------
+// Grouped form for MoE experts in the layout the reference's checkpoints and
+// ExpertReader hold them (experts/reader.py:142-251): per expert, e4m3 codes
+// [out, in] with one float32 scale per output row (BF16 [out, 1] in the
+// checkpoint), read in place -- each lane's 32 consecutive k bytes of a row
+// are the row-major layout already.  The stage computes, for the tokens
+// routed to each expert, the reference's expert_ffn (blocks/moe.py:122-141)
+// on the dequantized weights:
+//   DUAL (gate/up): y[a, n] = silu(s_g[n] * x_t . Wg[n]) * (s_u[n] * x_t . Wu[n])
+//   down:           y[a, n] = s_d[n] * h_a . Wd[n]
+// with x_t the float32 row of token t = a / row_div (gate/up) or the
+// intermediate row of assignment a (down), in the decoded-weight arithmetic
+// above (exact bf16 products of hi/lo activations, float32 accumulation).
+// The SiLU product is formed in float64 and rounded once, as the
+// reference's silu_mul_fused (quant/kernels.py:219-231).
+//
+// Grid: x = column blocks of 16*CG columns, y = tiles of the expert-sorted
+// schedule (ccq_moe_align with tile_m = 16*MT; tiles past meta[0] exit at
+// once).  The 8 waves are CG column groups x KH k parts; a chunk is KH*128 k
+// (KH = 2: the dense kernel's 64 columns x 256 k; KH = 4: 32 columns x 512 k,
+// for schedules too small to fill the chip with 64-column blocks).  The
+// valid rows of a tile are a prefix (an expert's rows are padded at the
+// end), so a wave loads only the activation pieces of valid rows and
+// zeroes the rest when staging; the k parts' partial sums are added in a
+// fixed order through the (then free) activation LDS.
+struct WqMoeP {
+  const float* x;             // activation rows, K floats each
+  const int32_t* rows;        // expert-sorted assignment ids per tile row, -1 = padding
+  const int32_t* tile_expert;
+  const int32_t* meta;        // meta[0] = tiles in the schedule
+  const uint8_t* w0;          // [E][N][K] e4m3 codes: gate (DUAL) or down
+  const uint8_t* w1;          // [E][N][K] e4m3 codes: up (DUAL)
+  const float* s0;            // [E][N] row scales of w0
+  const float* s1;            // [E][N] row scales of w1
+  float* y;                   // [assignments][N]
+  int64_t N, K;
+  int row_div;                // activation row of assignment a = a / row_div
+};
+
+template <bool DUAL, int MT, int PD, int KH>
+__global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
+  constexpr int CG = 8 / KH;                // 16-column groups per workgroup
+  constexpr int KC = 128 * KH;              // k per chunk
+  constexpr int RS = KC + 8;                // LDS row stride in bf16
+  constexpr int TM = 16 * MT;               // rows per tile
+  constexpr int NW = DUAL ? 2 : 1;          // weight matrices
+  constexpr int C4 = KC / 4;                // float4 pieces per activation row and chunk
+  constexpr int XR = TM * C4 / WQ_THREADS;  // activation pieces per thread and chunk
+  constexpr int LPC = 2 * NW + XR;          // loads per lane and chunk
+  static_assert(KH == 2 || KH == 4, "k parts");
+  static_assert(XR >= 1 && TM * C4 == XR * WQ_THREADS, "activation pieces");
+  static_assert(C4 % 64 == 0, "a wave's pieces lie in one row");
+  static_assert((PD - 1) * LPC < 64, "loads in flight fit vmcnt");
+  static_assert(NW * CG * (KH - 1) * MT * 64 * 16 <= 2 * 2 * TM * RS * 2, "partial sums fit the activation LDS");
+  __shared__ __align__(16) uint16_t X[2][2][TM][RS];  // [buffer][hi, lo][row][k]
+
+  const int tile = blockIdx.y;
+  if (tile >= p.meta[0]) return;  // uniform: the whole workgroup leaves before any barrier
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = wave % CG, kh = wave / CG;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int64_t N = p.N, K = p.K;
+  const int e = p.tile_expert[tile];
+  const int64_t n = (int64_t)blockIdx.x * (16 * CG) + 16 * cg + c16;
+  const int nch = (int)(K / KC);
+  const int64_t woff = (int64_t)e * N * K + imin64(n, N - 1) * K;  // columns past N read row N-1, never stored
+  const uint8_t* wrow0 = p.w0 + woff;
+  const uint8_t* wrow1 = DUAL ? p.w1 + woff : p.w0 + woff;
+  const int lane_k = kh * 128 + q * 32;  // first k of the lane's 32 in a chunk
+  const int32_t* trow = p.rows + (int64_t)tile * TM;
+
+  // activation piece j of a thread: row (64 wave + 512 j) / C4 of the tile
+  // (wave-uniform), float4 column (64 wave + lane + 512 j) % C4; a padding
+  // row points at row 0 (in bounds) and is zeroed when staged
+  const float* xp[XR];
+  uint32_t vmask = 0;
+  int nx = 0;
+#pragma unroll
+  for (int j = 0; j < XR; ++j) {
+    const int row = (64 * wave + WQ_THREADS * j) / C4;
+    const int a = trow[row];
+    if (a >= 0) {
+      vmask |= 1u << j;
+      nx = j + 1;
+    }
+    xp[j] = p.x + (int64_t)(a >= 0 ? a / p.row_div : 0) * K + 4 * ((64 * wave + lane + WQ_THREADS * j) % C4);
+  }
+
+  u32x4 wr0[PD][2];
+  u32x4 wr1[PD][2];
+  u32x4 xr[PD][XR];
+  auto issue = [&](int s, int c) {
+    const int64_t kb = (int64_t)c * KC;
+    const uint8_t* wp = wrow0 + kb + lane_k;
+    gload16_nt<0>(wr0[s][0], wp);
+    gload16_nt<16>(wr0[s][1], wp);
+    if constexpr (DUAL) {
+      const uint8_t* up = wrow1 + kb + lane_k;
+      gload16_nt<0>(wr1[s][0], up);
+      gload16_nt<16>(wr1[s][1], up);
+    }
+#pragma unroll
+    for (int j = 0; j < XR; ++j)
+      if (j < nx) wq_load16(xr[s][j], xp[j] + kb);
+  };
+  auto wait_slot = [&](int s, bool steady) {
+    if (steady)
+      wq_wait_nx<PD, 2 * NW, XR>(nx);
+    else
+      wq_wait<0>();
+    wq_tie(wr0[s][0]);
+    wq_tie(wr0[s][1]);
+    if constexpr (DUAL) {
+      wq_tie(wr1[s][0]);
+      wq_tie(wr1[s][1]);
+    }
+#pragma unroll
+    for (int j = 0; j < XR; ++j) wq_tie(xr[s][j]);
+  };
+  auto stage_x = [&](int s, int buf) {
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+      const int idx = tid + WQ_THREADS * j, row = idx / C4, col4 = idx % C4;
+      float4 v = __builtin_bit_cast(float4, xr[s][j]);
+      if (!((vmask >> j) & 1u)) v = make_float4(0.f, 0.f, 0.f, 0.f);
+      const uint32_t h01 = bf16x2_bits(v.x, v.y), h23 = bf16x2_bits(v.z, v.w);
+      const uint32_t l01 = bf16x2_bits(v.x - __uint_as_float(h01 << 16), v.y - __uint_as_float(h01 & 0xffff0000u));
+      const uint32_t l23 = bf16x2_bits(v.z - __uint_as_float(h23 << 16), v.w - __uint_as_float(h23 & 0xffff0000u));
+      *reinterpret_cast<u32x2*>(&X[buf][0][row][4 * col4]) = u32x2{h01, h23};
+      *reinterpret_cast<u32x2*>(&X[buf][1][row][4 * col4]) = u32x2{l01, l23};
+    }
+  };
+
+  f32x4 acc0[MT], acc1[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc0[t] = acc1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < PD; ++s)
+    if (s < nch) issue(s, s);
+
+  for (int c0 = 0; c0 < nch; c0 += PD) {
+#pragma unroll
+    for (int s = 0; s < PD; ++s) {
+      const int c = c0 + s;
+      if (c < nch) {
+        const int buf = c & 1;
+        wait_slot(s, c + PD - 1 < nch);  // steady: chunks c+1..c+PD-1 were issued after chunk c
+        stage_x(s, buf);
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bf16x8 b0 = wq_decode<WQ_FP8_ROW>(wr0[s], i, 1.f);
+          bf16x8 b1 = b0;
+          if constexpr (DUAL) b1 = wq_decode<WQ_FP8_ROW>(wr1[s], i, 1.f);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&X[buf][0][16 * t + c16][lane_k + 8 * i]);
+            const bf16x8 al = *reinterpret_cast<const bf16x8*>(&X[buf][1][16 * t + c16][lane_k + 8 * i]);
+            acc0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b0, acc0[t], 0, 0, 0);
+            acc0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b0, acc0[t], 0, 0, 0);
+            if constexpr (DUAL) {
+              acc1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b1, acc1[t], 0, 0, 0);
+              acc1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b1, acc1[t], 0, 0, 0);
+            }
+          }
+        }
+        if (c + PD < nch) issue(s, c + PD);
+      }
+    }
+  }
+
+  // k parts 1..KH-1 -> LDS (the activation buffers are free once every wave
+  // is past its last chunk); part 0 adds them in order and finishes
+  __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(&X[0][0][0][0]);
+  auto red_at = [&](int w, int part, int t) -> f32x4& {
+    return red[(((w * CG + cg) * (KH - 1) + part) * MT + t) * 64 + lane];
+  };
+  if (kh > 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      red_at(0, kh - 1, t) = acc0[t];
+      if constexpr (DUAL) red_at(1, kh - 1, t) = acc1[t];
+    }
+  }
+  __syncthreads();
+  if (kh != 0 || n >= N) return;
+#pragma unroll
+  for (int part = 0; part < KH - 1; ++part)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      acc0[t] += red_at(0, part, t);
+      if constexpr (DUAL) acc1[t] += red_at(1, part, t);
+    }
+  const float sc0 = p.s0[(int64_t)e * N + n];
+  const float sc1 = DUAL ? p.s1[(int64_t)e * N + n] : 0.f;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int a = trow[16 * t + 4 * q + i];
+      if (a < 0) continue;
+      float v;
+      if constexpr (DUAL) {
+        const double g = (double)(acc0[t][i] * sc0), u = (double)(acc1[t][i] * sc1);
+        v = (float)(g / (1.0 + exp(-g)) * u);
+      } else {
+        v = acc0[t][i] * sc0;
+      }
+      p.y[(int64_t)a * N + n] = v;
+    }
+}
+
+// Ring depth per row-tile count (two weight matrices in the gate/up stage).
+template <bool DUAL, int MT>
+constexpr int wq_moe_depth() {
+  return DUAL ? (MT == 1 ? 4 : (MT == 2 ? 3 : 2)) : (MT == 1 ? 6 : (MT == 2 ? 4 : 3));
+}
+
+template <bool DUAL>
+static int wq_moe_launch(const WqMoeP& p, int mt, int kh, int64_t max_tiles, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(p.N, 16 * (8 / kh)), (unsigned)max_tiles);
+  if (mt == 1 && kh == 4)
+    launch((wq_moe_kernel<DUAL, 1, wq_moe_depth<DUAL, 1>(), 4>), grid, dim3(WQ_THREADS), 0, st, p);
+  else if (mt == 1)
+    launch((wq_moe_kernel<DUAL, 1, wq_moe_depth<DUAL, 1>(), 2>), grid, dim3(WQ_THREADS), 0, st, p);
+  else if (mt == 2)
+    launch((wq_moe_kernel<DUAL, 2, wq_moe_depth<DUAL, 2>(), 2>), grid, dim3(WQ_THREADS), 0, st, p);
+  else
+    launch((wq_moe_kernel<DUAL, 4, wq_moe_depth<DUAL, 4>(), 2>), grid, dim3(WQ_THREADS), 0, st, p);
+  return launch_status(DUAL ? "moe_fp8row gate_up" : "moe_fp8row down");
+}
+
+
+// ------------------------------------------------------------ MoE host --
+namespace {
+
+struct F8RowLayout {
+  int64_t n, max_tiles;
+  int mt, kh_gate_up, kh_down;
+  size_t off_sorted, off_tile_expert, off_meta, off_counts, off_inter, off_rows, off_align, total;
+};
+
+size_t a256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int device_cus_now() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
+}
+
+// Tile height from the mean rows per routed expert: 16-row tiles for decode
+// batches, 32 or 64 when experts hold more rows (each tile reads its
+// expert's weights once).  32-column blocks (KH = 4) when 64-column blocks
+// would leave most compute units idle.
+F8RowLayout f8row_layout(int64_t T, int64_t k, const ccq_fp8row_experts* ex, bool with_cus) {
+  F8RowLayout L = {};
+  const int64_t E = ex->num_experts, H = ex->hidden, I = ex->inter;
+  L.n = T * k;
+  const int64_t routed = L.n < E ? L.n : E;
+  const int64_t avg = cdiv(L.n, routed > 0 ? routed : 1);
+  L.mt = avg <= 8 ? 1 : (avg <= 24 ? 2 : 4);
+  const int64_t tile_m = 16 * L.mt;
+  L.max_tiles = ccq_moe_align_max_tiles(L.n, E, tile_m);
+  const int64_t cus = with_cus ? device_cus_now() : 256;
+  L.kh_gate_up = (L.mt == 1 && H % 512 == 0 && cdiv(I, 64) * routed < 2 * cus) ? 4 : 2;
+  L.kh_down = (L.mt == 1 && I % 512 == 0 && cdiv(H, 64) * routed < 2 * cus) ? 4 : 2;
+  size_t o = 0;
+  L.off_sorted = o;
+  o += a256((size_t)L.max_tiles * tile_m * 4);
+  L.off_tile_expert = o;
+  o += a256((size_t)L.max_tiles * 4);
+  L.off_meta = o;
+  o += 256;
+  L.off_counts = o;
+  o += a256((size_t)E * 4);
+  L.off_inter = o;
+  o += a256((size_t)L.n * I * 4);
+  L.off_rows = o;
+  o += a256((size_t)L.n * H * 4);
+  L.off_align = o;
+  o += a256(align_scratch_bytes(L.n, E));
+  L.total = o;
+  return L;
+}
+
+int check_fp8row_experts(const ccq_fp8row_experts* ex, const char* name) {
+  CCQ_REQUIRE(ex != nullptr, "%s: null experts descriptor", name);
+  CCQ_REQUIRE(ex->num_experts >= 1 && ex->num_experts <= 1024, "%s: num_experts=%lld outside [1, 1024]", name,
+              (long long)ex->num_experts);
+  CCQ_REQUIRE(ex->hidden > 0 && ex->hidden % WQ_KC == 0 && ex->inter > 0 && ex->inter % WQ_KC == 0,
+              "%s: hidden=%lld and inter=%lld must be positive multiples of %d", name, (long long)ex->hidden,
+              (long long)ex->inter, WQ_KC);
+  CCQ_REQUIRE(ex->w_gate && ex->w_up && ex->w_down && ex->s_gate && ex->s_up && ex->s_down,
+              "%s: null expert weight or scale pointer", name);
+  CCQ_REQUIRE(aligned(ex->w_gate, 16) && aligned(ex->w_up, 16) && aligned(ex->w_down, 16),
+              "%s: expert weights must be 16-byte aligned", name);
+  return 0;
+}
+
+int moe_fp8row_ffn(const float* x, const int64_t* ids, const float* weights, void* y, int y_dtype, int64_t T,
+                   int64_t k, const ccq_fp8row_experts* ex, void* workspace, size_t workspace_bytes, void* stream,
+                   const float* shared, float shared_gate, const char* name) {
+  int rc = check_fp8row_experts(ex, name);
+  if (rc) return rc;
+  CCQ_REQUIRE(T >= 0 && T <= 65535 && k >= 1 && k <= ex->num_experts, "%s: bad T=%lld / k=%lld", name,
+              (long long)T, (long long)k);
+  CCQ_REQUIRE(T * k <= 65536, "%s: T*k=%lld > 65536", name, (long long)(T * k));
+  CCQ_REQUIRE(y_dtype == CCQ_F32 || y_dtype == CCQ_F16 || y_dtype == CCQ_BF16, "%s: bad y_dtype %d", name, y_dtype);
+  if (T == 0) return 0;
+  CCQ_REQUIRE(x && ids && weights && y, "%s: null pointer", name);
+  CCQ_REQUIRE(aligned(x, 16), "%s: x must be 16-byte aligned", name);
+  const F8RowLayout L = f8row_layout(T, k, ex, true);
+  CCQ_REQUIRE(L.max_tiles >= 1 && L.max_tiles <= 65535, "%s: %lld tiles exceed the grid", name,
+              (long long)L.max_tiles);
+  CCQ_REQUIRE(workspace && workspace_bytes >= L.total && aligned(workspace, 256),
+              "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", name, L.total, workspace_bytes);
+  hipStream_t st = as_stream(stream);
+  char* ws = (char*)workspace;
+  int32_t* sorted = (int32_t*)(ws + L.off_sorted);
+  int32_t* tile_expert = (int32_t*)(ws + L.off_tile_expert);
+  int32_t* meta = (int32_t*)(ws + L.off_meta);
+  int32_t* counts = (int32_t*)(ws + L.off_counts);
+  float* inter = (float*)(ws + L.off_inter);
+  float* rows = (float*)(ws + L.off_rows);
+  const int64_t E = ex->num_experts, H = ex->hidden, I = ex->inter;
+  rc = launch_align(ids, L.n, E, 16 * L.mt, sorted, tile_expert, meta, counts, st, ws + L.off_align,
+                    L.total - L.off_align);
+  if (rc) return rc;
+  WqMoeP g = {x, sorted, tile_expert, meta, ex->w_gate, ex->w_up, ex->s_gate, ex->s_up, inter, I, H, (int)k};
+  rc = wq_moe_launch<true>(g, L.mt, L.kh_gate_up, L.max_tiles, st);
+  if (rc) return rc;
+  WqMoeP d = {inter, sorted, tile_expert, meta, ex->w_down, nullptr, ex->s_down, nullptr, rows, H, I, 1};
+  rc = wq_moe_launch<false>(d, L.mt, L.kh_down, L.max_tiles, st);
+  if (rc) return rc;
+  return launch_combine(rows, CCQ_F32, weights, ids, E, y, y_dtype, T, k, H, st, shared, shared_gate);
+}
+
+}  // namespace
+
 }  // namespace ccq
 
 using namespace ccq;
@@ -345,4 +698,25 @@ extern "C" int ccq_wq_mfma_linear_f32(const float* x, const uint8_t* w, const vo
   CCQ_REQUIRE(cdiv(batch, 64) <= 65535, "ccq_wq_mfma_linear_f32: batch too large");
   return wq_mfma_linear(fmt, x, w, scale, group_size, scale2, y, batch, in_features, out_features,
                         as_stream(stream), "ccq_wq_mfma_linear_f32");
+}
+
+extern "C" size_t ccq_moe_fp8row_workspace_size(int64_t T, int64_t k, const ccq_fp8row_experts* ex) {
+  if (T <= 0 || k <= 0 || check_fp8row_experts(ex, "ccq_moe_fp8row_workspace_size") != 0) return 0;
+  return f8row_layout(T, k, ex, false).total;
+}
+
+extern "C" int ccq_moe_fp8row_ffn(const float* x, const int64_t* ids, const float* weights, void* y, int y_dtype,
+                                  int64_t T, int64_t k, const ccq_fp8row_experts* ex, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  return moe_fp8row_ffn(x, ids, weights, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream, nullptr, 0.f,
+                        "ccq_moe_fp8row_ffn");
+}
+
+extern "C" int ccq_moe_fp8row_ffn_shared(const float* x, const int64_t* ids, const float* weights,
+                                         const float* shared, float shared_gate, void* y, int y_dtype, int64_t T,
+                                         int64_t k, const ccq_fp8row_experts* ex, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  CCQ_REQUIRE(shared || T == 0, "ccq_moe_fp8row_ffn_shared: null shared");
+  return moe_fp8row_ffn(x, ids, weights, y, y_dtype, T, k, ex, workspace, workspace_bytes, stream, shared,
+                        shared_gate, "ccq_moe_fp8row_ffn_shared");
 }

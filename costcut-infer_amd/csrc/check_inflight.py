@@ -36,7 +36,7 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-featu
          "-packed-fp32-ops", f"-I{INCLUDE}", "--cuda-device-only"]
 # source -> pattern of the kernels to check (every instance in the build)
 TARGETS = {"ccq_fp8.hip": r"_ZN3ccq17fp8_moe_rb_kernel\w+",
-           "ccq_wmfma.hip": r"_ZN3ccq14wq_mfma_kernel\w+"}
+           "ccq_wmfma.hip": r"_ZN3ccq(?:14wq_mfma_kernel|13wq_moe_kernel)\w+"}
 
 
 def _overlap(a, b):

@@ -525,6 +525,49 @@ int ccq_moe_fp8_ffn_shared(const void* x, int x_dtype, const int64_t* ids, const
                            int64_t T, int64_t k, const ccq_fp8_experts* ex, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * MoE experts in the reference's own checkpoint format: FP8 e4m3 codes
+ * [out, in] with one float32 scale per output row (the checkpoint's BF16
+ * [out, 1] scale, widened), as ExpertReader._fill / _dequant_seg read them
+ * (experts/reader.py:142-251): gate/up w [E][I][H], s [E][I]; down
+ * w [E][H][I], s [E][H].  Used in place: no re-pack.
+ * ---------------------------------------------------------------------- */
+typedef struct ccq_fp8row_experts {
+  const uint8_t* w_gate; const float* s_gate;
+  const uint8_t* w_up;   const float* s_up;
+  const uint8_t* w_down; const float* s_down;
+  int64_t num_experts, hidden, inter;
+} ccq_fp8row_experts;
+
+/* Workspace bytes of ccq_moe_fp8row_ffn (schedule, float32 intermediate and
+ * down rows; no initial contents required). */
+size_t ccq_moe_fp8row_workspace_size(int64_t T, int64_t k, const ccq_fp8row_experts* ex);
+
+/* The routed experts' FFN and weighted combine on per-row FP8 experts, in
+ * the reference's float32 arithmetic: x [T, H] f32, ids [T, k] int64,
+ * weights [T, k] f32 (ids outside [0, E) contribute nothing), y [T, H]
+ * (y_dtype CCQ_F32 | CCQ_BF16 | CCQ_F16).  For each routed expert e:
+ * h = silu(x W_g^T) * (x W_u^T), rows = h W_d^T with W = fp8(w) * s[row]
+ * (products exact: weights decoded to bf16, activations split into bf16
+ * hi + lo; float32 accumulation; SiLU product in float64, rounded once);
+ * y[t] = sum over slots of weights[t,s] * rows[t,s] in slot order.
+ * hidden and inter must be multiples of 256, T*k <= 65536, E <= 1024.
+ * Replaces the per-expert loop of ExpertPipeline.step
+ * (experts/pipeline.py:155-179): reader.get + expert_ffn
+ * (blocks/moe.py:122-141) + the weighted add, for reader slots in this
+ * format. */
+int ccq_moe_fp8row_ffn(const float* x, const int64_t* ids, const float* weights, void* y, int y_dtype,
+                       int64_t T, int64_t k, const ccq_fp8row_experts* ex, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ccq_moe_fp8row_ffn with the shared expert's output shared [T, H] f32
+ * added in the combine's epilogue as ccq_moe_combine_shared does
+ * (experts/pipeline.py:181-190, blocks/moe.py:177-179). */
+int ccq_moe_fp8row_ffn_shared(const float* x, const int64_t* ids, const float* weights,
+                              const float* shared, float shared_gate, void* y, int y_dtype, int64_t T,
+                              int64_t k, const ccq_fp8row_experts* ex, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,7 +50,7 @@ def test_fp8_block_slots_and_fused_layer(gpu, tmp_path, scale_name):
         y = ExpertPipeline(r).step(0, x, gate_w, top_k=2)
     finally:
         r.close()
-    logits = (torch.from_numpy(x).to(gpu) @ torch.from_numpy(gate_w).to(gpu).T).cpu().numpy()
+    logits = ExpertPipeline.router_logits(x, gate_w).cpu().numpy()  # the step's own router
     w0, ids0 = omoe.topk_softmax(logits, 2)
     yr = np.zeros_like(x)
     for e in range(E):
@@ -95,7 +95,7 @@ def test_compressed_tensors_int4_slots_and_fused_layer(gpu, tmp_path):
         y = ExpertPipeline(r).step(0, x, gate_w, top_k=2)
     finally:
         r.close()
-    logits = (torch.from_numpy(x).to(gpu) @ torch.from_numpy(gate_w).to(gpu).T).cpu().numpy()
+    logits = ExpertPipeline.router_logits(x, gate_w).cpu().numpy()  # the step's own router
     w0, ids0 = omoe.topk_softmax(logits, 2)
     lookup = lambda e: tuple(oawq.dequant(*ref[(0, e, p)], G) for p in ("gate", "up", "down"))  # noqa: E731
     yr = omoe.moe_combine(torch.from_numpy(x).to(torch.bfloat16).float().numpy(), ids0, w0, lookup)

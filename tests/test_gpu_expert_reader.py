@@ -64,18 +64,34 @@ def test_unreadable_segment_times_out(gpu, tmp_path):
         r.close()
 
 
-@pytest.mark.parametrize("H,I", [(2048, 512), (64, 64)])
-def test_pipeline_over_fp8_reader(gpu, tmp_path, H, I):
-    """The per-expert path over an FP8 per-row checkpoint with the Ornith
-    shapes (hidden 2048, expert intermediate 512: gate/up stored [512, 2048],
-    down [2048, 512]) and with hidden == inter, where a missing transpose
-    would go unnoticed by the shapes: y = sum_e w * down(silu(x Wg^T) *
-    (x Wu^T)) with W as stored, i.e. x @ W.T."""
+class _PerExpertOnly:
+    """A reader that offers no whole-layer form, so the pipeline takes the
+    reference's per-expert path (reader.get + expert_ffn + combine)."""
+
+    def __init__(self, r):
+        self._r = r
+
+    def __getattr__(self, name):
+        if name == "experts":
+            raise AttributeError(name)
+        return getattr(self._r, name)
+
+
+@pytest.mark.parametrize("H,I,per_expert", [(2048, 512, False), (2048, 512, True), (64, 64, False)])
+def test_pipeline_over_fp8_reader(gpu, tmp_path, H, I, per_expert):
+    """An FP8 per-row checkpoint with the Ornith shapes (hidden 2048, expert
+    intermediate 512: gate/up stored [512, 2048], down [2048, 512]) -- the
+    layer handed over whole (Fp8RowExperts, fused kernels) or read per
+    expert -- and with hidden == inter, where a missing transpose would go
+    unnoticed by the shapes (per expert: not a multiple of 256): y = sum_e w
+    * down(silu(x Wg^T) * (x Wu^T)) with W as stored, i.e. x @ W.T."""
+    from ccut.blocks import moe
     from ccut.experts import ExpertPipeline
 
     ref = write_fp8(tmp_path, L=1, E=4, H=H, I=I)
     r = _reader(tmp_path, 1, 4)
-    pipe = ExpertPipeline(r)
+    fused = not per_expert and H % 256 == 0 and I % 256 == 0
+    pipe = ExpertPipeline(_PerExpertOnly(r) if per_expert else r)
     rng = np.random.default_rng(3)
     x = (rng.standard_normal((6, H)) * 0.05).astype(np.float32)
     gate_w = (rng.standard_normal((4, H)) * 0.2).astype(np.float32)
@@ -83,7 +99,7 @@ def test_pipeline_over_fp8_reader(gpu, tmp_path, H, I):
         y = pipe.step(0, x, gate_w, top_k=2)
     finally:
         pipe.close()
-    logits = (torch.from_numpy(x).to(gpu) @ torch.from_numpy(gate_w).to(gpu).T).cpu().numpy()
+    logits = ExpertPipeline.router_logits(x, gate_w).cpu().numpy()  # the step's own router
     w0, ids0 = omoe.topk_softmax(logits, 2)
     W = {e: tuple(orq.fp8_dequant_mat(*ref[(0, e, p)]) for p in ("gate", "up", "down")) for e in range(4)}
     yr = np.zeros_like(x)
@@ -94,7 +110,11 @@ def test_pipeline_over_fp8_reader(gpu, tmp_path, H, I):
             yr[t] += w0[t, s_] * ((g / (1.0 + np.exp(-g.astype(np.float64))) * u).astype(np.float32) @ wd.T)
     assert y.shape == (6, H)
     assert np.abs(y - yr).max() <= 1e-4 * np.abs(yr).max()
-    assert pipe.metrics.steps == 1 and pipe.metrics.ring_misses >= 1
+    assert pipe.metrics.steps == 1
+    if fused:
+        assert isinstance(r.experts(0), moe.Fp8RowExperts) and pipe.metrics.ring_misses == 0
+    else:
+        assert pipe.metrics.ring_misses >= 1
 
 
 def test_awq_reader_slots_and_fused_layer(gpu, tmp_path):
@@ -116,7 +136,7 @@ def test_awq_reader_slots_and_fused_layer(gpu, tmp_path):
         y = ExpertPipeline(r).step(0, x, gate_w, top_k=2)
     finally:
         r.close()
-    logits = (torch.from_numpy(x).to(gpu) @ torch.from_numpy(gate_w).to(gpu).T).cpu().numpy()
+    logits = ExpertPipeline.router_logits(x, gate_w).cpu().numpy()  # the step's own router
     w0, ids0 = omoe.topk_softmax(logits, 2)
     lookup = lambda e: tuple(oawq.dequant(*ref[(0, e, p)], G) for p in ("gate", "up", "down"))  # noqa: E731
     xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()

@@ -56,8 +56,10 @@ def _case(seed, T=8, E=16, H=64, I=32):
 
 
 def _logits(gpu, x, gate_w):
-    # the step's router GEMM, same operands on the same device
-    return (torch.from_numpy(x).to(gpu) @ torch.from_numpy(gate_w).to(gpu).T).cpu().numpy()
+    # the step's own router, same operands on the same device
+    from ccut.experts import ExpertPipeline
+
+    return ExpertPipeline.router_logits(x, gate_w).cpu().numpy()
 
 
 def test_step_per_expert_reader_matches_oracle(gpu):

@@ -22,4 +22,4 @@ CHECK = ROOT / "costcut-infer_amd" / "csrc" / "check_inflight.py"
 def test_no_inflight_register_use():
     r = subprocess.run([sys.executable, str(CHECK)], capture_output=True, text=True, timeout=900)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-2000:]
-    assert "wq_mfma_kernel" in r.stdout and "fp8_moe_rb_kernel" in r.stdout
+    assert "wq_mfma_kernel" in r.stdout and "fp8_moe_rb_kernel" in r.stdout and "wq_moe_kernel" in r.stdout
