@@ -537,6 +537,48 @@ def bench_int4_prefill(T: int, dev, sets: int = 4):
     return res
 
 
+def bench_fp8row_moe(T: int, dev):
+    """MoE layer on experts in the reference checkpoint's own format (the
+    Ornith layout: e4m3 [out, in] with one BF16 scale per output row):
+    256 experts, top-8 (logits N(0,1)), hidden 2048, expert intermediate 512,
+    float32 activations; device time of whole ccq_moe_fp8row_ffn calls after
+    routing (align, gate/up + SiLU, down, combine).  One layer is 768 MiB;
+    the calls rotate over routings of distinct random logits so that the
+    experts read per rotation exceed 512 MiB (the 256 MiB Infinity Cache
+    cannot serve repeats).  Algorithmic bytes: the routed experts' codes and
+    BF16 row scales, x and y in float32."""
+    import torch
+
+    from ccut import workloads as wl
+    from ccut.blocks import moe
+
+    Ep, Hp, Ip, k = 256, 2048, 512, 8
+    ex = moe.Fp8RowExperts.from_rows(wl.fp8_row_weights(Ep, Ip, Hp, seed=91, device=dev),
+                                     wl.fp8_row_weights(Ep, Ip, Hp, seed=92, device=dev),
+                                     wl.fp8_row_weights(Ep, Hp, Ip, seed=93, device=dev))
+    x = wl.activations(T, Hp, seed=94, device=dev, dtype=torch.float32)
+    rot = max(2, min(32, (512 << 20) // max(1, min(T * k, Ep) * ex.bytes_per_expert) + 1))
+    routes, nb, seen = [], [], set()
+    for i in range(rot):
+        w, ids = moe.topk_softmax(wl.router_logits(T, Ep, seed=950 + i, device=dev), k, True)
+        u = torch.unique(ids)
+        seen.update(u.tolist())
+        routes.append((w, ids))
+        nb.append(int(u.numel()) * ex.bytes_per_expert + T * Hp * 4 * 2 + T * k * 12)
+    for w, ids in routes:
+        moe.moe_ffn_fp8row(x, ids, w, ex)
+    torch.cuda.synchronize()
+    t = device_time([lambda w=w, ids=ids: moe.moe_ffn_fp8row(x, ids, w, ex) for w, ids in routes],
+                    reps=max(1, 32 // rot))
+    b = sum(nb) / len(nb)
+    res = {"T": T, "us": t * 1e6, "bytes": b, "GBps": b / t / 1e9, "frac_hbm": b / t / PEAK_HBM,
+           "routings": rot, "distinct_bytes": len(seen) * ex.bytes_per_expert,
+           "TFLOPs": 2.0 * T * k * 3 * Hp * Ip / t / 1e12}
+    del ex
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_fp8_prefill(dev, T: int = 2048):
     """FP8 e4m3 block-scaled (128x128 weight blocks, per-token-per-128
     activations) MoE prefill layer: 256 experts, top-8 (logits N(0,1)),
@@ -801,6 +843,11 @@ def main():
             r = bench_mx(fmt, M, 4096, 14336, dev)
             extra[f"{fmt}_linear_k4096_n14336_m{M}"] = r
             log(f"{fmt} linear K=4096 N=14336 M={M}: {r['avg_us']:.2f} us, {r['GBps']:.0f} GB/s "
+                f"({r['frac_hbm']:.3f} of HBM peak)")
+        for Tr in (1, 16, 512):
+            r = bench_fp8row_moe(Tr, dev)
+            extra[f"fp8row_moe_ornith_T{Tr}"] = r
+            log(f"fp8 per-row (checkpoint format) MoE layer T={Tr}: {r['us']:.1f} us, {r['GBps']:.0f} GB/s "
                 f"({r['frac_hbm']:.3f} of HBM peak)")
         r = bench_fp8_prefill(dev)
         extra["fp8_moe_prefill_T2048"] = r

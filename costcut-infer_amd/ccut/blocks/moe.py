@@ -80,16 +80,38 @@ def route_experts(gate_logits, top_k: int, norm_topk: int):
     return _route(gate_logits, top_k, _MODE_ROUTE_NORM if norm_topk else _MODE_RAW_EXP)
 
 
+def _f32_weight(w) -> torch.Tensor:
+    """A float32 weight on the device, contiguous and 16-byte aligned (the
+    fp32 GEMM kernels' 16-byte loads)."""
+    t = _dev.to_device(w, torch.float32).contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _expert_shapes(H: int, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor, what: str) -> int:
+    I = wg.shape[1] if wg.dim() == 2 else -1
+    if wg.dim() != 2 or tuple(wg.shape) != (H, I) or tuple(wu.shape) != (H, I) or tuple(wd.shape) != (I, H):
+        raise ValueError(f"{what}: expert weights gate {tuple(wg.shape)}, up {tuple(wu.shape)}, down "
+                         f"{tuple(wd.shape)}; expected gate/up [hidden={H}, inter] and down [inter, hidden={H}]")
+    return I
+
+
 def expert_ffn(x, w_gate, w_up, w_down):
     """``down(silu(x @ Wg) * (x @ Wu))`` on already-dequantized float32
     weights ``Wg, Wu [hidden, inter]``, ``Wd [inter, hidden]`` (reference
-    ``moe.py:122-141``).  Library GEMMs + the float64 SiLU kernel."""
-    xd = _dev.to_device(x, torch.float32)
-    g = xd @ _dev.to_device(w_gate, torch.float32)
-    u = xd @ _dev.to_device(w_up, torch.float32)
-    h = torch.empty_like(g)
-    call("ccq_silu_mul", g.data_ptr(), u.data_ptr(), h.data_ptr(), g.numel(), _dev.stream_ptr())
-    y = h @ _dev.to_device(w_down, torch.float32)
+    ``moe.py:122-141``): ``ccq_expert_ffn_f32``, float32 products on the
+    fp32 matrix cores, the SiLU product in float64 (two launches)."""
+    xd = _dev.to_device(x, torch.float32).contiguous()
+    if xd.dim() != 2:
+        raise ValueError(f"x must be [rows, hidden], got {tuple(xd.shape)}")
+    rows, H = xd.shape
+    wg, wu, wd = _f32_weight(w_gate), _f32_weight(w_up), _f32_weight(w_down)
+    I = _expert_shapes(H, wg, wu, wd, "expert_ffn")
+    y = torch.empty((rows, H), dtype=torch.float32, device=xd.device)
+    if rows:
+        nbytes = lib().ccq_expert_ffn_f32_workspace_size(rows, I)
+        ws = _dev.workspace("expert_ffn_f32", nbytes, xd.device)
+        call("ccq_expert_ffn_f32", xd.data_ptr(), wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), y.data_ptr(), rows,
+             H, I, ws.data_ptr(), nbytes, _dev.stream_ptr(xd.device))
     return _dev.to_host(y) if _dev.is_host(x) else y
 
 
@@ -134,16 +156,23 @@ def moe_align(expert_ids, num_experts: int, tile_m: int = 16) -> Schedule:
 def moe_combine(x, expert_ids, weights, expert_outputs=None, expert_fn=expert_ffn, w_lookup=None, *,
                 shared=None, shared_gate: float = 1.0):
     """``y[t] = sum_e w[t,e] * expert_e(x[t])`` with the tokens of each expert
-    batched (reference ``moe.py:144-174``).  The grouping is computed on the
-    GPU; ``expert_fn`` is called once per expert, in first-appearance order,
-    with that expert's rows; the weighted sum is ``ccq_moe_combine``.
-    ``expert_outputs`` is accepted for signature compatibility (the reference
-    ignores it too).  Ids outside ``[0, E)`` contribute nothing."""
-    xd = _dev.to_device(x, torch.float32)
-    ids = _dev.to_device(expert_ids, torch.int64)
-    wts = _dev.to_device(weights, torch.float32)
+    batched (reference ``moe.py:144-174``).  With the default ``expert_fn``
+    and a ``w_lookup`` returning float32 ``(w_gate, w_up, w_down)``, the
+    whole layer is one grouped call (``ccq_moe_f32_ffn``: align, grouped
+    gate/up + SiLU, grouped down, combine); with another ``expert_fn``, the
+    grouping is computed on the GPU and ``expert_fn`` is called once per
+    expert, in first-appearance order, with that expert's rows, and the
+    weighted sum is ``ccq_moe_combine``.  ``expert_outputs`` is accepted for
+    signature compatibility (the reference ignores it too).  Negative ids
+    contribute nothing."""
+    xd = _dev.to_device(x, torch.float32).contiguous()
+    ids = _dev.to_device(expert_ids, torch.int64).contiguous()
+    wts = _dev.to_device(weights, torch.float32).contiguous()
     T, H = xd.shape
     k = ids.shape[1]
+    if expert_fn is expert_ffn and w_lookup is not None:
+        out = _moe_combine_f32(xd, ids, wts, w_lookup, shared, shared_gate)
+        return _dev.to_host(out) if _dev.is_host(x) else out
     E = int(ids.max().item()) + 1 if ids.numel() else 1
     sch = moe_align(ids, max(E, 1), tile_m=1).host()
     rows = torch.zeros((T * k, H), dtype=torch.float32, device=xd.device)
@@ -164,6 +193,42 @@ def moe_combine(x, expert_ids, weights, expert_outputs=None, expert_fn=expert_ff
     else:
         call("ccq_moe_combine", rows.data_ptr(), wts.data_ptr(), out.data_ptr(), 0, T, k, H, _dev.stream_ptr())
     return _dev.to_host(out) if _dev.is_host(x) else out
+
+
+def _moe_combine_f32(xd: torch.Tensor, ids: torch.Tensor, wts: torch.Tensor, w_lookup, shared,
+                     shared_gate: float) -> torch.Tensor:
+    """moe_combine's expert_ffn over float32 experts in one grouped call
+    (``ccq_moe_f32_ffn``): each routed expert's weights are looked up once,
+    and the kernels find them through device tables of pointers."""
+    T, H = xd.shape
+    k = ids.shape[1]
+    out = torch.empty((T, H), dtype=torch.float32, device=xd.device)
+    ids_h = ids.cpu().numpy()
+    routed = sorted(int(e) for e in np.unique(ids_h) if e >= 0)
+    if not routed:
+        out.zero_()
+        if shared is not None:
+            shared_expert_add(out, shared, shared_gate)
+        return out
+    E = routed[-1] + 1
+    keep, tabs, I = [], [[0] * E for _ in range(3)], None
+    for e in routed:
+        wg, wu, wd = (_f32_weight(w) for w in w_lookup(e))
+        Ie = _expert_shapes(H, wg, wu, wd, f"w_lookup({e})")
+        if I is not None and Ie != I:
+            raise ValueError(f"w_lookup({e}): inter={Ie}, other experts have {I}")
+        I = Ie
+        keep.append((wg, wu, wd))
+        for t, w in zip(tabs, (wg, wu, wd)):
+            t[e] = w.data_ptr()
+    tab = torch.tensor(tabs, dtype=torch.int64).to(xd.device)
+    nbytes = lib().ccq_moe_f32_workspace_size(T, k, E, H, I)
+    ws = _dev.workspace("moe_f32", nbytes, xd.device)
+    sd = _shared_rows(shared, T, H, xd.device) if shared is not None else None
+    call("ccq_moe_f32_ffn", xd.data_ptr(), ids.data_ptr(), wts.data_ptr(), tab[0].data_ptr(), tab[1].data_ptr(),
+         tab[2].data_ptr(), sd.data_ptr() if sd is not None else None, float(np.float32(shared_gate)),
+         out.data_ptr(), 0, T, k, E, H, I, ws.data_ptr(), nbytes, _dev.stream_ptr(xd.device))
+    return out
 
 
 def _shared_rows(shared, T: int, H: int, device) -> torch.Tensor:

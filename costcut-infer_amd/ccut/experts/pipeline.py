@@ -3,7 +3,7 @@
 metrics, on the GPU operators of this package.
 
 A step: speculative prefetch from the route history, the router
-``x @ gate_w.T`` (a library float32 GEMM), ``topk_softmax``, prefetch of the
+``x @ gate_w.T`` (``ccq_f32_gemm``), ``topk_softmax``, prefetch of the
 routed experts, the experts' FFN with the weighted combine, the shared expert
 and the metrics.  The expert weights come from ``reader`` in one of two ways:
 
@@ -14,8 +14,10 @@ and the metrics.  The expert weights come from ``reader`` in one of two ways:
   reference checkpoint's own format) as float32.
 * otherwise ``reader.get(layer, eid, timeout)`` per routed expert returning
   float32 ``(w_gate [hidden, inter], w_up [hidden, inter], w_down [inter,
-  hidden])``, the orientation ``expert_ffn`` takes: ``expert_ffn`` per
-  expert and ``moe_combine`` (reference ``pipeline.py:155-179``).  Weights
+  hidden])``, the orientation ``expert_ffn`` takes, then ``expert_ffn``
+  and the weighted add over all of them in one grouped call
+  (``moe_combine`` -> ``ccq_moe_f32_ffn``; reference
+  ``pipeline.py:155-179`` loops over the experts).  Weights
   of any other shape raise ``ValueError`` (the reference's reader hands over
   ``[out, in]`` slots here, ``pipeline.py:160-170``; this package's
   ``ExpertReader`` returns ``[in, out]``).
@@ -45,6 +47,7 @@ import numpy as np
 import torch
 
 from ccut import _dev
+from ccut._lib import call
 from ccut.blocks import moe
 
 __all__ = ["PipelineMetrics", "ExpertPipeline", "RouteHistory"]
@@ -131,12 +134,18 @@ class ExpertPipeline:
     @staticmethod
     def router_logits(x, gate_w) -> torch.Tensor:
         """The router ``x @ gate_w.T`` in float32 (reference
-        ``pipeline.py:145``) as a device tensor [T, E]."""
-        xd = _dev.to_device(x, torch.float32)
-        gw = _dev.to_device(gate_w, torch.float32)
+        ``pipeline.py:145``) as a device tensor [T, E]: ``ccq_f32_gemm`` with
+        ``gate_w`` as stored ([E, H]), float32 products on the fp32 matrix
+        cores."""
+        xd = _dev.to_device(x, torch.float32).contiguous()
+        gw = _dev.to_device(gate_w, torch.float32).contiguous()
         if xd.dim() != 2 or gw.dim() != 2 or xd.shape[1] != gw.shape[1]:
             raise ValueError(f"router: x {tuple(xd.shape)} and gate_w {tuple(gw.shape)} must be [T, H] and [E, H]")
-        return xd @ gw.T
+        T, H = xd.shape
+        E = gw.shape[0]
+        logits = torch.empty((T, E), dtype=torch.float32, device=xd.device)
+        call("ccq_f32_gemm", xd.data_ptr(), gw.data_ptr(), logits.data_ptr(), T, H, E, 1, _dev.stream_ptr(xd.device))
+        return logits
 
     def step(self, layer: int, x, gate_w, top_k: int = 8, norm_topk_prob: bool = True,
              shared_projs: dict | None = None, shared_gate: float = 1.0):
@@ -214,8 +223,9 @@ class ExpertPipeline:
     def _per_expert(self, layer: int, xd: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
                     flat_ids: list[int], s_out, shared_gate: float):
         """The reference's per-expert path (``pipeline.py:155-179``): each
-        routed expert's float32 weights from ``reader.get``, ``expert_ffn`` +
-        ``moe_combine``; timeouts as ``on_expert_timeout`` says."""
+        routed expert's float32 weights from ``reader.get``, then
+        ``expert_ffn`` + the weighted add for all of them in one grouped
+        ``moe_combine`` call; timeouts as ``on_expert_timeout`` says."""
         H = xd.shape[1]
         resolved: dict[int, tuple] = {}
         for eid in sorted(set(e for e in flat_ids if e >= 0)):

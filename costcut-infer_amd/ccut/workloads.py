@@ -6,7 +6,10 @@ offline).  Distributions:
 * MoE routing: logits ``N(0,1)`` (plus a per-expert bias ``N(0, 2)`` for the
   skewed router), softmax, top-k;
 * FP8 block weights: ``clip(N(0, 0.02), +-448)`` cast to e4m3fn, float32
-  ``128x128`` block scales ``|N(0,1)| * 0.01 + 1e-3``.
+  ``128x128`` block scales ``|N(0,1)| * 0.01 + 1e-3``;
+* FP8 per-row weights (the reference checkpoint's expert format):
+  ``clip(N(0, 0.02), +-448)`` cast to e4m3fn, one scale per output row
+  ``|N(0,1)| * 0.01 + 1e-3`` rounded to BF16 as the checkpoint stores it.
 
 Everything is drawn from a ``torch.Generator`` on the target device so the
 large expert sets are generated in HBM.
@@ -66,3 +69,14 @@ def fp8_block_weights(E: int, N: int, K: int, seed: int = 0, device="cuda", bloc
         w[e] = v.to(torch.float8_e4m3fn).view(torch.uint8)
     s = torch.randn((E, N // block, K // block), generator=g, device=device).abs() * 0.01 + 1e-3
     return w, s.float().contiguous()
+
+
+def fp8_row_weights(E: int, N: int, K: int, seed: int = 0, device="cuda"):
+    """``(w [E, N, K] e4m3fn bytes as uint8, s [E, N] f32 holding BF16 values)``."""
+    g = gen(seed, device)
+    w = torch.empty((E, N, K), dtype=torch.uint8, device=device)
+    for e in range(E):
+        v = (torch.randn((N, K), generator=g, device=device) * 0.02).clamp_(-448, 448)
+        w[e] = v.to(torch.float8_e4m3fn).view(torch.uint8)
+    s = torch.randn((E, N), generator=g, device=device).abs() * 0.01 + 1e-3
+    return w, s.to(torch.bfloat16).float().contiguous()

@@ -568,6 +568,51 @@ int ccq_moe_fp8row_ffn_shared(const float* x, const int64_t* ids, const float* w
                               int64_t k, const ccq_fp8row_experts* ex, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Float32 products on already-float32 operands (fp32 MFMA: float32
+ * products, float32 accumulation, operands never rounded)
+ * ---------------------------------------------------------------------- */
+
+/* y [M, N] = x [M, K] @ w^T for w [N, K] (trans_w = 1: the router
+ * x @ gate_w.T, experts/pipeline.py:145) or x @ w for w [K, N]
+ * (trans_w = 0: the products of expert_ffn, blocks/moe.py:137-141).
+ * Row-major, leading dimensions = row lengths; any shape (16-byte loads
+ * when K, N and the pointers allow). */
+int ccq_f32_gemm(const float* x, const float* w, float* y, int64_t M, int64_t K, int64_t N, int trans_w,
+                 void* stream);
+
+/* Workspace bytes of ccq_expert_ffn_f32 (the [rows, inter] intermediate). */
+size_t ccq_expert_ffn_f32_workspace_size(int64_t rows, int64_t inter);
+
+/* expert_ffn on float32 weights (blocks/moe.py:122-141): y [rows, hidden] =
+ * (silu(x @ w_gate) * (x @ w_up)) @ w_down with w_gate / w_up [hidden,
+ * inter], w_down [inter, hidden]; the SiLU product in float64, rounded once
+ * (silu_mul_fused, quant/kernels.py:219-231).  Two launches (gate/up with
+ * the SiLU epilogue, down). */
+int ccq_expert_ffn_f32(const float* x, const float* w_gate, const float* w_up, const float* w_down, float* y,
+                       int64_t rows, int64_t hidden, int64_t inter, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* Workspace bytes of ccq_moe_f32_ffn. */
+size_t ccq_moe_f32_workspace_size(int64_t T, int64_t k, int64_t num_experts, int64_t hidden, int64_t inter);
+
+/* moe_combine with expert_ffn over float32 expert weights found through
+ * device tables of E pointers each (w_gate[e], w_up[e] [hidden, inter],
+ * w_down[e] [inter, hidden]; every pointer 16-byte aligned; a null entry
+ * makes that expert's rows zero): the assignments grouped by expert
+ * (ccq_moe_align, 64-row tiles), one grouped gate/up launch with the SiLU
+ * epilogue and one grouped down launch over all experts, then the weighted
+ * combine in slot order with shared_gate * shared added when shared is not
+ * null.  x [T, hidden] f32, ids [T, k] (outside [0, E): left out),
+ * weights [T, k] f32, y [T, hidden] of y_dtype.  Replaces the per-expert
+ * loop of moe_combine (blocks/moe.py:144-174) and of ExpertPipeline.step
+ * (experts/pipeline.py:155-190) for readers that hand over float32 slots. */
+int ccq_moe_f32_ffn(const float* x, const int64_t* ids, const float* weights,
+                    const float* const* w_gate, const float* const* w_up, const float* const* w_down,
+                    const float* shared, float shared_gate, void* y, int y_dtype, int64_t T, int64_t k,
+                    int64_t num_experts, int64_t hidden, int64_t inter, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
