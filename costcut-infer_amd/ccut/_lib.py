@@ -136,7 +136,8 @@ SIGNATURES: dict[str, tuple] = {
                                   _sz, _vp]),
     "ccq_moe_fp8row_ffn_shared": (_int, [_vp, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _i64, _i64,
                                          ctypes.POINTER(ccq_fp8row_experts), _vp, _sz, _vp]),
-    "ccq_f32_gemm": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "ccq_f32_gemm_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "ccq_f32_gemm": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
     "ccq_expert_ffn_f32_workspace_size": (_sz, [_i64, _i64]),
     "ccq_expert_ffn_f32": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "ccq_moe_f32_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),

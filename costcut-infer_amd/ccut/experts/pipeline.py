@@ -47,7 +47,7 @@ import numpy as np
 import torch
 
 from ccut import _dev
-from ccut._lib import call
+from ccut._lib import call, lib
 from ccut.blocks import moe
 
 __all__ = ["PipelineMetrics", "ExpertPipeline", "RouteHistory"]
@@ -144,7 +144,10 @@ class ExpertPipeline:
         T, H = xd.shape
         E = gw.shape[0]
         logits = torch.empty((T, E), dtype=torch.float32, device=xd.device)
-        call("ccq_f32_gemm", xd.data_ptr(), gw.data_ptr(), logits.data_ptr(), T, H, E, 1, _dev.stream_ptr(xd.device))
+        nbytes = lib().ccq_f32_gemm_workspace_size(T, H, E)
+        ws = _dev.workspace("f32_gemm", nbytes, xd.device) if nbytes else None
+        call("ccq_f32_gemm", xd.data_ptr(), gw.data_ptr(), logits.data_ptr(), T, H, E, 1,
+             ws.data_ptr() if ws is not None else None, nbytes, _dev.stream_ptr(xd.device))
         return logits
 
     def step(self, layer: int, x, gate_w, top_k: int = 8, norm_topk_prob: bool = True,

@@ -13,7 +13,8 @@
 //
 // Tiling: a workgroup of 4 waves owns a 64 x 64 block of the output; K runs
 // in slabs of 16, double-buffered in LDS with one barrier per slab, the
-// next slab held in registers while the current one is multiplied.  The
+// next two slabs' loads in flight in registers while the current one is
+// multiplied.  The
 // A slab is stored k-major ([k][row]) and the B slab [k][col], so the 16
 // lanes that read one MFMA operand column touch 16 consecutive words.  Wave
 // (wr, wc) computes rows 32 wr .. +31 x columns 32 wc .. +31 as 2 x 2 MFMA
@@ -54,6 +55,7 @@ struct F32GP {
   float* c;                     // output rows (dense: row m; grouped: row = assignment id)
   int64_t ldc;
   int64_t M, N, K;              // M: rows of a dense product
+  int64_t kchunk;               // K per split (gridDim.z splits); partial sums to c + split * M * ldc
 };
 
 // 4 consecutive floats at p, of which `avail` (may be <= 0) are in bounds
@@ -81,7 +83,11 @@ __global__ __launch_bounds__(FG_THREADS) void f32_gemm_kernel(const F32GP p) {
   __shared__ __align__(16) float Bs[2][NB][FG_BK][FG_RS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t N = p.N, K = p.K;
+  const int64_t N = p.N;
+  // split z of gridDim.z: k in [kbeg, kbeg + K), written to its own partial slice
+  const int64_t kbeg = (int64_t)blockIdx.z * p.kchunk;
+  const int64_t K = imin64(p.kchunk, p.K - kbeg);
+  float* const cout = p.c + (int64_t)blockIdx.z * p.M * p.ldc;
   const int64_t n0 = (int64_t)blockIdx.x * FG_BN;
   const float* b0 = p.b0;
   const float* b1 = p.b1;
@@ -114,11 +120,13 @@ __global__ __launch_bounds__(FG_THREADS) void f32_gemm_kernel(const F32GP p) {
   if constexpr (GROUPED) {
     const int a = trow[am];
     a_ok = a >= 0;
-    arow = p.a + (int64_t)(a_ok ? a / p.row_div : 0) * p.lda;
+    arow = p.a + (int64_t)(a_ok ? a / p.row_div : 0) * p.lda + kbeg;
   } else {
     a_ok = m0 + am < p.M;
-    arow = p.a + (a_ok ? m0 + am : 0) * p.lda;
+    arow = p.a + (a_ok ? m0 + am : 0) * p.lda + kbeg;
   }
+  b0 += BT ? kbeg : kbeg * p.ldb;
+  if constexpr (DUAL) b1 += BT ? kbeg : kbeg * p.ldb;
   // B [K, N]: thread loads k tid / 16, columns 4 (tid % 16) .. +3;
   // B [N, K]: thread loads column tid % 64, k 4 (tid / 64) .. +3
   const int bk = BT ? 4 * (tid >> 6) : (tid >> 4);
@@ -170,13 +178,7 @@ __global__ __launch_bounds__(FG_THREADS) void f32_gemm_kernel(const F32GP p) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t nslab = cdiv(K, FG_BK);
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int64_t s = 0; s < nslab; ++s) {
-    const int buf = (int)(s & 1);
-    if (s + 1 < nslab) load((s + 1) * FG_BK);
+  auto mma = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < FG_BK; kk += 4) {
       float av[2], bv[NB][2];
@@ -194,7 +196,41 @@ __global__ __launch_bounds__(FG_THREADS) void f32_gemm_kernel(const F32GP p) {
           for (int j = 0; j < 2; ++j)
             acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[b][j], acc[b][i][j], 0, 0, 0);
     }
-    if (s + 1 < nslab) store(buf ^ 1);
+  };
+
+  // slab s + 1 is in LDS buffer (s + 1) & 1 before slab s's products end,
+  // and slab s + 2's loads are in flight meanwhile (two register sets, the
+  // loop unrolled by two so that each set has fixed registers)
+  const int64_t nslab = cdiv(K, FG_BK);
+  load(0);
+  store(0);
+  float4 xa = ra, xb0 = rb0, xb1 = rb1;  // register set of odd slabs
+  if (nslab > 1) {
+    load(FG_BK);
+    xa = ra, xb0 = rb0, xb1 = rb1;
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < nslab; s += 2) {
+    // even slab s in LDS 0, slab s + 1 in (xa, xb0, xb1)
+    if (s + 2 < nslab) load((s + 2) * FG_BK);
+    mma(0);
+    if (s + 1 < nslab) {
+      float4 ta = ra, tb0 = rb0, tb1 = rb1;
+      ra = xa, rb0 = xb0, rb1 = xb1;
+      store(1);
+      ra = ta, rb0 = tb0, rb1 = tb1;
+    }
+    __syncthreads();
+    if (s + 1 >= nslab) break;
+    // odd slab s + 1 in LDS 1, slab s + 2 in (ra, rb0, rb1)
+    if (s + 3 < nslab) {
+      const float4 ta = ra, tb0 = rb0, tb1 = rb1;
+      load((s + 3) * FG_BK);
+      xa = ra, xb0 = rb0, xb1 = rb1;
+      ra = ta, rb0 = tb0, rb1 = tb1;
+    }
+    mma(1);
+    if (s + 2 < nslab) store(0);
     __syncthreads();
   }
 
@@ -224,14 +260,25 @@ __global__ __launch_bounds__(FG_THREADS) void f32_gemm_kernel(const F32GP p) {
         } else {
           v = acc[0][i][j][t];
         }
-        p.c[orow * p.ldc + n] = v;
+        cout[orow * p.ldc + n] = v;
       }
   }
 }
 
+// y = the sum of `splits` partial products in split order (deterministic)
+__global__ __launch_bounds__(256) void f32_splitk_sum_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                             int64_t n, int splits) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float v = part[i];
+    for (int s = 1; s < splits; ++s) v += part[(int64_t)s * n + i];
+    y[i] = v;
+  }
+}
+
 template <bool BT, bool DUAL, bool GROUPED>
-static int f32_launch(const F32GP& p, int64_t tiles_y, bool vec, hipStream_t st, const char* name) {
-  const dim3 grid((unsigned)cdiv(p.N, FG_BN), (unsigned)tiles_y);
+static int f32_launch(F32GP p, int64_t tiles_y, bool vec, hipStream_t st, const char* name, int splits = 1) {
+  if (splits == 1) p.kchunk = p.K;
+  const dim3 grid((unsigned)cdiv(p.N, FG_BN), (unsigned)tiles_y, (unsigned)splits);
   if (vec)
     launch((f32_gemm_kernel<BT, DUAL, GROUPED, true>), grid, dim3(FG_THREADS), 0, st, p);
   else
@@ -245,6 +292,131 @@ static int f32_launch(const F32GP& p, int64_t tiles_y, bool vec, hipStream_t st,
 static bool f32_vec_ok(const float* a, int64_t lda, const void* b, int64_t ldb, bool bt, int64_t K, int64_t N) {
   return aligned(a, 16) && (b == nullptr || aligned(b, 16)) && lda % 4 == 0 && ldb % 4 == 0 && K % 4 == 0 &&
          (bt || N % 4 == 0);
+}
+
+
+// y [M, N] = x [M, K] @ w^T for w [N, K] and few rows (the router at decode
+// batch sizes): the tiled kernel would be one workgroup walking K.  Here a
+// workgroup is 4 waves x RT weight rows (output columns); lane l streams
+// floats 4 l + 256 i of each of its rows in 16-byte pieces, all of a row's
+// pieces in flight at once for K <= 2048; BB rows of x per pass are staged
+// in LDS (zeros past M); the per-lane products of the RT x BB outputs are
+// summed over the wave by halving exchanges, in a fixed order.  Requires
+// K % 4 == 0 and 16-byte aligned x, w.
+constexpr int FS_RT = 2;
+constexpr int FS_LDS = 64 * 1024;
+
+template <int V>
+__device__ __forceinline__ float fs_wave_sum(float (&v)[V], int lane) {
+#pragma unroll
+  for (int m = 1, n = V; m < V; m <<= 1, n >>= 1) {
+    const bool up = (lane & m) != 0;
+#pragma unroll
+    for (int j = 0; j < n / 2; ++j) {
+      const float keep = up ? v[2 * j + 1] : v[2 * j];
+      const float send = up ? v[2 * j] : v[2 * j + 1];
+      v[j] = keep + __shfl_xor(send, m, 64);
+    }
+  }
+  float t = v[0];
+#pragma unroll
+  for (int m = V; m < 64; m <<= 1) t += __shfl_xor(t, m, 64);
+  return t;  // lane l: the sum of value l % V
+}
+
+template <int BB>
+__global__ __launch_bounds__(256) void f32_skinny_nt_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            float* __restrict__ y, int64_t M, int64_t K, int64_t N) {
+  extern __shared__ __align__(16) float xs[];  // [BB][K]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t m0 = (int64_t)blockIdx.y * BB;
+  const int nb = (int)imin64(BB, M - m0);
+  const int64_t q4 = K / 4, nq = BB * q4;
+  for (int64_t i0 = 0; i0 < nq; i0 += 8 * 256) {  // 8 loads in flight per thread
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + 256 * u + tid, b = i / q4;
+      v[u] = i < nq && b < nb ? *reinterpret_cast<const float4*>(x + (m0 + b) * K + 4 * (i - b * q4))
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + 256 * u + tid;
+      if (i < nq) *reinterpret_cast<float4*>(&xs[4 * i]) = v[u];
+    }
+  }
+  __syncthreads();
+  const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * FS_RT;
+  if (n0 >= N) return;
+  const float* wr[FS_RT];
+#pragma unroll
+  for (int r = 0; r < FS_RT; ++r) wr[r] = w + imin64(n0 + r, N - 1) * K;  // past N: row N-1, not stored
+  float acc[FS_RT][BB];
+#pragma unroll
+  for (int r = 0; r < FS_RT; ++r)
+#pragma unroll
+    for (int b = 0; b < BB; ++b) acc[r][b] = 0.f;
+  constexpr int U = 8;  // pieces per row in flight
+  for (int64_t k0 = 4 * lane; k0 < K; k0 += 256 * U) {
+    float4 wv[U][FS_RT];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < FS_RT; ++r)
+        wv[u][r] = k0 + 256 * u < K
+                       ? __builtin_bit_cast(float4, __builtin_nontemporal_load(
+                                                        reinterpret_cast<const f32x4*>(wr[r] + k0 + 256 * u)))
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (k0 + 256 * u >= K) break;
+#pragma unroll
+      for (int b = 0; b < BB; ++b) {
+        const float4 xv = *reinterpret_cast<const float4*>(&xs[b * K + k0 + 256 * u]);
+#pragma unroll
+        for (int r = 0; r < FS_RT; ++r) {
+          acc[r][b] = fmaf(xv.x, wv[u][r].x, acc[r][b]);
+          acc[r][b] = fmaf(xv.y, wv[u][r].y, acc[r][b]);
+          acc[r][b] = fmaf(xv.z, wv[u][r].z, acc[r][b]);
+          acc[r][b] = fmaf(xv.w, wv[u][r].w, acc[r][b]);
+        }
+      }
+    }
+  }
+  float flat[FS_RT * BB];
+#pragma unroll
+  for (int r = 0; r < FS_RT; ++r)
+#pragma unroll
+    for (int b = 0; b < BB; ++b) flat[r * BB + b] = acc[r][b];
+  const float v = fs_wave_sum<FS_RT * BB>(flat, lane);
+  if (lane < FS_RT * BB) {
+    const int r = lane / BB, b = lane % BB;
+    if (n0 + r < N && b < nb) y[(m0 + b) * N + n0 + r] = v;
+  }
+}
+
+// rows per pass of the skinny kernel (0: not taken): the fewest passes
+// whose x rows fit the LDS; every pass re-reads w, so at most 4 passes
+static int f32_skinny_bb(int64_t M, int64_t K) {
+  int bb = 1;
+  while (bb < 16 && bb < M && (int64_t)(2 * bb) * K * 4 <= FS_LDS) bb *= 2;
+  if ((int64_t)bb * K * 4 > FS_LDS) return 0;
+  return cdiv(M, bb) <= 4 ? bb : 0;
+}
+
+static int f32_skinny_launch(int bb, const float* x, const float* w, float* y, int64_t M, int64_t K, int64_t N,
+                             hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(N, 4 * FS_RT), (unsigned)cdiv(M, bb));
+  const size_t lds = (size_t)bb * K * 4;
+  switch (bb) {
+    case 1: launch((f32_skinny_nt_kernel<1>), grid, dim3(256), lds, st, x, w, y, M, K, N); break;
+    case 2: launch((f32_skinny_nt_kernel<2>), grid, dim3(256), lds, st, x, w, y, M, K, N); break;
+    case 4: launch((f32_skinny_nt_kernel<4>), grid, dim3(256), lds, st, x, w, y, M, K, N); break;
+    case 8: launch((f32_skinny_nt_kernel<8>), grid, dim3(256), lds, st, x, w, y, M, K, N); break;
+    default: launch((f32_skinny_nt_kernel<16>), grid, dim3(256), lds, st, x, w, y, M, K, N); break;
+  }
+  return launch_status("ccq_f32_gemm (skinny)");
 }
 
 namespace {
@@ -285,8 +457,28 @@ F32MoeLayout f32_moe_layout(int64_t T, int64_t k, int64_t E, int64_t H, int64_t 
 
 using namespace ccq;
 
+// K splits of the tiled kernel: enough (64 x 64 tile, split) items for two
+// per compute unit, each split at least 256 deep (a multiple of the slab)
+static int64_t f32_kchunk(int64_t M, int64_t K, int64_t N) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const int64_t tiles = cdiv(M, FG_BM) * cdiv(N, FG_BN);
+  int64_t splits = cdiv(2 * (int64_t)cus, tiles);
+  if (splits > K / 256) splits = K / 256;
+  if (splits <= 1) return K;
+  return cdiv(cdiv(K, splits), FG_BK) * FG_BK;
+}
+
+extern "C" size_t ccq_f32_gemm_workspace_size(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  const int64_t kc = f32_kchunk(M, K, N);
+  return kc >= K ? 0 : (size_t)cdiv(K, kc) * M * N * 4;
+}
+
 extern "C" int ccq_f32_gemm(const float* x, const float* w, float* y, int64_t M, int64_t K, int64_t N, int trans_w,
-                            void* stream) {
+                            void* workspace, size_t workspace_bytes, void* stream) {
   CCQ_REQUIRE(M >= 0 && K >= 0 && N >= 0, "ccq_f32_gemm: negative shape");
   CCQ_REQUIRE(trans_w == 0 || trans_w == 1, "ccq_f32_gemm: trans_w=%d (0: w [K, N], 1: w [N, K])", trans_w);
   if (M == 0 || N == 0) return 0;
@@ -304,8 +496,24 @@ extern "C" int ccq_f32_gemm(const float* x, const float* w, float* y, int64_t M,
   p.K = K;
   const bool vec = f32_vec_ok(x, K, w, p.ldb, trans_w, K, N);
   hipStream_t st = as_stream(stream);
-  return trans_w ? f32_launch<true, false, false>(p, cdiv(M, FG_BM), vec, st, "ccq_f32_gemm")
-                 : f32_launch<false, false, false>(p, cdiv(M, FG_BM), vec, st, "ccq_f32_gemm");
+  if (trans_w && vec) {
+    const int bb = f32_skinny_bb(M, K);
+    if (bb > 0 && cdiv(M, bb) <= 65535) return f32_skinny_launch(bb, x, w, y, M, K, N, st);
+  }
+  const int64_t kc = f32_kchunk(M, K, N);
+  const int64_t splits = cdiv(K, kc);
+  const bool split = splits > 1 && workspace != nullptr && workspace_bytes >= (size_t)splits * M * N * 4 &&
+                     aligned(workspace, 16) && splits <= 65535;
+  if (split) {  // partial products per K range, then their sum in split order
+    p.c = (float*)workspace;
+    p.kchunk = kc;
+  }
+  const int sp = split ? (int)splits : 1;
+  int rc = trans_w ? f32_launch<true, false, false>(p, cdiv(M, FG_BM), vec, st, "ccq_f32_gemm", sp)
+                   : f32_launch<false, false, false>(p, cdiv(M, FG_BM), vec, st, "ccq_f32_gemm", sp);
+  if (rc || !split) return rc;
+  launch(f32_splitk_sum_kernel, dim3(grid_for(M * N, 256)), dim3(256), 0, st, (const float*)workspace, y, M * N, sp);
+  return launch_status("ccq_f32_gemm (split-K sum)");
 }
 
 extern "C" size_t ccq_expert_ffn_f32_workspace_size(int64_t rows, int64_t inter) {

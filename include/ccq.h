@@ -573,13 +573,20 @@ int ccq_moe_fp8row_ffn_shared(const float* x, const int64_t* ids, const float* w
  * products, float32 accumulation, operands never rounded)
  * ---------------------------------------------------------------------- */
 
+/* Workspace bytes ccq_f32_gemm can use to split K when the output has too
+ * few 64 x 64 tiles to fill the GPU (0: no split for this shape). */
+size_t ccq_f32_gemm_workspace_size(int64_t M, int64_t K, int64_t N);
+
 /* y [M, N] = x [M, K] @ w^T for w [N, K] (trans_w = 1: the router
  * x @ gate_w.T, experts/pipeline.py:145) or x @ w for w [K, N]
  * (trans_w = 0: the products of expert_ffn, blocks/moe.py:137-141).
  * Row-major, leading dimensions = row lengths; any shape (16-byte loads
- * when K, N and the pointers allow). */
+ * when K, N and the pointers allow).  With the workspace of
+ * ccq_f32_gemm_workspace_size, small outputs split K over workgroups and
+ * add the partial sums in split order (deterministic); workspace may be
+ * null (no split). */
 int ccq_f32_gemm(const float* x, const float* w, float* y, int64_t M, int64_t K, int64_t N, int trans_w,
-                 void* stream);
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes of ccq_expert_ffn_f32 (the [rows, inter] intermediate). */
 size_t ccq_expert_ffn_f32_workspace_size(int64_t rows, int64_t inter);

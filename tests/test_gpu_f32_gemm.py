@@ -37,7 +37,8 @@ def _rel(got, ref):
     return float(np.abs(np.asarray(got, np.float64) - ref).max() / np.abs(ref).max())
 
 
-@pytest.mark.parametrize("T,E,H", [(16, 64, 2048), (1, 256, 2048), (2048, 256, 7168), (5, 7, 33), (70, 130, 260)])
+@pytest.mark.parametrize("T,E,H", [(16, 64, 2048), (1, 256, 2048), (2048, 256, 7168), (5, 7, 33), (70, 130, 260),
+                                   (3, 200, 132), (16, 256, 7168)])
 def test_router_logits_vs_float64(gpu, T, E, H):
     """x @ gate_w.T with gate_w as stored [E, H]; the top-k ids of those
     logits are the oracle's bit for bit (routing on the same logits)."""
@@ -59,19 +60,27 @@ def test_router_logits_vs_float64(gpu, T, E, H):
     assert np.abs(w.cpu().numpy() - w0).max() <= 1e-6
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 2048, 512), (37, 512, 2048), (64, 256, 64), (3, 30, 10), (130, 100, 66)])
+@pytest.mark.parametrize("M,K,N", [(1, 2048, 512), (37, 512, 2048), (64, 256, 64), (3, 30, 10), (130, 100, 66),
+                                   (200, 3000, 72)])
 def test_f32_gemm_nn_vs_float64(gpu, M, K, N):
     """x @ w for w [K, N] (expert_ffn's orientation), 16-byte and
     per-element load paths, ragged tiles."""
-    from ccut._lib import call
+    from ccut._lib import call, lib
 
     rng = np.random.default_rng(M + K + N)
     x = rng.standard_normal((M, K)).astype(np.float32)
     w = rng.standard_normal((K, N)).astype(np.float32)
     xd, wd = torch.from_numpy(x).to(gpu), torch.from_numpy(w).to(gpu)
     y = torch.empty((M, N), dtype=torch.float32, device=gpu)
-    call("ccq_f32_gemm", xd.data_ptr(), wd.data_ptr(), y.data_ptr(), M, K, N, 0, None)
-    assert _rel(y.cpu().numpy(), x.astype(np.float64) @ w.astype(np.float64)) <= 1e-5
+    call("ccq_f32_gemm", xd.data_ptr(), wd.data_ptr(), y.data_ptr(), M, K, N, 0, None, 0, None)
+    ref = x.astype(np.float64) @ w.astype(np.float64)
+    assert _rel(y.cpu().numpy(), ref) <= 1e-5
+    nbytes = lib().ccq_f32_gemm_workspace_size(M, K, N)
+    if nbytes:  # K split over workgroups, partial sums added in split order
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+        y2 = torch.empty((M, N), dtype=torch.float32, device=gpu)
+        call("ccq_f32_gemm", xd.data_ptr(), wd.data_ptr(), y2.data_ptr(), M, K, N, 0, ws.data_ptr(), nbytes, None)
+        assert _rel(y2.cpu().numpy(), ref) <= 1e-5
 
 
 def test_expert_ffn_f32_ornith_shapes(gpu):
