@@ -15,7 +15,7 @@ import numpy as np
 import torch
 
 from ccut import _dev
-from ccut._lib import call
+from ccut._lib import call, lib
 from ccut.quant.spec import LayerQuantSpec, QuantDType, QuantKey
 
 __all__ = ["QuantizeMethodBase", "LinearMethod", "UnquantizedMethod", "make_method_for_spec"]
@@ -57,8 +57,8 @@ def _return(y: torch.Tensor, x):
 
 
 class UnquantizedMethod(QuantizeMethodBase):
-    """BF16/FP16/FP32 pass-through (reference ``method.py:65-75``); a plain
-    library GEMM on the device."""
+    """BF16/FP16/FP32 pass-through (reference ``method.py:65-75``): the
+    weight widened to float32, ``x @ W.T`` on ``ccq_f32_gemm``."""
 
     compute_path = "bf16"
 
@@ -68,7 +68,24 @@ class UnquantizedMethod(QuantizeMethodBase):
     def apply(self, weight_bytes, scales, x):
         xd = _f32_input(x)
         w = _unpack_weight(weight_bytes, self.weight_dtype).reshape(-1, xd.shape[1])
-        return _return(xd @ w.T, x)
+        return _return(f32_linear(xd, w), x)
+
+
+def f32_linear(xd: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``xd [batch, in] @ w.T`` for a float32 device weight ``w [out, in]``
+    (``ccq_f32_gemm``: float32 products on the fp32 matrix cores)."""
+    xd = xd.contiguous()
+    w = w.contiguous()
+    batch, in_f = xd.shape
+    out_f = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != in_f:
+        raise ValueError(f"weight {tuple(w.shape)} does not match in_features={in_f}")
+    y = torch.empty((batch, out_f), dtype=torch.float32, device=xd.device)
+    nbytes = lib().ccq_f32_gemm_workspace_size(batch, in_f, out_f)
+    ws = _dev.workspace("f32_gemm", nbytes, xd.device) if nbytes else None
+    call("ccq_f32_gemm", xd.data_ptr(), w.data_ptr(), y.data_ptr(), batch, in_f, out_f, 1,
+         ws.data_ptr() if ws is not None else None, nbytes, _dev.stream_ptr(xd.device))
+    return y
 
 
 def _unpack_weight(weight_bytes, dtype: str) -> torch.Tensor:
@@ -124,7 +141,7 @@ class LinearMethod(QuantizeMethodBase):
             return fp8_linear_f32(weight_bytes, scale, x)
         xd = _f32_input(x)
         w = _unpack_weight(weight_bytes, self.key.weight_dtype).reshape(-1, xd.shape[1])
-        return _return(xd @ w.T, x)
+        return _return(f32_linear(xd, w), x)
 
 
 def fp8_linear_f32(weight_bytes, scale, x):

@@ -130,11 +130,19 @@ class WeightOnlyMethod(QuantizeMethodBase):
             w = self.prepare(weight_bytes, scales)
             if isinstance(x, torch.Tensor) and x.is_cuda and x.dtype in (torch.float16, torch.bfloat16):
                 return awq.gemm(x, w)
-            # float32 / host activations: bfloat16 inputs to the MFMA (the
-            # range of float32, so no activation overflows as it would in
-            # float16 above 65504), float32 out
+            # float32 / host activations, float32 out: the MFMA takes them
+            # as float16 (11 significant bits) when every |x| fits its
+            # range, else as bfloat16 (8 bits, float32's range); the sums
+            # and the output stay float32, so nothing else can overflow
             xd = _dev.to_device(x, torch.float32)
-            y = awq.gemm(xd.to(torch.bfloat16), w, out_dtype=torch.float32)
+            if xd.numel() == 0:
+                amax = 0.0
+            elif _dev.is_host(x):
+                amax = float(np.abs(np.asarray(x, np.float32)).max())
+            else:
+                amax = float(xd.abs().amax().item())
+            xdt = torch.float16 if np.isfinite(amax) and amax <= 65504.0 else torch.bfloat16
+            y = awq.gemm(xd.to(xdt), w, out_dtype=torch.float32)
             return _return(y, x)
         if self.weight_dtype == QuantDType.INT4:
             scale = scales.get(self.scale_name) if self.scale_name else None

@@ -13,6 +13,11 @@ from oracle import awq as oawq
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-2          # the path's stated tolerance (relative to max|y_ref|)
+# Regression bounds of the benchmark configurations: about 3x the error
+# measured on MI355X, below the 2e-2 contract, so that a several-fold loss of
+# accuracy fails even while the contract still holds
+REGRESS_C1 = 8e-4
+REGRESS_C2 = 1.2e-3
 TIGHT = 2e-3        # float32 outputs: only accumulation order differs
 
 
@@ -105,13 +110,19 @@ def test_gemm_parity_groups(gpu, G):
 
 def test_gemm_config_single_linear_k2048_n5632(gpu):
     """x fp16 [1, 2048], W int4 2048 -> 5632, group 128, fp16 out."""
-    assert _gemm_case(gpu, 1, 2048, 5632, 128, torch.float16, torch.float16, seed=1) <= TOL
+    err = _gemm_case(gpu, 1, 2048, 5632, 128, torch.float16, torch.float16, seed=1)
+    print(f"[C1] awq gemv K=2048 N=5632: rel err {err:.3e}")
+    assert err <= TOL
+    assert err <= REGRESS_C1  # measured 2.65e-4 (fp16 output rounding dominates)
 
 
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_gemm_config_skinny_k4096_n14336(gpu, M):
     """K=4096 N=14336 group 128, M in {1, 4, 16}, fp16 in/out."""
-    assert _gemm_case(gpu, M, 4096, 14336, 128, torch.float16, torch.float16, seed=10 + M) <= TOL
+    err = _gemm_case(gpu, M, 4096, 14336, 128, torch.float16, torch.float16, seed=10 + M)
+    print(f"[C2] awq gemm K=4096 N=14336 M={M}: rel err {err:.3e}")
+    assert err <= TOL
+    assert err <= REGRESS_C2  # measured 3.2e-4 .. 4.0e-4 for M = 16, 4, 1
 
 
 def test_weight_only_method_awq(gpu):
@@ -133,11 +144,14 @@ def test_weight_only_method_awq(gpu):
     y = m.apply(qw, scales, x)
     assert isinstance(y, np.ndarray) and y.shape == (3, N) and y.dtype == np.float32
     ref = oawq.linear(x, qw, qz, s, G)
-    # x enters the MFMA as bf16 (one rounding of the float32 input)
-    assert np.abs(y - ref).max() <= TOL * np.abs(ref).max()
+    # x enters the MFMA as fp16 (|x| < 65504: one rounding to 11 significant
+    # bits of the float32 input)
+    err = np.abs(y - ref).max() / np.abs(ref).max()
+    print(f"awq apply float32 x (fp16 MFMA inputs): rel err {err:.3e}")
+    assert err <= 1e-3
     y2 = m.apply(qw, scales, x)  # second call reuses the prepared weights
     assert np.array_equal(y, y2)
-    # activations past the float16 range stay finite (bf16 keeps float32's range)
+    # activations past the float16 range go as bf16 (float32's range) and stay finite
     xb = x * np.float32(1e6)
     yb = m.apply(qw, scales, xb)
     refb = oawq.linear(xb, qw, qz, s, G)

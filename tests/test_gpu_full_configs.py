@@ -14,7 +14,7 @@ checked bit for bit on the whole batch against the oracle; outputs within
 max|dy| <= 2e-2 * max|y_ref| of the oracle's restatement of the reference
 algorithm (dequantize, then float32 matmuls with a float32 intermediate,
 expert_ffn + moe_combine of blocks/moe.py:122-174): every token for the int4
-layer, 32 tokens spread over the batch for the FP8 layer (its oracle
+layer, 256 tokens spread over the batch for the FP8 layer (its oracle
 dequantizes each routed expert's 44 MB of weights on the host)."""
 
 from __future__ import annotations
@@ -33,6 +33,12 @@ from oracle import moe as omoe
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-2
+# regression bounds: about 3x the error measured on MI355X, below the
+# contract (FP8 layer 2.2e-3 over 256 tokens: the e4m3 activations and the
+# two-part e4m3 intermediate; int4 layers 3.8e-3 / 3.4e-3 at T = 512 / 4096:
+# the bf16 intermediate and down rows)
+REGRESS_C4 = 7e-3
+REGRESS_C5 = 1.2e-2
 
 
 def _ffn_schedule(ws: torch.Tensor, n: int, E: int, tile_m: int):
@@ -87,7 +93,7 @@ def test_fp8_block_moe_prefill_full_layer(gpu):
     yh = y.cpu().numpy()
     assert np.isfinite(yh).all()
 
-    toks = np.arange(0, T, T // 32)
+    toks = np.arange(0, T, T // 256)
     xs = x[torch.from_numpy(toks).to(gpu)].float().cpu().numpy()
     need: dict[int, list[int]] = {}
     for j, t in enumerate(toks):
@@ -112,6 +118,7 @@ def test_fp8_block_moe_prefill_full_layer(gpu):
     err = np.abs(yh[toks] - ref).max() / np.abs(ref).max()
     print(f"[fp8 full layer] {len(need)} experts checked, rel err {err:.3e}", flush=True)
     assert err <= TOL
+    assert err <= REGRESS_C4
 
 
 @pytest.mark.parametrize("T", [512, 4096])
@@ -148,3 +155,4 @@ def test_int4_moe_prefill_full_layer(gpu, T):
     print(f"[int4 full layer] T={T}: experts used {int((counts > 0).sum())}, rows per expert "
           f"{int(counts.min())}..{int(counts.max())}, rel err {err:.3e}", flush=True)
     assert err <= TOL
+    assert err <= REGRESS_C5

@@ -14,6 +14,9 @@ from oracle import moe as omoe
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-2
+# regression bound of the decode configuration: about 3x the error measured
+# on MI355X, below the contract
+REGRESS_C3 = 8e-3
 
 
 def _experts(E, H, I, G, seed):
@@ -68,7 +71,10 @@ def test_moe_w4_group64_f16(gpu):
 def test_moe_w4_decode_config(gpu, T):
     """64 experts, top-6, hidden 2048, expert intermediate 1408, group 128,
     bf16 activations and output."""
-    assert _run(gpu, E=64, H=2048, I=1408, G=128, T=T, k=6, seed=100 + T, ydt=torch.bfloat16) <= TOL
+    err = _run(gpu, E=64, H=2048, I=1408, G=128, T=T, k=6, seed=100 + T, ydt=torch.bfloat16)
+    print(f"[C3] moe decode T={T}: rel err {err:.3e}")
+    assert err <= TOL
+    assert err <= REGRESS_C3  # measured 2.7e-3 (T=1), 2.4e-3 (T=16): bf16 intermediate and output
 
 
 @pytest.mark.parametrize("T,k,E", [(64, 2, 8), (200, 2, 8), (96, 4, 6)])
