@@ -373,21 +373,24 @@ struct WqMoeP {
   int row_div;                // activation row of assignment a = a / row_div
 };
 
-template <bool DUAL, int MT, int PD, int KH>
+template <bool DUAL, int MT, int PD, int KH, int CW>
 __global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
-  constexpr int CG = 8 / KH;                // 16-column groups per workgroup
+  constexpr int CG = 8 / KH;                // 16-column groups of waves per workgroup
   constexpr int KC = 128 * KH;              // k per chunk
   constexpr int RS = KC + 8;                // LDS row stride in bf16
   constexpr int TM = 16 * MT;               // rows per tile
   constexpr int NW = DUAL ? 2 : 1;          // weight matrices
+  constexpr int NM = NW * CW;               // (matrix, column group) fragments per wave
+  constexpr int COLS = 16 * CG * CW;        // columns per workgroup
   constexpr int C4 = KC / 4;                // float4 pieces per activation row and chunk
   constexpr int XR = TM * C4 / WQ_THREADS;  // activation pieces per thread and chunk
-  constexpr int LPC = 2 * NW + XR;          // loads per lane and chunk
+  constexpr int LPC = 2 * NM + XR;          // loads per lane and chunk
   static_assert(KH == 2 || KH == 4, "k parts");
+  static_assert(CW == 1 || CW == 2, "column groups per wave");
   static_assert(XR >= 1 && TM * C4 == XR * WQ_THREADS, "activation pieces");
   static_assert(C4 % 64 == 0, "a wave's pieces lie in one row");
   static_assert((PD - 1) * LPC < 64, "loads in flight fit vmcnt");
-  static_assert(NW * CG * (KH - 1) * MT * 64 * 16 <= 2 * 2 * TM * RS * 2, "partial sums fit the activation LDS");
+  static_assert(NM * CG * (KH - 1) * MT * 64 * 16 <= 2 * 2 * TM * RS * 2, "partial sums fit the activation LDS");
   __shared__ __align__(16) uint16_t X[2][2][TM][RS];  // [buffer][hi, lo][row][k]
 
   const int tile = blockIdx.y;
@@ -398,12 +401,20 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
   const int c16 = lane & 15, q = lane >> 4;
   const int64_t N = p.N, K = p.K;
   const int e = p.tile_expert[tile];
-  const int64_t n = (int64_t)blockIdx.x * (16 * CG) + 16 * cg + c16;
+  // column group c of the wave: column (block * COLS) + c * 16 * CG + 16 * cg + c16
+  int64_t ncol[CW];
+#pragma unroll
+  for (int c = 0; c < CW; ++c) ncol[c] = (int64_t)blockIdx.x * COLS + c * 16 * CG + 16 * cg + c16;
   const int nch = (int)(K / KC);
-  const int64_t woff = (int64_t)e * N * K + imin64(n, N - 1) * K;  // columns past N read row N-1, never stored
-  const uint8_t* wrow0 = p.w0 + woff;
-  const uint8_t* wrow1 = DUAL ? p.w1 + woff : p.w0 + woff;
   const int lane_k = kh * 128 + q * 32;  // first k of the lane's 32 in a chunk
+  // fragment m = w * CW + c: matrix w (gate / up, or down), column group c;
+  // columns past N read row N-1, never stored
+  const uint8_t* wrow[NM];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int c = 0; c < CW; ++c)
+      wrow[w * CW + c] = (w == 0 ? p.w0 : p.w1) + (int64_t)e * N * K + imin64(ncol[c], N - 1) * K + lane_k;
   const int32_t* trow = p.rows + (int64_t)tile * TM;
 
   // activation piece j of a thread: row (64 wave + 512 j) / C4 of the tile
@@ -423,18 +434,14 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
     xp[j] = p.x + (int64_t)(a >= 0 ? a / p.row_div : 0) * K + 4 * ((64 * wave + lane + WQ_THREADS * j) % C4);
   }
 
-  u32x4 wr0[PD][2];
-  u32x4 wr1[PD][2];
+  u32x4 wr[PD][NM][2];
   u32x4 xr[PD][XR];
   auto issue = [&](int s, int c) {
     const int64_t kb = (int64_t)c * KC;
-    const uint8_t* wp = wrow0 + kb + lane_k;
-    gload16_nt<0>(wr0[s][0], wp);
-    gload16_nt<16>(wr0[s][1], wp);
-    if constexpr (DUAL) {
-      const uint8_t* up = wrow1 + kb + lane_k;
-      gload16_nt<0>(wr1[s][0], up);
-      gload16_nt<16>(wr1[s][1], up);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      gload16_nt<0>(wr[s][m][0], wrow[m] + kb);
+      gload16_nt<16>(wr[s][m][1], wrow[m] + kb);
     }
 #pragma unroll
     for (int j = 0; j < XR; ++j)
@@ -442,14 +449,13 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
   };
   auto wait_slot = [&](int s, bool steady) {
     if (steady)
-      wq_wait_nx<PD, 2 * NW, XR>(nx);
+      wq_wait_nx<PD, 2 * NM, XR>(nx);
     else
       wq_wait<0>();
-    wq_tie(wr0[s][0]);
-    wq_tie(wr0[s][1]);
-    if constexpr (DUAL) {
-      wq_tie(wr1[s][0]);
-      wq_tie(wr1[s][1]);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      wq_tie(wr[s][m][0]);
+      wq_tie(wr[s][m][1]);
     }
 #pragma unroll
     for (int j = 0; j < XR; ++j) wq_tie(xr[s][j]);
@@ -468,9 +474,11 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
     }
   };
 
-  f32x4 acc0[MT], acc1[MT];
+  f32x4 acc[NM][MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc0[t] = acc1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int s = 0; s < PD; ++s)
@@ -487,18 +495,17 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
         lds_barrier();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bf16x8 b0 = wq_decode<WQ_FP8_ROW>(wr0[s], i, 1.f);
-          bf16x8 b1 = b0;
-          if constexpr (DUAL) b1 = wq_decode<WQ_FP8_ROW>(wr1[s], i, 1.f);
+          bf16x8 b[NM];
+#pragma unroll
+          for (int m = 0; m < NM; ++m) b[m] = wq_decode<WQ_FP8_ROW>(wr[s][m], i, 1.f);
 #pragma unroll
           for (int t = 0; t < MT; ++t) {
             const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&X[buf][0][16 * t + c16][lane_k + 8 * i]);
             const bf16x8 al = *reinterpret_cast<const bf16x8*>(&X[buf][1][16 * t + c16][lane_k + 8 * i]);
-            acc0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b0, acc0[t], 0, 0, 0);
-            acc0[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b0, acc0[t], 0, 0, 0);
-            if constexpr (DUAL) {
-              acc1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b1, acc1[t], 0, 0, 0);
-              acc1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b1, acc1[t], 0, 0, 0);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+              acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[m], acc[m][t], 0, 0, 0);
+              acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[m], acc[m][t], 0, 0, 0);
             }
           }
         }
@@ -511,64 +518,78 @@ __global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
   // is past its last chunk); part 0 adds them in order and finishes
   __syncthreads();
   f32x4* red = reinterpret_cast<f32x4*>(&X[0][0][0][0]);
-  auto red_at = [&](int w, int part, int t) -> f32x4& {
-    return red[(((w * CG + cg) * (KH - 1) + part) * MT + t) * 64 + lane];
+  auto red_at = [&](int m, int part, int t) -> f32x4& {
+    return red[(((m * CG + cg) * (KH - 1) + part) * MT + t) * 64 + lane];
   };
   if (kh > 0) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      red_at(0, kh - 1, t) = acc0[t];
-      if constexpr (DUAL) red_at(1, kh - 1, t) = acc1[t];
-    }
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) red_at(m, kh - 1, t) = acc[m][t];
   }
   __syncthreads();
-  if (kh != 0 || n >= N) return;
+  if (kh != 0) return;
 #pragma unroll
   for (int part = 0; part < KH - 1; ++part)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      acc0[t] += red_at(0, part, t);
-      if constexpr (DUAL) acc1[t] += red_at(1, part, t);
-    }
-  const float sc0 = p.s0[(int64_t)e * N + n];
-  const float sc1 = DUAL ? p.s1[(int64_t)e * N + n] : 0.f;
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+      for (int t = 0; t < MT; ++t) acc[m][t] += red_at(m, part, t);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int a = trow[16 * t + 4 * q + i];
-      if (a < 0) continue;
-      float v;
-      if constexpr (DUAL) {
-        const double g = (double)(acc0[t][i] * sc0), u = (double)(acc1[t][i] * sc1);
-        v = (float)(g / (1.0 + exp(-g)) * u);
-      } else {
-        v = acc0[t][i] * sc0;
+  for (int c = 0; c < CW; ++c) {
+    const int64_t n = ncol[c];
+    if (n >= N) continue;
+    const float sc0 = p.s0[(int64_t)e * N + n];
+    const float sc1 = DUAL ? p.s1[(int64_t)e * N + n] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int a = trow[16 * t + 4 * q + i];
+        if (a < 0) continue;
+        float v;
+        if constexpr (DUAL) {
+          const double g = (double)(acc[c][t][i] * sc0), u = (double)(acc[CW + c][t][i] * sc1);
+          v = (float)(g / (1.0 + exp(-g)) * u);
+        } else {
+          v = acc[c][t][i] * sc0;
+        }
+        p.y[(int64_t)a * N + n] = v;
       }
-      p.y[(int64_t)a * N + n] = v;
-    }
+  }
 }
 
-// Ring depth per row-tile count (two weight matrices in the gate/up stage).
-template <bool DUAL, int MT>
+// Ring depth per row-tile count and fragments per wave.
+template <bool DUAL, int MT, int CW>
 constexpr int wq_moe_depth() {
-  return DUAL ? (MT == 1 ? 4 : (MT == 2 ? 3 : 2)) : (MT == 1 ? 6 : (MT == 2 ? 4 : 3));
+  return (DUAL ? 2 : 1) * CW == 1 ? (MT == 1 ? 6 : (MT == 2 ? 4 : 3))
+         : (DUAL ? 2 : 1) * CW == 2 ? (MT == 1 ? 4 : (MT == 2 ? 3 : 2))
+                                    : (MT <= 2 ? 3 : 2);
 }
 
+// cw = 2 (128-column workgroups: each staged activation chunk feeds twice
+// the weights) for tiles of 32+ rows, except the gate/up stage's 64-row
+// tiles (its registers would spill); 16-row tiles keep narrow workgroups
+// (more of them for the few experts of a decode batch)
 template <bool DUAL>
 static int wq_moe_launch(const WqMoeP& p, int mt, int kh, int64_t max_tiles, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(p.N, 16 * (8 / kh)), (unsigned)max_tiles);
+  const int cw = (mt == 2 || (!DUAL && mt == 4)) ? 2 : 1;
+  const dim3 grid((unsigned)cdiv(p.N, 16 * (8 / kh) * cw), (unsigned)max_tiles);
+#define CCQ_WQM(MT_, KH_, CW_) \
+  launch((wq_moe_kernel<DUAL, MT_, wq_moe_depth<DUAL, MT_, CW_>(), KH_, CW_>), grid, dim3(WQ_THREADS), 0, st, p)
   if (mt == 1 && kh == 4)
-    launch((wq_moe_kernel<DUAL, 1, wq_moe_depth<DUAL, 1>(), 4>), grid, dim3(WQ_THREADS), 0, st, p);
+    CCQ_WQM(1, 4, 1);
   else if (mt == 1)
-    launch((wq_moe_kernel<DUAL, 1, wq_moe_depth<DUAL, 1>(), 2>), grid, dim3(WQ_THREADS), 0, st, p);
+    CCQ_WQM(1, 2, 1);
   else if (mt == 2)
-    launch((wq_moe_kernel<DUAL, 2, wq_moe_depth<DUAL, 2>(), 2>), grid, dim3(WQ_THREADS), 0, st, p);
+    CCQ_WQM(2, 2, 2);
+  else if constexpr (DUAL)
+    CCQ_WQM(4, 2, 1);
   else
-    launch((wq_moe_kernel<DUAL, 4, wq_moe_depth<DUAL, 4>(), 2>), grid, dim3(WQ_THREADS), 0, st, p);
+    CCQ_WQM(4, 2, 2);
+#undef CCQ_WQM
   return launch_status(DUAL ? "moe_fp8row gate_up" : "moe_fp8row down");
 }
-
 
 // ------------------------------------------------------------ MoE host --
 namespace {
