@@ -373,8 +373,9 @@ struct WqMoeP {
   int row_div;                // activation row of assignment a = a / row_div
 };
 
-template <bool DUAL, int MT, int PD, int KH, int CW>
-__global__ __launch_bounds__(WQ_THREADS) void wq_moe_kernel(const WqMoeP p) {
+// WPE: waves per SIMD the registers must allow (4: two workgroups per CU)
+template <bool DUAL, int MT, int PD, int KH, int CW, int WPE = 1>
+__global__ __launch_bounds__(WQ_THREADS, WPE) void wq_moe_kernel(const WqMoeP p) {
   constexpr int CG = 8 / KH;                // 16-column groups of waves per workgroup
   constexpr int KC = 128 * KH;              // k per chunk
   constexpr int RS = KC + 8;                // LDS row stride in bf16
@@ -571,14 +572,34 @@ constexpr int wq_moe_depth() {
 // the weights) for tiles of 32+ rows, except the gate/up stage's 64-row
 // tiles (its registers would spill); 16-row tiles keep narrow workgroups
 // (more of them for the few experts of a decode batch)
+// A stage whose K is at most two chunks (the down stage, K = inter = 512)
+// runs with a 2-deep ring and registers for two workgroups per CU: each
+// workgroup's life is about one load latency, so the CU needs two of them.
 template <bool DUAL>
 static int wq_moe_launch(const WqMoeP& p, int mt, int kh, int64_t max_tiles, hipStream_t st) {
   const int cw = (mt == 2 || (!DUAL && mt == 4)) ? 2 : 1;
   const dim3 grid((unsigned)cdiv(p.N, 16 * (8 / kh) * cw), (unsigned)max_tiles);
 #define CCQ_WQM(MT_, KH_, CW_) \
   launch((wq_moe_kernel<DUAL, MT_, wq_moe_depth<DUAL, MT_, CW_>(), KH_, CW_>), grid, dim3(WQ_THREADS), 0, st, p)
+#define CCQ_WQS(MT_, KH_, CW_) \
+  launch((wq_moe_kernel<false, MT_, 2, KH_, CW_, 4>), grid, dim3(WQ_THREADS), 0, st, p)
+  if constexpr (!DUAL) {
+    if (p.K <= 2 * 128 * kh) {
+      if (mt == 1 && kh == 4)
+        CCQ_WQS(1, 4, 1);
+      else if (mt == 1)
+        CCQ_WQS(1, 2, 1);
+      else if (mt == 2)
+        CCQ_WQS(2, 2, 2);
+      else
+        CCQ_WQS(4, 2, 2);
+      return launch_status("moe_fp8row down");
+    }
+  }
   if (mt == 1 && kh == 4)
     CCQ_WQM(1, 4, 1);
+  else if (mt == 1 && DUAL)  // 16-row gate/up tiles: a 3-deep ring, two workgroups per CU
+    launch((wq_moe_kernel<true, 1, 3, 2, 1, 4>), grid, dim3(WQ_THREADS), 0, st, p);
   else if (mt == 1)
     CCQ_WQM(1, 2, 1);
   else if (mt == 2)
@@ -588,6 +609,7 @@ static int wq_moe_launch(const WqMoeP& p, int mt, int kh, int64_t max_tiles, hip
   else
     CCQ_WQM(4, 2, 2);
 #undef CCQ_WQM
+#undef CCQ_WQS
   return launch_status(DUAL ? "moe_fp8row gate_up" : "moe_fp8row down");
 }
 
