@@ -217,3 +217,52 @@ def test_wq_mfma_rejects_bad_args(lib):
     assert f(p, p, p, p, 4, 256, 8, 2, 8, 1.0, None) == CCQ_EINVAL and "group_size" in last_error()
     assert f(ctypes.c_void_p(260), p, p, p, 4, 256, 8, 0, 0, 1.0, None) == CCQ_EINVAL and "aligned" in last_error()
     assert f(p, p, None, p, 0, 256, 8, 3, 32, 1.0, None) == 0  # empty batch: nothing to do
+
+
+def test_fp8row_moe_rejects_bad_args(lib):
+    from ccut._lib import CCQ_EINVAL, ccq_fp8row_experts, last_error
+
+    p = ctypes.c_void_p(256)
+    ex = ccq_fp8row_experts(256, 256, 256, 256, 256, 256, 8, 2048, 512)
+    f = lib.ccq_moe_fp8row_ffn
+    assert f(p, p, p, p, 0, 4, 2, None, p, 1 << 20, None) == CCQ_EINVAL and "null experts" in last_error()
+    bad = ccq_fp8row_experts(256, 256, 256, 256, 256, 256, 8, 2000, 512)
+    assert f(p, p, p, p, 0, 4, 2, ctypes.byref(bad), p, 1 << 20, None) == CCQ_EINVAL and "multiples of 256" in last_error()
+    unaligned = ccq_fp8row_experts(264, 256, 256, 256, 256, 256, 8, 2048, 512)
+    assert f(p, p, p, p, 0, 4, 2, ctypes.byref(unaligned), p, 1 << 20, None) == CCQ_EINVAL and "aligned" in last_error()
+    assert f(p, p, p, p, 0, 4, 9, ctypes.byref(ex), p, 1 << 20, None) == CCQ_EINVAL  # k > E
+    assert f(p, p, p, p, 0, 30000, 8, ctypes.byref(ex), p, 1 << 20, None) == CCQ_EINVAL and "65536" in last_error()
+    assert f(p, p, p, p, 7, 4, 2, ctypes.byref(ex), p, 1 << 20, None) == CCQ_EINVAL and "y_dtype" in last_error()
+    assert f(ctypes.c_void_p(260), p, p, p, 0, 4, 2, ctypes.byref(ex), p, 1 << 20, None) == CCQ_EINVAL
+    assert f(p, p, p, p, 0, 4, 2, ctypes.byref(ex), p, 64, None) == CCQ_EINVAL and "workspace" in last_error()
+    assert f(p, p, p, p, 0, 0, 2, ctypes.byref(ex), None, 0, None) == 0  # no tokens: nothing to do
+    assert lib.ccq_moe_fp8row_workspace_size(16, 8, ctypes.byref(ex)) > 16 * 8 * (2048 + 512) * 4
+    assert lib.ccq_moe_fp8row_workspace_size(16, 8, ctypes.byref(bad)) == 0
+    assert lib.ccq_moe_fp8row_ffn_shared(p, p, p, None, 1.0, p, 0, 4, 2, ctypes.byref(ex), p, 1 << 20,
+                                         None) == CCQ_EINVAL and "shared" in last_error()
+
+
+def test_f32_gemm_rejects_bad_args(lib):
+    from ccut._lib import CCQ_EINVAL, last_error
+
+    p = ctypes.c_void_p(256)
+    assert lib.ccq_f32_gemm(p, p, p, 4, 64, 8, 2, None, 0, None) == CCQ_EINVAL and "trans_w" in last_error()
+    assert lib.ccq_f32_gemm(p, p, p, -1, 64, 8, 0, None, 0, None) == CCQ_EINVAL and "negative" in last_error()
+    assert lib.ccq_f32_gemm(p, None, p, 4, 64, 8, 0, None, 0, None) == CCQ_EINVAL and "null" in last_error()
+    assert lib.ccq_f32_gemm(p, p, p, 0, 64, 8, 1, None, 0, None) == 0  # no rows
+    assert lib.ccq_f32_gemm_workspace_size(4, 64, 8) == 0  # too shallow to split
+    assert lib.ccq_expert_ffn_f32(p, p, p, p, p, 4, 64, 32, p, 16, None) == CCQ_EINVAL and "workspace" in last_error()
+    assert lib.ccq_expert_ffn_f32(p, p, p, p, p, 4, 0, 32, p, 1 << 20, None) == CCQ_EINVAL
+    assert lib.ccq_expert_ffn_f32_workspace_size(4, 32) == 4 * 32 * 4
+    f = lib.ccq_moe_f32_ffn
+    assert f(p, p, p, p, p, p, None, 0.0, p, 0, 4, 2, 2000, 64, 32, p, 1 << 20, None) == CCQ_EINVAL  # E > 1024
+    assert f(p, p, p, None, p, p, None, 0.0, p, 0, 4, 2, 8, 64, 32, p, 1 << 20, None) == CCQ_EINVAL and "null" in last_error()
+    assert f(p, p, p, p, p, p, None, 0.0, p, 0, 4, 2, 8, 64, 32, p, 64, None) == CCQ_EINVAL and "workspace" in last_error()
+    assert lib.ccq_moe_f32_workspace_size(4, 2, 8, 64, 32) > 0
+
+
+def test_launch_timer_arguments(lib):
+    from ccut._lib import CCQ_EINVAL, last_error
+
+    assert lib.ccq_launch_timer(ctypes.c_void_p(256), None) == CCQ_EINVAL and "both" in last_error()
+    assert lib.ccq_launch_timer(None, None) == 0  # clears
