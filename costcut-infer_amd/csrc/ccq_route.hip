@@ -519,12 +519,99 @@ __global__ __launch_bounds__(256) void align_chunk_scatter_kernel(const int64_t*
   }
 }
 
+// The same schedule for small batches (decode: n <= 256 assignments) in one
+// wave, with no barrier: lane l holds assignments l, 64 + l, 128 + l,
+// 192 + l; ballots over the expert id bits match each assignment with the
+// lanes of every chunk holding the same expert, which gives its rank among
+// them (assignment order), its expert's count and whether it is the
+// expert's first appearance; an exclusive scan over the first appearances,
+// in assignment order, gives the padded bases.  Experts' bases and counts
+// go through LDS (the lanes of an expert read its first lane's values).
+constexpr int kSmallN = 256;
+constexpr int kSmallChunks = kSmallN / 64;
+
+__global__ __launch_bounds__(64) void moe_align_small_kernel(const int64_t* __restrict__ ids, int n, int E,
+                                                             int tile_m, int32_t* __restrict__ sorted_ids,
+                                                             int32_t* __restrict__ tile_expert,
+                                                             int32_t* __restrict__ meta,
+                                                             int32_t* __restrict__ counts_out) {
+  __shared__ int sbase[kMaxE];
+  __shared__ int scnt[kMaxE];
+  const int lane = threadIdx.x;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int e = lane; e < E; e += 64) scnt[e] = 0;
+  int key[kSmallChunks], rank[kSmallChunks], cnt[kSmallChunks];
+  uint64_t vm[kSmallChunks];
+#pragma unroll
+  for (int c = 0; c < kSmallChunks; ++c) {
+    const int a = 64 * c + lane;
+    const int64_t v = a < n ? ids[a] : -1;
+    key[c] = (v >= 0 && v < E) ? (int)v : -1;
+    vm[c] = __ballot(key[c] >= 0);
+    rank[c] = 0;
+    cnt[c] = 0;
+  }
+  const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int d = 0; d < kSmallChunks; ++d) {
+    uint64_t bd[10];
+#pragma unroll
+    for (int b = 0; b < 10; ++b) bd[b] = b < nbits ? __ballot(key[d] >= 0 && ((key[d] >> b) & 1)) : 0ull;
+#pragma unroll
+    for (int c = 0; c < kSmallChunks; ++c) {
+      uint64_t m = key[c] >= 0 ? vm[d] : 0ull;
+#pragma unroll
+      for (int b = 0; b < 10; ++b)
+        if (b < nbits) m &= ((key[c] >> b) & 1) ? bd[b] : ~bd[b];
+      cnt[c] += (int)__popcll(m);
+      if (d < c) rank[c] += (int)__popcll(m);
+      if (d == c) rank[c] += (int)__popcll(m & lt);
+    }
+  }
+  // first appearances in assignment order: the experts' order and padded bases
+  int carry = 0, nact = 0;
+#pragma unroll
+  for (int c = 0; c < kSmallChunks; ++c) {
+    const bool first = key[c] >= 0 && rank[c] == 0;
+    const int pd = first ? (int)cdiv(cnt[c], tile_m) * tile_m : 0;
+    int incl = pd;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (first) {
+      const int bs = carry + incl - pd;
+      sbase[key[c]] = bs;
+      scnt[key[c]] = cnt[c];
+      for (int j = cnt[c]; j < pd; ++j) sorted_ids[bs + j] = -1;
+      for (int t = bs / tile_m; t < (bs + pd) / tile_m; ++t) tile_expert[t] = key[c];
+    }
+    carry += __shfl(incl, 63, 64);
+    nact += (int)__popcll(__ballot(first));
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the bases and counts above, before any lane reads them
+#pragma unroll
+  for (int c = 0; c < kSmallChunks; ++c)
+    if (key[c] >= 0) sorted_ids[sbase[key[c]] + rank[c]] = 64 * c + lane;
+  for (int e = lane; e < E; e += 64) counts_out[e] = scnt[e];
+  if (lane == 0) {
+    meta[0] = carry / tile_m;
+    meta[1] = nact;
+  }
+}
+
 size_t align_scratch_bytes(int64_t n, int64_t E) { return (size_t)2 * cdiv(n, kChunk) * E * 4; }
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
                  int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
                  size_t scratch_bytes) {
   const int64_t nchunks = cdiv(n, kChunk);
+  if (n <= kSmallN && E <= kMaxE) {  // decode batches: one wave
+    launch(moe_align_small_kernel, dim3(1), dim3(64), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
+           tile_expert, meta, counts);
+    return launch_status("moe_align (small)");
+  }
   // below ~6K assignments one workgroup is faster than three launches
   if (scratch == nullptr || n <= 6 * kChunk || scratch_bytes < align_scratch_bytes(n, E)) {
     launch(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,

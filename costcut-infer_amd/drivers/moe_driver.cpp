@@ -12,6 +12,13 @@
 //   moe_driver gemm M K N reps copies
 //                           AWQ g128 linear y [M, N] = x [M, K] @ W,
 //                           ccq_w4_gemm over `copies` rotating weight sets
+//   moe_driver f8r T reps   MoE layer on per-row FP8 experts (the reference
+//                           checkpoint's format): 256 experts top-8, hidden
+//                           2048, inter 512, float32 activations,
+//                           ccq_moe_fp8row_ffn (prints the distinct experts)
+//   moe_driver f32 M K N reps
+//                           float32 y [M, N] = x [M, K] @ w^T, w [N, K]
+//                           (the router), ccq_f32_gemm with its workspace
 //   moe_driver wq fmt M K N reps copies
 //                           decoded-weight MFMA linear (float32 x and y),
 //                           ccq_wq_mfma_linear_f32: fmt 0 FP8 row scale,
@@ -96,7 +103,73 @@ static int run_wq(int argc, char** argv) {
   return 0;
 }
 
+static int run_f8r(int argc, char** argv) {
+  const int64_t T = argc > 2 ? atoll(argv[2]) : 16;
+  const int reps = argc > 3 ? atoi(argv[3]) : 12;
+  const int64_t E = 256, H = 2048, I = 512, k = 8;
+  std::mt19937 g(91);
+  std::vector<int64_t> ids(T * k);
+  std::vector<float> wts(T * k, 1.0f / k);
+  std::vector<int> used(E, 0);
+  for (int64_t t = 0; t < T; ++t) {  // k distinct experts per token
+    std::vector<int> perm(E);
+    for (int e = 0; e < E; ++e) perm[e] = e;
+    std::shuffle(perm.begin(), perm.end(), g);
+    for (int j = 0; j < k; ++j) { ids[t * k + j] = perm[j]; used[perm[j]] = 1; }
+  }
+  int u = 0;
+  for (int x : used) u += x;
+  printf("f8r T=%lld: %d distinct experts routed\n", (long long)T, u);
+  int64_t* d_ids = (int64_t*)dalloc(T * k * 8);
+  float* d_w = (float*)dalloc(T * k * 4);
+  CK(hipMemcpy(d_ids, ids.data(), T * k * 8, hipMemcpyHostToDevice));
+  CK(hipMemcpy(d_w, wts.data(), T * k * 4, hipMemcpyHostToDevice));
+  ccq_fp8row_experts ex = {};
+  void* wg = dalloc(E * I * H); fill_rand_u32(wg, E * I * H / 4, 1, 0xB7B7B7B7u, 0x20202020u);  // finite e4m3
+  void* wu = dalloc(E * I * H); fill_rand_u32(wu, E * I * H / 4, 2, 0xB7B7B7B7u, 0x20202020u);
+  void* wd = dalloc(E * H * I); fill_rand_u32(wd, E * H * I / 4, 3, 0xB7B7B7B7u, 0x20202020u);
+  void* sg = dalloc(E * I * 4); fill_rand_u32(sg, E * I, 4, 0x007FFFFFu, 0x3C000000u);
+  void* su = dalloc(E * I * 4); fill_rand_u32(su, E * I, 5, 0x007FFFFFu, 0x3C000000u);
+  void* sd = dalloc(E * H * 4); fill_rand_u32(sd, E * H, 6, 0x007FFFFFu, 0x3C000000u);
+  ex.w_gate = (const uint8_t*)wg; ex.s_gate = (const float*)sg;
+  ex.w_up = (const uint8_t*)wu; ex.s_up = (const float*)su;
+  ex.w_down = (const uint8_t*)wd; ex.s_down = (const float*)sd;
+  ex.num_experts = E; ex.hidden = H; ex.inter = I;
+  void* x = dalloc(T * H * 4);
+  fill_rand_u32(x, T * H, 7, 0x807FFFFFu, 0x3F000000u);  // floats of magnitude [0.5, 1)
+  void* y = dalloc(T * H * 4);
+  const size_t wsb = ccq_moe_fp8row_workspace_size(T, k, &ex);
+  void* ws = dalloc(wsb);
+  for (int r = 0; r < reps; ++r) {
+    const int rc = ccq_moe_fp8row_ffn((const float*)x, d_ids, d_w, y, CCQ_F32, T, k, &ex, ws, wsb, nullptr);
+    if (rc) { printf("rc=%d %s\n", rc, ccq_last_error()); return 4; }
+  }
+  CK(hipDeviceSynchronize());
+  printf("f8r T=%lld workspace %zu bytes, reps %d done\n", (long long)T, wsb, reps);
+  return 0;
+}
+
+static int run_f32(int argc, char** argv) {
+  const int64_t M = argc > 2 ? atoll(argv[2]) : 16, K = argc > 3 ? atoll(argv[3]) : 2048,
+                N = argc > 4 ? atoll(argv[4]) : 64;
+  const int reps = argc > 5 ? atoi(argv[5]) : 20;
+  void* x = dalloc(M * K * 4); fill_rand_u32(x, M * K, 7, 0x807FFFFFu, 0x3F000000u);
+  void* w = dalloc(N * K * 4); fill_rand_u32(w, N * K, 8, 0x807FFFFFu, 0x3C000000u);
+  void* y = dalloc(M * N * 4);
+  const size_t wsb = ccq_f32_gemm_workspace_size(M, K, N);
+  void* ws = wsb ? dalloc(wsb) : nullptr;
+  for (int r = 0; r < reps; ++r) {
+    const int rc = ccq_f32_gemm((const float*)x, (const float*)w, (float*)y, M, K, N, 1, ws, wsb, nullptr);
+    if (rc) { printf("rc=%d %s\n", rc, ccq_last_error()); return 4; }
+  }
+  CK(hipDeviceSynchronize());
+  printf("f32 M=%lld K=%lld N=%lld workspace %zu reps %d done\n", (long long)M, (long long)K, (long long)N, wsb, reps);
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  if (argc > 1 && !strcmp(argv[1], "f8r")) return run_f8r(argc, argv);
+  if (argc > 1 && !strcmp(argv[1], "f32")) return run_f32(argc, argv);
   if (argc > 1 && !strcmp(argv[1], "gemm")) return run_gemm(argc, argv);
   if (argc > 1 && !strcmp(argv[1], "wq")) return run_wq(argc, argv);
   const bool fp8 = argc > 1 && !strcmp(argv[1], "fp8");

@@ -129,7 +129,12 @@ def _align_check(ids: np.ndarray, E: int, tile_m: int):
 
 
 @pytest.mark.parametrize("T,E,k,tile_m", [(1, 64, 6, 16), (16, 64, 6, 16), (100, 256, 8, 64),
-                                          (2048, 256, 8, 128), (513, 128, 8, 32), (7, 8, 8, 1)])
+                                          (2048, 256, 8, 128), (513, 128, 8, 32), (7, 8, 8, 1),
+                                          # one-wave schedule of small batches (<= 256 assignments): the
+                                          # largest batch, 10 id bits, 128-row tiles, one expert; 257 is
+                                          # the first batch of the workgroup kernel
+                                          (32, 256, 8, 16), (20, 1000, 8, 16), (16, 8, 8, 128), (10, 1, 1, 16),
+                                          (257, 16, 1, 16)])
 def test_align_permutation_bitexact(gpu, T, E, k, tile_m):
     rng = np.random.default_rng(T + E)
     lg = rng.standard_normal((T, E)).astype(np.float32)
