@@ -528,23 +528,23 @@ __global__ __launch_bounds__(256) void align_chunk_scatter_kernel(const int64_t*
 // in assignment order, gives the padded bases.  Experts' bases and counts
 // go through LDS (the lanes of an expert read its first lane's values).
 constexpr int kSmallN = 256;
-constexpr int kSmallChunks = kSmallN / 64;
 
+// NCH chunks of 64 assignments (n <= 64 NCH), NB expert id bits (E <= 2^NB):
+// both compile-time, so the ballot matching is straight-line code
+template <int NCH, int NB>
 __global__ __launch_bounds__(64) void moe_align_small_kernel(const int64_t* __restrict__ ids, int n, int E,
                                                              int tile_m, int32_t* __restrict__ sorted_ids,
                                                              int32_t* __restrict__ tile_expert,
                                                              int32_t* __restrict__ meta,
                                                              int32_t* __restrict__ counts_out) {
-  __shared__ int sbase[kMaxE];
-  __shared__ int scnt[kMaxE];
+  __shared__ int sbase[1 << NB];
+  __shared__ int scnt[1 << NB];
   const int lane = threadIdx.x;
-  int nbits = 1;
-  while ((1 << nbits) < E) ++nbits;
   for (int e = lane; e < E; e += 64) scnt[e] = 0;
-  int key[kSmallChunks], rank[kSmallChunks], cnt[kSmallChunks];
-  uint64_t vm[kSmallChunks];
+  int key[NCH], rank[NCH], cnt[NCH];
+  uint64_t vm[NCH];
 #pragma unroll
-  for (int c = 0; c < kSmallChunks; ++c) {
+  for (int c = 0; c < NCH; ++c) {
     const int a = 64 * c + lane;
     const int64_t v = a < n ? ids[a] : -1;
     key[c] = (v >= 0 && v < E) ? (int)v : -1;
@@ -554,16 +554,15 @@ __global__ __launch_bounds__(64) void moe_align_small_kernel(const int64_t* __re
   }
   const uint64_t lt = (1ull << lane) - 1ull;
 #pragma unroll
-  for (int d = 0; d < kSmallChunks; ++d) {
-    uint64_t bd[10];
+  for (int d = 0; d < NCH; ++d) {
+    uint64_t bd[NB];
 #pragma unroll
-    for (int b = 0; b < 10; ++b) bd[b] = b < nbits ? __ballot(key[d] >= 0 && ((key[d] >> b) & 1)) : 0ull;
+    for (int b = 0; b < NB; ++b) bd[b] = __ballot(key[d] >= 0 && ((key[d] >> b) & 1));
 #pragma unroll
-    for (int c = 0; c < kSmallChunks; ++c) {
+    for (int c = 0; c < NCH; ++c) {
       uint64_t m = key[c] >= 0 ? vm[d] : 0ull;
 #pragma unroll
-      for (int b = 0; b < 10; ++b)
-        if (b < nbits) m &= ((key[c] >> b) & 1) ? bd[b] : ~bd[b];
+      for (int b = 0; b < NB; ++b) m &= ((key[c] >> b) & 1) ? bd[b] : ~bd[b];
       cnt[c] += (int)__popcll(m);
       if (d < c) rank[c] += (int)__popcll(m);
       if (d == c) rank[c] += (int)__popcll(m & lt);
@@ -572,10 +571,11 @@ __global__ __launch_bounds__(64) void moe_align_small_kernel(const int64_t* __re
   // first appearances in assignment order: the experts' order and padded bases
   int carry = 0, nact = 0;
 #pragma unroll
-  for (int c = 0; c < kSmallChunks; ++c) {
+  for (int c = 0; c < NCH; ++c) {
     const bool first = key[c] >= 0 && rank[c] == 0;
-    const int pd = first ? (int)cdiv(cnt[c], tile_m) * tile_m : 0;
+    const int pd = first ? (cnt[c] + tile_m - 1) / tile_m * tile_m : 0;
     int incl = pd;
+#pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const int o = __shfl_up(incl, off, 64);
       if (lane >= off) incl += o;
@@ -592,13 +592,39 @@ __global__ __launch_bounds__(64) void moe_align_small_kernel(const int64_t* __re
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the bases and counts above, before any lane reads them
 #pragma unroll
-  for (int c = 0; c < kSmallChunks; ++c)
+  for (int c = 0; c < NCH; ++c)
     if (key[c] >= 0) sorted_ids[sbase[key[c]] + rank[c]] = 64 * c + lane;
   for (int e = lane; e < E; e += 64) counts_out[e] = scnt[e];
   if (lane == 0) {
     meta[0] = carry / tile_m;
     meta[1] = nact;
   }
+}
+
+template <int NCH>
+static void launch_align_small_nb(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
+                                  int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
+#define CCQ_ALS(NB)                                                                                          \
+  launch((moe_align_small_kernel<NCH, NB>), dim3(1), dim3(64), 0, st, ids, n, E, tile_m, sorted_ids, tile_expert, \
+         meta, counts)
+  if (E <= 64)
+    CCQ_ALS(6);
+  else if (E <= 256)
+    CCQ_ALS(8);
+  else
+    CCQ_ALS(10);
+#undef CCQ_ALS
+}
+
+// n <= kSmallN, E <= 1024
+static void launch_align_small(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
+                               int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
+  if (n <= 64)
+    launch_align_small_nb<1>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+  else if (n <= 128)
+    launch_align_small_nb<2>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+  else
+    launch_align_small_nb<4>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
 }
 
 size_t align_scratch_bytes(int64_t n, int64_t E) { return (size_t)2 * cdiv(n, kChunk) * E * 4; }
@@ -608,8 +634,7 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
                  size_t scratch_bytes) {
   const int64_t nchunks = cdiv(n, kChunk);
   if (n <= kSmallN && E <= kMaxE) {  // decode batches: one wave
-    launch(moe_align_small_kernel, dim3(1), dim3(64), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
-           tile_expert, meta, counts);
+    launch_align_small(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st);
     return launch_status("moe_align (small)");
   }
   // below ~6K assignments one workgroup is faster than three launches

@@ -354,7 +354,8 @@ int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale,
 // schedule (ccq_moe_align with tile_m = 16*MT; tiles past meta[0] exit at
 // once).  The 8 waves are CG column groups x KH k parts; a chunk is KH*128 k
 // (KH = 2: the dense kernel's 64 columns x 256 k; KH = 4: 32 columns x 512 k,
-// for schedules too small to fill the chip with 64-column blocks).  The
+// KH = 8: 16 columns x 1024 k, for schedules too small to fill the chip
+// with wider blocks).  The
 // valid rows of a tile are a prefix (an expert's rows are padded at the
 // end), so a wave loads only the activation pieces of valid rows and
 // zeroes the rest when staging; the k parts' partial sums are added in a
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(WQ_THREADS, WPE) void wq_moe_kernel(const WqMoeP p)
   constexpr int C4 = KC / 4;                // float4 pieces per activation row and chunk
   constexpr int XR = TM * C4 / WQ_THREADS;  // activation pieces per thread and chunk
   constexpr int LPC = 2 * NM + XR;          // loads per lane and chunk
-  static_assert(KH == 2 || KH == 4, "k parts");
+  static_assert(KH == 2 || KH == 4 || KH == 8, "k parts");
   static_assert(CW == 1 || CW == 2, "column groups per wave");
   static_assert(XR >= 1 && TM * C4 == XR * WQ_THREADS, "activation pieces");
   static_assert(C4 % 64 == 0, "a wave's pieces lie in one row");
@@ -596,7 +597,9 @@ static int wq_moe_launch(const WqMoeP& p, int mt, int kh, int64_t max_tiles, hip
       return launch_status("moe_fp8row down");
     }
   }
-  if (mt == 1 && kh == 4)
+  if (mt == 1 && kh == 8 && DUAL)  // 16-column blocks, 1024-k chunks: the few experts of a tiny batch
+    launch((wq_moe_kernel<true, 1, 2, 8, 1>), grid, dim3(WQ_THREADS), 0, st, p);
+  else if (mt == 1 && kh == 4)
     CCQ_WQM(1, 4, 1);
   else if (mt == 1 && DUAL)  // 16-row gate/up tiles: a 3-deep ring, two workgroups per CU
     launch((wq_moe_kernel<true, 1, 3, 2, 1, 4>), grid, dim3(WQ_THREADS), 0, st, p);
@@ -647,6 +650,7 @@ F8RowLayout f8row_layout(int64_t T, int64_t k, const ccq_fp8row_experts* ex, boo
   L.max_tiles = ccq_moe_align_max_tiles(L.n, E, tile_m);
   const int64_t cus = with_cus ? device_cus_now() : 256;
   L.kh_gate_up = (L.mt == 1 && H % 512 == 0 && cdiv(I, 64) * routed < 2 * cus) ? 4 : 2;
+  if (L.kh_gate_up == 4 && H % 1024 == 0 && cdiv(I, 32) * routed < 2 * cus) L.kh_gate_up = 8;
   L.kh_down = (L.mt == 1 && I % 512 == 0 && cdiv(H, 64) * routed < 2 * cus) ? 4 : 2;
   size_t o = 0;
   L.off_sorted = o;

@@ -70,10 +70,11 @@ def _experts(lay, gpu):
 
 
 # (E, H, I, T, k): 16-row tiles with 32-column blocks in both stages
-# (H, I multiples of 512), 16-row tiles with 64-column blocks, 32- and
-# 64-row tiles, ragged expert loads
-CASES = [(8, 512, 512, 3, 2), (8, 256, 256, 5, 2), (4, 256, 512, 40, 2), (4, 512, 256, 64, 2),
-         (6, 256, 256, 37, 3)]
+# (H, I multiples of 512), 16-column gate/up blocks over 1024-k chunks
+# (H a multiple of 1024, a tiny batch), 16-row tiles with 64-column blocks,
+# 32- and 64-row tiles, ragged expert loads
+CASES = [(8, 512, 512, 3, 2), (8, 1024, 256, 2, 2), (8, 256, 256, 5, 2), (4, 256, 512, 40, 2),
+         (4, 512, 256, 64, 2), (6, 256, 256, 37, 3)]
 
 
 @pytest.mark.parametrize("E,H,I,T,k", CASES)
