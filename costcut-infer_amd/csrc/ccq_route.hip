@@ -627,6 +627,173 @@ static void launch_align_small(const int64_t* ids, int n, int E, int tile_m, int
     launch_align_small_nb<4>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
 }
 
+// The same schedule for mid-size batches (kSmallN < n <= kMidN) in one
+// workgroup of 16 waves: wave w holds chunks w*CPW .. w*CPW + CPW - 1 of 64
+// assignments (lane l: assignment 64 c + l of its chunks), so wave order,
+// then chunk order, then lane order is assignment order.  Per chunk, ballots
+// over the NB expert id bits give every assignment the lanes with its expert
+// and its rank among them; the chunk's lowest such lane adds the chunk's
+// count to the wave's per-expert count in LDS (its old value, broadcast, is
+// the count of that expert in the wave's earlier chunks) and keeps the
+// expert's first appearance (LDS min).  An exclusive scan over the waves of
+// every expert's counts, the first appearances ranked in assignment order
+// (ballots, per-wave totals), a scan over the ranks of the padded sizes, and
+// each assignment lands at base + earlier waves' count + its rank in the wave.
+// Compile-time NB and CPW keep the matching straight-line code.
+constexpr int kMidN = 8192;
+
+template <int NB, int CPW>
+__global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __restrict__ ids, int n, int E,
+                                                             int tile_m, int32_t* __restrict__ sorted_ids,
+                                                             int32_t* __restrict__ tile_expert,
+                                                             int32_t* __restrict__ meta,
+                                                             int32_t* __restrict__ counts_out) {
+  __shared__ int wcnt[kAlignWaves * (1 << NB)];  // [wave][expert]: counts, then exclusive offsets
+  __shared__ int cnt[1 << NB], first[1 << NB], base[1 << NB], inv[1 << NB];
+  __shared__ int wtot[kAlignWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int key[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int a = (w * CPW + c) * 64 + lane;
+    const int64_t v = a < n ? ids[a] : -1;
+    key[c] = (v >= 0 && v < E) ? (int)v : -1;
+  }
+  for (int i = tid; i < kAlignWaves * E; i += 1024) wcnt[(i / E) * (1 << NB) + i % E] = 0;
+  for (int e = tid; e < E; e += 1024) first[e] = 0x7fffffff;
+  __syncthreads();
+
+  // pass A: rank of each assignment among the wave's assignments of its expert
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int pos[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int e = key[c];
+    const bool valid = e >= 0;
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const uint64_t bb = __ballot(valid && ((e >> b) & 1));
+      m &= ((e >> b) & 1) ? bb : ~bb;
+    }
+    m = valid ? m : 0ull;
+    const int r = (int)__popcll(m & lt);
+    int old = 0;
+    if (valid && r == 0) {
+      old = atomicAdd(&wcnt[w * (1 << NB) + e], (int)__popcll(m));
+      atomicMin(&first[e], (w * CPW + c) * 64 + lane);
+    }
+    old = __shfl(old, valid ? (int)__builtin_ctzll(m) : lane, 64);
+    pos[c] = old + r;
+  }
+  __syncthreads();
+
+  // per-expert exclusive offsets over the waves; first appearances per wave
+  for (int e = tid; e < E; e += 1024) {
+    int run = 0;
+#pragma unroll
+    for (int i = 0; i < kAlignWaves; ++i) {
+      const int c = wcnt[i * (1 << NB) + e];
+      wcnt[i * (1 << NB) + e] = run;
+      run += c;
+    }
+    cnt[e] = run;
+    counts_out[e] = run;
+  }
+  uint64_t fl[CPW];
+  int nfl = 0;
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int a = (w * CPW + c) * 64 + lane;
+    fl[c] = __ballot(key[c] >= 0 && first[key[c]] == a);
+    nfl += (int)__popcll(fl[c]);
+  }
+  if (lane == 0) wtot[w] = nfl;
+  __syncthreads();
+
+  // experts in first-appearance order
+  int before = 0, nactive = 0;
+#pragma unroll
+  for (int i = 0; i < kAlignWaves; ++i) {
+    const int t = wtot[i];
+    before += i < w ? t : 0;
+    nactive += t;
+  }
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    if ((fl[c] >> lane) & 1) inv[before + (int)__popcll(fl[c] & lt)] = key[c];
+    before += (int)__popcll(fl[c]);
+  }
+  __syncthreads();
+
+  // padded bases in rank order: wave w scans ranks 64 w .. 64 w + 63
+  const int rk = 64 * w + lane;
+  const int pd = rk < nactive ? (cnt[inv[rk]] + tile_m - 1) / tile_m * tile_m : 0;
+  int incl = pd;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wtot[w] = incl;  // every wave read the flag totals before the last barrier
+  __syncthreads();
+  int boff = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < kAlignWaves; ++i) {
+    const int t = wtot[i];
+    boff += i < w ? t : 0;
+    total += t;
+  }
+  if (rk < nactive) base[inv[rk]] = boff + incl - pd;
+  if (tid == 0) {
+    meta[0] = total / tile_m;
+    meta[1] = nactive;
+  }
+  __syncthreads();
+
+  // positions, then each expert's padding and tiles (a wave per expert)
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int e = key[c];
+    if (e >= 0) sorted_ids[base[e] + wcnt[w * (1 << NB) + e] + pos[c]] = (w * CPW + c) * 64 + lane;
+  }
+  for (int i = w; i < nactive; i += kAlignWaves) {
+    const int e = inv[i];
+    const int b = base[e], c = cnt[e];
+    const int p = (c + tile_m - 1) / tile_m * tile_m;
+    for (int j = c + lane; j < p; j += 64) sorted_ids[b + j] = -1;
+    for (int t = b / tile_m + lane; t < (b + p) / tile_m; t += 64) tile_expert[t] = e;
+  }
+}
+
+template <int CPW>
+static void launch_align_mid_nb(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
+                                int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
+#define CCQ_ALM(NB)                                                                                          \
+  launch((moe_align_mid_kernel<NB, CPW>), dim3(1), dim3(1024), 0, st, ids, n, E, tile_m, sorted_ids,        \
+         tile_expert, meta, counts)
+  if (E <= 64)
+    CCQ_ALM(6);
+  else if (E <= 256)
+    CCQ_ALM(8);
+  else
+    CCQ_ALM(10);
+#undef CCQ_ALM
+}
+
+// kSmallN < n <= kMidN, E <= 1024
+static void launch_align_mid(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
+                             int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
+  if (n <= 1024)
+    launch_align_mid_nb<1>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+  else if (n <= 2048)
+    launch_align_mid_nb<2>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+  else if (n <= 4096)
+    launch_align_mid_nb<4>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+  else
+    launch_align_mid_nb<8>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+}
+
 size_t align_scratch_bytes(int64_t n, int64_t E) { return (size_t)2 * cdiv(n, kChunk) * E * 4; }
 
 int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
@@ -637,8 +804,13 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
     launch_align_small(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st);
     return launch_status("moe_align (small)");
   }
-  // below ~6K assignments one workgroup is faster than three launches
-  if (scratch == nullptr || n <= 6 * kChunk || scratch_bytes < align_scratch_bytes(n, E)) {
+  if (n <= kMidN && E <= kMaxE) {  // one workgroup, straight-line matching
+    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st);
+    return launch_status("moe_align (mid)");
+  }
+  // larger batches: three launches over many workgroups when there is
+  // scratch for the per-chunk counts, else the generic one-workgroup kernel
+  if (scratch == nullptr || scratch_bytes < align_scratch_bytes(n, E)) {
     launch(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, (int)n, (int)E, (int)tile_m, sorted_ids,
                        tile_expert, meta, counts);
     return launch_status("moe_align");

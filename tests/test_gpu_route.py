@@ -134,12 +134,36 @@ def _align_check(ids: np.ndarray, E: int, tile_m: int):
                                           # largest batch, 10 id bits, 128-row tiles, one expert; 257 is
                                           # the first batch of the workgroup kernel
                                           (32, 256, 8, 16), (20, 1000, 8, 16), (16, 8, 8, 128), (10, 1, 1, 16),
-                                          (257, 16, 1, 16)])
+                                          (257, 16, 1, 16),
+                                          # one-workgroup schedule of mid-size batches (257 .. 8192
+                                          # assignments, 1 .. 8 chunks per wave): 1024 experts, 8 experts
+                                          # (many repeats per chunk), the largest batch, 7-row tiles
+                                          (512, 256, 8, 16), (200, 1024, 10, 128), (1024, 8, 8, 64),
+                                          (300, 1000, 3, 7), (129, 64, 8, 128), (1025, 64, 8, 128)])
 def test_align_permutation_bitexact(gpu, T, E, k, tile_m):
     rng = np.random.default_rng(T + E)
     lg = rng.standard_normal((T, E)).astype(np.float32)
     _, ids = omoe.topk_softmax(lg, k)
     _align_check(ids, E, tile_m)
+
+
+@pytest.mark.parametrize("T,E", [(512, 128), (512, 256)])
+def test_align_skewed_router_mid(gpu, T, E):
+    """The int4 (128 experts) and FP8 per-row (256 experts) prefill
+    layers at T=512 top-8: skewed experts with several 128-row tiles."""
+    rng = np.random.default_rng(T + E + 1)
+    lg = (rng.standard_normal((T, E)) + rng.standard_normal((1, E)) * 2.0).astype(np.float32)
+    _, ids = omoe.topk_softmax(lg, 8)
+    _align_check(ids, E, 128)
+
+
+@pytest.mark.parametrize("n,E", [(3000, 37), (8192, 1024), (300, 5)])
+def test_align_raw_ids_mid(gpu, n, E):
+    """Arbitrary id streams (repeats inside a chunk, ids outside [0, E)
+    dropped) on the mid-size schedule."""
+    rng = np.random.default_rng(n + E)
+    ids = rng.integers(-2, E + 3, size=(n, 1)).astype(np.int64)
+    _align_check(ids, E, 16)
 
 
 def test_align_skewed_router_t4096(gpu):
