@@ -610,7 +610,7 @@ constexpr int RT_MAXTILES = RT_MAXN / 16 + RT_MAXN;  // ccq_moe_align_max_tiles(
 struct RouteSmem {
   float lg[RT_MAXLG];
   int sid[RT_MAXN];  // expert of each assignment, -1 = dropped
-  int cnt[RT_MAXE], base[RT_MAXE];
+  int cnt[RT_MAXE], base[RT_MAXE], rank_of[RT_MAXE];
   int sorted[RT_MAXTILES * 16];
   int tile_expert[RT_MAXTILES];
   int ntiles, nactive;
@@ -635,22 +635,36 @@ __device__ __forceinline__ int wave_incl_sum(int v) {
   return v;
 }
 
-// Whole workgroup (blockDim.x = 512); ends with the schedule in rs and a
-// barrier.
-__device__ void route_decode(const W4SP& p, RouteSmem& rs) {
+// Top-k of the batch in every workgroup (blockDim.x = 512): logits (from
+// route_logits_load) staged in LDS, rs.sid[a] = expert of assignment a (-1:
+// dropped), rs.cnt[e] = assignments of expert e; workgroup 0 writes ids and
+// weights out.  LDS-only barriers, so weight loads issued before it stay in
+// flight.
+constexpr int RT_LGV = RT_MAXLG / 512;  // logits per thread of a 512-thread workgroup
+
+// The batch's logits into registers (thread t: logits t, t + 512, ...).
+__device__ __forceinline__ void route_logits_load(const W4SP& p, float (&lgv)[RT_LGV]) {
+  const int tid = threadIdx.x, TE = p.rT * p.rE;
+#pragma unroll
+  for (int j = 0; j < RT_LGV; ++j) lgv[j] = tid + 512 * j < TE ? p.logits[tid + 512 * j] : 0.f;
+}
+
+__device__ void route_topk(const W4SP& p, RouteSmem& rs, const float (&lgv)[RT_LGV]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   // E logits per token, Es experts in the schedule (E + the shared one),
   // ks assignment slots per token (the shared one last)
-  const int T = p.rT, E = p.rE, k = p.rk, ks = k + p.rshared, Es = E + p.rshared, n = T * ks;
-  const int nslots = n + 15 * min(n, Es);  // the padded schedule is at most this long
+  const int T = p.rT, E = p.rE, k = p.rk, ks = k + p.rshared, Es = E + p.rshared;
   for (int e = tid; e < Es; e += blockDim.x) rs.cnt[e] = 0;
-  for (int i = tid; i < nslots; i += blockDim.x) rs.sorted[i] = -1;
-  for (int i = tid; i < T * E; i += blockDim.x) rs.lg[i] = p.logits[i];
-  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < RT_LGV; ++j)
+    if (tid + 512 * j < T * E) rs.lg[tid + 512 * j] = lgv[j];
+  lds_barrier();
   auto keep = [&](int t, float w, int id) {
     if (lane < k) {
       const int a = t * ks + lane;
-      rs.sid[a] = id >= 0 && id < E ? id : -1;
+      const bool ok = id >= 0 && id < E;
+      rs.sid[a] = ok ? id : -1;
+      if (ok) atomicAdd(&rs.cnt[id], 1);
       if (blockIdx.x == 0) {
         p.ids_out[a] = id;
         p.wts_out[a] = w;
@@ -658,6 +672,7 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
     } else if (lane == k && p.rshared) {
       const int a = t * ks + k;
       rs.sid[a] = E;
+      atomicAdd(&rs.cnt[E], 1);
       if (blockIdx.x == 0) {
         p.ids_out[a] = E;
         p.wts_out[a] = p.rshared_w;
@@ -685,7 +700,18 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
       keep(t, w, id);
     }
   }
-  __syncthreads();
+  lds_barrier();
+}
+
+// The schedule of ccq_moe_align (16-row tiles) from rs.sid, built by wave 0
+// of workgroup 0 and published for the down and combine kernels.  Barriers
+// are LDS-only, so the caller's weight loads stay in flight.
+__device__ void route_schedule(const W4SP& p, RouteSmem& rs) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = p.rT, k = p.rk, ks = k + p.rshared, Es = p.rE + p.rshared, n = T * ks;
+  const int nslots = n + 15 * min(n, Es);  // the padded schedule is at most this long
+  for (int i = tid; i < nslots; i += blockDim.x) rs.sorted[i] = -1;
+  lds_barrier();
   if (wave == 0) {
     int nbits = 1;
     while ((1 << nbits) < Es) ++nbits;  // <= 8
@@ -732,7 +758,6 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
       if (first) {
         const int bs = carry + incl - pd;
         rs.base[key[c]] = bs;
-        rs.cnt[key[c]] = cnt[c];
         for (int t = bs / 16; t < (bs + pd) / 16; ++t) rs.tile_expert[t] = key[c];
       }
       carry += __builtin_amdgcn_readlane(incl, 63);
@@ -749,20 +774,20 @@ __device__ void route_decode(const W4SP& p, RouteSmem& rs) {
       rs.nactive = nact;
     }
   }
-  __syncthreads();
-  if (blockIdx.x == 0) {  // the schedule of the down and combine kernels
-    const int nt = rs.ntiles;
-    for (int i = tid; i < nt * 16; i += blockDim.x) p.sched_rows[i] = rs.sorted[i];
-    for (int i = tid; i < nt; i += blockDim.x) p.sched_tile_expert[i] = rs.tile_expert[i];
-    for (int x = tid; x < Es; x += blockDim.x) p.sched_counts[x] = rs.cnt[x];
-    if (tid == 0) {
-      p.sched_meta[0] = nt;
-      p.sched_meta[1] = rs.nactive;
-    }
+  lds_barrier();
+  const int nt = rs.ntiles;
+  for (int i = tid; i < nt * 16; i += blockDim.x) p.sched_rows[i] = rs.sorted[i];
+  for (int i = tid; i < nt; i += blockDim.x) p.sched_tile_expert[i] = rs.tile_expert[i];
+  for (int x = tid; x < Es; x += blockDim.x) p.sched_counts[x] = rs.cnt[x];
+  if (tid == 0) {
+    p.sched_meta[0] = nt;
+    p.sched_meta[1] = rs.nactive;
   }
+  lds_barrier();  // every wave has read the scratch before the first job reuses the space
 }
 
-constexpr int WS_DEPTH = 2;  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
+constexpr int WS_DEPTH = 2;
+constexpr int RT_LEAD = 2;  // jobs workgroup 0 of a routed gate/up stage gives up for building the schedule  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
 
 // Quads per job of the streaming kernel for a stage of N columns and K rows
 // (0: the kernel does not take it).  EPI_SILU always pairs gate and up; two
@@ -814,10 +839,87 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     }
   };
   if constexpr (routed) load_frags(a, r16 < p.rT ? r16 : 0);
-  int ntiles;
+  // routed: the expert of each job tile and, per token, its assignment in
+  // the tile (-1: not routed there), in the second-tile fragment area
+  // (unused with token rows)
+  int* const ste = reinterpret_cast<int*>(&xb[0]);
+  int* const tok2a = ste + RT_MAXTILES;
+  static_assert(!ROUTE || (MT == 2 && (RT_MAXTILES * 17) * 4 <= XB * 16), "routed tables fit the fragment area");
+  // ---- the weight stream: a wave's share of one job is MT x NQ tiles (16 B
+  // per lane) and the scale/zero words of its k-tiles for the 16 columns of
+  // each quad (lane l: column l & 15, (m, q) pair l >> 4).  Every load is
+  // issued unconditionally, so that the compiler's count of loads in flight
+  // stays exact and each wait leaves the later jobs' loads in flight: a slot
+  // past the end of the range reads the first KiB of the weights (and the
+  // first words of the scales) instead, the same lines for every workgroup,
+  // which stay in L2 ----
+  const int zmq = (lane >> 4) < MT * NQ ? lane >> 4 : 0;
+  const int zq = zmq % NQ, zkt = min(wave + 8 * (zmq / NQ), KT - 1);
+  // column job nj of expert e_x (real = false: the hot line)
+  auto load_ej = [&](int e_x, int nj, bool real, u32x4 (&w)[MT][NQ], uint32_t& z) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int kt = min(wave + 8 * m, KT - 1);
+      const bool live = real && wave + 8 * m < KT;  // k-tiles past K: the hot line too
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const uint32_t* base = EPI == EPI_SILU && q == 1 ? p.w1 : p.w0;
+        int64_t off = (int64_t)e_x * p.w_es +
+                      ((int64_t)(EPI == EPI_SILU ? nj : nj * NQ + q) * KT + kt) * 256;
+        off = live ? off : 0;
+        // the select stays on the offset (the compiler would otherwise load
+        // from both addresses and select the data); the base keeps the
+        // pointer in the global address space
+        asm volatile("" : "+s"(off));
+        // non-temporal: read once (measured 8% faster than plain loads for the
+        // gate/up stage of a 16-token decode batch)
+        w[m][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + off) + lane);
+      }
+    }
+    const uint32_t* zbase = EPI == EPI_SILU && zq == 1 ? p.sz1 : p.sz0;
+    int64_t zoff = (int64_t)e_x * p.sz_es + ((int64_t)(EPI == EPI_SILU ? nj : nj * NQ + zq) * 16 + r16) * szw + zkt;
+    zoff = real ? zoff : lane;
+    asm volatile("" : "+v"(zoff));
+    z = zbase[zoff];
+  };
+  u32x4 wv[D][MT][NQ];
+  uint32_t zv[D];
+
+  int ntiles, lead = 0;
   if constexpr (routed) {
-    route_decode(p, rs);
+    // The job tiles are the routed experts in id order (tile r: expert
+    // ste[r]), straight from the top-k: the gate/up jobs need no schedule,
+    // so the weight loads start right after it.  Workgroup 0 builds the
+    // published schedule (first-appearance order) once its loads are in
+    // flight, and takes RT_LEAD fewer jobs.
+    const int Es = p.rE + p.rshared, na = p.rT * p.row_div;
+    float lgv[RT_LGV];
+    route_logits_load(p, lgv);
+    route_topk(p, rs, lgv);
+    for (int i = tid; i < min(na, Es) * 16; i += blockDim.x) tok2a[i] = -1;
+    if (wave == 0) {
+      int carry = 0;
+      for (int c = 0; c < Es; c += 64) {
+        const int e = c + lane;
+        const bool used = e < Es && rs.cnt[e] > 0;
+        const uint64_t m = __ballot(used);
+        if (used) {
+          const int r = carry + popc64(m & ((1ull << lane) - 1ull));
+          rs.rank_of[e] = r;
+          ste[r] = e;
+        }
+        carry += popc64(m);
+      }
+      if (lane == 0) rs.ntiles = carry;
+    }
+    lds_barrier();
+    for (int i = tid; i < na; i += blockDim.x) {
+      const int e = rs.sid[i];
+      if (e >= 0) tok2a[rs.rank_of[e] * 16 + i / p.row_div] = i;
+    }
     ntiles = __builtin_amdgcn_readfirstlane(rs.ntiles);
+    lead = ntiles * NJ >= 4 * (int)gridDim.x ? RT_LEAD : 0;
+    lds_barrier();  // every wave has read the routing scratch before the first job reuses the space
   } else {
     ntiles = p.meta != nullptr ? p.meta[0] : p.tiles;
   }
@@ -829,9 +931,15 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // slower)
   constexpr bool IL = EPI == EPI_STORE;
   const int J = ntiles * NJ;
-  const int lo = IL ? (int)blockIdx.x : (int)((int64_t)blockIdx.x * J / gridDim.x);
-  const int hi = IL ? J : (int)((int64_t)(blockIdx.x + 1) * J / gridDim.x);
-  if (lo >= hi) return;
+  auto split = [&](int b) { return b == 0 ? 0 : max(0, (int)((int64_t)b * (J + lead) / gridDim.x) - lead); };
+  const int lo = IL ? (int)blockIdx.x : split(blockIdx.x);
+  const int hi = IL ? J : split(blockIdx.x + 1);
+  if (lo >= hi) {
+    if constexpr (routed) {
+      if (blockIdx.x == 0) route_schedule(p, rs);
+    }
+    return;
+  }
   const int n = IL ? (hi - lo + (int)gridDim.x - 1) / (int)gridDim.x : hi - lo;
   const int tA = IL ? 0 : lo / NJ, ntl = IL ? 1 : (hi - 1) / NJ - tA + 1;  // the range covers 1 or 2 tiles
   const int tB = ntl > 1 ? tA + 1 : tA;
@@ -840,21 +948,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // ---- experts and row ids of the range's tiles: scalar loads, issued
   // together; lane r16 keeps row r16 ----
   int exA = 0, exB = 0, rid[2] = {-1, -1};
-  // routed: each tile's expert and, per token, its assignment in the tile
-  // (-1: not routed there), copied out of the routing scratch into the
-  // second-tile fragment area (unused with token rows)
-  int* const ste = reinterpret_cast<int*>(&xb[0]);
-  int* const tok2a = ste + RT_MAXTILES;
-  static_assert(!ROUTE || (MT == 2 && (RT_MAXTILES * 17) * 4 <= XB * 16), "routed tables fit the fragment area");
-  if constexpr (routed) {  // the schedule routed above, in LDS
-    for (int i = tid; i < ntiles * 16; i += blockDim.x) tok2a[i] = -1;
-    for (int t = tid; t < ntiles; t += blockDim.x) ste[t] = rs.tile_expert[t];
-    __syncthreads();
-    for (int i = tid; i < ntiles * 16; i += blockDim.x) {
-      const int asg = rs.sorted[i];
-      if (asg >= 0) tok2a[(i & ~15) + asg / p.row_div] = asg;
-    }
-    __syncthreads();  // every wave has read the routing scratch before the first job reuses the space
+  if (routed) {  // token rows: the tables above
   } else if (p.rows != nullptr) {  // expert schedule (rows and tile_expert both set)
     const int32_t* ra = p.rows + (int64_t)tA * 16;
     const int32_t* rb = p.rows + (int64_t)tB * 16;
@@ -887,50 +981,18 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     if constexpr (MT == 2) load_frags(b, rB / p.row_div);
   }
 
-  // ---- the weight stream: a wave's share of one job is MT x NQ tiles (16 B
-  // per lane) and the scale/zero words of its k-tiles for the 16 columns of
-  // each quad (lane l: column l & 15, (m, q) pair l >> 4).  Every load is
-  // issued unconditionally, so that the compiler's count of loads in flight
-  // stays exact and each wait leaves the later jobs' loads in flight: a slot
-  // past the end of the range reads the first KiB of the weights (and the
-  // first words of the scales) instead, the same lines for every workgroup,
-  // which stay in L2 ----
-  const int zmq = (lane >> 4) < MT * NQ ? lane >> 4 : 0;
-  const int zq = zmq % NQ, zkt = min(wave + 8 * (zmq / NQ), KT - 1);
   auto load = [&](int i, u32x4 (&w)[MT][NQ], uint32_t& z) {
     const bool real = i < n;
     const int job = job_of(real ? i : 0);
     const int tl = job / NJ, nj = job - tl * NJ;
     const int e_x = routed ? __builtin_amdgcn_readfirstlane(ste[tl]) : (tl == tA ? exA : exB);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const int kt = min(wave + 8 * m, KT - 1);
-      const bool live = real && wave + 8 * m < KT;  // k-tiles past K: the hot line too
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const uint32_t* base = EPI == EPI_SILU && q == 1 ? p.w1 : p.w0;
-        int64_t off = (int64_t)e_x * p.w_es +
-                      ((int64_t)(EPI == EPI_SILU ? nj : nj * NQ + q) * KT + kt) * 256;
-        off = live ? off : 0;
-        // the select stays on the offset (the compiler would otherwise load
-        // from both addresses and select the data); the base keeps the
-        // pointer in the global address space
-        asm volatile("" : "+s"(off));
-        // non-temporal: read once (measured 8% faster than plain loads for the
-        // gate/up stage of a 16-token decode batch)
-        w[m][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + off) + lane);
-      }
-    }
-    const uint32_t* zbase = EPI == EPI_SILU && zq == 1 ? p.sz1 : p.sz0;
-    int64_t zoff = (int64_t)e_x * p.sz_es + ((int64_t)(EPI == EPI_SILU ? nj : nj * NQ + zq) * 16 + r16) * szw + zkt;
-    zoff = real ? zoff : lane;
-    asm volatile("" : "+v"(zoff));
-    z = zbase[zoff];
+    load_ej(e_x, nj, real, w, z);
   };
-  u32x4 wv[D][MT][NQ];
-  uint32_t zv[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) load(d, wv[d], zv[d]);
+  if constexpr (routed) {
+    if (blockIdx.x == 0) route_schedule(p, rs);
+  }
 
   // park the second tile's fragments in LDS, group sums of the first
   if constexpr (MT == 2) {
