@@ -348,3 +348,65 @@ def test_route_gate_up_stage_matches_forward(gpu):
     rc = lib.ccq_moe_w4_route_gate_up(xb.data_ptr(), CCQ_BF16, lgb.data_ptr(), Tb, k, 1, None, None,
                                       ctypes.byref(desc), wsb.data_ptr(), nb, None)
     assert rc == CCQ_EUNSUPPORTED and "decode batch" in _lib.last_error()
+
+
+def test_decode_forward_repeated_calls_bitexact(gpu):
+    """The decode layer from router logits (routing inside the gate/up
+    kernel, jobs over the routed experts in id order): calls alternating
+    T=16 / T=1 at the C3 shapes, on one workspace and on fresh workspaces of
+    arbitrary contents (all ones, random bytes), give the bits of the stage
+    entry points run one by one."""
+    import ctypes
+
+    from ccut import _dev, _lib
+    from ccut._lib import call
+    from ccut.blocks import moe
+
+    lib = _lib.lib()
+    E, H, I, G, k = 64, 2048, 1408, 128, 6
+    gate, up, down = _experts(E, H, I, G, seed=5)
+    dev = lambda t: tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    ex = moe.W4Experts.from_awq(dev(gate), dev(up), dev(down), group_size=G)
+    desc = ex.descriptor()
+    vp = ctypes.c_void_p
+    cases = []
+    for T in (16, 1):
+        g = torch.Generator().manual_seed(100 + T)
+        x = torch.randn((T, H), generator=g).to(torch.bfloat16).to(gpu)
+        lg = torch.randn((T, E), generator=g).to(gpu)
+        w, ids = moe.topk_softmax(lg, k, True)
+        sch = moe.moe_align(ids, E, 16)
+        mt = sch.tile_expert.numel()
+        inter = torch.empty((T * k, I), dtype=x.dtype, device=gpu)
+        rows = torch.empty((T * k, H), dtype=torch.float32, device=gpu)
+        call("ccq_moe_w4_gate_up", x.data_ptr(), _lib.CCQ_BF16, k, sch.sorted_ids.data_ptr(),
+             sch.tile_expert.data_ptr(), sch.meta.data_ptr(), mt, inter.data_ptr(), desc, _dev.stream_ptr())
+        call("ccq_moe_w4_down", inter.data_ptr(), _lib.CCQ_BF16, sch.sorted_ids.data_ptr(),
+             sch.tile_expert.data_ptr(), sch.meta.data_ptr(), mt, rows.data_ptr(), desc, _dev.stream_ptr())
+        y_st = torch.empty((T, H), dtype=torch.float32, device=gpu)
+        call("ccq_moe_combine", rows.data_ptr(), w.data_ptr(), y_st.data_ptr(), _lib.CCQ_F32, T, k, H,
+             _dev.stream_ptr())
+        cases.append((T, x, lg, y_st))
+    nbytes = lib.ccq_moe_w4_workspace_size(16, k, ctypes.byref(desc))
+    shared_ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+
+    def forward(T, x, lg, ws):
+        y = torch.empty((T, H), dtype=torch.float32, device=gpu)
+        rc = lib.ccq_moe_w4_forward(vp(x.data_ptr()), _lib.CCQ_BF16, vp(lg.data_ptr()), T, k, 1, None, None,
+                                    vp(y.data_ptr()), _lib.CCQ_F32, ctypes.byref(desc), vp(ws.data_ptr()), nbytes,
+                                    vp(_dev.stream_ptr(gpu)))
+        assert rc == 0, _lib.last_error()
+        return y
+
+    outs = []
+    for it in range(12):
+        for T, x, lg, y_st in cases:
+            outs.append((forward(T, x, lg, shared_ws), y_st))
+    for fill in (0xFF, None):
+        ws = torch.full((nbytes,), fill, dtype=torch.uint8, device=gpu) if fill is not None else \
+            torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=gpu)
+        for T, x, lg, y_st in cases:
+            outs.append((forward(T, x, lg, ws), y_st))
+    torch.cuda.synchronize()
+    for y, y_st in outs:
+        assert torch.equal(y, y_st)
