@@ -32,7 +32,10 @@ decoded-weight MFMA kernel), INT8 W8A8, the FP8 quantizers; the prefill workload
 as TFLOP/s against the matching dense MFMA peak: int4 MoE prefill (128
 experts, skewed top-8, hidden 2048, inter 768, T = 512 and 4096, bf16 MFMA,
 4 rotating weight sets) and FP8 block MoE prefill (256 experts, top-8,
-T = 2048, hidden 7168, inter 2048, FP8 MFMA).  ``cpu_baseline`` times the
+T = 2048, hidden 7168, inter 2048, FP8 MFMA); the MoE layer on the
+reference checkpoint's own expert format (e4m3 [out, in] with per-row
+scales, 256 experts, top-8, hidden 2048, inter 512, float32 activations)
+at T = 1, 16 and 512 (GB/s of the routed experts' bytes).  ``cpu_baseline`` times the
 reference's algorithm (the CPU oracle: dequant to float32, BLAS matmuls,
 per-expert grouping) on the host, per workload, in two variants: dequant on
 every call, and matmuls on cached float32 weights.
