@@ -635,11 +635,6 @@ __device__ __forceinline__ int wave_incl_sum(int v) {
   return v;
 }
 
-// Top-k of the batch in every workgroup (blockDim.x = 512): logits (from
-// route_logits_load) staged in LDS, rs.sid[a] = expert of assignment a (-1:
-// dropped), rs.cnt[e] = assignments of expert e; workgroup 0 writes ids and
-// weights out.  LDS-only barriers, so weight loads issued before it stay in
-// flight.
 constexpr int RT_LGV = RT_MAXLG / 512;  // logits per thread of a 512-thread workgroup
 
 // The batch's logits into registers (thread t: logits t, t + 512, ...).
@@ -649,6 +644,11 @@ __device__ __forceinline__ void route_logits_load(const W4SP& p, float (&lgv)[RT
   for (int j = 0; j < RT_LGV; ++j) lgv[j] = tid + 512 * j < TE ? p.logits[tid + 512 * j] : 0.f;
 }
 
+// Top-k of the batch in every workgroup (blockDim.x = 512): the logits
+// (from route_logits_load) staged in LDS, rs.sid[a] = expert of assignment
+// a (-1: dropped), rs.cnt[e] = assignments of expert e; workgroup 0 writes
+// ids and weights out.  LDS-only barriers, so weight loads issued before it
+// stay in flight.
 __device__ void route_topk(const W4SP& p, RouteSmem& rs, const float (&lgv)[RT_LGV]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   // E logits per token, Es experts in the schedule (E + the shared one),
@@ -786,8 +786,8 @@ __device__ void route_schedule(const W4SP& p, RouteSmem& rs) {
   lds_barrier();  // every wave has read the scratch before the first job reuses the space
 }
 
-constexpr int WS_DEPTH = 2;
-constexpr int RT_LEAD = 2;  // jobs workgroup 0 of a routed gate/up stage gives up for building the schedule  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
+constexpr int WS_DEPTH = 2;  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
+constexpr int RT_LEAD = 2;   // jobs workgroup 0 of a routed gate/up stage gives up for building the schedule
 
 // Quads per job of the streaming kernel for a stage of N columns and K rows
 // (0: the kernel does not take it).  EPI_SILU always pairs gate and up; two
