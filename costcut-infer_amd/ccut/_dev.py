@@ -48,6 +48,20 @@ def to_device(a, dtype: torch.dtype | None = None) -> torch.Tensor:
     return t.to(dev, non_blocking=False).contiguous()
 
 
+def half_for_mfma(x_f32: torch.Tensor, host=None) -> torch.dtype:
+    """The 16-bit type float32 activations take into a bf16 / fp16 MFMA:
+    float16 (11 significant bits) when every |x| is finite and fits its
+    range, else bfloat16 (8 bits, float32's range).  ``host``: the same
+    values as a host array, when the caller has them (no device read)."""
+    if x_f32.numel() == 0:
+        amax = 0.0
+    elif host is not None:
+        amax = float(np.abs(np.asarray(host, np.float32)).max())
+    else:
+        amax = float(x_f32.abs().amax().item())
+    return torch.float16 if np.isfinite(amax) and amax <= 65504.0 else torch.bfloat16
+
+
 def to_host(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().numpy()
 

@@ -135,13 +135,7 @@ class WeightOnlyMethod(QuantizeMethodBase):
             # range, else as bfloat16 (8 bits, float32's range); the sums
             # and the output stay float32, so nothing else can overflow
             xd = _dev.to_device(x, torch.float32)
-            if xd.numel() == 0:
-                amax = 0.0
-            elif _dev.is_host(x):
-                amax = float(np.abs(np.asarray(x, np.float32)).max())
-            else:
-                amax = float(xd.abs().amax().item())
-            xdt = torch.float16 if np.isfinite(amax) and amax <= 65504.0 else torch.bfloat16
+            xdt = _dev.half_for_mfma(xd, x if _dev.is_host(x) else None)
             y = awq.gemm(xd.to(xdt), w, out_dtype=torch.float32)
             return _return(y, x)
         if self.weight_dtype == QuantDType.INT4:
