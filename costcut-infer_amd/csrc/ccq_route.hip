@@ -64,6 +64,36 @@ __device__ __forceinline__ uint64_t match_key(int key, bool valid, int nbits) {
   return valid ? same : 0ull;
 }
 
+// The padding (-1) after each active expert's rows and the tile -> expert
+// map, for a workgroup of nw waves and at most 64 nw active experts.  Lane l
+// of wave w looks up rank w + nw l once (its expert, first padding slot,
+// padding count, first tile and tile count); the wave then walks its ranks,
+// taking each one's values from that lane, and its lanes store the rank's
+// padding slots and tile entries side by side.  inv[r] = expert of rank r,
+// base / cnt by expert.  No barrier.
+__device__ void fill_padding_and_tiles(int nactive, int tile_m, const int* inv, const int* base, const int* cnt,
+                                       int32_t* __restrict__ sorted_ids, int32_t* __restrict__ tile_expert) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int r = w + nw * lane;
+  int e = 0, pad0 = 0, npad = 0, t0 = 0, nt = 0;
+  if (r < nactive) {
+    e = inv[r];
+    const int b = base[e], c = cnt[e];
+    nt = (c + tile_m - 1) / tile_m;
+    pad0 = b + c;
+    npad = nt * tile_m - c;
+    t0 = b / tile_m;
+  }
+  const int nr = nactive > w ? (nactive - w + nw - 1) / nw : 0;  // ranks of this wave, <= 64
+  for (int i = 0; i < nr; ++i) {
+    const int ei = __builtin_amdgcn_readlane(e, i), p0 = __builtin_amdgcn_readlane(pad0, i);
+    const int np = __builtin_amdgcn_readlane(npad, i), ti = __builtin_amdgcn_readlane(t0, i);
+    const int nti = __builtin_amdgcn_readlane(nt, i);
+    for (int j = lane; j < np; j += 64) sorted_ids[p0 + j] = -1;
+    for (int j = lane; j < nti; j += 64) tile_expert[ti + j] = ei;
+  }
+}
+
 __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restrict__ ids, int n, int E,
                                                          int tile_m, int32_t* __restrict__ sorted_ids,
                                                          int32_t* __restrict__ tile_expert,
@@ -203,15 +233,7 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
       __builtin_amdgcn_wave_barrier();
     }
   }
-  // padding and tile -> expert map: a wave per expert, its lanes over the
-  // expert's padding slots and tiles
-  for (int i = w; i < nactive; i += kAlignWaves) {
-    const int e = sm.inv[i];
-    const int b = sm.base[e], c = sm.cnt[e];
-    const int p = (int)cdiv(c, tile_m) * tile_m;
-    for (int j = c + lane; j < p; j += 64) sorted_ids[b + j] = -1;
-    for (int t = b / tile_m + lane; t < (b + p) / tile_m; t += 64) tile_expert[t] = e;
-  }
+  fill_padding_and_tiles(nactive, tile_m, sm.inv, sm.base, sm.cnt, sorted_ids, tile_expert);
 }
 
 // y[t, h] = sum_s w[t, s] * rows[t*k + s, h], slot order, float32.  Slots
@@ -460,13 +482,7 @@ __global__ __launch_bounds__(1024) void align_plan_kernel(int E, int nchunks, in
   }
   __syncthreads();
   for (int e = tid; e < E; e += 1024) cfirst[e] = cnt[e] > 0 ? base[e] : 0;  // row 0 of the table: the bases
-  for (int r = w; r < na; r += 16) {  // padding and tile -> expert: one wave per expert
-    const int e = inv[r];
-    const int b = base[e], c = cnt[e];
-    const int p = (int)cdiv(c, tile_m) * tile_m;
-    for (int j = c + lane; j < p; j += 64) sorted_ids[b + j] = -1;
-    for (int t = b / tile_m + lane; t < (b + p) / tile_m; t += 64) tile_expert[t] = e;
-  }
+  fill_padding_and_tiles(na, tile_m, inv, base, cnt, sorted_ids, tile_expert);
 }
 
 __global__ __launch_bounds__(256) void align_chunk_scatter_kernel(const int64_t* __restrict__ ids, int n, int E,
@@ -641,6 +657,7 @@ static void launch_align_small(const int64_t* ids, int n, int E, int tile_m, int
 // each assignment lands at base + earlier waves' count + its rank in the wave.
 // Compile-time NB and CPW keep the matching straight-line code.
 constexpr int kMidN = 8192;
+constexpr int kMidStage = 16384;  // padded sorted-list length staged in LDS (64 KB)
 
 template <int NB, int CPW>
 __global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __restrict__ ids, int n, int E,
@@ -649,8 +666,9 @@ __global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __re
                                                              int32_t* __restrict__ meta,
                                                              int32_t* __restrict__ counts_out) {
   __shared__ int wcnt[kAlignWaves * (1 << NB)];  // [wave][expert]: counts, then exclusive offsets
-  __shared__ int cnt[1 << NB], first[1 << NB], base[1 << NB], inv[1 << NB];
+  __shared__ int cnt[1 << NB], first[1 << NB], base[1 << NB], inv[1 << NB], tstart[1 << NB];
   __shared__ int wtot[kAlignWaves];
+  __shared__ int stage[kMidStage];  // the padded sorted list, when it fits
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int key[CPW];
 #pragma unroll
@@ -744,25 +762,47 @@ __global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __re
     boff += i < w ? t : 0;
     total += t;
   }
-  if (rk < nactive) base[inv[rk]] = boff + incl - pd;
+  if (rk < nactive) {
+    base[inv[rk]] = boff + incl - pd;
+    tstart[rk] = (boff + incl - pd) / tile_m;
+  }
   if (tid == 0) {
     meta[0] = total / tile_m;
     meta[1] = nactive;
   }
+  const bool staged = total <= kMidStage;  // the same in every wave
+  if (staged)
+    for (int i = tid; i < total; i += 1024) stage[i] = -1;
   __syncthreads();
 
-  // positions, then each expert's padding and tiles (a wave per expert)
+  if (staged) {
+    // the list is assembled in LDS and written out in order: one workgroup's
+    // scattered 4-byte stores to HBM would queue behind each other
 #pragma unroll
-  for (int c = 0; c < CPW; ++c) {
-    const int e = key[c];
-    if (e >= 0) sorted_ids[base[e] + wcnt[w * (1 << NB) + e] + pos[c]] = (w * CPW + c) * 64 + lane;
-  }
-  for (int i = w; i < nactive; i += kAlignWaves) {
-    const int e = inv[i];
-    const int b = base[e], c = cnt[e];
-    const int p = (c + tile_m - 1) / tile_m * tile_m;
-    for (int j = c + lane; j < p; j += 64) sorted_ids[b + j] = -1;
-    for (int t = b / tile_m + lane; t < (b + p) / tile_m; t += 64) tile_expert[t] = e;
+    for (int c = 0; c < CPW; ++c) {
+      const int e = key[c];
+      if (e >= 0) stage[base[e] + wcnt[w * (1 << NB) + e] + pos[c]] = (w * CPW + c) * 64 + lane;
+    }
+    __syncthreads();
+    for (int i = tid; i < total; i += 1024) sorted_ids[i] = stage[i];
+    for (int t = tid; t < total / tile_m; t += 1024) {
+      int lo = 0, hi = nactive - 1;  // the largest rank whose first tile is <= t
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tstart[mid] <= t)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      tile_expert[t] = inv[lo];
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int e = key[c];
+      if (e >= 0) sorted_ids[base[e] + wcnt[w * (1 << NB) + e] + pos[c]] = (w * CPW + c) * 64 + lane;
+    }
+    fill_padding_and_tiles(nactive, tile_m, inv, base, cnt, sorted_ids, tile_expert);
   }
 }
 
