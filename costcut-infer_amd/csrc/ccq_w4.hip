@@ -1400,19 +1400,29 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
       const float sxr = *reinterpret_cast<const float*>(S + GG_SX_OFF + (mw * 64 + rt * 32 + c32) * 4);
       za[rt] = mine ? -sxr : za[rt];
     }
+    // the k-steps in two straight-line forms (one or two 32-row tiles), so no
+    // branch splits the dequantization of one fragment from the MFMAs of the
+    // one before
+    auto ksteps = [&](auto two_c) {
+      constexpr bool TWO = decltype(two_c)::value;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (s == 4) mid();
-      V a[2];
+      for (int s = 0; s < 8; ++s) {
+        if (s == 4) mid();
+        V a[2];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) a[rt] = *reinterpret_cast<const V*>(S + rt * 32 * 256 + adoff[s]);
+        for (int rt = 0; rt < (TWO ? 2 : 1); ++rt) a[rt] = *reinterpret_cast<const V*>(S + rt * 32 * 256 + adoff[s]);
 #pragma unroll
-      for (int c = 0; c < C32; ++c) {
-        const V b = dq_b3<AT>(bq[c][s & 1][s >> 1], mask_s, magic_v);
-        t[0][c] = mfma32(a[0], b, s == 0 ? f32x16{} : t[0][c]);
-        if (two) t[1][c] = mfma32(a[1], b, s == 0 ? f32x16{} : t[1][c]);
+        for (int c = 0; c < C32; ++c) {
+          const V b = dq_b3<AT>(bq[c][s & 1][s >> 1], mask_s, magic_v);
+          t[0][c] = mfma32(a[0], b, s == 0 ? f32x16{} : t[0][c]);
+          if constexpr (TWO) t[1][c] = mfma32(a[1], b, s == 0 ? f32x16{} : t[1][c]);
+        }
       }
-    }
+    };
+    if (two)
+      ksteps(std::true_type{});
+    else
+      ksteps(std::false_type{});
     if (!late) fold(sc, two);
 #pragma unroll
     for (int c = 0; c < C32; ++c) scp[c] = sc[c];
