@@ -239,21 +239,22 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restri
 // y[t, h] = sum_s w[t, s] * rows[t*k + s, h], slot order, float32.  Slots
 // whose id is outside [0, E) (dropped by the schedule) contribute nothing.
 // rows are float32 (RT = CCQ_F32) or bf16 (RT = CCQ_BF16); with VEC each
-// thread takes 16 bytes of a row (4 or 8 columns).  The ids, weights and
-// rows of up to 16 slots are loaded before their FMAs (one memory round
-// trip per 16 slots, not one per slot); a dropped slot's row is read and
-// not used.
+// thread takes 16 bytes of a row (4 or 8 columns) and, with yvec (y aligned
+// for it), stores its columns in one vector store.  The ids, weights and
+// rows of up to KMAX slots (8 or 16) are loaded before their FMAs (one
+// memory round trip per KMAX slots, not one per slot); a dropped slot's row
+// is read and not used.
 // With shared (the shared expert's output [T, H] f32), the epilogue adds
 // shared_gate * shared[t, h] to the sum, as shared_expert_add does
 // (blocks/moe.py:177-179): the product rounded to float32, then the add.
-template <int YT, int RT, bool VEC>
+template <int YT, int RT, bool VEC, int KMAX>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ rows,
                                                           const float* __restrict__ wts,
                                                           const int64_t* __restrict__ ids, int64_t E,
                                                           void* __restrict__ y, int64_t T, int k, int64_t H,
-                                                          const float* __restrict__ shared, float shared_gate) {
+                                                          const float* __restrict__ shared, float shared_gate,
+                                                          int yvec) {
   constexpr int CW = VEC ? (RT == CCQ_F32 ? 4 : 8) : 1;
-  constexpr int KMAX = 16;
   const int64_t t = blockIdx.y;
   const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * CW;
   if (h >= H) return;
@@ -308,6 +309,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
       acc[c] = acc[c] + g;
     }
   }
+  if constexpr (VEC) {
+    if (yvec) {
+      const int64_t o = t * H + h;
+      if constexpr (YT == CCQ_F32) {
+#pragma unroll
+        for (int c = 0; c < CW; c += 4)
+          *reinterpret_cast<f32x4*>((float*)y + o + c) = f32x4{acc[c], acc[c + 1], acc[c + 2], acc[c + 3]};
+      } else {
+        uint32_t wv2[CW / 2];
+#pragma unroll
+        for (int c = 0; c < CW; c += 2)
+          wv2[c / 2] = YT == CCQ_BF16 ? (f32_to_bf16_bits(acc[c]) | (f32_to_bf16_bits(acc[c + 1]) << 16))
+                                      : (f32_to_f16_bits(acc[c]) | (f32_to_f16_bits(acc[c + 1]) << 16));
+        if constexpr (CW == 8)
+          *reinterpret_cast<u32x4*>((uint16_t*)y + o) = u32x4{wv2[0], wv2[1], wv2[2], wv2[3]};
+        else
+          *reinterpret_cast<u32x2*>((uint16_t*)y + o) = u32x2{wv2[0], wv2[1]};
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int c = 0; c < CW; ++c) {
     const int64_t o = t * H + h + c;
@@ -320,21 +342,35 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
   }
 }
 
+template <int RT, bool VEC, int KMAX>
+static void launch_combine_k(const void* rows, const float* wts, const int64_t* ids, int64_t E, void* y,
+                             int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared,
+                             float sg) {
+  constexpr int CW = VEC ? (RT == CCQ_F32 ? 4 : 8) : 1;
+  const int64_t cols = VEC ? H / CW : H;
+  dim3 grid((unsigned)cdiv(cols, 256), (unsigned)T);
+  const int yvec = VEC && aligned(y, (size_t)CW * (y_dtype == CCQ_F32 ? 4 : 2)) ? 1 : 0;
+  if (y_dtype == CCQ_F32)
+    launch((moe_combine_kernel<CCQ_F32, RT, VEC, KMAX>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+                       (int)k, H, shared, sg, yvec);
+  else if (y_dtype == CCQ_BF16)
+    launch((moe_combine_kernel<CCQ_BF16, RT, VEC, KMAX>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+                       (int)k, H, shared, sg, yvec);
+  else
+    launch((moe_combine_kernel<CCQ_F16, RT, VEC, KMAX>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
+                       (int)k, H, shared, sg, yvec);
+}
+
+// slots per round trip: 8 for k <= 8 (the registers of 16 would halve the
+// workgroups resident per compute unit), else 16
 template <int RT, bool VEC>
 static void launch_combine_v(const void* rows, const float* wts, const int64_t* ids, int64_t E, void* y,
                              int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared,
                              float sg) {
-  const int64_t cols = VEC ? H / (RT == CCQ_F32 ? 4 : 8) : H;
-  dim3 grid((unsigned)cdiv(cols, 256), (unsigned)T);
-  if (y_dtype == CCQ_F32)
-    launch((moe_combine_kernel<CCQ_F32, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
-                       (int)k, H, shared, sg);
-  else if (y_dtype == CCQ_BF16)
-    launch((moe_combine_kernel<CCQ_BF16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
-                       (int)k, H, shared, sg);
+  if (k <= 8)
+    launch_combine_k<RT, VEC, 8>(rows, wts, ids, E, y, y_dtype, T, k, H, st, shared, sg);
   else
-    launch((moe_combine_kernel<CCQ_F16, RT, VEC>), grid, dim3(256), 0, st, rows, wts, ids, E, y, T,
-                       (int)k, H, shared, sg);
+    launch_combine_k<RT, VEC, 16>(rows, wts, ids, E, y, y_dtype, T, k, H, st, shared, sg);
 }
 
 // rows_dtype CCQ_F32 or CCQ_BF16; shared optional (16-byte aligned for the
