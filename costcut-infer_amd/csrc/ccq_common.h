@@ -178,6 +178,25 @@ enum WqFmt { WQ_FP8_ROW = 0, WQ_INT8_ROW = 1, WQ_MXFP8 = 2, WQ_MXFP4 = 3 };
 int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale, int group_size, float scale2,
                    float* y, int64_t M, int64_t K, int64_t N, hipStream_t stream, const char* name);
 
+// ------------------------------------ schedule + row group sums (host) --
+// Row group sums run beside a schedule: out[r * ldo + g] = the float32 sum,
+// in a fixed order, of the 128 activations of group g of row r (r < M,
+// g < KT; x bf16 or f16, rows 16-byte aligned).  launch_align_sums
+// (ccq_route.hip) builds the schedule as launch_align does and, when the
+// schedule is the one-workgroup mid-size kernel, runs the sums in the same
+// launch on further workgroups (done = true); otherwise it launches nothing
+// of them (done = false).
+struct AlignSums {
+  const void* x;
+  int x_bf16;
+  int64_t ldx, M, KT;
+  float* out;
+  int64_t ldo;
+};
+int launch_align_sums(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                      int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
+                      size_t scratch_bytes, const AlignSums& sums, bool& done);
+
 // --------------------------------------------------------- wave helpers --
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 

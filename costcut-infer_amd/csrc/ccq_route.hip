@@ -695,12 +695,42 @@ static void launch_align_small(const int64_t* ids, int n, int E, int tile_m, int
 constexpr int kMidN = 8192;
 constexpr int kMidStage = 16384;  // padded sorted-list length staged in LDS (64 KB)
 
+// Thread gt of the row group sums (AlignSums): 16 lanes per (row, group), 8
+// activations per lane summed in order, then across the 16 lanes by
+// butterfly -- the arithmetic of row_group_sums_kernel (ccq_w4.hip).
+__device__ void align_side_sums(const AlignSums& s, int64_t gt) {
+  const int64_t g = gt >> 4;
+  const int part = threadIdx.x & 15;
+  const bool ok = g < s.M * s.KT;
+  const int64_t row = ok ? g / s.KT : 0, kt = ok ? g - row * s.KT : 0;
+  float acc = 0.f;
+  if (ok) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(s.x) + row * s.ldx +
+                                                    kt * 128 + part * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t b = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      acc += s.x_bf16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
+  if (ok && part == 0) s.out[row * s.ldo + kt] = acc;
+}
+
+// Workgroup 0 builds the schedule; workgroups 1.. (launched only with row
+// group sums to run) take 1024 sum threads each.
 template <int NB, int CPW>
 __global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __restrict__ ids, int n, int E,
                                                              int tile_m, int32_t* __restrict__ sorted_ids,
                                                              int32_t* __restrict__ tile_expert,
                                                              int32_t* __restrict__ meta,
-                                                             int32_t* __restrict__ counts_out) {
+                                                             int32_t* __restrict__ counts_out,
+                                                             const AlignSums sums) {
+  if (blockIdx.x > 0) {
+    align_side_sums(sums, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
+    return;
+  }
   __shared__ int wcnt[kAlignWaves * (1 << NB)];  // [wave][expert]: counts, then exclusive offsets
   __shared__ int cnt[1 << NB], first[1 << NB], base[1 << NB], inv[1 << NB], tstart[1 << NB];
   __shared__ int wtot[kAlignWaves];
@@ -842,12 +872,15 @@ __global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __re
   }
 }
 
+// sums.x != nullptr: the row group sums on workgroups 1..
 template <int CPW>
 static void launch_align_mid_nb(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
-                                int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
+                                int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st,
+                                const AlignSums& sums) {
+  const unsigned grid = 1u + (sums.x != nullptr ? (unsigned)cdiv(sums.M * sums.KT * 16, 1024) : 0u);
 #define CCQ_ALM(NB)                                                                                          \
-  launch((moe_align_mid_kernel<NB, CPW>), dim3(1), dim3(1024), 0, st, ids, n, E, tile_m, sorted_ids,        \
-         tile_expert, meta, counts)
+  launch((moe_align_mid_kernel<NB, CPW>), dim3(grid), dim3(1024), 0, st, ids, n, E, tile_m, sorted_ids,     \
+         tile_expert, meta, counts, sums)
   if (E <= 64)
     CCQ_ALM(6);
   else if (E <= 256)
@@ -859,15 +892,16 @@ static void launch_align_mid_nb(const int64_t* ids, int n, int E, int tile_m, in
 
 // kSmallN < n <= kMidN, E <= 1024
 static void launch_align_mid(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
-                             int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st) {
+                             int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st,
+                             const AlignSums& sums) {
   if (n <= 1024)
-    launch_align_mid_nb<1>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+    launch_align_mid_nb<1>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
   else if (n <= 2048)
-    launch_align_mid_nb<2>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+    launch_align_mid_nb<2>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
   else if (n <= 4096)
-    launch_align_mid_nb<4>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+    launch_align_mid_nb<4>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
   else
-    launch_align_mid_nb<8>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st);
+    launch_align_mid_nb<8>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
 }
 
 size_t align_scratch_bytes(int64_t n, int64_t E) { return (size_t)2 * cdiv(n, kChunk) * E * 4; }
@@ -881,7 +915,7 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
     return launch_status("moe_align (small)");
   }
   if (n <= kMidN && E <= kMaxE) {  // one workgroup, straight-line matching
-    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st);
+    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st, AlignSums{});
     return launch_status("moe_align (mid)");
   }
   // larger batches: three launches over many workgroups when there is
@@ -900,6 +934,18 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
   launch(align_chunk_scatter_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
                      cfirst, sorted_ids);
   return launch_status("moe_align (chunked)");
+}
+
+int launch_align_sums(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                      int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
+                      size_t scratch_bytes, const AlignSums& sums, bool& done) {
+  done = false;
+  if (n > kSmallN && n <= kMidN && E <= kMaxE && sums.x != nullptr && sums.M * sums.KT * 16 < ((int64_t)1 << 31)) {
+    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
+    done = true;
+    return launch_status("moe_align (mid) + row group sums");
+  }
+  return launch_align(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes);
 }
 
 }  // namespace ccq

@@ -2146,16 +2146,20 @@ static int moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const floa
   float* rows = (float*)(ws + L.off_rows);
 
   CCQ_REQUIRE(L.max_tiles * 2 <= 65535, "ccq_moe_w4_ffn: too many tiles");
-  rc = launch_align(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st, ws + L.off_align,
-                    L.total - L.off_align);
-  if (rc) return rc;
   if (L.grouped) {
     const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
     CCQ_REQUIRE(T * H * 2 < (int64_t)1 << 32 && L.n * I * 2 < (int64_t)1 << 32,
                 "ccq_moe_w4_ffn: activations exceed 4 GiB");
     float* sx = (float*)(ws + L.off_sx);
     float* sxh = (float*)(ws + L.off_sxh);
-    rc = launch_row_group_sums(x, x_dtype == CCQ_BF16, H, T, H, sx, H / 128, st);
+    // the layer input's row group sums, in the schedule's launch where it is
+    // the one-workgroup kernel
+    bool sums_done = false;
+    const AlignSums as = {x, x_dtype == CCQ_BF16 ? 1 : 0, H, T, H / 128, sx, H / 128};
+    rc = launch_align_sums(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st,
+                           ws + L.off_align, L.total - L.off_align, as, sums_done);
+    if (rc) return rc;
+    if (!sums_done) rc = launch_row_group_sums(x, x_dtype == CCQ_BF16, H, T, H, sx, H / 128, st);
     if (rc) return rc;
     W4GP g = {};
     g.x = x;
@@ -2208,6 +2212,9 @@ static int moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const floa
     rc = launch_group_gemm<EPI_ROWS>(d, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.max_tiles, st);
     if (rc) return rc;
   } else {
+    rc = launch_align(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st,
+                      ws + L.off_align, L.total - L.off_align);
+    if (rc) return rc;
     rc = run_gate_up(x, x_dtype, k, sorted, tile_expert, meta, L.max_tiles, inter, ex, st);
     if (rc) return rc;
     rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
