@@ -94,6 +94,29 @@ __device__ void fill_padding_and_tiles(int nactive, int tile_m, const int* inv, 
   }
 }
 
+// Thread gt of the row group sums (AlignSums): 16 lanes per (row, group), 8
+// activations per lane summed in order, then across the 16 lanes by
+// butterfly -- the arithmetic of row_group_sums_kernel (ccq_w4.hip).
+__device__ void align_side_sums(const AlignSums& s, int64_t gt) {
+  const int64_t g = gt >> 4;
+  const int part = threadIdx.x & 15;
+  const bool ok = g < s.M * s.KT;
+  const int64_t row = ok ? g / s.KT : 0, kt = ok ? g - row * s.KT : 0;
+  float acc = 0.f;
+  if (ok) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(s.x) + row * s.ldx +
+                                                    kt * 128 + part * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t b = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      acc += s.x_bf16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
+  if (ok && part == 0) s.out[row * s.ldo + kt] = acc;
+}
+
 __global__ __launch_bounds__(1024) void moe_align_kernel(const int64_t* __restrict__ ids, int n, int E,
                                                          int tile_m, int32_t* __restrict__ sorted_ids,
                                                          int32_t* __restrict__ tile_expert,
@@ -449,7 +472,11 @@ __global__ __launch_bounds__(1024) void align_plan_kernel(int E, int nchunks, in
                                                           const int32_t* __restrict__ ccnt,
                                                           int32_t* __restrict__ cfirst, int32_t* __restrict__ sorted_ids,
                                                           int32_t* __restrict__ tile_expert, int32_t* __restrict__ meta,
-                                                          int32_t* __restrict__ counts_out) {
+                                                          int32_t* __restrict__ counts_out, const AlignSums sums) {
+  if (blockIdx.x > 0) {  // launched only with row group sums to run beside the plan
+    align_side_sums(sums, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
+    return;
+  }
   __shared__ int cnt[kMaxE], base[kMaxE], inv[kMaxE];
   __shared__ __align__(16) int key[kMaxE];  // first appearance, INT_MAX for unused experts
   __shared__ int nactive;
@@ -695,29 +722,6 @@ static void launch_align_small(const int64_t* ids, int n, int E, int tile_m, int
 constexpr int kMidN = 8192;
 constexpr int kMidStage = 16384;  // padded sorted-list length staged in LDS (64 KB)
 
-// Thread gt of the row group sums (AlignSums): 16 lanes per (row, group), 8
-// activations per lane summed in order, then across the 16 lanes by
-// butterfly -- the arithmetic of row_group_sums_kernel (ccq_w4.hip).
-__device__ void align_side_sums(const AlignSums& s, int64_t gt) {
-  const int64_t g = gt >> 4;
-  const int part = threadIdx.x & 15;
-  const bool ok = g < s.M * s.KT;
-  const int64_t row = ok ? g / s.KT : 0, kt = ok ? g - row * s.KT : 0;
-  float acc = 0.f;
-  if (ok) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(s.x) + row * s.ldx +
-                                                    kt * 128 + part * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t b = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      acc += s.x_bf16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
-    }
-  }
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, 64);
-  if (ok && part == 0) s.out[row * s.ldo + kt] = acc;
-}
-
 // Workgroup 0 builds the schedule; workgroups 1.. (launched only with row
 // group sums to run) take 1024 sum threads each.
 template <int NB, int CPW>
@@ -906,16 +910,22 @@ static void launch_align_mid(const int64_t* ids, int n, int E, int tile_m, int32
 
 size_t align_scratch_bytes(int64_t n, int64_t E) { return (size_t)2 * cdiv(n, kChunk) * E * 4; }
 
-int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
-                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
-                 size_t scratch_bytes) {
+// sums.x != nullptr: the row group sums also run, on extra workgroups of
+// the one-workgroup launch (mid-size kernel or chunked plan; done = true),
+// when the schedule has one; with the small and the generic kernels they
+// are left to the caller (done = false)
+static int launch_align_side(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                             int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
+                             size_t scratch_bytes, const AlignSums& sums, bool& done) {
+  done = false;
   const int64_t nchunks = cdiv(n, kChunk);
   if (n <= kSmallN && E <= kMaxE) {  // decode batches: one wave
     launch_align_small(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st);
     return launch_status("moe_align (small)");
   }
   if (n <= kMidN && E <= kMaxE) {  // one workgroup, straight-line matching
-    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st, AlignSums{});
+    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
+    done = sums.x != nullptr;
     return launch_status("moe_align (mid)");
   }
   // larger batches: three launches over many workgroups when there is
@@ -929,23 +939,30 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
   int32_t* cfirst = ccnt + nchunks * E;
   launch(align_chunk_count_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
                      cfirst);
-  launch(align_plan_kernel, dim3(1), dim3(1024), 0, st, (int)E, (int)nchunks, (int)tile_m, ccnt, cfirst,
-                     sorted_ids, tile_expert, meta, counts);
+  const unsigned pgrid = 1u + (sums.x != nullptr ? (unsigned)cdiv(sums.M * sums.KT * 16, 1024) : 0u);
+  launch(align_plan_kernel, dim3(pgrid), dim3(1024), 0, st, (int)E, (int)nchunks, (int)tile_m, ccnt, cfirst,
+                     sorted_ids, tile_expert, meta, counts, sums);
+  done = sums.x != nullptr;
   launch(align_chunk_scatter_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
                      cfirst, sorted_ids);
   return launch_status("moe_align (chunked)");
+}
+
+int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
+                 size_t scratch_bytes) {
+  bool done = false;
+  return launch_align_side(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes,
+                           AlignSums{}, done);
 }
 
 int launch_align_sums(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
                       int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
                       size_t scratch_bytes, const AlignSums& sums, bool& done) {
   done = false;
-  if (n > kSmallN && n <= kMidN && E <= kMaxE && sums.x != nullptr && sums.M * sums.KT * 16 < ((int64_t)1 << 31)) {
-    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
-    done = true;
-    return launch_status("moe_align (mid) + row group sums");
-  }
-  return launch_align(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes);
+  const bool fits = sums.x != nullptr && sums.M * sums.KT * 16 < ((int64_t)1 << 31);
+  return launch_align_side(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes,
+                           fits ? sums : AlignSums{}, done);
 }
 
 }  // namespace ccq
