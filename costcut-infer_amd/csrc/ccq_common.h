@@ -178,24 +178,29 @@ enum WqFmt { WQ_FP8_ROW = 0, WQ_INT8_ROW = 1, WQ_MXFP8 = 2, WQ_MXFP4 = 3 };
 int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale, int group_size, float scale2,
                    float* y, int64_t M, int64_t K, int64_t N, hipStream_t stream, const char* name);
 
-// ------------------------------------ schedule + row group sums (host) --
-// Row group sums run beside a schedule: out[r * ldo + g] = the float32 sum,
-// in a fixed order, of the 128 activations of group g of row r (r < M,
-// g < KT; x bf16 or f16, rows 16-byte aligned).  launch_align_sums
-// (ccq_route.hip) builds the schedule as launch_align does and, when the
-// schedule is the one-workgroup mid-size kernel, runs the sums in the same
-// launch on further workgroups (done = true); otherwise it launches nothing
-// of them (done = false).
-struct AlignSums {
+// ------------------------------- schedule + activation side work (host) --
+// Work on the layer input that runs beside a schedule, 16 threads per (row
+// r < M, 128-column group g < KT): ALIGN_SIDE_SUMS, out[r * ldo + g] = the
+// float32 sum, in a fixed order, of the group's 128 activations (x bf16 or
+// f16, rows 16-byte aligned).  launch_align_side (ccq_route.hip) builds the
+// schedule as launch_align does and, when the schedule has a one-workgroup
+// launch (the mid-size kernel or the chunked plan), runs the side work on
+// further workgroups of that launch (done = true); otherwise it launches
+// nothing of it (done = false).  (The FP8 activation quantizer beside the
+// chunked plan measured slower than its own launch: 43.7 against 16.5 +
+// 20.5 µs at 2048 x 7168.)
+enum AlignSideKind { ALIGN_SIDE_NONE = 0, ALIGN_SIDE_SUMS = 1 };
+struct AlignSide {
+  int kind;
   const void* x;
-  int x_bf16;
+  int x_dtype;
   int64_t ldx, M, KT;
   float* out;
   int64_t ldo;
 };
-int launch_align_sums(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+int launch_align_side(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
                       int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
-                      size_t scratch_bytes, const AlignSums& sums, bool& done);
+                      size_t scratch_bytes, const AlignSide& side, bool& done);
 
 // --------------------------------------------------------- wave helpers --
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }

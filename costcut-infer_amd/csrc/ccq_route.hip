@@ -94,10 +94,10 @@ __device__ void fill_padding_and_tiles(int nactive, int tile_m, const int* inv, 
   }
 }
 
-// Thread gt of the row group sums (AlignSums): 16 lanes per (row, group), 8
-// activations per lane summed in order, then across the 16 lanes by
-// butterfly -- the arithmetic of row_group_sums_kernel (ccq_w4.hip).
-__device__ void align_side_sums(const AlignSums& s, int64_t gt) {
+// Thread gt of the side work (AlignSide), the row group sums: 16 lanes per
+// (row, group), 8 activations per lane summed in order, then across the 16
+// lanes by butterfly -- the arithmetic of row_group_sums_kernel (ccq_w4.hip).
+__device__ void align_side_work(const AlignSide& s, int64_t gt) {
   const int64_t g = gt >> 4;
   const int part = threadIdx.x & 15;
   const bool ok = g < s.M * s.KT;
@@ -109,7 +109,7 @@ __device__ void align_side_sums(const AlignSums& s, int64_t gt) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const uint32_t b = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      acc += s.x_bf16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+      acc += s.x_dtype == CCQ_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
     }
   }
 #pragma unroll
@@ -472,9 +472,9 @@ __global__ __launch_bounds__(1024) void align_plan_kernel(int E, int nchunks, in
                                                           const int32_t* __restrict__ ccnt,
                                                           int32_t* __restrict__ cfirst, int32_t* __restrict__ sorted_ids,
                                                           int32_t* __restrict__ tile_expert, int32_t* __restrict__ meta,
-                                                          int32_t* __restrict__ counts_out, const AlignSums sums) {
-  if (blockIdx.x > 0) {  // launched only with row group sums to run beside the plan
-    align_side_sums(sums, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
+                                                          int32_t* __restrict__ counts_out, const AlignSide side) {
+  if (blockIdx.x > 0) {  // launched only with side work to run beside the plan
+    align_side_work(side, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
     return;
   }
   __shared__ int cnt[kMaxE], base[kMaxE], inv[kMaxE];
@@ -722,17 +722,17 @@ static void launch_align_small(const int64_t* ids, int n, int E, int tile_m, int
 constexpr int kMidN = 8192;
 constexpr int kMidStage = 16384;  // padded sorted-list length staged in LDS (64 KB)
 
-// Workgroup 0 builds the schedule; workgroups 1.. (launched only with row
-// group sums to run) take 1024 sum threads each.
+// Workgroup 0 builds the schedule; workgroups 1.. (launched only with side
+// work to run) take 1024 of its threads each.
 template <int NB, int CPW>
 __global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __restrict__ ids, int n, int E,
                                                              int tile_m, int32_t* __restrict__ sorted_ids,
                                                              int32_t* __restrict__ tile_expert,
                                                              int32_t* __restrict__ meta,
                                                              int32_t* __restrict__ counts_out,
-                                                             const AlignSums sums) {
+                                                             const AlignSide side) {
   if (blockIdx.x > 0) {
-    align_side_sums(sums, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
+    align_side_work(side, (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
     return;
   }
   __shared__ int wcnt[kAlignWaves * (1 << NB)];  // [wave][expert]: counts, then exclusive offsets
@@ -876,15 +876,15 @@ __global__ __launch_bounds__(1024) void moe_align_mid_kernel(const int64_t* __re
   }
 }
 
-// sums.x != nullptr: the row group sums on workgroups 1..
+// side.kind != ALIGN_SIDE_NONE: the side work on workgroups 1..
 template <int CPW>
 static void launch_align_mid_nb(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
                                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st,
-                                const AlignSums& sums) {
-  const unsigned grid = 1u + (sums.x != nullptr ? (unsigned)cdiv(sums.M * sums.KT * 16, 1024) : 0u);
+                                const AlignSide& side) {
+  const unsigned grid = 1u + (side.kind != ALIGN_SIDE_NONE ? (unsigned)cdiv(side.M * side.KT * 16, 1024) : 0u);
 #define CCQ_ALM(NB)                                                                                          \
   launch((moe_align_mid_kernel<NB, CPW>), dim3(grid), dim3(1024), 0, st, ids, n, E, tile_m, sorted_ids,     \
-         tile_expert, meta, counts, sums)
+         tile_expert, meta, counts, side)
   if (E <= 64)
     CCQ_ALM(6);
   else if (E <= 256)
@@ -897,26 +897,26 @@ static void launch_align_mid_nb(const int64_t* ids, int n, int E, int tile_m, in
 // kSmallN < n <= kMidN, E <= 1024
 static void launch_align_mid(const int64_t* ids, int n, int E, int tile_m, int32_t* sorted_ids,
                              int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st,
-                             const AlignSums& sums) {
+                             const AlignSide& side) {
   if (n <= 1024)
-    launch_align_mid_nb<1>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
+    launch_align_mid_nb<1>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, side);
   else if (n <= 2048)
-    launch_align_mid_nb<2>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
+    launch_align_mid_nb<2>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, side);
   else if (n <= 4096)
-    launch_align_mid_nb<4>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
+    launch_align_mid_nb<4>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, side);
   else
-    launch_align_mid_nb<8>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
+    launch_align_mid_nb<8>(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, side);
 }
 
 size_t align_scratch_bytes(int64_t n, int64_t E) { return (size_t)2 * cdiv(n, kChunk) * E * 4; }
 
-// sums.x != nullptr: the row group sums also run, on extra workgroups of
-// the one-workgroup launch (mid-size kernel or chunked plan; done = true),
-// when the schedule has one; with the small and the generic kernels they
-// are left to the caller (done = false)
-static int launch_align_side(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+// side.kind != ALIGN_SIDE_NONE: the side work also runs, on extra
+// workgroups of the one-workgroup launch (mid-size kernel or chunked plan;
+// done = true), when the schedule has one; with the small and the generic
+// kernels it is left to the caller (done = false)
+static int launch_align_impl(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
                              int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
-                             size_t scratch_bytes, const AlignSums& sums, bool& done) {
+                             size_t scratch_bytes, const AlignSide& side, bool& done) {
   done = false;
   const int64_t nchunks = cdiv(n, kChunk);
   if (n <= kSmallN && E <= kMaxE) {  // decode batches: one wave
@@ -924,8 +924,8 @@ static int launch_align_side(const int64_t* ids, int64_t n, int64_t E, int64_t t
     return launch_status("moe_align (small)");
   }
   if (n <= kMidN && E <= kMaxE) {  // one workgroup, straight-line matching
-    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st, sums);
-    done = sums.x != nullptr;
+    launch_align_mid(ids, (int)n, (int)E, (int)tile_m, sorted_ids, tile_expert, meta, counts, st, side);
+    done = side.kind != ALIGN_SIDE_NONE;
     return launch_status("moe_align (mid)");
   }
   // larger batches: three launches over many workgroups when there is
@@ -939,10 +939,10 @@ static int launch_align_side(const int64_t* ids, int64_t n, int64_t E, int64_t t
   int32_t* cfirst = ccnt + nchunks * E;
   launch(align_chunk_count_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
                      cfirst);
-  const unsigned pgrid = 1u + (sums.x != nullptr ? (unsigned)cdiv(sums.M * sums.KT * 16, 1024) : 0u);
+  const unsigned pgrid = 1u + (side.kind != ALIGN_SIDE_NONE ? (unsigned)cdiv(side.M * side.KT * 16, 1024) : 0u);
   launch(align_plan_kernel, dim3(pgrid), dim3(1024), 0, st, (int)E, (int)nchunks, (int)tile_m, ccnt, cfirst,
-                     sorted_ids, tile_expert, meta, counts, sums);
-  done = sums.x != nullptr;
+                     sorted_ids, tile_expert, meta, counts, side);
+  done = side.kind != ALIGN_SIDE_NONE;
   launch(align_chunk_scatter_kernel, dim3((unsigned)nchunks), dim3(256), 0, st, ids, (int)n, (int)E, ccnt,
                      cfirst, sorted_ids);
   return launch_status("moe_align (chunked)");
@@ -952,17 +952,17 @@ int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32
                  int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
                  size_t scratch_bytes) {
   bool done = false;
-  return launch_align_side(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes,
-                           AlignSums{}, done);
+  return launch_align_impl(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes,
+                           AlignSide{}, done);
 }
 
-int launch_align_sums(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+int launch_align_side(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
                       int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
-                      size_t scratch_bytes, const AlignSums& sums, bool& done) {
+                      size_t scratch_bytes, const AlignSide& side, bool& done) {
   done = false;
-  const bool fits = sums.x != nullptr && sums.M * sums.KT * 16 < ((int64_t)1 << 31);
-  return launch_align_side(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes,
-                           fits ? sums : AlignSums{}, done);
+  const bool fits = side.kind != ALIGN_SIDE_NONE && side.M * side.KT * 16 < ((int64_t)1 << 31);
+  return launch_align_impl(ids, n, E, tile_m, sorted_ids, tile_expert, meta, counts, st, scratch, scratch_bytes,
+                           fits ? side : AlignSide{}, done);
 }
 
 }  // namespace ccq

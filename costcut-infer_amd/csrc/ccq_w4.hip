@@ -2155,9 +2155,9 @@ static int moe_w4_ffn(const void* x, int x_dtype, const int64_t* ids, const floa
     // the layer input's row group sums, in the schedule's launch where it is
     // the one-workgroup kernel
     bool sums_done = false;
-    const AlignSums as = {x, x_dtype == CCQ_BF16 ? 1 : 0, H, T, H / 128, sx, H / 128};
-    rc = launch_align_sums(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st,
-                           ws + L.off_align, L.total - L.off_align, as, sums_done);
+    const AlignSide side = {ALIGN_SIDE_SUMS, x, x_dtype, H, T, H / 128, sx, H / 128};
+    rc = launch_align_side(ids, L.n, ex->num_experts, L.tile_m, sorted, tile_expert, meta, counts, st,
+                           ws + L.off_align, L.total - L.off_align, side, sums_done);
     if (rc) return rc;
     if (!sums_done) rc = launch_row_group_sums(x, x_dtype == CCQ_BF16, H, T, H, sx, H / 128, st);
     if (rc) return rc;
