@@ -178,6 +178,20 @@ enum WqFmt { WQ_FP8_ROW = 0, WQ_INT8_ROW = 1, WQ_MXFP8 = 2, WQ_MXFP4 = 3 };
 int wq_mfma_linear(int fmt, const float* x, const uint8_t* w, const void* scale, int group_size, float scale2,
                    float* y, int64_t M, int64_t K, int64_t N, hipStream_t stream, const char* name);
 
+// ------------------------------ expert schedule and combine (host side) --
+// ccq_route.hip: the expert-sorted schedule of ccq_moe_align (scratch: the
+// per-chunk tables of the many-workgroup form, align_scratch_bytes; without
+// it larger batches take the one-workgroup kernel) and the weighted combine
+// of ccq_moe_combine (rows float32 or bf16; shared: the shared expert's
+// output, added after the routed sum).
+int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
+                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch = nullptr,
+                 size_t scratch_bytes = 0);
+size_t align_scratch_bytes(int64_t n, int64_t E);
+int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
+                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared = nullptr,
+                   float shared_gate = 0.f);
+
 // ------------------------------- schedule + activation side work (host) --
 // Work on the layer input that runs beside a schedule, 16 threads per (row
 // r < M, 128-column group g < KT): ALIGN_SIDE_SUMS, out[r * ldo + g] = the

@@ -26,14 +26,6 @@
 
 namespace ccq {
 
-int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
-                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
-                 size_t scratch_bytes);
-size_t align_scratch_bytes(int64_t n, int64_t E);
-int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
-                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared,
-                   float shared_gate);
-
 constexpr int FG_BM = 64, FG_BN = 64, FG_BK = 16, FG_THREADS = 256;
 // LDS row stride in floats: an MFMA operand read takes 16 consecutive words
 // from each of 4 slab rows; 16 words of padding put the 4 rows' words in

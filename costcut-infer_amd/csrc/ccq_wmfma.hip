@@ -35,14 +35,6 @@
 
 namespace ccq {
 
-int launch_align(const int64_t* ids, int64_t n, int64_t E, int64_t tile_m, int32_t* sorted_ids,
-                 int32_t* tile_expert, int32_t* meta, int32_t* counts, hipStream_t st, void* scratch,
-                 size_t scratch_bytes);
-size_t align_scratch_bytes(int64_t n, int64_t E);
-int launch_combine(const void* rows, int rows_dtype, const float* wts, const int64_t* ids, int64_t E, void* y,
-                   int y_dtype, int64_t T, int64_t k, int64_t H, hipStream_t st, const float* shared,
-                   float shared_gate);
-
 constexpr int WQ_KC = 256;                 // k per chunk
 constexpr int WQ_CG = 4;                   // 16-column groups per workgroup
 constexpr int WQ_THREADS = 512;            // 8 waves: 4 column groups x 2 k halves
