@@ -233,11 +233,13 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   const int nx = ((int)gridDim.x - xcd + 7) >> 3;
   const int items_x = (ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0) * nblk;
   if (wx >= items_x) return;
-  const int nmine = (items_x - wx + nx - 1) / nx;
+  // rounds of nx items in alternating direction, as in the int4 kernel
+  auto item_of = [&](int j) { return j * nx + ((j & 1) ? nx - 1 - wx : wx); };
+  const int nmine = items_x / nx + (item_of(items_x / nx) < items_x ? 1 : 0);
   const int KB = p.KB;
   const int total = nmine * KB;
 
-  auto tile_of = [&](int j) { return xcd + 8 * ((wx + j * nx) / nblk); };
+  auto tile_of = [&](int j) { return xcd + 8 * (item_of(j) / nblk); };
   // row ids of item j into Rid[j % 3] (+ expert id copies): DMA from the
   // schedule, or the rows of a dense tile; called two items ahead
   auto fetch_rows = [&](int j) {
@@ -274,8 +276,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_kernel(const Fp8GP p) {
   const bool has_sw = wave >= 6 && wave - 6 < NSW;
   const int ncopy = NA + BPW + (has_sa ? 1 : 0) + (has_sw ? 1 : 0);
   auto make_plan = [&](int j, Plan& P) {
-    const int li = wx + j * nx;
-    P.nb = li % nblk;
+    P.nb = item_of(j) % nblk;
     const int* R = Rid[j % 3];
     const int ex = p.tile_expert != nullptr ? __builtin_amdgcn_readfirstlane(R[F8_BM]) : 0;
     P.nvalid = (int)(__popcll(__ballot(R[lane] >= 0)) + __popcll(__ballot(R[64 + lane] >= 0)));
@@ -595,10 +596,12 @@ __global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
   const int nx = ((int)gridDim.x - xcd + 7) >> 3;
   const int items_x = (ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0) * nblk;
   if (wx >= items_x) return;
-  const int nmine = (items_x - wx + nx - 1) / nx;
+  // rounds of nx items in alternating direction, as in the int4 kernel
+  auto item_of = [&](int j) { return j * nx + ((j & 1) ? nx - 1 - wx : wx); };
+  const int nmine = items_x / nx + (item_of(items_x / nx) < items_x ? 1 : 0);
   const int KB = p.KB;
 
-  auto tile_of = [&](int j) { return xcd + 8 * ((wx + j * nx) / nblk); };
+  auto tile_of = [&](int j) { return xcd + 8 * (item_of(j) / nblk); };
   auto fetch_rows = [&](int j) {  // row ids of item j (+ its expert) into Rid[j % 3], by DMA
     if (j >= nmine) return;
     const int tile = tile_of(j);
@@ -628,8 +631,7 @@ __global__ __launch_bounds__(RB_NW * 64) void fp8_moe_rb_kernel(const Fp8GP p) {
   auto make_plan = [&](int j, Plan& P) {
     // (lane values recomputed here, not kept live across the K loop)
     const int lane = lane_id_here(), c32 = lane & 31, h = lane >> 5;
-    const int li = wx + j * nx;
-    P.nb = li % nblk;
+    P.nb = item_of(j) % nblk;
     const int* R = Rid[j % 3];
     const int ex = __builtin_amdgcn_readfirstlane(R[F8_BM]);
     P.nvalid = (int)(__popcll(__ballot(R[lane] >= 0)) + __popcll(__ballot(R[64 + lane] >= 0)));

@@ -1227,13 +1227,20 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
   const int nx = ((int)gridDim.x - xcd + 7) >> 3;
   const int items_x = (ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0) * nblk;
   if (wx >= items_x) return;
-  const int nmine = (items_x - wx + nx - 1) / nx;
+  // Items are dealt in rounds of nx, alternating direction: the workgroup
+  // that takes a round's first item takes the next round's last.  The
+  // schedule lists experts by first appearance, which tends to put the full
+  // tiles of often-routed experts early and part-filled tiles late, so the
+  // alternation pairs heavy items with light ones (measured against plain
+  // round-robin: T=512 top-8 layer, 128 experts, gate/up -5%, down -13%).
+  auto item_of = [&](int j) { return j * nx + ((j & 1) ? nx - 1 - wx : wx); };
+  const int nmine = items_x / nx + (item_of(items_x / nx) < items_x ? 1 : 0);
   const int KT = p.KT;
   const int total = nmine * KT;  // k-steps of this workgroup
 
   // ---- row ids: rows of item j go to Rid[j % 3], copied (DMA) at the first
   // k-step of item j - 2; Rid[.][GG_BM..] holds the item's expert ----
-  auto tile_of = [&](int j) { return xcd + 8 * ((wx + j * nx) / nblk); };
+  auto tile_of = [&](int j) { return xcd + 8 * (item_of(j) / nblk); };
   auto fetch_rows = [&](int j) {  // waves 5..7
     if (j >= nmine) return;
     const int tile = tile_of(j);
@@ -1261,8 +1268,7 @@ __global__ __launch_bounds__(512) void w4_group_gemm_kernel(const W4GP p) {
   const bool has_sx = wave == 4 || wave == 5;
   const int ncopy = 4 + BPW + (has_sz ? 1 : 0) + (has_sx ? 1 : 0);
   auto make_plan = [&](int j, Plan& P) {
-    const int li = wx + j * nx;
-    P.nb = li % nblk;
+    P.nb = item_of(j) % nblk;
     const int* R = Rid[j % 3];
     const int ex = p.tile_expert != nullptr ? __builtin_amdgcn_readfirstlane(R[GG_BM]) : 0;
     // valid rows form a prefix of the tile
