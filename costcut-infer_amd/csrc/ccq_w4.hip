@@ -581,6 +581,18 @@ struct W4SP {
   int32_t* sched_tile_expert;  // [tiles]
   int32_t* sched_meta;         // [2]
   int32_t* sched_counts;       // [rE]
+  // routed down stage (EPI_ROWS with ROUTE): the assignments' rows of x are
+  // the MFMA rows (rT of them, at most 16); rows, tile_expert and meta are the
+  // gate/up stage's schedule (tiles = its capacity); every workgroup takes
+  // one 16-column block across all tiles and combines the assignments'
+  // rows into y [cT, N]: y[t] = sum over slots of cwts[t*ck + s] * row
+  // (slots with cids outside [0, cE) skipped), as moe_combine_kernel does
+  const float* cwts;
+  const int64_t* cids;
+  int64_t cE;
+  void* cy;
+  int64_t ldcy;
+  int cy_dtype, cT, ck;
 };
 
 // ---- routing of a decode batch inside a workgroup ----
@@ -779,6 +791,11 @@ __device__ void route_schedule(const W4SP& p, RouteSmem& rs) {
 }
 
 constexpr int WS_DEPTH = 2;  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
+// Routed down stage with the combine: at most RD_MAXA assignments (one
+// 16-row MFMA tile), RD_DEPTH jobs in flight per wave (a workgroup's jobs
+// are one per routed expert, so all of them at once for up to six experts)
+constexpr int RD_MAXA = 16;
+constexpr int RD_DEPTH = 6;
 constexpr int RT_LEAD = 2;   // jobs workgroup 0 of a routed gate/up stage gives up for building the schedule
 
 // Quads per job of the streaming kernel for a stage of N columns and K rows
@@ -796,7 +813,10 @@ static int stream_nq(int EPI, int64_t N, int64_t K, int64_t G) {
 template <typename AT, typename ST, int EPI, int MT, int NQ, bool ROUTE = false>
 __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   using V = typename Act<AT>::vec;
-  constexpr int D = WS_DEPTH;
+  // routed down stage with the combine (see W4SP): a workgroup's jobs are
+  // one column block of each routed expert, all of them in flight at once
+  constexpr bool RDOWN = ROUTE && EPI == EPI_ROWS;
+  constexpr int D = RDOWN ? RD_DEPTH : WS_DEPTH;
   static_assert(EPI != EPI_SILU || NQ == 2, "gate and up quads");
   static_assert(MT * NQ <= 4, "one scale/zero word per lane covers a wave's share of a job");
   static_assert(D % 2 == 0, "jobs are reduced in pairs");
@@ -811,8 +831,10 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // the routing scratch lives in the partial-sum buffer, unused until the
   // first job
   RouteSmem& rs = *reinterpret_cast<RouteSmem*>(&part[0][0][0][0][0]);
-  static_assert(!ROUTE || (EPI == EPI_SILU && sizeof(RouteSmem) <= sizeof(part)), "routing in gate/up only");
-  constexpr bool routed = ROUTE;  // p.logits is set exactly for this instance
+  static_assert(!ROUTE || EPI == EPI_ROWS || (EPI == EPI_SILU && sizeof(RouteSmem) <= sizeof(part)),
+                "routing in gate/up only");
+  static_assert(!RDOWN || NQ == 1, "routed down: 16-column blocks");
+  constexpr bool routed = ROUTE;  // token (or assignment) rows; p.logits is set exactly for routed gate/up
   const int r16 = lane & 15, kq = lane >> 4;
   // activation fragments, lane r16 holding MFMA row r16.  A routed batch
   // (T <= 16 tokens) multiplies every expert's weights by all its tokens:
@@ -836,7 +858,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // (unused with token rows)
   int* const ste = reinterpret_cast<int*>(&xb[0]);
   int* const tok2a = ste + RT_MAXTILES;
-  static_assert(!ROUTE || (MT == 2 && (RT_MAXTILES * 17) * 4 <= XB * 16), "routed tables fit the fragment area");
+  float* const rv = reinterpret_cast<float*>(tok2a + RT_MAXTILES * 16);  // routed down: [16 assignments][16 columns]
+  static_assert(!ROUTE || (MT == 2 && (RT_MAXTILES * 17 + 256) * 4 <= XB * 16), "routed tables fit the fragment area");
   // ---- the weight stream: a wave's share of one job is MT x NQ tiles (16 B
   // per lane) and the scale/zero words of its k-tiles for the 16 columns of
   // each quad (lane l: column l & 15, (m, q) pair l >> 4).  Every load is
@@ -878,7 +901,20 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   uint32_t zv[D];
 
   int ntiles, lead = 0;
-  if constexpr (routed) {
+  if constexpr (RDOWN) {
+    // the gate/up stage's schedule (at most RD_MAXA assignments, so at most
+    // that many one-tile experts), read in one round trip up to its
+    // capacity: ste[tile] = expert, tok2a[tile][a] = a for its assignments
+    const int cap = min(p.tiles, RD_MAXA);
+    const int rw = tid < cap * 16 ? p.rows[tid] : -1;
+    const int te = tid < cap ? p.tile_expert[tid] : 0;
+    ntiles = min(p.meta[0], cap);
+    for (int i = tid; i < RD_MAXA * 16; i += blockDim.x) tok2a[i] = -1;
+    lds_barrier();
+    if (tid < ntiles * 16 && rw >= 0 && rw < RD_MAXA) tok2a[(tid >> 4) * 16 + rw] = rw;
+    if (tid < ntiles) ste[tid] = te;
+    lds_barrier();
+  } else if constexpr (routed) {
     // The job tiles are the routed experts in id order (tile r: expert
     // ste[r]), straight from the top-k: the gate/up jobs need no schedule,
     // so the weight loads start right after it.  Workgroup 0 builds the
@@ -921,15 +957,36 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // faster than contiguous ranges on a load-only copy of the stream; for
   // the routed stage, whose consecutive jobs then change experts, 12%
   // slower)
-  constexpr bool IL = EPI == EPI_STORE;
+  constexpr bool IL = EPI == EPI_STORE || RDOWN;  // routed down: gridDim.x = column blocks
   const int J = ntiles * NJ;
   auto split = [&](int b) { return b == 0 ? 0 : max(0, (int)((int64_t)b * (J + lead) / gridDim.x) - lead); };
   const int lo = IL ? (int)blockIdx.x : split(blockIdx.x);
   const int hi = IL ? J : split(blockIdx.x + 1);
+  // routed down: the combine of moe_combine_kernel for this block's 16
+  // columns (slots in order, fmaf, slots of dropped assignments skipped)
+  auto combine = [&]() {
+    if (tid < p.cT * 16) {
+      const int t = tid >> 4, c = tid & 15;
+      float acc = 0.f;
+      for (int s = 0; s < p.ck; ++s) {
+        const int a = t * p.ck + s;
+        const int64_t e = p.cids[a];
+        if (e >= 0 && e < p.cE) acc = fmaf(p.cwts[a], rv[a * 16 + c], acc);
+      }
+      const int64_t o = (int64_t)t * p.ldcy + (int64_t)blockIdx.x * 16 + c;
+      if (p.cy_dtype == CCQ_F32)
+        reinterpret_cast<float*>(p.cy)[o] = acc;
+      else if (p.cy_dtype == CCQ_BF16)
+        reinterpret_cast<uint16_t*>(p.cy)[o] = (uint16_t)f32_to_bf16_bits(acc);
+      else
+        reinterpret_cast<uint16_t*>(p.cy)[o] = (uint16_t)f32_to_f16_bits(acc);
+    }
+  };
   if (lo >= hi) {
-    if constexpr (routed) {
+    if constexpr (routed && !RDOWN) {
       if (blockIdx.x == 0) route_schedule(p, rs);
     }
+    if constexpr (RDOWN) combine();  // no routed assignment: zeros
     return;
   }
   const int n = IL ? (hi - lo + (int)gridDim.x - 1) / (int)gridDim.x : hi - lo;
@@ -982,7 +1039,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   };
 #pragma unroll
   for (int d = 0; d < D; ++d) load(d, wv[d], zv[d]);
-  if constexpr (routed) {
+  if constexpr (routed && !RDOWN) {
     if (blockIdx.x == 0) route_schedule(p, rs);
   }
 
@@ -1080,6 +1137,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     if constexpr (EPI == EPI_SILU) {
       const float g = v[0], up = v[1];
       store_val(p.y, o + nj * 16, g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * up, p.y_dtype);
+    } else if constexpr (RDOWN) {
+      (void)o;
+      rv[orow * 16 + (l & 15)] = v[0];  // the assignment's row, this block's columns
     } else {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) store_val(p.y, o + (nj * NQ + q) * 16, v[q], p.y_dtype);
@@ -1125,6 +1185,10 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
       compute(wv[d], zv[d], (i >> 1) & 1, i & 1);
     }
     if ((d & 1) && i - 1 < n) pair_done(i);
+  }
+  if constexpr (RDOWN) {
+    lds_barrier();  // every job's rows in rv
+    combine();
   }
 }
 
@@ -2302,6 +2366,63 @@ static int launch_route_gate_up(const void* x, int x_dtype, const float* logits,
   return launch_stream<EPI_SILU>(w, 2, x_dtype == CCQ_BF16, ex->scale_dtype == CCQ_BF16, L.max_tiles, st);
 }
 
+// The down stage and the combine of a decode batch of at most RD_MAXA
+// assignments in one launch, on the schedule the routed gate/up stage
+// published: one workgroup per 16 output columns takes that block of every
+// routed expert (the assignments' intermediate rows are its MFMA rows) and
+// writes y as moe_combine_kernel does, bit for bit (each row's products are
+// the down stage's, and the slots are summed in the same order).
+static bool route_down_fits(const ccq_w4_experts* ex, int64_t T, int64_t ks) {
+  return T * ks <= RD_MAXA && ex->group_size == 128 && ex->hidden % 16 == 0 && ex->inter % 128 == 0 &&
+         ex->inter / 128 <= 16;
+}
+
+static int launch_route_down(const void* inter, int x_dtype, int64_t T, int64_t ks, const int64_t* ids,
+                             const float* wts, void* y, int y_dtype, const ccq_w4_experts* ex, char* ws,
+                             const MoeLayout& L, hipStream_t st) {
+  const int64_t H = ex->hidden, I = ex->inter, G = ex->group_size;
+  W4SP w = {};
+  w.x = inter;
+  w.ldx = I;
+  w.rows = (const int32_t*)(ws + L.off_sorted);
+  w.row_div = 1;
+  w.tile_expert = (const int32_t*)(ws + L.off_tile_expert);
+  w.meta = (const int32_t*)(ws + L.off_meta);
+  w.tiles = (int)L.max_tiles;
+  w.w0 = (const uint32_t*)ex->w_down;
+  w.sz0 = ex->sz_down;
+  w.szw = (int)sz_words_per_column(I, G);
+  w.w_es = I * H / 8;
+  w.sz_es = H * w.szw;
+  w.N = (int)H;
+  w.K = (int)I;
+  w.KT = (int)(I / 128);
+  w.nib_mask = 0x000F000Fu;
+  w.rT = (int)(T * ks);
+  w.cwts = wts;
+  w.cids = ids;
+  w.cE = ex->num_experts;
+  w.cy = y;
+  w.ldcy = H;
+  w.cy_dtype = y_dtype;
+  w.cT = (int)T;
+  w.ck = (int)ks;
+  const dim3 grid((unsigned)(H / 16)), block(512);
+  const bool xb = x_dtype == CCQ_BF16, sb = ex->scale_dtype == CCQ_BF16;
+  if (xb) {
+    if (sb)
+      launch((w4_stream_kernel<__bf16, __bf16, EPI_ROWS, 2, 1, true>), grid, block, 0, st, w);
+    else
+      launch((w4_stream_kernel<__bf16, _Float16, EPI_ROWS, 2, 1, true>), grid, block, 0, st, w);
+  } else {
+    if (sb)
+      launch((w4_stream_kernel<_Float16, __bf16, EPI_ROWS, 2, 1, true>), grid, block, 0, st, w);
+    else
+      launch((w4_stream_kernel<_Float16, _Float16, EPI_ROWS, 2, 1, true>), grid, block, 0, st, w);
+  }
+  return launch_status("w4 routed down + combine");
+}
+
 extern "C" int ccq_moe_w4_route_gate_up(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
                                         int mode, int64_t* ids_out, float* weights_out, const ccq_w4_experts* ex,
                                         void* workspace, size_t workspace_bytes, void* stream) {
@@ -2345,6 +2466,8 @@ extern "C" int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logit
   // gate/up + SiLU with the routing done inside its workgroups
   rc = launch_route_gate_up(x, x_dtype, logits, T, k, mode, ids, wts, ex, ws, L, st);
   if (rc) return rc;
+  if (route_down_fits(ex, T, k))  // down and combine in one launch
+    return launch_route_down(inter, x_dtype, T, k, ids, wts, y, y_dtype, ex, ws, L, st);
   rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
   if (rc) return rc;
   return launch_combine(rows, CCQ_F32, wts, ids, ex->num_experts, y, y_dtype, T, k, H, st);
@@ -2405,6 +2528,8 @@ extern "C" int ccq_moe_w4_forward_shared(const void* x, int x_dtype, const float
   float* rows = (float*)(ws + L.off_rows);
   rc = launch_route_gate_up(x, x_dtype, logits, T, k, mode, ids, wts, ex, ws, L, st, 1, shared_gate);
   if (rc) return rc;
+  if (route_down_fits(ex, T, ks))  // down and combine in one launch
+    return launch_route_down(inter, x_dtype, T, ks, ids, wts, y, y_dtype, ex, ws, L, st);
   rc = run_down(inter, x_dtype, sorted, tile_expert, meta, L.max_tiles, rows, ex, st);
   if (rc) return rc;
   return launch_combine(rows, CCQ_F32, wts, ids, ex->num_experts, y, y_dtype, T, ks, ex->hidden, st);
