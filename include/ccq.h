@@ -394,15 +394,15 @@ int ccq_moe_w4_ffn_shared(const void* x, int x_dtype, const int64_t* ids, const 
  * receive the routing (either may be null: the workspace keeps it);
  * workspace as ccq_moe_w4_ffn.  Decode batches (T <= 16, T*k <= 256, E <= 256,
  * T*E <= 4096, k <= 16) route inside the gate/up kernel's workgroups (three launches in
- * all); larger ones run the routing kernel and ccq_moe_w4_ffn.  Same results
- * either way.  Replaces moe_forward (models/generic.py:348-378): topk_softmax
+ * all; two when T*k <= 16, whose down kernel also combines); larger ones run
+ * the routing kernel and ccq_moe_w4_ffn.  Same results either way.  Replaces moe_forward (models/generic.py:348-378): topk_softmax
  * + expert grouping + expert_ffn + combine. */
 int ccq_moe_w4_forward(const void* x, int x_dtype, const float* logits, int64_t T, int64_t k,
                        int mode, int64_t* ids_out, float* weights_out, void* y, int y_dtype,
                        const ccq_w4_experts* ex, void* workspace, size_t workspace_bytes,
                        void* stream);
 
-/* The first of ccq_moe_w4_forward's three launches for a decode batch: the
+/* The first of ccq_moe_w4_forward's launches for a decode batch: the
  * gate/up + SiLU kernel that routes the batch inside its workgroups, leaving
  * the routing (ids_out / weights_out, or the workspace), the expert schedule
  * and the intermediate in the workspace exactly as ccq_moe_w4_forward does
