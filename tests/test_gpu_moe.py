@@ -137,12 +137,16 @@ def test_moe_w4_forward_matches_routed_ffn(gpu, E, H, I, T, k, norm):
     assert torch.equal(out, y_ref)
 
 
-@pytest.mark.parametrize("T,k,ydt", [(1, 6, torch.bfloat16), (16, 6, torch.float32), (16, 6, torch.bfloat16),
+@pytest.mark.parametrize("T,k,ydt", [(1, 6, torch.bfloat16), (2, 6, torch.bfloat16), (2, 8, torch.float32),
+                                      (3, 5, torch.float16), (16, 6, torch.float32), (16, 6, torch.bfloat16),
                                       (40, 4, torch.float16), (64, 6, torch.float32), (65, 6, torch.float32)])
 def test_moe_w4_layer_matches_stage_kernels(gpu, T, k, ydt):
     """The layer calls (routing inside the gate/up kernel for moe_forward_w4)
     give the same bits as the stage entry points run one by one: moe_align,
-    ccq_moe_w4_gate_up, ccq_moe_w4_down, ccq_moe_combine."""
+    ccq_moe_w4_gate_up, ccq_moe_w4_down, ccq_moe_combine.  Batches of at most
+    16 assignments (T=1..3 here, 16 at T=2 top-8) take the forward's
+    down-and-combine launch, whose slot sums must follow the combine's order
+    also when tokens share experts."""
     from ccut import _dev
     from ccut._lib import call
     from ccut.blocks import moe
