@@ -68,6 +68,76 @@ __global__ __launch_bounds__(256) void fp8_act_quant_kernel(const void* __restri
   }
 }
 
+// The same with 16-byte loads (x 16-byte aligned, ldx a multiple of 8 bf16 /
+// f16 or 4 float32 values), the 16-lane amax on DPP moves (max is a
+// selection, so the order of the steps does not change it) and the
+// hardware RNE conversion (v_cvt_pk_fp8_f32, equal to f32_to_fp8_rne for
+// every |v| <= 460; here |v| <= 448 (1 + 2^-22)); a lane with a NaN among
+// its quotients (a NaN or infinite input) encodes them in software (NaN ->
+// 0x7F whatever its sign).
+template <int XT>
+__global__ __launch_bounds__(256) void fp8_act_quant_vec_kernel(const void* __restrict__ x, int64_t ldx,
+                                                                uint8_t* __restrict__ q, int64_t ldq,
+                                                                float* __restrict__ s, int64_t lds_,
+                                                                int64_t rows, int64_t KB) {
+  const int lane = threadIdx.x & 63;
+  const int sub = lane & 15;
+  const int64_t nblk = rows * KB;
+  const int64_t stride = (int64_t)gridDim.x * 16;
+  for (int64_t b = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; b < nblk; b += stride) {
+    const int64_t row = b / KB, kb = b - row * KB;
+    const int64_t c0 = kb * 128 + 8 * sub;
+    float v[8];
+    if constexpr (XT == CCQ_F32) {
+      const f32x4* xp = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(x) + row * ldx + c0);
+      const f32x4 a = xp[0], c = xp[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = c[e];
+      }
+    } else {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(x) + row * ldx + c0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t h = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        v[e] = XT == CCQ_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+      }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0xB1, 0xf, 0xf, false)));
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x4E, 0xf, 0xf, false)));
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x124, 0xf, 0xf, false)));
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x128, 0xf, 0xf, false)));
+    const float sc = fmaxf(amax, kAmaxFloor) / kFp8Max;
+    float d[8];
+    bool nan = false;  // a NaN or infinite input makes a NaN quotient
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      d[e] = v[e] / sc;
+      nan = nan || d[e] != d[e];
+    }
+    uint32_t lo, hi;
+    if (!nan) {
+      int a = __builtin_amdgcn_cvt_pk_fp8_f32(d[0], d[1], 0, false);
+      lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(d[2], d[3], a, true);
+      int c = __builtin_amdgcn_cvt_pk_fp8_f32(d[4], d[5], 0, false);
+      hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(d[6], d[7], c, true);
+    } else {
+      lo = 0;
+      hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lo |= f32_to_fp8_rne(d[e]) << (8 * e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hi |= f32_to_fp8_rne(d[4 + e]) << (8 * e);
+    }
+    *reinterpret_cast<uint2*>(q + row * ldq + c0) = make_uint2(lo, hi);
+    if (sub == 0) s[row * lds_ + kb] = sc;
+  }
+}
+
 // ----------------------------------------------------------- re-pack --
 // Tiled layout: 2 KiB chunks, one per (16-column tile nt, K block kb), in
 // the order [nt / 8][kb][nt % 8]: the 8 tiles of a 128-column block are
@@ -1062,6 +1132,15 @@ int launch_act_quant(const void* x, int x_dtype, int64_t ldx, int64_t rows, int6
                      float* s, int64_t lds_, hipStream_t st) {
   const int64_t KB = K / 128;
   const dim3 grid(grid_of(rows * KB * 16, 256));
+  if (aligned(x, 16) && ldx % (x_dtype == CCQ_F32 ? 4 : 8) == 0) {
+    if (x_dtype == CCQ_BF16)
+      launch(fp8_act_quant_vec_kernel<CCQ_BF16>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
+    else if (x_dtype == CCQ_F16)
+      launch(fp8_act_quant_vec_kernel<CCQ_F16>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
+    else
+      launch(fp8_act_quant_vec_kernel<CCQ_F32>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
+    return launch_status("fp8 act quant");
+  }
   if (x_dtype == CCQ_BF16)
     launch(fp8_act_quant_kernel<CCQ_BF16>, grid, dim3(256), 0, st, x, ldx, q, ldq, s, lds_, rows, KB);
   else if (x_dtype == CCQ_F16)
