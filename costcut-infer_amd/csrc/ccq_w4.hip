@@ -859,7 +859,10 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   int* const ste = reinterpret_cast<int*>(&xb[0]);
   int* const tok2a = ste + RT_MAXTILES;
   float* const rv = reinterpret_cast<float*>(tok2a + RT_MAXTILES * 16);  // routed down: [16 assignments][16 columns]
-  static_assert(!ROUTE || (MT == 2 && (RT_MAXTILES * 17 + 256) * 4 <= XB * 16), "routed tables fit the fragment area");
+  float* const cw_s = rv + RD_MAXA * 16;                                   // routed down: slot weights,
+  int* const cok_s = reinterpret_cast<int*>(cw_s + RD_MAXA);               // and whether the slot is routed
+  static_assert(!ROUTE || (MT == 2 && (RT_MAXTILES * 17 + RD_MAXA * 18) * 4 <= XB * 16),
+                "routed tables fit the fragment area");
   // ---- the weight stream: a wave's share of one job is MT x NQ tiles (16 B
   // per lane) and the scale/zero words of its k-tiles for the 16 columns of
   // each quad (lane l: column l & 15, (m, q) pair l >> 4).  Every load is
@@ -908,7 +911,15 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     const int cap = min(p.tiles, RD_MAXA);
     const int rw = tid < cap * 16 ? p.rows[tid] : -1;
     const int te = tid < cap ? p.tile_expert[tid] : 0;
+    // the combine's slot weights and ids, in the same round trip
+    const int na = p.cT * p.ck;
+    const float cw = tid < na ? p.cwts[tid] : 0.f;
+    const int64_t ci = tid < na ? p.cids[tid] : -1;
     ntiles = min(p.meta[0], cap);
+    if (tid < na) {
+      cw_s[tid] = cw;
+      cok_s[tid] = ci >= 0 && ci < p.cE ? 1 : 0;
+    }
     for (int i = tid; i < RD_MAXA * 16; i += blockDim.x) tok2a[i] = -1;
     lds_barrier();
     if (tid < ntiles * 16 && rw >= 0 && rw < RD_MAXA) tok2a[(tid >> 4) * 16 + rw] = rw;
@@ -970,8 +981,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
       float acc = 0.f;
       for (int s = 0; s < p.ck; ++s) {
         const int a = t * p.ck + s;
-        const int64_t e = p.cids[a];
-        if (e >= 0 && e < p.cE) acc = fmaf(p.cwts[a], rv[a * 16 + c], acc);
+        if (cok_s[a]) acc = fmaf(cw_s[a], rv[a * 16 + c], acc);
       }
       const int64_t o = (int64_t)t * p.ldcy + (int64_t)blockIdx.x * 16 + c;
       if (p.cy_dtype == CCQ_F32)
@@ -1030,11 +1040,15 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     if constexpr (MT == 2) load_frags(b, rB / p.row_div);
   }
 
+  // routed down: lane l holds the expert of tile l (at most RD_MAXA tiles),
+  // so a job's expert is a readlane rather than an LDS round trip
+  const int ste_v = RDOWN && lane < ntiles ? ste[lane] : 0;
   auto load = [&](int i, u32x4 (&w)[MT][NQ], uint32_t& z) {
     const bool real = i < n;
     const int job = job_of(real ? i : 0);
     const int tl = job / NJ, nj = job - tl * NJ;
-    const int e_x = routed ? __builtin_amdgcn_readfirstlane(ste[tl]) : (tl == tA ? exA : exB);
+    const int e_x = RDOWN ? __builtin_amdgcn_readlane(ste_v, tl)
+                          : (routed ? __builtin_amdgcn_readfirstlane(ste[tl]) : (tl == tA ? exA : exB));
     load_ej(e_x, nj, real, w, z);
   };
 #pragma unroll
