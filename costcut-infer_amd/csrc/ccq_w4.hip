@@ -999,7 +999,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     if constexpr (RDOWN) combine();  // no routed assignment: zeros
     return;
   }
-  const int n = IL ? (hi - lo + (int)gridDim.x - 1) / (int)gridDim.x : hi - lo;
+  const int n = RDOWN ? ntiles : (IL ? (hi - lo + (int)gridDim.x - 1) / (int)gridDim.x : hi - lo);
   const int tA = IL ? 0 : lo / NJ, ntl = IL ? 1 : (hi - 1) / NJ - tA + 1;  // the range covers 1 or 2 tiles
   const int tB = ntl > 1 ? tA + 1 : tA;
   auto job_of = [&](int i) { return IL ? lo + i * (int)gridDim.x : lo + i; };
@@ -1046,7 +1046,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   auto load = [&](int i, u32x4 (&w)[MT][NQ], uint32_t& z) {
     const bool real = i < n;
     const int job = job_of(real ? i : 0);
-    const int tl = job / NJ, nj = job - tl * NJ;
+    // routed down: job i is tile i of this workgroup's column block
+    const int tl = RDOWN ? (real ? i : 0) : job / NJ, nj = RDOWN ? (int)blockIdx.x : job - tl * NJ;
     const int e_x = RDOWN ? __builtin_amdgcn_readlane(ste_v, tl)
                           : (routed ? __builtin_amdgcn_readfirstlane(ste[tl]) : (tl == tA ? exA : exB));
     load_ej(e_x, nj, real, w, z);
@@ -1129,8 +1130,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
 
   // sum of the 8 waves' partials of one job (fixed order) and the store;
   // thread u of the half-workgroup holds row 4*(l/16) + i4 of column l%16
-  auto reduce = [&](int job, int pp, int jj) {
-    const int tl = job / NJ, nj = job - tl * NJ, ts = tl == tA ? 0 : 1;
+  auto reduce = [&](int ii, int pp, int jj) {  // ii: the workgroup's job index
+    const int job = job_of(ii);
+    const int tl = RDOWN ? ii : job / NJ, nj = RDOWN ? (int)blockIdx.x : job - tl * NJ, ts = tl == tA ? 0 : 1;
     const int u = tid & 255, l = u >> 2, i4 = u & 3, row = 4 * (l >> 4) + i4;
     const int orow = routed ? tok2a[tl * 16 + row] : (row < (ts == 0 ? nvalid0 : nvalid1) ? Rid[ts][row] : -1);
     if (orow < 0) return;
@@ -1178,7 +1180,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   auto pair_done = [&](int i) {  // jobs i - 1 and i are in LDS
     lds_barrier();
     const int jj = wave >> 2;
-    if (i - 1 + jj < n) reduce(job_of(i - 1 + jj), (i >> 1) & 1, jj);
+    if (i - 1 + jj < n) reduce(i - 1 + jj, (i >> 1) & 1, jj);
   };
   const int nfull = n / D * D;
   for (int g = 0; g < nfull; g += D) {
