@@ -1003,6 +1003,22 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   const int tA = IL ? 0 : lo / NJ, ntl = IL ? 1 : (hi - 1) / NJ - tA + 1;  // the range covers 1 or 2 tiles
   const int tB = ntl > 1 ? tA + 1 : tA;
   auto job_of = [&](int i) { return IL ? lo + i * (int)gridDim.x : lo + i; };
+  // a contiguous range covers at most two tiles: job i's tile and column
+  // from the range's first column nj0, without a run-time division per job
+  const int nj0 = IL ? 0 : lo - tA * NJ;
+  auto tile_col = [&](int i, int job, int& tl, int& nj) {
+    if constexpr (RDOWN) {  // job i is tile i of this workgroup's column block
+      tl = i;
+      nj = (int)blockIdx.x;
+    } else if constexpr (IL) {
+      tl = job / NJ;
+      nj = job - tl * NJ;
+    } else {
+      const int c = nj0 + i;
+      tl = c >= NJ ? tA + 1 : tA;
+      nj = c >= NJ ? c - NJ : c;
+    }
+  };
 
   // ---- experts and row ids of the range's tiles: scalar loads, issued
   // together; lane r16 keeps row r16 ----
@@ -1046,8 +1062,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   auto load = [&](int i, u32x4 (&w)[MT][NQ], uint32_t& z) {
     const bool real = i < n;
     const int job = job_of(real ? i : 0);
-    // routed down: job i is tile i of this workgroup's column block
-    const int tl = RDOWN ? (real ? i : 0) : job / NJ, nj = RDOWN ? (int)blockIdx.x : job - tl * NJ;
+    int tl, nj;
+    tile_col(real ? i : 0, job, tl, nj);
     const int e_x = RDOWN ? __builtin_amdgcn_readlane(ste_v, tl)
                           : (routed ? __builtin_amdgcn_readfirstlane(ste[tl]) : (tl == tA ? exA : exB));
     load_ej(e_x, nj, real, w, z);
@@ -1132,7 +1148,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // thread u of the half-workgroup holds row 4*(l/16) + i4 of column l%16
   auto reduce = [&](int ii, int pp, int jj) {  // ii: the workgroup's job index
     const int job = job_of(ii);
-    const int tl = RDOWN ? ii : job / NJ, nj = RDOWN ? (int)blockIdx.x : job - tl * NJ, ts = tl == tA ? 0 : 1;
+    int tl, nj;
+    tile_col(ii, job, tl, nj);
+    const int ts = tl == tA ? 0 : 1;
     const int u = tid & 255, l = u >> 2, i4 = u & 3, row = 4 * (l >> 4) + i4;
     const int orow = routed ? tok2a[tl * 16 + row] : (row < (ts == 0 ? nvalid0 : nvalid1) ? Rid[ts][row] : -1);
     if (orow < 0) return;
