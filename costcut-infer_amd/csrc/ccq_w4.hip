@@ -970,7 +970,10 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // slower)
   constexpr bool IL = EPI == EPI_STORE || RDOWN;  // routed down: gridDim.x = column blocks
   const int J = ntiles * NJ;
-  auto split = [&](int b) { return b == 0 ? 0 : max(0, (int)((int64_t)b * (J + lead) / gridDim.x) - lead); };
+  // (32-bit: b * (J + lead) < 256 * 2^23 for the schedules this kernel takes)
+  auto split = [&](int b) {
+    return b == 0 ? 0 : max(0, (int)((uint32_t)b * (uint32_t)(J + lead) / gridDim.x) - lead);
+  };
   const int lo = IL ? (int)blockIdx.x : split(blockIdx.x);
   const int hi = IL ? J : split(blockIdx.x + 1);
   // routed down: the combine of moe_combine_kernel for this block's 16
@@ -1744,6 +1747,9 @@ static void launch_stream_t(const W4SP& p, int nq, dim3 grid, hipStream_t st) {
 template <int EPI>
 static int launch_stream(const W4SP& p, int nq, int x_bf16, int s_bf16, int64_t tiles, hipStream_t st) {
   if (p.KT > 16 && (tiles != 1 || p.meta != nullptr)) return arg_error("w4 stream gemm: K > 2048 needs a single row tile");
+  // the kernel splits a schedule's jobs over the workgroups in 32-bit arithmetic
+  if ((p.meta != nullptr || p.logits != nullptr) && tiles * (p.N / 16) >= (1 << 23))
+    return arg_error("w4 stream gemm: %lld tiles x N=%d is too large a schedule", (long long)tiles, p.N);
   const int64_t jobs = tiles * (p.N / (EPI == EPI_SILU ? 16 : 16 * nq)), cus = device_cus();
   const dim3 grid((unsigned)(jobs < cus ? jobs : cus));
   if (x_bf16) {
