@@ -1055,8 +1055,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   if constexpr (!routed) {
     const int rA = rid[0] >= 0 ? rid[0] : __shfl(rid[0], 0, 64);
     const int rB = rid[1] >= 0 ? rid[1] : __shfl(rid[1], 0, 64);
-    load_frags(a, rA / p.row_div);
-    if constexpr (MT == 2) load_frags(b, rB / p.row_div);
+    const int rd = p.row_div;  // 1 for the down stage: no division
+    load_frags(a, rd == 1 ? rA : rA / rd);
+    if constexpr (MT == 2) load_frags(b, rd == 1 ? rB : rB / rd);
   }
 
   // routed down: lane l holds the expert of tile l (at most RD_MAXA tiles),
