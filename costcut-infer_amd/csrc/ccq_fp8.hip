@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void fp8_act_quant_kernel(const void* __restri
   const int64_t nblk = rows * KB;
   const int64_t stride = (int64_t)gridDim.x * 16;
   for (int64_t b = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; b < nblk; b += stride) {
-    const int64_t row = b / KB, kb = b - row * KB;
+    const int64_t row = (int64_t)((uint32_t)b / (uint32_t)KB), kb = b - row * KB;  // rows * KB < 2^31
     const int64_t c0 = kb * 128 + 8 * sub;
     float v[8];
 #pragma unroll
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void fp8_act_quant_vec_kernel(const void* __re
   const int64_t nblk = rows * KB;
   const int64_t stride = (int64_t)gridDim.x * 16;
   for (int64_t b = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; b < nblk; b += stride) {
-    const int64_t row = b / KB, kb = b - row * KB;
+    const int64_t row = (int64_t)((uint32_t)b / (uint32_t)KB), kb = b - row * KB;  // rows * KB < 2^31
     const int64_t c0 = kb * 128 + 8 * sub;
     float v[8];
     if constexpr (XT == CCQ_F32) {
@@ -1131,6 +1131,7 @@ static int grid_of(int64_t n, int block) {
 int launch_act_quant(const void* x, int x_dtype, int64_t ldx, int64_t rows, int64_t K, uint8_t* q, int64_t ldq,
                      float* s, int64_t lds_, hipStream_t st) {
   const int64_t KB = K / 128;
+  if (rows * KB >= (1LL << 31)) return arg_error("fp8 act quant: %lld rows x K/128=%lld too large", (long long)rows, (long long)KB);
   const dim3 grid(grid_of(rows * KB * 16, 256));
   if (aligned(x, 16) && ldx % (x_dtype == CCQ_F32 ? 4 : 8) == 0) {
     if (x_dtype == CCQ_BF16)

@@ -101,7 +101,8 @@ __device__ void align_side_work(const AlignSide& s, int64_t gt) {
   const int64_t g = gt >> 4;
   const int part = threadIdx.x & 15;
   const bool ok = g < s.M * s.KT;
-  const int64_t row = ok ? g / s.KT : 0, kt = ok ? g - row * s.KT : 0;
+  // (32-bit division: M * KT < 2^31, checked where the side work is set up)
+  const int64_t row = ok ? (int64_t)((uint32_t)g / (uint32_t)s.KT) : 0, kt = ok ? g - row * s.KT : 0;
   float acc = 0.f;
   if (ok) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(s.x) + row * s.ldx +

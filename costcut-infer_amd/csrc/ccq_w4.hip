@@ -1685,7 +1685,7 @@ __global__ __launch_bounds__(256) void row_group_sums_kernel(const AT* __restric
   const int64_t g = gt >> 4;
   const int part = threadIdx.x & 15;
   const bool ok = g < M * KT;
-  const int64_t row = ok ? g / KT : 0, kt = ok ? g - row * KT : 0;
+  const int64_t row = ok ? (int64_t)((uint32_t)g / (uint32_t)KT) : 0, kt = ok ? g - row * KT : 0;  // M * KT < 2^31
   float s = 0.f;
   if (ok) {
     const V v = *reinterpret_cast<const V*>(x + row * ldx + kt * 128 + part * 8);
@@ -1700,6 +1700,7 @@ __global__ __launch_bounds__(256) void row_group_sums_kernel(const AT* __restric
 static int launch_row_group_sums(const void* x, int x_bf16, int64_t ldx, int64_t M, int64_t K, float* out,
                                  int64_t ldo, hipStream_t st, int32_t* rows_out = nullptr, int64_t nrows_out = 0) {
   const int64_t KT = K / 128, threads = M * KT * 16 > nrows_out ? M * KT * 16 : nrows_out;
+  if (M * KT >= (1LL << 31)) return arg_error("row group sums: M=%lld x K/128=%lld too large", (long long)M, (long long)KT);
   const int64_t blocks = cdiv(threads, 256);
   if (x_bf16)
     launch(row_group_sums_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
