@@ -1002,7 +1002,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     if constexpr (RDOWN) combine();  // no routed assignment: zeros
     return;
   }
-  const int n = RDOWN ? ntiles : (IL ? (hi - lo + (int)gridDim.x - 1) / (int)gridDim.x : hi - lo);
+  const int n = RDOWN ? ntiles
+                      : (IL ? (hi - lo <= (int)gridDim.x ? 1 : (hi - lo + (int)gridDim.x - 1) / (int)gridDim.x)
+                            : hi - lo);
   const int tA = IL ? 0 : lo / NJ, ntl = IL ? 1 : (hi - 1) / NJ - tA + 1;  // the range covers 1 or 2 tiles
   const int tB = ntl > 1 ? tA + 1 : tA;
   auto job_of = [&](int i) { return IL ? lo + i * (int)gridDim.x : lo + i; };
@@ -1014,7 +1016,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
       tl = i;
       nj = (int)blockIdx.x;
     } else if constexpr (IL) {
-      tl = job / NJ;
+      tl = p.tiles == 1 ? 0 : job / NJ;  // dense rows: usually one tile
       nj = job - tl * NJ;
     } else {
       const int c = nj0 + i;
