@@ -791,6 +791,7 @@ __device__ void route_schedule(const W4SP& p, RouteSmem& rs) {
 }
 
 constexpr int WS_DEPTH = 2;  // jobs of weights in flight per wave (2 measured faster than 4 or 6)
+constexpr int WS_DEPTH_MT1 = 4;  // the same with one k-tile per wave (K <= 1024)
 // Routed down stage with the combine: at most RD_MAXA assignments (one
 // 16-row MFMA tile), RD_DEPTH jobs in flight per wave (a workgroup's jobs
 // are one per routed expert, so all of them at once for up to six experts)
@@ -816,7 +817,8 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // routed down stage with the combine (see W4SP): a workgroup's jobs are
   // one column block of each routed expert, all of them in flight at once
   constexpr bool RDOWN = ROUTE && EPI == EPI_ROWS;
-  constexpr int D = RDOWN ? RD_DEPTH : WS_DEPTH;
+  constexpr int D = RDOWN ? RD_DEPTH : (MT == 1 ? WS_DEPTH_MT1 : WS_DEPTH);
+  static_assert(MT != 1 || (EPI == EPI_ROWS && !ROUTE), "one k-tile per wave: the down stage on a schedule");
   static_assert(EPI != EPI_SILU || NQ == 2, "gate and up quads");
   static_assert(MT * NQ <= 4, "one scale/zero word per lane covers a wave's share of a job");
   static_assert(D % 2 == 0, "jobs are reduced in pairs");
@@ -1059,7 +1061,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
     const int rB = rid[1] >= 0 ? rid[1] : __shfl(rid[1], 0, 64);
     const int rd = p.row_div;  // 1 for the down stage: no division
     load_frags(a, rd == 1 ? rA : rA / rd);
-    if constexpr (MT == 2) load_frags(b, rd == 1 ? rB : rB / rd);
+    if constexpr (MT <= 2) load_frags(b, rd == 1 ? rB : rB / rd);  // MT = 1: kept in registers
   }
 
   // routed down: lane l holds the expert of tile l (at most RD_MAXA tiles),
@@ -1143,8 +1145,12 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
   // k-tiles per wave) skips its MFMAs, which frees the SIMD for the partner
   // wave
   const bool one_live = MT == 2 && wave + 8 >= KT;  // wave-uniform
+  // one k-tile per wave: a wave past K only writes zero partials
+  const bool dead = MT == 1 && wave >= KT;
   auto compute = [&](const u32x4 (&w)[MT][NQ], uint32_t z, int pp, int jj) {
-    if (one_live)
+    if (dead)
+      compute_mm(std::integral_constant<int, 0>{}, w, z, pp, jj);
+    else if (one_live)
       compute_mm(std::integral_constant<int, 1>{}, w, z, pp, jj);
     else
       compute_mm(std::integral_constant<int, MT>{}, w, z, pp, jj);
@@ -1197,6 +1203,12 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(const W4SP p) {
         for (int m = 0; m < MT; ++m)
 #pragma unroll
           for (int j = 0; j < 4; ++j) a[m][j] = xb[((wave * MT + m) * 4 + j) * 64 + lane];
+        group_sums();
+      }
+    } else if constexpr (MT == 1 && !routed) {
+      if (i == iB) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[0][j] = b[0][j];
         group_sums();
       }
     }
@@ -1738,9 +1750,15 @@ static void launch_stream_t(const W4SP& p, int nq, dim3 grid, hipStream_t st) {
       launch((w4_stream_kernel<AT, ST, EPI, 2, 2, true>), grid, block, 0, st, p);
     else
       launch((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
-  } else if (nq == 2)  // two quads: K <= 2048, two k-tiles per wave
+  } else if (nq == 2) {  // two quads: K <= 2048, two k-tiles per wave
+    if constexpr (EPI == EPI_ROWS) {
+      if (p.KT <= 8) {  // K <= 1024: one k-tile per wave, four jobs in flight
+        launch((w4_stream_kernel<AT, ST, EPI, 1, 2>), grid, block, 0, st, p);
+        return;
+      }
+    }
     launch((w4_stream_kernel<AT, ST, EPI, 2, 2>), grid, block, 0, st, p);
-  else if constexpr (EPI != EPI_SILU) {
+  } else if constexpr (EPI != EPI_SILU) {
     if (mt4)
       launch((w4_stream_kernel<AT, ST, EPI, 4, 1>), grid, block, 0, st, p);
     else
